@@ -1,0 +1,201 @@
+#!/usr/bin/env python3
+"""Throughput benchmark of the MI355X backend (one JSON line on stdout).
+
+Workload (the headline configuration that fits one GPU): the PP-OCRv6
+medium detector, fp32, batch 8 of 3x416x736 seeded-pixel images with seeded
+weights at the reference tensor shapes.  A step is one pass of the detector
+over the batch; inputs are resident in HBM before the timed region, which is
+``--steps`` back-to-back passes between two stream synchronisations.
+
+Alongside ``value`` the line carries:
+* ``roofline``: the dominant kernel (most device time per step), its
+  algorithmic FLOPs (2 x MACs) or bytes per step over its HIP-event-timed
+  duration (events recorded on the stream the kernels run on), against the
+  MI355X peak (fp32 matrix 157.3 TFLOP/s, HBM 8 TB/s);
+* ``cpu_baseline``: the C++ restatement of the reference CPU path (the
+  parity oracle) timed on this host on a bounded sample of the same workload;
+* ``also``: the other benchmark configurations, measured after the timed
+  region.
+"""
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import tempfile
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "ppocr-rs_amd"))
+
+import numpy as np  # noqa: E402
+
+import ppocr_hip  # noqa: E402
+import seeded  # noqa: E402
+
+METRIC = "detector images/s @416×736 + rec lines/s @48×320; % HBM/MFMA roofline"
+PEAK_F32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+TMP = pathlib.Path(tempfile.gettempdir()) / "ppocr_bench_models"
+
+
+def weights(kind, size):
+    TMP.mkdir(parents=True, exist_ok=True)
+    path = TMP / f"{kind}_{size}.safetensors"
+    if not path.exists():
+        seeded.write_weights(path, kind, size, seed=1 if kind == "det" else 2)
+    return path
+
+
+def load(gpu, kind, size, shape):
+    cls = ppocr_hip.Detector if kind == "det" else ppocr_hip.Recognizer
+    return cls.load(gpu, weights(kind, size), size, shape)
+
+
+def inputs(kind, shape, seed=7):
+    return seeded.seeded_batch(shape[0], shape[2], shape[3], seed, detector=(kind == "det"))
+
+
+def throughput(model, x, warmup, steps):
+    total_ms = model.benchmark_stream(x, warmup, steps)
+    return total_ms
+
+
+def roofline(stats):
+    """Dominant kernel instance: the one with the most device time per step."""
+    groups = {}
+    for s in stats:
+        g = groups.setdefault(s["kernel"], {"ms": 0.0, "flops": 0.0, "bytes": 0.0, "launches": 0, "bound": s["bound"]})
+        g["ms"] += s["avg_ms"]
+        g["flops"] += s["flops"]
+        g["bytes"] += s["bytes"]
+        g["launches"] += 1
+    name, g = max(groups.items(), key=lambda kv: kv[1]["ms"])
+    secs = g["ms"] * 1e-3
+    if g["bound"] == "mfma":
+        achieved = g["flops"] / secs / 1e12
+        peak, unit = PEAK_F32_TFLOPS, "TFLOP/s"
+    else:
+        achieved = g["bytes"] / secs / 1e9
+        peak, unit = PEAK_HBM_GBS, "GB/s"
+    total_ms = sum(v["ms"] for v in groups.values())
+    return {
+        "bound": "mfma" if g["bound"] == "mfma" else "hbm",
+        "achieved": round(achieved, 3),
+        "peak": peak,
+        "unit": unit,
+        "frac": round(achieved / peak, 4),
+        "traffic": None,
+        "kernel": name,
+        "launches_per_step": g["launches"],
+        "avg_launch_ms": round(g["ms"] / g["launches"], 5),
+        "flops_per_launch": g["flops"] / g["launches"],
+        "bytes_per_launch": g["bytes"] / g["launches"],
+        "share_of_device_time": round(g["ms"] / total_ms, 3) if total_ms else None,
+    }
+
+
+def cpu_baseline(kind, size, shape, budget_s=12.0):
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    threads = min(os.cpu_count() or 1, 16)
+    oracle.set_threads(threads)
+    model = oracle.Model(kind, weights(kind, size), size)
+    one = (1,) + tuple(shape[1:])
+    x = inputs(kind, one)
+    model.forward(x)  # warm-up
+    runs, t0 = 0, time.perf_counter()
+    while True:
+        model.forward(x)
+        runs += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or runs >= 30:
+            break
+    unit = "images/s" if kind == "det" else "lines/s"
+    return {"value": round(runs * one[0] / el, 3), "unit": unit, "cores": threads, "kind": "port",
+            "sample": f"{runs} single-image passes of the {size} {'detector' if kind == 'det' else 'recognizer'} "
+                      f"at {one}, C++ restatement of the reference CPU path (fp32, OpenMP)"}
+
+
+def also(gpu, warmup, steps):
+    out = {}
+    configs = [
+        ("det", "tiny", (1, 3, 416, 736)),
+        ("det", "small", (1, 3, 416, 736)),
+        ("det", "small", (8, 3, 416, 736)),
+        ("det", "medium", (1, 3, 416, 736)),
+        ("det", "tiny", (1, 3, 832, 1472)),
+        ("rec", "tiny", (64, 3, 48, 320)),
+        ("rec", "small", (64, 3, 48, 320)),
+        ("rec", "medium", (256, 3, 48, 320)),
+    ]
+    for kind, size, shape in configs:
+        key = f"{size}_{kind}_{shape[0]}x{shape[2]}x{shape[3]}"
+        try:
+            m = load(gpu, kind, size, shape)
+            x = inputs(kind, shape)
+            ms = throughput(m, x, warmup, steps)
+            m.close()
+            unit = "images/s" if kind == "det" else "lines/s"
+            out[key] = {"value": round(shape[0] * steps / (ms / 1e3), 2), "unit": unit,
+                        "ms_per_step": round(ms / steps, 4)}
+        except Exception as e:  # report, keep going
+            out[key] = {"error": str(e)}
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extra", action="store_true", help="skip the other configurations")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the detector/recognizer path has no multi-GPU form in this build "
+              "(independent images shard across GPUs without communication); run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    kind, size, shape = "det", "medium", (8, 3, 416, 736)
+    gpu = ppocr_hip.Gpu(0)
+    model = load(gpu, kind, size, shape)
+    x = inputs(kind, shape)
+    total_ms = throughput(model, x, args.warmup, args.steps)
+    ms_per_step = total_ms / args.steps
+    value = shape[0] * args.steps / (total_ms / 1e3)
+    stats = model.profile(x, runs=max(3, min(args.steps, 10)))
+    roof = roofline(stats)
+    model.close()
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded uniform RGB8 pixels (BGR-normalised as the reference preprocess), "
+                "seeded weights at the reference tensor names/shapes",
+        "config": {"workload": "PP-OCRv6 medium detector, fp32, batch 8, input 8x3x416x736",
+                   "model_size": "medium", "batch": shape[0], "height": shape[2], "width": shape[3]},
+        "roofline": roof,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(kind, size, shape)
+    if not args.no_extra:
+        line["also"] = also(gpu, args.warmup, max(5, args.steps // 2))
+    gpu.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,162 @@
+/*
+ * ppocr_hip.h — C ABI of the MI355X (gfx950) backend for the PP-OCRv6
+ * detector and recognizer.
+ *
+ * This is the drop-in boundary for the reference's `ppocr_rs::gpu` direct
+ * model API (src/gpu/mod.rs:3-13).  Every entry point names the reference
+ * item it replaces.  Plain pointers and sizes only; no exception or abort
+ * crosses it; the library owns all device memory.  A handle may be used from
+ * any thread but not concurrently: forward calls serialise on a per-context
+ * mutex, as the reference's `Mutex<SharedWorkspace>` does
+ * (src/gpu/runtime.rs:75, :1753-1758).
+ */
+#ifndef PPOCR_HIP_H
+#define PPOCR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes, one per variant of the reference `gpu::Error`
+ * (src/gpu/error.rs:9-45). */
+typedef enum ppocr_status {
+  PPOCR_OK = 0,
+  PPOCR_ERR_READ_FILE = 1,
+  PPOCR_ERR_SAFETENSORS = 2,
+  PPOCR_ERR_TENSOR_NOT_FOUND = 3,
+  PPOCR_ERR_UNSUPPORTED_DTYPE = 4,
+  PPOCR_ERR_SHAPE_MISMATCH = 5,
+  PPOCR_ERR_TENSOR_SIZE_OVERFLOW = 6,
+  PPOCR_ERR_TENSOR_BYTE_LENGTH = 7,
+  PPOCR_ERR_INVALID_TENSOR_RANGE = 8,
+  PPOCR_ERR_INVALID_MODEL = 9,
+  PPOCR_ERR_INVALID_INPUT = 10,
+  PPOCR_ERR_GPU = 11
+} ppocr_status;
+
+/* `ModelSize` (src/models.rs), in the reference's declaration order. */
+typedef enum ppocr_model_size {
+  PPOCR_SIZE_MEDIUM = 0,
+  PPOCR_SIZE_SMALL = 1,
+  PPOCR_SIZE_TINY = 2
+} ppocr_model_size;
+
+/* Activation/weight storage precision.  F32 is the reference's arithmetic;
+ * BF16 keeps bf16 weights and activations with fp32 accumulation. */
+typedef enum ppocr_precision { PPOCR_F32 = 0, PPOCR_BF16 = 1 } ppocr_precision;
+
+typedef struct ppocr_hip_ctx ppocr_hip_ctx;     /* `gpu::Gpu` */
+typedef struct ppocr_hip_model ppocr_hip_model; /* `gpu::Detector` / `gpu::Recognizer` */
+typedef struct ppocr_hip_image ppocr_hip_image; /* `gpu::GpuImage` */
+
+/* Message of the last failed call on this thread (empty when none). */
+const char* ppocr_hip_last_error(void);
+
+/* Replaces `Gpu::new` (src/gpu/runtime.rs:94-167): opens `device`, creates
+ * the stream and the shared activation arena. */
+ppocr_status ppocr_hip_create(int device, ppocr_hip_ctx** out);
+void ppocr_hip_destroy(ppocr_hip_ctx* ctx);
+
+/* Replaces `Detector::load` (src/gpu/model.rs:50-93): loads a safetensors
+ * file, checks the tier's tensor count (350/271/271), folds BatchNorm, packs
+ * the weights, and plans the graph for the fixed input shape `nchw`
+ * ([N, 3, H, W], N > 0, H and W >= 32 and divisible by 32,
+ * src/gpu/model.rs:268-276). */
+ppocr_status ppocr_hip_detector_load(ppocr_hip_ctx* ctx, const char* safetensors_path, ppocr_model_size size,
+                                     const size_t nchw[4], ppocr_precision precision, ppocr_hip_model** out);
+
+/* Replaces `Recognizer::load` / `load_with_shared_weights`
+ * (src/gpu/model.rs:156-220): [N, 3, 48, W] with W >= 32 and divisible by 4
+ * (src/gpu/model.rs:278-286).  When `share_weights` is a recognizer loaded
+ * from the same file, its device weights are reused. */
+ppocr_status ppocr_hip_recognizer_load(ppocr_hip_ctx* ctx, const char* safetensors_path, ppocr_model_size size,
+                                       const size_t nchw[4], ppocr_precision precision,
+                                       const ppocr_hip_model* share_weights, ppocr_hip_model** out);
+
+void ppocr_hip_model_free(ppocr_hip_model* model);
+
+/* Output shape of `ModelOutput` (src/gpu/model.rs:37-41): detector
+ * [N, 1, H, W] (rank 4), recognizer [N, T, V] (rank 3). */
+ppocr_status ppocr_hip_output_shape(const ppocr_hip_model* model, size_t shape[4], size_t* rank);
+
+/* Replaces `Detector::forward` / `Recognizer::forward`
+ * (src/gpu/model.rs:95-114, :222-237): host NCHW float input of exactly the
+ * planned shape; writes the compact output (detector sigmoid probabilities,
+ * recognizer softmax probabilities) into `out` (capacity `out_cap` floats).
+ * Non-finite input or output is an error, as src/gpu/runtime.rs:1979-1983,
+ * :2217-2219. */
+ppocr_status ppocr_hip_forward(ppocr_hip_model* model, const float* nchw, size_t len, float* out, size_t out_cap);
+
+/* Replaces `Gpu::upload_rgb` (src/gpu/runtime.rs:174-229): RGB8, row-major
+ * HWC, `width * height * 3` bytes. */
+ppocr_status ppocr_hip_upload_rgb(ppocr_hip_ctx* ctx, uint32_t width, uint32_t height, const uint8_t* rgb,
+                                  size_t len, ppocr_hip_image** out);
+void ppocr_hip_image_free(ppocr_hip_image* image);
+
+/* Replaces `Detector::forward_image` / `Recognizer::forward_image` with
+ * `ImagePreprocess` (src/gpu/model.rs:116-138, :239-256,
+ * src/gpu/runtime.rs:52-70, :2086-2155).  The preprocessing follows the
+ * reference CPU path (src/preprocess.rs:78-123), including the integer
+ * rounding of the bilinear sample.  `corners` holds N quads of four (x, y)
+ * source points (top-left, top-right, bottom-right, bottom-left);
+ * `content_widths` holds N widths (NULL: the full canvas).  Unlike the
+ * reference, whose device path accepts N = 1 only (src/gpu/runtime.rs:2016),
+ * every crop of a recognizer batch is rectified on the device. */
+ppocr_status ppocr_hip_forward_image(ppocr_hip_model* model, const ppocr_hip_image* image, const float* corners,
+                                     const size_t* content_widths, size_t n, float* out, size_t out_cap);
+
+/* Device preprocessing alone (`prepare_detector` / `prepare_recognizer`,
+ * src/preprocess.rs:37-76): writes [3, canvas_h, canvas_w] NCHW floats,
+ * BGR-normalised with the detector (`detector` != 0) or recognizer
+ * statistics, columns >= content_width zero. */
+ppocr_status ppocr_hip_preprocess(ppocr_hip_ctx* ctx, const ppocr_hip_image* image, const float corners[8],
+                                  size_t canvas_w, size_t canvas_h, size_t content_width, int detector,
+                                  float* out_nchw);
+
+/* Replaces `Detector::benchmark` / `Recognizer::benchmark`
+ * (src/gpu/model.rs:140-148, src/gpu/runtime.rs:1798-1830): uploads once,
+ * runs `warmup` untimed passes, then `runs` timed passes, each timed from
+ * launch to completion; writes one duration in milliseconds per run. */
+ppocr_status ppocr_hip_benchmark(ppocr_hip_model* model, const float* nchw, size_t len, size_t warmup, size_t runs,
+                                 double* samples_ms);
+
+/* Throughput form of the benchmark: inputs already resident in HBM,
+ * `runs` passes launched back to back and synchronised once; writes the
+ * total elapsed milliseconds.  No counterpart in the reference, which
+ * synchronises every pass. */
+ppocr_status ppocr_hip_benchmark_stream(ppocr_hip_model* model, const float* nchw, size_t len, size_t warmup,
+                                        size_t runs, double* total_ms);
+
+/* Per-kernel timing record; replaces the PPOCR_GPU_PROFILE timestamp report
+ * (src/gpu/runtime.rs:1832-1933).  `flops` and `bytes` are the algorithmic
+ * work of one launch (2 x MACs; inputs + weights + outputs read or written
+ * once, logical channels). */
+typedef struct ppocr_kernel_stat {
+  char name[64];
+  char kernel[32];
+  double avg_ms;
+  double flops;
+  double bytes;
+  int bound; /* 0: HBM-bound, 1: matrix-core bound */
+} ppocr_kernel_stat;
+
+/* Runs `runs` passes with a HIP event around every launch (on the stream the
+ * kernels run on) and reports the mean duration per launch.  `count`
+ * receives the number of launches in one pass; at most `cap` are written. */
+ppocr_status ppocr_hip_profile(ppocr_hip_model* model, const float* nchw, size_t len, size_t runs,
+                               ppocr_kernel_stat* stats, size_t cap, size_t* count);
+
+/* Memory report (PPOCR_GPU_MEMORY_REPORT, src/gpu/runtime.rs:1486-1492,
+ * :1737-1742): arena bytes of this model's plan, the sum of its buffers
+ * without reuse, and device weight bytes. */
+ppocr_status ppocr_hip_memory_report(const ppocr_hip_model* model, size_t* arena_bytes, size_t* unplanned_bytes,
+                                     size_t* weight_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PPOCR_HIP_H */

@@ -1,0 +1,244 @@
+"""ctypes wrapper of the CPU parity oracle (test infrastructure only).
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's CPU-baseline leg load
+this module, as the checker or the CPU baseline.  The oracle restates the
+reference CPU path; see oracle.cpp for the per-function citations.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+SIZE_CODE = {"medium": 0, "small": 1, "tiny": 2}
+ACT = {"none": 0, "relu": 1, "gelu": 2, "silu": 3, "hsig6": 4, "hsig5": 5, "hswish": 6, "sigmoid": 7}
+
+_lib = None
+_F = ctypes.POINTER(ctypes.c_float)
+_I = ctypes.POINTER(ctypes.c_int)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"oracle library not built: {LIB_PATH} (run make -C oracle)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.oracle_last_error.restype = ctypes.c_char_p
+        L.oracle_detector_load.restype = ctypes.c_void_p
+        L.oracle_detector_load.argtypes = [ctypes.c_char_p, ctypes.c_int]
+        L.oracle_recognizer_load.restype = ctypes.c_void_p
+        L.oracle_recognizer_load.argtypes = [ctypes.c_char_p, ctypes.c_int]
+        L.oracle_model_free.argtypes = [ctypes.c_void_p]
+        L.oracle_forward.argtypes = [ctypes.c_void_p, _F, _I, _F, ctypes.c_size_t, _I]
+        L.oracle_erf.restype = ctypes.c_float
+        L.oracle_erf.argtypes = [ctypes.c_float]
+        L.oracle_act.restype = ctypes.c_float
+        L.oracle_act.argtypes = [ctypes.c_int, ctypes.c_float]
+        L.oracle_residual_mul.restype = ctypes.c_float
+        L.oracle_residual_mul.argtypes = [ctypes.c_float, ctypes.c_float]
+        L.oracle_layer_norm.argtypes = [_F, _F, _F, ctypes.c_int, ctypes.c_float]
+        L.oracle_softmax.argtypes = [_F, ctypes.c_int]
+        L.oracle_linear.argtypes = [_F, ctypes.c_long, ctypes.c_int, _F, ctypes.c_int, _F, ctypes.c_int,
+                                    ctypes.c_int, _F]
+        L.oracle_set_threads.argtypes = [ctypes.c_int]
+        _lib = L
+    return _lib
+
+
+def _f(a):
+    return a.ctypes.data_as(_F)
+
+
+def _i(a):
+    return a.ctypes.data_as(_I)
+
+
+def _check(rc):
+    if rc != 0:
+        raise RuntimeError(lib().oracle_last_error().decode())
+
+
+def set_threads(n):
+    lib().oracle_set_threads(int(n))
+
+
+class Model:
+    """A loaded oracle detector or recognizer."""
+
+    def __init__(self, kind, path, size):
+        L = lib()
+        load = L.oracle_detector_load if kind == "det" else L.oracle_recognizer_load
+        self.handle = load(str(path).encode(), SIZE_CODE[size])
+        if not self.handle:
+            raise RuntimeError(L.oracle_last_error().decode())
+        self.kind = kind
+        self.size = size
+
+    def output_len(self, shape):
+        n, _, h, w = shape
+        if self.kind == "det":
+            return n * h * w
+        classes = 6906 if self.size == "tiny" else 18710
+        return n * (w // 4 // 2 + 1) * classes
+
+    def forward(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        shape = np.array(x.shape, dtype=np.int32)
+        cap = self.output_len(x.shape)
+        out = np.empty(cap, dtype=np.float32)
+        oshape = np.zeros(4, dtype=np.int32)
+        _check(lib().oracle_forward(ctypes.c_void_p(self.handle), _f(x), _i(shape), _f(out), cap, _i(oshape)))
+        dims = [int(d) for d in oshape if d > 0]
+        return out[: int(np.prod(dims))].reshape(dims)
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            lib().oracle_model_free(ctypes.c_void_p(self.handle))
+            self.handle = None
+
+
+def preprocess(rgb, corners, canvas_w, canvas_h, content_w, detector=True):
+    rgb = np.ascontiguousarray(rgb, dtype=np.uint8)
+    sh, sw = rgb.shape[:2]
+    c = np.ascontiguousarray(np.asarray(corners, dtype=np.float32).reshape(8))
+    out = np.empty((3, canvas_h, canvas_w), dtype=np.float32)
+    _check(lib().oracle_preprocess(rgb.ctypes.data_as(ctypes.c_void_p), sw, sh, _f(c), canvas_w, canvas_h,
+                                   content_w, int(detector), _f(out)))
+    return out
+
+
+def conv2d(x, w, bias=None, stride=(1, 1), pads=(0, 0, 0, 0), groups=1, act="none"):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, c, h, wd = x.shape
+    co, _, kh, kw = w.shape
+    ho = (h + pads[0] + pads[2] - kh) // stride[0] + 1
+    wo = (wd + pads[1] + pads[3] - kw) // stride[1] + 1
+    out = np.empty((n, co, ho, wo), dtype=np.float32)
+    oshape = np.zeros(4, dtype=np.int32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    _check(lib().oracle_conv2d(_f(x), _i(np.array(x.shape, np.int32)), _f(w), _i(np.array(w.shape, np.int32)),
+                               None if b is None else _f(b), int(stride[0]), int(stride[1]),
+                               _i(np.array(pads, np.int32)), int(groups), ACT[act], _f(out), _i(oshape)))
+    return out
+
+
+def conv_transpose2x2(x, w, bias=None):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, c, h, wd = x.shape
+    out = np.empty((n, w.shape[1], 2 * h, 2 * wd), dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    _check(lib().oracle_conv_transpose2x2(_f(x), _i(np.array(x.shape, np.int32)), _f(w),
+                                          _i(np.array(w.shape, np.int32)), None if b is None else _f(b), _f(out)))
+    return out
+
+
+def linear(x, w, bias=None, act="none", softmax=False):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    k = w.shape[1]
+    rows = x.size // k
+    out = np.empty(x.shape[:-1] + (w.shape[0],), dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    _check(lib().oracle_linear(_f(x), rows, k, _f(w), w.shape[0], None if b is None else _f(b), ACT[act],
+                               int(softmax), _f(out)))
+    return out
+
+
+def softmax(v):
+    v = np.array(v, dtype=np.float32)
+    lib().oracle_softmax(_f(v), v.size)
+    return v
+
+
+def layer_norm(v, w, b, eps):
+    v = np.array(v, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    lib().oracle_layer_norm(_f(v), _f(w), _f(b), v.size, ctypes.c_float(eps))
+    return v
+
+
+def erf(x):
+    return lib().oracle_erf(float(x))
+
+
+def act(name, x):
+    return lib().oracle_act(ACT[name], float(x))
+
+
+def residual_mul(v, g):
+    return lib().oracle_residual_mul(float(v), float(g))
+
+
+def max_pool_same(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    _check(lib().oracle_max_pool_same(_f(x), _i(np.array(x.shape, np.int32)), _f(out)))
+    return out
+
+
+def avg_pool_3x2(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, c, h, w = x.shape
+    out = np.empty((n, c, (h - 3) // 3 + 1, (w - 2) // 2 + 1), dtype=np.float32)
+    oshape = np.zeros(4, dtype=np.int32)
+    _check(lib().oracle_avg_pool_3x2(_f(x), _i(np.array(x.shape, np.int32)), _f(out), _i(oshape)))
+    return out
+
+
+def upsample_add(feature, upper, scale):
+    f = np.array(feature, dtype=np.float32)
+    u = np.ascontiguousarray(upper, dtype=np.float32)
+    _check(lib().oracle_upsample_add(_f(f), _i(np.array(f.shape, np.int32)), _f(u),
+                                     _i(np.array(u.shape, np.int32)), int(scale)))
+    return f
+
+
+def upsample_cat(features, scales):
+    feats = [np.ascontiguousarray(f, dtype=np.float32) for f in features]
+    ptrs = (ctypes.POINTER(ctypes.c_float) * len(feats))(*[_f(f) for f in feats])
+    shapes = np.array([f.shape for f in feats], dtype=np.int32).reshape(-1)
+    n, _, h, w = feats[0].shape
+    c = sum(f.shape[1] for f in feats)
+    out = np.empty((n, c, h * scales[0], w * scales[0]), dtype=np.float32)
+    oshape = np.zeros(4, dtype=np.int32)
+    _check(lib().oracle_upsample_cat(len(feats), ptrs, _i(shapes), _i(np.array(scales, np.int32)), _f(out),
+                                     _i(oshape)))
+    return out
+
+
+def attention_context(qkv, heads):
+    qkv = np.ascontiguousarray(qkv, dtype=np.float32)
+    b, t, h3 = qkv.shape
+    out = np.empty((b, t, h3 // 3), dtype=np.float32)
+    _check(lib().oracle_attention(_f(qkv), b, t, h3 // 3, heads, _f(out)))
+    return out
+
+
+def factor_rank_one(w):
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    co, ci, k, _ = w.shape
+    dw = np.empty((ci, 1, k, k), dtype=np.float32)
+    pw = np.empty((co, ci, 1, 1), dtype=np.float32)
+    _check(lib().oracle_factor_rank_one(_f(w), ci, co, k, _f(dw), _f(pw)))
+    return dw, pw
+
+
+def fuse_intraclass(sym, sb, vert, vb, hor, hb):
+    sym = np.array(sym, dtype=np.float32)
+    sb = np.array(sb, dtype=np.float32)
+    co, ci, k, _ = sym.shape
+    _check(lib().oracle_fuse_intraclass(_f(sym), _f(sb), _f(np.ascontiguousarray(vert, np.float32)),
+                                        _f(np.ascontiguousarray(vb, np.float32)),
+                                        _f(np.ascontiguousarray(hor, np.float32)),
+                                        _f(np.ascontiguousarray(hb, np.float32)), co, ci, k))
+    return sym, sb

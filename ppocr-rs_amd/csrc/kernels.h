@@ -1,0 +1,132 @@
+// Kernel parameter blocks and host launchers of the gfx950 kernels.
+//
+// Activations live in one HBM arena in NHWC order: a tensor view is
+// (pointer to channel 0 of pixel 0, N, H, W, C, pixel stride).  A pixel
+// stride larger than C lets a producer write one channel slice of a wider
+// tensor (the channel concats of the stem and the FPN are never copied).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace ppocr {
+
+// Activation codes: the epilogue set of the reference
+// (src/gpu/runtime.rs:302-311, src/cpu/kernels/mod.rs:2376-2390).
+enum Act : int {
+  ACT_NONE = 0,
+  ACT_RELU = 1,
+  ACT_GELU = 2,
+  ACT_SILU = 3,
+  ACT_HSIG6 = 4,  // clamp(x/6 + 0.5, 0, 1): LCNet SE gate
+  ACT_HSIG5 = 5,  // clamp(x/5 + 0.5, 0, 1): neck SE gate
+  ACT_HSWISH = 6,
+  ACT_SIGMOID = 7,
+};
+
+// Implicit-GEMM convolution on the fp32 matrix cores.
+//   out[m, n] = act(sum_k A[m, k] * Wt[k, n] + bias[n])  (+ epilogue terms)
+// m: output pixel (n_img, oy, ox); n: output channel; k = (ky*kw + kx)*C + c.
+struct ConvParams {
+  const float* in;
+  int N, H, W, C, in_ps;
+  float* out;
+  int Ho, Wo, Co, out_ps;
+  const float* wt;  // packed [K][ldw], zero beyond Co
+  int ldw;
+  const float* bias;  // [Co] or null
+  int kh, kw, sh, sw, pt, pl;
+  int act;
+  const float* in_gate;   // [N][C]: A[m, k] = x * g[n_img, c] (SE prologue)
+  const float* res;       // residual added after the activation
+  int res_ps;
+  const float* res_gate;  // [N][Co]: residual term is res * g
+  const float* up;        // nearest-upsample-add source [N, Ho/up_s, Wo/up_s, Co]
+  int up_s, up_ps;
+  int rep;   // write each output pixel as a rep x rep block (upsample on write)
+  int mode;  // 0: conv; 1: 2x2 stride-2 transposed conv (columns j = tap*Co + o)
+  int out_h, out_w;  // dims of the tensor `out` points into (rep / mode 1)
+};
+
+// Depthwise k x k convolution (groups == C), 4 channels per lane.
+struct DwParams {
+  const float* in;
+  int N, H, W, C, in_ps;
+  float* out;
+  int Ho, Wo, out_ps;
+  const float* wt;  // [kh*kw][C]
+  const float* bias;
+  int kh, kw, sh, sw, pt, pl;
+  int act;
+  const float* res;  // out = res + act(dw(x) + b)
+  int res_ps;
+};
+
+// Squeeze-excitation gate: g[n, c] = gate_act(W2 relu(W1 mean(x) + b1) + b2).
+struct SeParams {
+  const float* in;
+  int N, HW, C, in_ps;
+  float* partial;  // [N][P][C] partial sums
+  int P;           // pixel chunks per image
+  const float* w1;  // [Cr][C]
+  const float* b1;
+  const float* w2;  // [C][Cr]
+  const float* b2;
+  int Cr;
+  int gate_act;
+  float* gate;  // [N][C]
+};
+
+void launch_conv(const ConvParams& p, hipStream_t s);
+// Name of the tile instance launch_conv picks for M rows x `cols` columns.
+const char* conv_tile_name(int M, int cols);
+void launch_depthwise(const DwParams& p, hipStream_t s);
+void launch_se(const SeParams& p, hipStream_t s);
+
+// NCHW (3 planes) -> NHWC with 4 channels (fourth channel zero).
+void launch_nchw_to_nhwc4(const float* in, float* out, int N, int H, int W, hipStream_t s);
+
+// Max pool 2x2, stride 1, pads (0,0,1,1) into a channel slice.
+void launch_maxpool_same(const float* in, int N, int H, int W, int C, int in_ps, float* out, int out_ps,
+                         hipStream_t s);
+
+// out = x + x*g[n,c] (two roundings) [+ upper[y/2, x/2]], written as
+// rep x rep blocks (rep = 1: plain) into a tensor of pixel stride out_ps.
+void launch_gate_residual(const float* in, int N, int H, int W, int C, int in_ps, const float* gate,
+                          const float* upper, int up_ps, float* out, int out_ps, int rep, hipStream_t s);
+
+// Average pool, kernel [3,2], stride [3,2], count_include_pad = false.
+void launch_avgpool32(const float* in, int N, int H, int W, int C, int in_ps, float* out, int Ho, int Wo,
+                      hipStream_t s);
+
+// Fused detector head tail: 2x2 s2 deconv (+bias, ReLU) then 2x2 s2 deconv to
+// one channel (+bias) and sigmoid; in [N, H, W, Ch] -> out [N, 4H, 4W].
+void launch_db_head_up(const float* in, int N, int H, int W, int Ch, int in_ps, const float* wu, const float* bu,
+                       const float* wf, float bf, float* out, hipStream_t s);
+
+// Row LayerNorm over C (eps), optional residual added after: out = LN(x) + r.
+void launch_layer_norm(const float* in, int rows, int C, const float* w, const float* b, float eps,
+                       const float* res, float* out, hipStream_t s);
+
+// Multi-head attention core on qkv [B, T, 3*hidden] -> ctx [B, T, hidden].
+void launch_attention(const float* qkv, int B, int T, int hidden, int heads, float* out, hipStream_t s);
+
+// In-place row softmax over `cols` columns.
+void launch_softmax_rows(float* x, long rows, int cols, hipStream_t s);
+
+// Quad-bilinear RGB8 sampling -> rounded -> normalised, written either as
+// NHWC4 (nhwc = 1, channel 3 zero) or NCHW planes.  One geometry per image:
+// corners [N][8], content widths [N].
+struct PreParams {
+  const uint32_t* rgb;  // packed RGB8 bytes, 4-byte aligned
+  int sw, sh;
+  const float* corners;
+  const int* content_w;
+  int N, cw, ch;
+  float scale[3], bias[3];
+  float* out;
+  int nhwc;
+};
+void launch_preprocess(const PreParams& p, hipStream_t s);
+
+}  // namespace ppocr

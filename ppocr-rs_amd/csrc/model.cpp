@@ -1,0 +1,992 @@
+// Plan builders: PP-OCRv6 detectors (tiny/small/medium) and recognizers
+// (tiny/small/medium) as lists of gfx950 kernel launches over NHWC views of
+// one activation arena.
+//
+// The architecture follows the reference CPU model (src/cpu/model.rs); the
+// load-time transforms are the reference's: BatchNorm folding
+// (src/cpu/model.rs:371-407, :1440-1477), rank-one factorisation of the
+// medium neck's 9x9 convs (:221-369) and intraclass kernel fusion
+// (:819-888).  Where the reference's WGSL path runs several kernels, this
+// plan fuses: SE gates are applied while the next 1x1 conv gathers its input
+// and again on its residual, FPN top-down adds and upsample-concats happen in
+// the producers' epilogues, and the DB head's two transposed convs and the
+// sigmoid run as one kernel.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "runtime.h"
+
+namespace ppocr {
+namespace {
+
+constexpr size_t NOW = SIZE_MAX;
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct ConvW {
+  size_t w = NOW, b = NOW;
+  int ldw = 0;
+  int ci = 0, ci_pad = 0, co = 0, kh = 1, kw = 1, sh = 1, sw = 1, pt = 0, pl = 0, pb = 0, pr = 0;
+  bool deconv = false;
+};
+
+struct DwW {
+  size_t w = NOW, b = NOW;
+  int c = 0, kh = 1, kw = 1, sh = 1, sw = 1, pt = 0, pl = 0, pb = 0, pr = 0;
+};
+
+struct SeW {
+  size_t w1 = NOW, b1 = NOW, w2 = NOW, b2 = NOW;
+  int c = 0, cr = 0, act = ACT_HSIG6;
+};
+
+struct Epi {
+  int act = ACT_NONE;
+  const View* in_gate = nullptr;
+  const View* res = nullptr;
+  const View* res_gate = nullptr;
+  const View* up = nullptr;
+  int up_s = 2;
+  int rep = 1;
+  const View* dst = nullptr;  // write into this (pre-allocated) view
+};
+
+struct BlockSpec {
+  int ci, co, sh, sw;
+  bool se;
+};
+
+class Builder {
+ public:
+  Builder(const SafeTensors& st, Plan& plan) : st_(st), plan_(plan) {}
+
+  // ------------------------------------------------------------ weights
+  HostTensor get(const std::string& name, const std::vector<int>& shape) { return st_.get(name, shape); }
+
+  // s = gamma / sqrt(var + 1e-5); W' = W s per output channel;
+  // b' = (b - mean) s + beta (src/cpu/model.rs:371-407).  `out_stride`
+  // and `inner` describe where output channel o's weights live:
+  // W[o * out_stride + i * inner_stride + j] for the transposed layout.
+  void fold_bn(std::vector<float>& W, std::vector<float>& b, const std::string& norm, int co, bool transposed = false,
+               int ci = 0) {
+    HostTensor g = get(norm + ".weight", {co}), be = get(norm + ".bias", {co});
+    HostTensor mu = get(norm + ".running_mean", {co}), var = get(norm + ".running_var", {co});
+    if (b.empty()) b.assign(co, 0.0f);
+    if (!transposed) {
+      size_t row = W.size() / co;
+      for (int o = 0; o < co; ++o) {
+        float s = g.v[o] / std::sqrt(var.v[o] + 1e-5f);
+        for (size_t i = 0; i < row; ++i) W[o * row + i] *= s;
+        b[o] = (b[o] - mu.v[o]) * s + be.v[o];
+      }
+    } else {  // IOHW [ci][co][k]
+      size_t k = W.size() / ((size_t)ci * co);
+      for (int o = 0; o < co; ++o) {
+        float s = g.v[o] / std::sqrt(var.v[o] + 1e-5f);
+        for (int i = 0; i < ci; ++i)
+          for (size_t t = 0; t < k; ++t) W[((size_t)i * co + o) * k + t] *= s;
+        b[o] = (b[o] - mu.v[o]) * s + be.v[o];
+      }
+    }
+  }
+
+  size_t put(const std::vector<float>& v) {
+    size_t off = round_up(plan_.weights.size(), 64);
+    plan_.weights.resize(off + v.size(), 0.0f);
+    std::copy(v.begin(), v.end(), plan_.weights.begin() + off);
+    return off;
+  }
+
+  // OIHW [co][ci][kh][kw] -> [k = (ky*kw + kx)*ci_pad + c][ldw].
+  ConvW pack_conv(const std::vector<float>& W, const std::vector<float>& b, int ci, int co, int kh, int kw, int sh,
+                  int sw, std::vector<int> pads, int ci_pad = 0) {
+    ConvW c;
+    c.ci = ci;
+    c.ci_pad = ci_pad ? ci_pad : ci;
+    c.co = co;
+    c.kh = kh, c.kw = kw, c.sh = sh, c.sw = sw;
+    c.pt = pads[0], c.pl = pads[1], c.pb = pads[2], c.pr = pads[3];
+    c.ldw = (int)round_up(co, 4);
+    size_t K = (size_t)kh * kw * c.ci_pad;
+    std::vector<float> packed(K * c.ldw, 0.0f);
+    for (int o = 0; o < co; ++o)
+      for (int i = 0; i < ci; ++i)
+        for (int ky = 0; ky < kh; ++ky)
+          for (int kx = 0; kx < kw; ++kx)
+            packed[((size_t)(ky * kw + kx) * c.ci_pad + i) * c.ldw + o] = W[(((size_t)o * ci + i) * kh + ky) * kw + kx];
+    c.w = put(packed);
+    if (!b.empty()) c.b = put(b);
+    return c;
+  }
+
+  // IOHW [ci][co][2][2] transposed conv -> [k = c][j = tap*co + o].
+  ConvW pack_deconv(const std::vector<float>& W, const std::vector<float>& b, int ci, int co) {
+    ConvW c;
+    c.ci = c.ci_pad = ci;
+    c.co = co;
+    c.deconv = true;
+    c.ldw = (int)round_up(4 * co, 4);
+    std::vector<float> packed((size_t)ci * c.ldw, 0.0f);
+    for (int i = 0; i < ci; ++i)
+      for (int o = 0; o < co; ++o)
+        for (int t = 0; t < 4; ++t) packed[(size_t)i * c.ldw + t * co + o] = W[((size_t)i * co + o) * 4 + t];
+    c.w = put(packed);
+    if (!b.empty()) c.b = put(b);
+    return c;
+  }
+
+  // [c][kh*kw] -> [kh*kw][c].
+  DwW pack_dw(const std::vector<float>& W, const std::vector<float>& b, int c, int kh, int kw, int sh, int sw,
+              std::vector<int> pads) {
+    DwW d;
+    d.c = c, d.kh = kh, d.kw = kw, d.sh = sh, d.sw = sw;
+    d.pt = pads[0], d.pl = pads[1], d.pb = pads[2], d.pr = pads[3];
+    std::vector<float> packed((size_t)kh * kw * c);
+    for (int ch = 0; ch < c; ++ch)
+      for (int t = 0; t < kh * kw; ++t) packed[(size_t)t * c + ch] = W[(size_t)ch * kh * kw + t];
+    d.w = put(packed);
+    if (!b.empty()) d.b = put(b);
+    return d;
+  }
+
+  // Conv2d::load (src/cpu/model.rs:89-107) and Conv2d::load_bn (:110-131).
+  ConvW conv_w(const std::string& p, int ci, int co, int kh, int kw, int sh, int sw, std::vector<int> pads, bool bias,
+               const std::string& norm = "", int ci_pad = 0) {
+    std::string wname = norm.empty() ? p + ".weight" : p + ".convolution.weight";
+    std::string bname = norm.empty() ? p + ".bias" : p + ".convolution.bias";
+    std::vector<float> W = get(wname, {co, ci, kh, kw}).v;
+    std::vector<float> b;
+    if (bias) b = get(bname, {co}).v;
+    if (!norm.empty()) fold_bn(W, b, p + "." + norm, co);
+    return pack_conv(W, b, ci, co, kh, kw, sh, sw, pads, ci_pad);
+  }
+
+  DwW dw_w(const std::string& p, int c, int kh, int kw, int sh, int sw, std::vector<int> pads, bool bias,
+           const std::string& norm = "") {
+    std::string wname = norm.empty() ? p + ".weight" : p + ".convolution.weight";
+    std::vector<float> W = get(wname, {c, 1, kh, kw}).v;
+    std::vector<float> b;
+    if (bias) b = get(p + ".bias", {c}).v;
+    if (!norm.empty()) fold_bn(W, b, p + "." + norm, c);
+    return pack_dw(W, b, c, kh, kw, sh, sw, pads);
+  }
+
+  SeW se_w(const std::string& reduce, const std::string& expand, int c, int cr, int act) {
+    SeW s;
+    s.c = c, s.cr = cr, s.act = act;
+    s.w1 = put(get(reduce + ".weight", {cr, c, 1, 1}).v);
+    s.b1 = put(get(reduce + ".bias", {cr}).v);
+    s.w2 = put(get(expand + ".weight", {c, cr, 1, 1}).v);
+    s.b2 = put(get(expand + ".bias", {c}).v);
+    return s;
+  }
+
+  // Linear::new (src/cpu/backend.rs:1244-1280): weight [out][in] + bias.
+  ConvW linear_w(const std::string& p, int fin, int fout) {
+    std::vector<float> W = get(p + ".weight", {fout, fin}).v;
+    std::vector<float> b = get(p + ".bias", {fout}).v;
+    return pack_conv(W, b, fin, fout, 1, 1, 1, 1, {0, 0, 0, 0});
+  }
+
+  // ------------------------------------------------------------ values
+  View alloc(int n, int h, int w, int c, const std::string& name, int ps = 0) {
+    Buffer b;
+    b.elems = (size_t)n * h * w * (ps ? ps : c);
+    b.name = name;
+    plan_.bufs.push_back(b);
+    View v;
+    v.buf = (int)plan_.bufs.size() - 1;
+    v.n = n, v.h = h, v.w = w, v.c = c, v.ps = ps ? ps : c;
+    return v;
+  }
+
+  static View slice(View v, int c0, int c) {
+    v.off += c0;
+    v.c = c;
+    return v;
+  }
+
+  void add_op(Op op) {
+    int idx = (int)plan_.ops.size();
+    for (int b : op.reads) touch(b, idx);
+    for (int b : op.writes) touch(b, idx);
+    plan_.ops.push_back(std::move(op));
+  }
+
+  void touch(int b, int idx) {
+    Buffer& buf = plan_.bufs[b];
+    if (buf.first < 0 || idx < buf.first) buf.first = idx;
+    buf.last = std::max(buf.last, idx);
+  }
+
+  // ------------------------------------------------------------ ops
+  View conv(const View& x, const ConvW& w, const Epi& e, const std::string& name) {
+    if (x.c != w.ci_pad) raise(PPOCR_ERR_INVALID_MODEL, name + ": input has " + std::to_string(x.c) + " channels");
+    int Ho, Wo;
+    if (w.deconv) {
+      Ho = x.h, Wo = x.w;
+    } else {
+      Ho = (x.h + w.pt + w.pb - w.kh) / w.sh + 1;
+      Wo = (x.w + w.pl + w.pr - w.kw) / w.sw + 1;
+    }
+    int oh = w.deconv ? 2 * Ho : Ho * e.rep, ow = w.deconv ? 2 * Wo : Wo * e.rep;
+    View out;
+    if (e.dst) {
+      out = *e.dst;
+      if (out.h != oh || out.w != ow || out.c != w.co || out.n != x.n)
+        raise(PPOCR_ERR_INVALID_MODEL, name + ": destination shape mismatch");
+    } else {
+      out = alloc(x.n, oh, ow, w.co, name);
+    }
+    View in = x;
+    View res = e.res ? *e.res : View();
+    View rg = e.res_gate ? *e.res_gate : View();
+    View ig = e.in_gate ? *e.in_gate : View();
+    View up = e.up ? *e.up : View();
+    bool has_res = e.res, has_rg = e.res_gate, has_ig = e.in_gate, has_up = e.up;
+    ConvParams base{};
+    base.N = x.n, base.H = x.h, base.W = x.w, base.C = x.c, base.in_ps = x.ps;
+    base.Ho = Ho, base.Wo = Wo, base.Co = w.co, base.out_ps = out.ps;
+    base.ldw = w.ldw;
+    base.kh = w.kh, base.kw = w.kw, base.sh = w.sh, base.sw = w.sw, base.pt = w.pt, base.pl = w.pl;
+    base.act = e.act;
+    base.res_ps = has_res ? res.ps : 0;
+    base.up_s = e.up_s;
+    base.up_ps = has_up ? up.ps : 0;
+    base.rep = e.rep;
+    base.mode = w.deconv ? 1 : 0;
+    base.out_h = oh, base.out_w = ow;
+    size_t wo = w.w, bo = w.b;
+    Op op;
+    op.name = name;
+    op.kernel = conv_tile_name(x.n * Ho * Wo, w.deconv ? 4 * w.co : w.co);
+    op.bound = 1;
+    double M = (double)x.n * Ho * Wo;
+    double K = (double)w.kh * w.kw * w.ci;
+    double cols = w.deconv ? 4.0 * w.co : w.co;
+    op.flops = 2.0 * M * cols * K;
+    op.bytes = 4.0 * ((double)x.pixels() * w.ci + K * cols + (double)out.pixels() * w.co +
+                      (has_res ? M * w.co : 0.0) + (has_up ? (double)up.pixels() * w.co : 0.0));
+    op.reads = {x.buf};
+    if (has_res) op.reads.push_back(res.buf);
+    if (has_rg) op.reads.push_back(rg.buf);
+    if (has_ig) op.reads.push_back(ig.buf);
+    if (has_up) op.reads.push_back(up.buf);
+    op.writes = {out.buf};
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      ConvParams p = base;
+      p.in = ex.ptr(in);
+      p.out = ex.ptr(out);
+      p.wt = ex.w(wo);
+      p.bias = ex.w(bo);
+      p.in_gate = has_ig ? ex.ptr(ig) : nullptr;
+      p.res = has_res ? ex.ptr(res) : nullptr;
+      p.res_gate = has_rg ? ex.ptr(rg) : nullptr;
+      p.up = has_up ? ex.ptr(up) : nullptr;
+      launch_conv(p, s);
+    };
+    add_op(std::move(op));
+    return out;
+  }
+
+  View depthwise(const View& x, const DwW& w, int act, const View* res, const std::string& name) {
+    if (x.c != w.c) raise(PPOCR_ERR_INVALID_MODEL, name + ": channel mismatch");
+    int Ho = (x.h + w.pt + w.pb - w.kh) / w.sh + 1;
+    int Wo = (x.w + w.pl + w.pr - w.kw) / w.sw + 1;
+    View out = alloc(x.n, Ho, Wo, w.c, name);
+    DwParams base{};
+    base.N = x.n, base.H = x.h, base.W = x.w, base.C = x.c, base.in_ps = x.ps;
+    base.Ho = Ho, base.Wo = Wo, base.out_ps = out.ps;
+    base.kh = w.kh, base.kw = w.kw, base.sh = w.sh, base.sw = w.sw, base.pt = w.pt, base.pl = w.pl;
+    base.act = act;
+    View in = x;
+    View r = res ? *res : View();
+    bool has_res = res;
+    base.res_ps = has_res ? r.ps : 0;
+    size_t wo = w.w, bo = w.b;
+    Op op;
+    op.name = name;
+    op.kernel = "depthwise";
+    op.flops = 2.0 * out.pixels() * w.c * w.kh * w.kw;
+    op.bytes = 4.0 * ((double)x.pixels() * w.c + (double)out.pixels() * w.c * (has_res ? 2 : 1) + w.kh * w.kw * w.c);
+    op.reads = {x.buf};
+    if (has_res) op.reads.push_back(r.buf);
+    op.writes = {out.buf};
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      DwParams p = base;
+      p.in = ex.ptr(in);
+      p.out = ex.ptr(out);
+      p.wt = ex.w(wo);
+      p.bias = ex.w(bo);
+      p.res = has_res ? ex.ptr(r) : nullptr;
+      launch_depthwise(p, s);
+    };
+    add_op(std::move(op));
+    return out;
+  }
+
+  // Squeeze-excitation gate [N,1,1,C] of x (src/cpu/model.rs:456-493,
+  // :1069-1105).
+  View se(const View& x, const SeW& w, const std::string& name) {
+    int HW = x.h * x.w;
+    int P = std::max(1, std::min(HW / 64, std::max(1, 1024 / x.n)));
+    View part = alloc(x.n, P, 1, x.c, name + ".partial");
+    View gate = alloc(x.n, 1, 1, x.c, name);
+    SeParams base{};
+    base.N = x.n, base.HW = HW, base.C = x.c, base.in_ps = x.ps, base.P = P, base.Cr = w.cr, base.gate_act = w.act;
+    View in = x;
+    SeW ww = w;
+    Op op;
+    op.name = name;
+    op.kernel = "se_gate";
+    op.flops = 2.0 * x.n * ((double)HW * x.c + 2.0 * x.c * w.cr);
+    op.bytes = 4.0 * ((double)x.pixels() * x.c + 2.0 * x.c * w.cr + x.n * x.c);
+    op.reads = {x.buf};
+    op.writes = {part.buf, gate.buf};
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      SeParams p = base;
+      p.in = ex.ptr(in);
+      p.partial = ex.ptr(part);
+      p.w1 = ex.w(ww.w1);
+      p.b1 = ex.w(ww.b1);
+      p.w2 = ex.w(ww.w2);
+      p.b2 = ex.w(ww.b2);
+      p.gate = ex.ptr(gate);
+      launch_se(p, s);
+    };
+    add_op(std::move(op));
+    return gate;
+  }
+
+  // x + x*g [+ up2(upper)], written (optionally replicated) into dst.
+  void gate_residual(const View& x, const View& g, const View* upper, const View& dst, int rep,
+                     const std::string& name) {
+    View in = x, gate = g, out = dst;
+    View up = upper ? *upper : View();
+    bool has_up = upper;
+    Op op;
+    op.name = name;
+    op.kernel = "gate_residual";
+    op.bytes = 4.0 * ((double)x.pixels() * x.c * (1 + rep * rep) + (has_up ? (double)up.pixels() * x.c : 0.0));
+    op.reads = {x.buf, g.buf};
+    if (has_up) op.reads.push_back(up.buf);
+    op.writes = {dst.buf};
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      launch_gate_residual(ex.ptr(in), in.n, in.h, in.w, in.c, in.ps, ex.ptr(gate), has_up ? ex.ptr(up) : nullptr,
+                           has_up ? up.ps : 0, ex.ptr(out), out.ps, rep, s);
+    };
+    add_op(std::move(op));
+  }
+
+  void maxpool_same(const View& x, const View& dst, const std::string& name) {
+    View in = x, out = dst;
+    Op op;
+    op.name = name;
+    op.kernel = "maxpool_same";
+    op.bytes = 8.0 * x.pixels() * x.c;
+    op.reads = {x.buf};
+    op.writes = {dst.buf};
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      launch_maxpool_same(ex.ptr(in), in.n, in.h, in.w, in.c, in.ps, ex.ptr(out), out.ps, s);
+    };
+    add_op(std::move(op));
+  }
+
+  View avgpool32(const View& x, const std::string& name) {
+    int Ho = (x.h - 3) / 3 + 1, Wo = (x.w - 2) / 2 + 1;
+    View out = alloc(x.n, Ho, Wo, x.c, name);
+    View in = x;
+    Op op;
+    op.name = name;
+    op.kernel = "avgpool";
+    op.bytes = 4.0 * ((double)x.pixels() * x.c + (double)out.pixels() * x.c);
+    op.reads = {x.buf};
+    op.writes = {out.buf};
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      launch_avgpool32(ex.ptr(in), in.n, in.h, in.w, in.c, in.ps, ex.ptr(out), out.h, out.w, s);
+    };
+    add_op(std::move(op));
+    return out;
+  }
+
+  View layer_norm(const View& x, const std::string& p, const View* res, const std::string& name) {
+    int C = x.c;
+    size_t wo = put(get(p + ".weight", {C}).v), bo = put(get(p + ".bias", {C}).v);
+    View out = alloc(x.n, x.h, x.w, C, name);
+    View in = x;
+    View r = res ? *res : View();
+    bool has_res = res;
+    Op op;
+    op.name = name;
+    op.kernel = "layer_norm";
+    op.bytes = 4.0 * ((double)x.pixels() * C * (has_res ? 3 : 2) + 2 * C);
+    op.reads = {x.buf};
+    if (has_res) op.reads.push_back(r.buf);
+    op.writes = {out.buf};
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      launch_layer_norm(ex.ptr(in), (int)in.pixels(), C, ex.w(wo), ex.w(bo), 1e-6f, has_res ? ex.ptr(r) : nullptr,
+                        ex.ptr(out), s);
+    };
+    add_op(std::move(op));
+    return out;
+  }
+
+  View attention(const View& qkv, int hidden, int heads, const std::string& name) {
+    View out = alloc(qkv.n, qkv.h, qkv.w, hidden, name);
+    View in = qkv;
+    int T = qkv.h * qkv.w;
+    if ((size_t)16 * T * 4 > 160 * 1024) raise(PPOCR_ERR_INVALID_INPUT, "recognizer sequence too long for attention");
+    Op op;
+    op.name = name;
+    op.kernel = "attention";
+    op.flops = 2.0 * qkv.n * heads * (double)T * T * (hidden / heads) * 2.0;
+    op.bytes = 4.0 * ((double)qkv.pixels() * 3 * hidden + (double)out.pixels() * hidden);
+    op.reads = {qkv.buf};
+    op.writes = {out.buf};
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      launch_attention(ex.ptr(in), in.n, T, hidden, heads, ex.ptr(out), s);
+    };
+    add_op(std::move(op));
+    return out;
+  }
+
+  void softmax(const View& x, const std::string& name) {
+    View io = x;
+    Op op;
+    op.name = name;
+    op.kernel = "softmax";
+    op.bytes = 8.0 * x.pixels() * x.c;
+    op.reads = {x.buf};
+    op.writes = {x.buf};
+    op.launch = [=](const Exec& ex, hipStream_t s) { launch_softmax_rows(ex.ptr(io), (long)io.pixels(), io.c, s); };
+    add_op(std::move(op));
+  }
+
+  // NCHW staging buffer -> NHWC with 4 channels.
+  View input(const size_t nchw[4]) {
+    int n = (int)nchw[0], h = (int)nchw[2], w = (int)nchw[3];
+    View st = alloc(n, 3, h, w, "input.nchw");
+    plan_.staging = st.buf;
+    View x = alloc(n, h, w, 4, "input");
+    Op op;
+    op.name = "input";
+    op.kernel = "nchw_to_nhwc";
+    op.bytes = 4.0 * 7.0 * n * h * w;
+    op.reads = {st.buf};
+    op.writes = {x.buf};
+    op.launch = [=](const Exec& ex, hipStream_t s) { launch_nchw_to_nhwc4(ex.ptr(st), ex.ptr(x), n, h, w, s); };
+    add_op(std::move(op));
+    plan_.input = x;
+    return x;
+  }
+
+  Plan& plan() { return plan_; }
+
+ private:
+  const SafeTensors& st_;
+  Plan& plan_;
+};
+
+// ------------------------------------------------------------------ backbone
+
+// LcNetBlock (src/cpu/model.rs:509-603).
+View lcnet_block(Builder& B, const View& x, const std::string& p, BlockSpec s) {
+  bool residual = s.ci == s.co && s.sh == 1 && s.sw == 1;
+  DwW tw = residual ? B.dw_w(p + ".token_conv", s.ci, 3, 3, s.sh, s.sw, {1, 1, 1, 1}, true)
+                    : B.dw_w(p + ".token_conv", s.ci, 3, 3, s.sh, s.sw, {1, 1, 1, 1}, false, "normalization");
+  View t = B.depthwise(x, tw, ACT_NONE, nullptr, p + ".token_conv");
+  View gate;
+  bool has_se = s.se;
+  if (has_se) {
+    std::string q = p + ".token_squeeze_excitation.convolutions";
+    SeW sw = B.se_w(q + ".0", q + ".2", s.ci, s.ci / 4, ACT_HSIG6);
+    gate = B.se(t, sw, p + ".se");
+  }
+  ConvW c1 = B.conv_w(p + ".channel_conv1", s.ci, 2 * s.ci, 1, 1, 1, 1, {0, 0, 0, 0}, false, "normalization");
+  ConvW c2 = B.conv_w(p + ".channel_conv2", 2 * s.ci, s.co, 1, 1, 1, 1, {0, 0, 0, 0}, false, "normalization");
+  Epi e1;
+  e1.act = ACT_GELU;
+  if (has_se) e1.in_gate = &gate;
+  View h = B.conv(t, c1, e1, p + ".channel_conv1");
+  Epi e2;
+  if (residual) {
+    e2.res = &t;
+    if (has_se) e2.res_gate = &gate;
+  }
+  return B.conv(h, c2, e2, p + ".channel_conv2");
+}
+
+// LargeStem (src/cpu/model.rs:626-693): the max-pool and stem2b write the two
+// halves of the concat stem3 reads.
+View large_stem(Builder& B, const View& x, int mid, int out) {
+  std::string p = "model.backbone.encoder.convolution";
+  Epi relu;
+  relu.act = ACT_RELU;
+  ConvW s1 = B.conv_w(p + ".stem1", 3, mid, 3, 3, 2, 2, {1, 1, 1, 1}, false, "normalization", 4);
+  View e = B.conv(x, s1, relu, p + ".stem1");
+  ConvW s2a = B.conv_w(p + ".stem2a", mid, mid / 2, 2, 2, 1, 1, {0, 0, 1, 1}, false, "normalization");
+  View a = B.conv(e, s2a, relu, p + ".stem2a");
+  View merged = B.alloc(e.n, e.h, e.w, 2 * mid, p + ".concat");
+  View pooled_slot = Builder::slice(merged, 0, mid);
+  View branch_slot = Builder::slice(merged, mid, mid);
+  B.maxpool_same(e, pooled_slot, p + ".pool");
+  ConvW s2b = B.conv_w(p + ".stem2b", mid / 2, mid, 2, 2, 1, 1, {0, 0, 1, 1}, false, "normalization");
+  Epi into = relu;
+  into.dst = &branch_slot;
+  B.conv(a, s2b, into, p + ".stem2b");
+  ConvW s3 = B.conv_w(p + ".stem3", 2 * mid, mid, 3, 3, 2, 2, {1, 1, 1, 1}, false, "normalization");
+  View t = B.conv(merged, s3, relu, p + ".stem3");
+  ConvW s4 = B.conv_w(p + ".stem4", mid, out, 1, 1, 1, 1, {0, 0, 0, 0}, false, "normalization");
+  return B.conv(t, s4, relu, p + ".stem4");
+}
+
+// SmallStem (src/cpu/model.rs:695-733): 3x3 s2 BN GELU, 3x3 s2 BN.
+View small_stem(Builder& B, const View& x, int mid, int out) {
+  std::string p = "model.backbone.encoder.convolution";
+  ConvW c1 = B.conv_w(p + ".conv1", 3, mid, 3, 3, 2, 2, {1, 1, 1, 1}, false, "normalization", 4);
+  Epi gelu;
+  gelu.act = ACT_GELU;
+  View h = B.conv(x, c1, gelu, p + ".conv1");
+  ConvW c2 = B.conv_w(p + ".conv2", mid, out, 3, 3, 2, 2, {1, 1, 1, 1}, false, "normalization");
+  return B.conv(h, c2, Epi{}, p + ".conv2");
+}
+
+std::vector<View> backbone(Builder& B, const View& x, int mid, int out, bool large,
+                           const std::vector<std::vector<BlockSpec>>& stages) {
+  View h = large ? large_stem(B, x, mid, out) : small_stem(B, x, mid, out);
+  std::vector<View> outs;
+  for (size_t s = 0; s < stages.size(); ++s) {
+    for (size_t b = 0; b < stages[s].size(); ++b)
+      h = lcnet_block(B, h, "model.backbone.encoder.blocks." + std::to_string(s) + ".blocks." + std::to_string(b),
+                      stages[s][b]);
+    outs.push_back(h);
+  }
+  return outs;
+}
+
+// detector_stages_for_channels (src/cpu/model.rs:1648-1673).
+std::vector<std::vector<BlockSpec>> detector_stages(const int c[4]) {
+  return {{{c[0], c[0], 1, 1, true}, {c[0], c[0], 1, 1, false}},
+          {{c[0], c[1], 2, 2, false}, {c[1], c[1], 1, 1, true}, {c[1], c[1], 1, 1, false}},
+          {{c[1], c[2], 2, 2, false},
+           {c[2], c[2], 1, 1, true},
+           {c[2], c[2], 1, 1, false},
+           {c[2], c[2], 1, 1, true},
+           {c[2], c[2], 1, 1, false}},
+          {{c[2], c[3], 2, 2, false}, {c[3], c[3], 1, 1, true}, {c[3], c[3], 1, 1, false}}};
+}
+
+// recognizer stage tables (src/cpu/model.rs:2057-2122).
+std::vector<std::vector<BlockSpec>> recognizer_stages(int size) {
+  auto alt = [](std::vector<BlockSpec> v, int c) {
+    for (int i = 0; i < 6; ++i) v.push_back({c, c, 1, 1, i % 2 == 0});
+    return v;
+  };
+  if (size == PPOCR_SIZE_MEDIUM)
+    return {{{128, 128, 1, 1, true}},
+            {{128, 256, 1, 1, false}, {256, 256, 1, 1, false}, {256, 256, 1, 1, true}},
+            alt({{256, 512, 2, 1, false}}, 512),
+            {{512, 768, 2, 1, false}, {768, 768, 1, 1, true}, {768, 768, 1, 1, false}}};
+  if (size == PPOCR_SIZE_SMALL)
+    return {{{96, 96, 1, 1, true}},
+            {{96, 96, 1, 1, false}, {96, 96, 1, 1, false}},
+            alt({{96, 192, 2, 1, false}}, 192),
+            {{192, 384, 2, 1, false}, {384, 384, 1, 1, true}, {384, 384, 1, 1, false}}};
+  return {{{48, 48, 1, 1, true}},
+          {{48, 48, 1, 1, false}},
+          {{48, 96, 2, 1, false}, {96, 96, 1, 1, true}, {96, 96, 1, 1, false}},
+          {{96, 160, 2, 1, false}, {160, 160, 1, 1, true}, {160, 160, 1, 1, false}, {160, 160, 1, 1, false}}};
+}
+
+// ------------------------------------------------------------------ necks
+
+// RepLkFpn (src/cpu/model.rs:1197-1254).  Level i of the concat goes to
+// channel slot 3 - i (deepest first) upsampled by 2^i.
+View rep_lk_fpn(Builder& B, const std::vector<View>& st, const int chans[4], int nc, int k) {
+  const int q = nc / 4;
+  std::vector<View> h(4), g(4), fused(4);
+  for (int i = 0; i < 4; ++i) {
+    std::string p = "model.neck.insert_conv." + std::to_string(i);
+    ConvW w = B.conv_w(p + ".in_conv", chans[i], nc, 1, 1, 1, 1, {0, 0, 0, 0}, false);
+    h[i] = B.conv(st[i], w, Epi{}, p + ".in_conv");
+    SeW sw = B.se_w(p + ".squeeze_excitation_block.conv1", p + ".squeeze_excitation_block.conv2", nc, nc / 4,
+                    ACT_HSIG5);
+    g[i] = B.se(h[i], sw, p + ".se");
+  }
+  for (int i = 3; i >= 0; --i) {
+    fused[i] = B.alloc(h[i].n, h[i].h, h[i].w, nc, "model.neck.fused." + std::to_string(i));
+    B.gate_residual(h[i], g[i], i < 3 ? &fused[i + 1] : nullptr, fused[i], 1, "model.neck.fused." + std::to_string(i));
+  }
+  const View& f0 = fused[0];
+  View cat = B.alloc(f0.n, f0.h, f0.w, nc, "model.neck.concat");
+  for (int i = 0; i < 4; ++i) {
+    std::string p = "model.neck.input_conv." + std::to_string(i);
+    int pd = k / 2;
+    DwW dw = B.dw_w(p + ".depthwise_convolution", nc, k, k, 1, 1, {pd, pd, pd, pd}, true);
+    View d = B.depthwise(fused[i], dw, ACT_NONE, nullptr, p + ".depthwise_convolution");
+    ConvW pw = B.conv_w(p + ".pointwise_convolution", nc, q, 1, 1, 1, 1, {0, 0, 0, 0}, false);
+    View pt = B.conv(d, pw, Epi{}, p + ".pointwise_convolution");
+    SeW sw = B.se_w(p + ".squeeze_excitation_module.conv1", p + ".squeeze_excitation_module.conv2", q, q / 4,
+                    ACT_HSIG5);
+    View gi = B.se(pt, sw, p + ".se");
+    View slot = Builder::slice(cat, (3 - i) * q, q);
+    B.gate_residual(pt, gi, nullptr, slot, 1 << i, p + ".out");
+  }
+  return cat;
+}
+
+// factor_rank_one_conv_weight (src/cpu/model.rs:221-369): per input channel,
+// four power iterations in double precision on the O x k^2 matrix, then the
+// separability check.  Returns dw [ci][k*k] and pw [co][ci].
+void factor_rank_one(const std::string& name, const std::vector<float>& W, int ci, int co, int k,
+                     std::vector<float>& dw, std::vector<float>& pw) {
+  const int sp = k * k;
+  for (float v : W)
+    if (!std::isfinite(v)) raise(PPOCR_ERR_INVALID_MODEL, name + ": rank-one weight contains non-finite values");
+  dw.assign((size_t)ci * sp, 0.0f);
+  pw.assign((size_t)co * ci, 0.0f);
+  std::vector<double> dir(sp), sc(co);
+  auto at = [&](int o, int c, int i) { return (double)W[((size_t)o * ci + c) * sp + i]; };
+  for (int c = 0; c < ci; ++c) {
+    int best = 0;
+    double best_e = 0.0;
+    for (int o = 0; o < co; ++o) {
+      double e = 0.0;
+      for (int i = 0; i < sp; ++i) e += at(o, c, i) * at(o, c, i);
+      if (e > best_e) best = o, best_e = e;
+    }
+    if (best_e == 0.0) continue;
+    double nrm = std::sqrt(best_e);
+    for (int i = 0; i < sp; ++i) dir[i] = at(best, c, i) / nrm;
+    for (int it = 0; it < 4; ++it) {
+      double energy = 0.0;
+      for (int o = 0; o < co; ++o) {
+        double s = 0.0;
+        for (int i = 0; i < sp; ++i) s += at(o, c, i) * dir[i];
+        sc[o] = s;
+        energy += s * s;
+      }
+      if (!(std::isfinite(energy) && energy > 0.0))
+        raise(PPOCR_ERR_INVALID_MODEL, name + ": rank-one factorization became degenerate");
+      double n2 = 0.0;
+      for (int i = 0; i < sp; ++i) {
+        double s = 0.0;
+        for (int o = 0; o < co; ++o) s += at(o, c, i) * sc[o];
+        dir[i] = s / energy;
+        n2 += dir[i] * dir[i];
+      }
+      n2 = std::sqrt(n2);
+      if (!(std::isfinite(n2) && n2 > 0.0))
+        raise(PPOCR_ERR_INVALID_MODEL, name + ": rank-one spatial factor became degenerate");
+      for (int i = 0; i < sp; ++i) dir[i] /= n2;
+    }
+    for (int o = 0; o < co; ++o) {
+      double s = 0.0;
+      for (int i = 0; i < sp; ++i) s += at(o, c, i) * dir[i];
+      pw[(size_t)o * ci + c] = (float)s;
+    }
+    for (int i = 0; i < sp; ++i) dw[(size_t)c * sp + i] = (float)dir[i];
+  }
+  double max_src = 0, max_err = 0, src_e = 0, err_e = 0;
+  for (int o = 0; o < co; ++o)
+    for (int c = 0; c < ci; ++c)
+      for (int i = 0; i < sp; ++i) {
+        float e = W[((size_t)o * ci + c) * sp + i];
+        float a = pw[(size_t)o * ci + c] * dw[(size_t)c * sp + i];
+        double err = std::fabs((double)(e - a));
+        max_src = std::max(max_src, (double)std::fabs(e));
+        max_err = std::max(max_err, err);
+        src_e += (double)e * e;
+        err_e += err * err;
+      }
+  double rel = src_e == 0.0 ? 0.0 : std::sqrt(err_e / src_e);
+  if (!(max_err <= max_src * 1e-5 + 1e-12 && rel <= 1e-6))
+    raise(PPOCR_ERR_INVALID_MODEL, name + ": fused convolution is not rank-one separable");
+}
+
+// RankOneConv2d (src/cpu/model.rs:165-219): depthwise k x k then 1x1 + bias.
+View rank_one(Builder& B, const View& x, const std::string& p, int ci, int co, int k, const Epi& e) {
+  std::vector<float> W = B.get(p + ".weight", {co, ci, k, k}).v;
+  std::vector<float> dwv, pwv;
+  factor_rank_one(p, W, ci, co, k, dwv, pwv);
+  int pd = k / 2;
+  DwW dw = B.pack_dw(dwv, {}, ci, k, k, 1, 1, {pd, pd, pd, pd});
+  View d = B.depthwise(x, dw, ACT_NONE, nullptr, p + ".depthwise");
+  ConvW pw = B.pack_conv(pwv, B.get(p + ".bias", {co}).v, ci, co, 1, 1, 1, 1, {0, 0, 0, 0});
+  return B.conv(d, pw, e, p + ".pointwise");
+}
+
+// fuse_intraclass_conv (src/cpu/model.rs:819-906).
+ConvW intraclass_conv(Builder& B, const std::string& p, const std::string& ratio, int k) {
+  std::vector<float> W = B.get(p + ".symmetric_conv_long_" + ratio + ".weight", {32, 32, k, k}).v;
+  std::vector<float> b = B.get(p + ".symmetric_conv_long_" + ratio + ".bias", {32}).v;
+  std::vector<float> vw = B.get(p + ".vertical_long_to_small_conv_" + ratio + ".weight", {32, 32, k, 1}).v;
+  std::vector<float> vb = B.get(p + ".vertical_long_to_small_conv_" + ratio + ".bias", {32}).v;
+  std::vector<float> hw = B.get(p + ".horizontal_small_to_long_conv_" + ratio + ".weight", {32, 32, 1, k}).v;
+  std::vector<float> hb = B.get(p + ".horizontal_small_to_long_conv_" + ratio + ".bias", {32}).v;
+  int ctr = k / 2;
+  for (int o = 0; o < 32; ++o)
+    for (int i = 0; i < 32; ++i) {
+      size_t bo = ((size_t)o * 32 + i) * k;
+      for (int r = 0; r < k; ++r) W[bo * k + r * k + ctr] += vw[bo + r];
+      for (int c = 0; c < k; ++c) W[bo * k + ctr * k + c] += hw[bo + c];
+    }
+  for (int o = 0; o < 32; ++o) {
+    b[o] += vb[o];
+    b[o] += hb[o];
+  }
+  return B.pack_conv(W, b, 32, 32, k, k, 1, 1, {ctr, ctr, ctr, ctr});
+}
+
+// DetectorNeck, medium (src/cpu/model.rs:948-1067).
+View medium_neck(Builder& B, const std::vector<View>& st) {
+  const int chans[4] = {128, 256, 512, 896};
+  std::string n = "model.neck";
+  std::vector<View> td(4);
+  for (int i = 3; i >= 0; --i) {
+    std::string p = n + ".input_channel_adjustment_convolution." + std::to_string(i);
+    ConvW w = B.conv_w(p, chans[i], 256, 1, 1, 1, 1, {0, 0, 0, 0}, false);
+    Epi e;
+    if (i < 3) e.up = &td[i + 1];
+    td[i] = B.conv(st[i], w, e, p);
+  }
+  std::vector<View> bu(4);
+  for (int i = 0; i < 4; ++i) {
+    View proj = rank_one(B, td[i], n + ".input_feature_projection_convolution." + std::to_string(i), 256, 64, 9, Epi{});
+    if (i == 0) {
+      bu[i] = proj;
+    } else {
+      std::string p = n + ".path_aggregation_head_convolution." + std::to_string(i - 1);
+      ConvW w = B.conv_w(p, 64, 64, 3, 3, 2, 2, {1, 1, 1, 1}, false);
+      Epi e;
+      e.res = &proj;
+      bu[i] = B.conv(bu[i - 1], w, e, p);
+    }
+  }
+  const View& b0 = bu[0];
+  View cat = B.alloc(b0.n, b0.h, b0.w, 256, n + ".concat");
+  for (int i = 0; i < 4; ++i) {
+    View lat = rank_one(B, bu[i], n + ".path_aggregation_lateral_convolution." + std::to_string(i), 64, 64, 9, Epi{});
+    std::string p = n + ".intraclass_blocks." + std::to_string(i);
+    ConvW red = B.conv_w(p + ".conv_reduce_channel", 64, 32, 1, 1, 1, 1, {0, 0, 0, 0}, true);
+    View r = B.conv(lat, red, Epi{}, p + ".conv_reduce_channel");
+    View l7 = B.conv(r, intraclass_conv(B, p, "longratio", 7), Epi{}, p + ".long");
+    View l5 = B.conv(l7, intraclass_conv(B, p, "midratio", 5), Epi{}, p + ".mid");
+    View l3 = B.conv(l5, intraclass_conv(B, p, "shortratio", 3), Epi{}, p + ".short");
+    ConvW fin = B.conv_w(p + ".conv_final", 32, 64, 1, 1, 1, 1, {0, 0, 0, 0}, true, "norm");
+    View slot = Builder::slice(cat, (3 - i) * 64, 64);
+    Epi e;
+    e.act = ACT_RELU;
+    e.res = &lat;
+    e.rep = 1 << i;
+    e.dst = &slot;
+    B.conv(l3, fin, e, p + ".conv_final");
+  }
+  return cat;
+}
+
+// DetectorHead (src/cpu/model.rs:1479-1521).
+void detector_head(Builder& B, const View& x, int nc) {
+  int h = nc / 4;
+  if (h != 16 && h != 24 && h != 64) raise(PPOCR_ERR_INVALID_MODEL, "unsupported detector head width");
+  ConvW down = B.conv_w("head.conv_down", nc, h, 3, 3, 1, 1, {1, 1, 1, 1}, false, "norm");
+  Epi relu;
+  relu.act = ACT_RELU;
+  View d = B.conv(x, down, relu, "head.conv_down");
+  std::vector<float> wu = B.get("head.conv_up.convolution.weight", {h, h, 2, 2}).v;
+  std::vector<float> bu = B.get("head.conv_up.convolution.bias", {h}).v;
+  B.fold_bn(wu, bu, "head.conv_up.norm", h, true, h);
+  std::vector<float> wf = B.get("head.conv_final.weight", {h, 1, 2, 2}).v;
+  float bf = B.get("head.conv_final.bias", {1}).v[0];
+  size_t owu = B.put(wu), obu = B.put(bu), owf = B.put(wf);
+  Plan& plan = B.plan();
+  View out = B.alloc(x.n, 4 * d.h, 4 * d.w, 1, "output");
+  plan.output = out.buf;
+  plan.output_elems = out.pixels();
+  plan.output_shape = {(size_t)x.n, 1, (size_t)out.h, (size_t)out.w};
+  View in = d;
+  Op op;
+  op.name = "head.conv_up+conv_final";
+  op.kernel = "db_head_up";
+  op.flops = 2.0 * d.pixels() * (4.0 * h * h + 16.0 * h);
+  op.bytes = 4.0 * ((double)d.pixels() * h + (double)out.pixels() + 4.0 * h * h + 4.0 * h);
+  op.reads = {d.buf};
+  op.writes = {out.buf};
+  op.launch = [=](const Exec& ex, hipStream_t s) {
+    launch_db_head_up(ex.ptr(in), in.n, in.h, in.w, in.c, in.ps, ex.w(owu), ex.w(obu), ex.w(owf), bf, ex.ptr(out), s);
+  };
+  B.add_op(std::move(op));
+}
+
+void validate_detector_shape(const size_t s[4]) {
+  if (s[0] == 0 || s[1] != 3 || s[2] < 32 || s[3] < 32 || s[2] % 32 || s[3] % 32)
+    raise(PPOCR_ERR_INVALID_INPUT,
+          "detector expects [N, 3, H, W] with N > 0, H/W >= 32 and divisible by 32; got [" + std::to_string(s[0]) +
+              ", " + std::to_string(s[1]) + ", " + std::to_string(s[2]) + ", " + std::to_string(s[3]) + "]");
+  if (s[0] > (1u << 16) || s[2] > (1u << 15) || s[3] > (1u << 15) || s[0] * s[2] * s[3] > (size_t)INT32_MAX / 64)
+    raise(PPOCR_ERR_INVALID_INPUT, "detector input shape is too large");
+}
+
+void validate_recognizer_shape(const size_t s[4]) {
+  if (s[0] == 0 || s[1] != 3 || s[2] != 48 || s[3] < 32 || s[3] % 4)
+    raise(PPOCR_ERR_INVALID_INPUT,
+          "recognizer expects [N, 3, 48, W] with N > 0, W >= 32 and divisible by 4; got [" + std::to_string(s[0]) +
+              ", " + std::to_string(s[1]) + ", " + std::to_string(s[2]) + ", " + std::to_string(s[3]) + "]");
+  if (s[0] > (1u << 16) || s[3] > (1u << 15) || s[0] * s[3] > (size_t)INT32_MAX / 1024)
+    raise(PPOCR_ERR_INVALID_INPUT, "recognizer input shape is too large");
+}
+
+}  // namespace
+
+// Detector::load (src/gpu/model.rs:50-93; architecture src/cpu/model.rs:1546-1609).
+Plan build_detector(const SafeTensors& st, int size, const size_t nchw[4]) {
+  validate_detector_shape(nchw);
+  const size_t expected = size == PPOCR_SIZE_MEDIUM ? 350 : 271;
+  const char* tier = size == PPOCR_SIZE_MEDIUM ? "medium" : size == PPOCR_SIZE_SMALL ? "small" : "tiny";
+  if (st.size() != expected)
+    raise(PPOCR_ERR_INVALID_MODEL, std::string(tier) + " detector has " + std::to_string(st.size()) +
+                                       " tensors; expected " + std::to_string(expected));
+  Plan plan;
+  plan.detector = true;
+  Builder B(st, plan);
+  int chans[4], mid, out, nc;
+  if (size == PPOCR_SIZE_MEDIUM) {
+    const int c[4] = {128, 256, 512, 896};
+    std::copy(c, c + 4, chans);
+    mid = 64, out = 128, nc = 256;
+  } else if (size == PPOCR_SIZE_SMALL) {
+    const int c[4] = {48, 96, 192, 384};
+    std::copy(c, c + 4, chans);
+    mid = 24, out = 48, nc = 96;
+  } else {
+    const int c[4] = {32, 48, 64, 160};
+    std::copy(c, c + 4, chans);
+    mid = 16, out = 32, nc = 64;
+  }
+  View x = B.input(nchw);
+  std::vector<View> stages = backbone(B, x, mid, out, true, detector_stages(chans));
+  View neck = size == PPOCR_SIZE_MEDIUM ? medium_neck(B, stages)
+                                        : rep_lk_fpn(B, stages, chans, nc, size == PPOCR_SIZE_SMALL ? 7 : 5);
+  detector_head(B, neck, nc);
+  plan_arena(plan);
+  return plan;
+}
+
+// Recognizer::load (src/gpu/model.rs:156-220; architecture
+// src/cpu/model.rs:1961-2039).
+Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4]) {
+  validate_recognizer_shape(nchw);
+  const size_t expected = size == PPOCR_SIZE_MEDIUM ? 269 : size == PPOCR_SIZE_SMALL ? 250 : 150;
+  const char* tier = size == PPOCR_SIZE_MEDIUM ? "medium" : size == PPOCR_SIZE_SMALL ? "small" : "tiny";
+  if (st.size() != expected)
+    raise(PPOCR_ERR_INVALID_MODEL, std::string(tier) + " recognizer has " + std::to_string(st.size()) +
+                                       " tensors; expected " + std::to_string(expected));
+  Plan plan;
+  plan.detector = false;
+  Builder B(st, plan);
+  View x = B.input(nchw);
+  bool tiny = size == PPOCR_SIZE_TINY;
+  int mid = size == PPOCR_SIZE_MEDIUM ? 64 : size == PPOCR_SIZE_SMALL ? 48 : 24;
+  int out = size == PPOCR_SIZE_MEDIUM ? 128 : size == PPOCR_SIZE_SMALL ? 96 : 48;
+  std::vector<View> stages = backbone(B, x, mid, out, !tiny, recognizer_stages(size));
+  View pooled = B.avgpool32(stages.back(), "pool");
+  if (pooled.h != 1) raise(PPOCR_ERR_INVALID_MODEL, "recognizer pooling must produce height 1");
+  const int classes = tiny ? 6906 : 18710;
+  View logits_dst = B.alloc(pooled.n, 1, pooled.w, classes, "output");
+  plan.output = logits_dst.buf;
+  plan.output_elems = logits_dst.pixels() * classes;
+  plan.output_shape = {(size_t)pooled.n, (size_t)pooled.w, (size_t)classes};
+  Epi into;
+  into.dst = &logits_dst;
+  if (tiny) {
+    // TinyRecognizerHead (src/cpu/model.rs:1913-1936) with Conv1dBn (:1877-1911).
+    std::vector<float> w1 = B.get("head.conv1.weight", {160, 1, 5}).v, b1;
+    B.fold_bn(w1, b1, "head.norm1", 160);
+    DwW dw = B.pack_dw(w1, b1, 160, 1, 5, 1, 1, {0, 2, 0, 2});
+    View h = B.depthwise(pooled, dw, ACT_HSWISH, nullptr, "head.conv1");
+    std::vector<float> w2 = B.get("head.conv2.weight", {160, 160, 1}).v, b2;
+    B.fold_bn(w2, b2, "head.norm2", 160);
+    ConvW c2 = B.pack_conv(w2, b2, 160, 160, 1, 1, 1, 1, {0, 0, 0, 0});
+    Epi hs;
+    hs.act = ACT_HSWISH;
+    h = B.conv(h, c2, hs, "head.conv2");
+    h = B.conv(h, B.linear_w("head.fc1", 160, 80), Epi{}, "head.fc1");
+    B.conv(h, B.linear_w("head.fc2", 80, classes), into, "head.fc2");
+  } else {
+    // LightSvtrRecognizerHead / RecEncoder (src/cpu/model.rs:1686-1875).
+    int ci = size == PPOCR_SIZE_MEDIUM ? 768 : 384;
+    int hid = size == PPOCR_SIZE_MEDIUM ? 192 : 120;
+    int mlp = size == PPOCR_SIZE_MEDIUM ? 768 : 240;
+    std::string e = "head.encoder";
+    Epi silu;
+    silu.act = ACT_SILU;
+    View skip = B.conv(pooled, B.conv_w(e + ".conv_block.0", ci, hid, 1, 1, 1, 1, {0, 0, 0, 0}, false, "normalization"),
+                       silu, e + ".conv_block.0");
+    View h = B.conv(pooled, B.conv_w(e + ".conv_block.1", ci, hid, 1, 1, 1, 1, {0, 0, 0, 0}, false, "normalization"),
+                    silu, e + ".conv_block.1");
+    DwW lw = B.dw_w(e + ".conv_block.2", hid, 1, 7, 1, 1, {0, 3, 0, 3}, false, "normalization");
+    h = B.depthwise(h, lw, ACT_SILU, &h, e + ".conv_block.2");
+    for (int i = 0; i < 2; ++i) {
+      std::string p = e + ".svtr_block." + std::to_string(i);
+      View a = B.layer_norm(h, p + ".layer_norm1", nullptr, p + ".layer_norm1");
+      View qkv = B.conv(a, B.linear_w(p + ".self_attn.qkv", hid, 3 * hid), Epi{}, p + ".self_attn.qkv");
+      View ctx = B.attention(qkv, hid, 8, p + ".self_attn");
+      Epi r1;
+      r1.res = &h;
+      View h1 = B.conv(ctx, B.linear_w(p + ".self_attn.projection", hid, hid), r1, p + ".self_attn.projection");
+      View a2 = B.layer_norm(h1, p + ".layer_norm2", nullptr, p + ".layer_norm2");
+      View m = B.conv(a2, B.linear_w(p + ".mlp.fc1", hid, mlp), silu, p + ".mlp.fc1");
+      Epi r2;
+      r2.res = &h1;
+      h = B.conv(m, B.linear_w(p + ".mlp.fc2", mlp, hid), r2, p + ".mlp.fc2");
+    }
+    View y = B.layer_norm(h, e + ".norm", &skip, e + ".norm");
+    B.conv(y, B.linear_w("head.head", hid, classes), into, "head.head");
+  }
+  B.softmax(logits_dst, "softmax");
+  plan_arena(plan);
+  return plan;
+}
+
+// Interval packing of buffer lifetimes: largest first, each at the lowest
+// offset that overlaps no placed buffer whose lifetime intersects its own.
+void plan_arena(Plan& plan) {
+  const int end = (int)plan.ops.size();
+  for (auto& b : plan.bufs) {
+    if (b.first < 0) b.first = b.last = 0;
+  }
+  plan.bufs[plan.staging].first = 0;
+  plan.bufs[plan.output].last = end;
+  std::vector<int> order(plan.bufs.size());
+  for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
+  std::sort(order.begin(), order.end(), [&](int a, int b) {
+    if (plan.bufs[a].elems != plan.bufs[b].elems) return plan.bufs[a].elems > plan.bufs[b].elems;
+    return a < b;
+  });
+  std::vector<int> placed;
+  size_t total = 0, unplanned = 0;
+  for (int id : order) {
+    Buffer& b = plan.bufs[id];
+    size_t size = round_up(b.elems, 64);
+    unplanned += size;
+    std::vector<std::pair<size_t, size_t>> busy;
+    for (int o : placed) {
+      const Buffer& q = plan.bufs[o];
+      if (q.first <= b.last && b.first <= q.last) busy.push_back({q.arena_off, q.arena_off + round_up(q.elems, 64)});
+    }
+    std::sort(busy.begin(), busy.end());
+    size_t off = 0;
+    for (auto& r : busy) {
+      if (r.first >= off + size) break;
+      off = std::max(off, r.second);
+    }
+    b.arena_off = off;
+    total = std::max(total, off + size);
+    placed.push_back(id);
+  }
+  plan.arena_elems = total;
+  plan.unplanned_elems = unplanned;
+}
+
+}  // namespace ppocr

@@ -1,0 +1,265 @@
+"""Python mirror of the reference's ``ppocr_rs::gpu`` API over the C ABI.
+
+The classes follow the reference's direct-model API (``src/gpu/mod.rs:3-13``):
+``Gpu`` (``Gpu::new``, ``upload_rgb``), ``Detector`` / ``Recognizer``
+(``load``, ``forward``, ``forward_image``, ``benchmark``) returning
+``ModelOutput`` (shape + values), and ``GpuError`` carrying the status code
+of the reference ``gpu::Error`` variant (``src/gpu/error.rs:9-45``).
+
+Everything runs in ``libppocr_hip.so`` (include/ppocr_hip.h); this module
+only marshals arguments.  It raises when the library is missing: there is no
+fallback path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = pathlib.Path(os.environ.get("PPOCR_HIP_LIB", HERE / "libppocr_hip.so"))
+
+SIZE_CODE = {"medium": 0, "small": 1, "tiny": 2}
+PRECISION = {"f32": 0, "bf16": 1}
+STATUS = {
+    0: "Ok", 1: "ReadFile", 2: "Safetensors", 3: "TensorNotFound", 4: "UnsupportedDtype",
+    5: "ShapeMismatch", 6: "TensorSizeOverflow", 7: "TensorByteLength", 8: "InvalidTensorRange",
+    9: "InvalidModel", 10: "InvalidInput", 11: "Gpu",
+}
+
+# Every symbol include/ppocr_hip.h declares.
+EXPORTS = (
+    "ppocr_hip_last_error", "ppocr_hip_create", "ppocr_hip_destroy", "ppocr_hip_detector_load",
+    "ppocr_hip_recognizer_load", "ppocr_hip_model_free", "ppocr_hip_output_shape", "ppocr_hip_forward",
+    "ppocr_hip_upload_rgb", "ppocr_hip_image_free", "ppocr_hip_forward_image", "ppocr_hip_preprocess",
+    "ppocr_hip_benchmark", "ppocr_hip_benchmark_stream", "ppocr_hip_profile", "ppocr_hip_memory_report",
+)
+
+
+class GpuError(RuntimeError):
+    """A failed C-ABI call; ``kind`` names the reference ``gpu::Error`` variant."""
+
+    def __init__(self, code, message):
+        super().__init__(f"{STATUS.get(code, code)}: {message}")
+        self.code = code
+        self.kind = STATUS.get(code, str(code))
+
+
+class KernelStat(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 64), ("kernel", ctypes.c_char * 32), ("avg_ms", ctypes.c_double),
+                ("flops", ctypes.c_double), ("bytes", ctypes.c_double), ("bound", ctypes.c_int)]
+
+
+_lib = None
+_SZ = ctypes.POINTER(ctypes.c_size_t)
+_F = ctypes.POINTER(ctypes.c_float)
+_D = ctypes.POINTER(ctypes.c_double)
+_VP = ctypes.c_void_p
+
+
+def lib():
+    """Loads libppocr_hip.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"HIP backend library missing: {LIB_PATH} (build it with make -C ppocr-rs_amd)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.ppocr_hip_last_error.restype = ctypes.c_char_p
+        L.ppocr_hip_create.argtypes = [ctypes.c_int, ctypes.POINTER(_VP)]
+        L.ppocr_hip_destroy.argtypes = [_VP]
+        L.ppocr_hip_detector_load.argtypes = [_VP, ctypes.c_char_p, ctypes.c_int, _SZ, ctypes.c_int,
+                                              ctypes.POINTER(_VP)]
+        L.ppocr_hip_recognizer_load.argtypes = [_VP, ctypes.c_char_p, ctypes.c_int, _SZ, ctypes.c_int, _VP,
+                                                ctypes.POINTER(_VP)]
+        L.ppocr_hip_model_free.argtypes = [_VP]
+        L.ppocr_hip_output_shape.argtypes = [_VP, _SZ, _SZ]
+        L.ppocr_hip_forward.argtypes = [_VP, _F, ctypes.c_size_t, _F, ctypes.c_size_t]
+        L.ppocr_hip_upload_rgb.argtypes = [_VP, ctypes.c_uint32, ctypes.c_uint32, _VP, ctypes.c_size_t,
+                                           ctypes.POINTER(_VP)]
+        L.ppocr_hip_image_free.argtypes = [_VP]
+        L.ppocr_hip_forward_image.argtypes = [_VP, _VP, _F, _SZ, ctypes.c_size_t, _F, ctypes.c_size_t]
+        L.ppocr_hip_preprocess.argtypes = [_VP, _VP, _F, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
+                                           ctypes.c_int, _F]
+        L.ppocr_hip_benchmark.argtypes = [_VP, _F, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _D]
+        L.ppocr_hip_benchmark_stream.argtypes = [_VP, _F, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _D]
+        L.ppocr_hip_profile.argtypes = [_VP, _F, ctypes.c_size_t, ctypes.c_size_t, ctypes.POINTER(KernelStat),
+                                        ctypes.c_size_t, _SZ]
+        L.ppocr_hip_memory_report.argtypes = [_VP, _SZ, _SZ, _SZ]
+        _lib = L
+    return _lib
+
+
+def _check(code):
+    if code != 0:
+        raise GpuError(code, lib().ppocr_hip_last_error().decode(errors="replace"))
+
+
+def _f32(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a, a.ctypes.data_as(_F)
+
+
+def _sizes(values):
+    arr = (ctypes.c_size_t * len(values))(*[int(v) for v in values])
+    return arr
+
+
+@dataclass
+class ModelOutput:
+    """``gpu::ModelOutput`` (src/gpu/model.rs:37-41)."""
+
+    shape: list
+    values: np.ndarray
+
+    def array(self):
+        return self.values.reshape(self.shape)
+
+
+class Gpu:
+    """``gpu::Gpu`` (src/gpu/runtime.rs:94-229): one device, stream and arena."""
+
+    def __init__(self, device=0):
+        h = _VP()
+        _check(lib().ppocr_hip_create(int(device), ctypes.byref(h)))
+        self.handle = h
+        self._children = []
+
+    def upload_rgb(self, rgb):
+        """``Gpu::upload_rgb``: RGB8 HWC array -> device image."""
+        rgb = np.ascontiguousarray(rgb, dtype=np.uint8)
+        if rgb.ndim != 3 or rgb.shape[2] != 3:
+            raise ValueError("expected an HxWx3 uint8 image")
+        h = _VP()
+        _check(lib().ppocr_hip_upload_rgb(self.handle, rgb.shape[1], rgb.shape[0], rgb.ctypes.data_as(_VP), rgb.size,
+                                          ctypes.byref(h)))
+        return GpuImage(self, h, rgb.shape[1], rgb.shape[0])
+
+    def preprocess(self, image, corners, canvas_w, canvas_h, content_width=None, detector=True):
+        """Device ``prepare_detector`` / ``prepare_recognizer`` of one quad -> [3, h, w]."""
+        c, cp = _f32(np.asarray(corners, dtype=np.float32).reshape(8))
+        out = np.empty((3, canvas_h, canvas_w), dtype=np.float32)
+        _check(lib().ppocr_hip_preprocess(self.handle, image.handle, cp, canvas_w, canvas_h,
+                                          canvas_w if content_width is None else content_width, int(detector),
+                                          out.ctypes.data_as(_F)))
+        return out
+
+    def close(self):
+        for child in self._children:
+            child.close()
+        self._children.clear()
+        if self.handle:
+            lib().ppocr_hip_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class GpuImage:
+    def __init__(self, gpu, handle, width, height):
+        self.gpu, self.handle, self.width, self.height = gpu, handle, width, height
+
+    def close(self):
+        if self.handle:
+            lib().ppocr_hip_image_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class _Model:
+    def __init__(self, gpu, handle, input_shape):
+        self.gpu = gpu
+        self.handle = handle
+        self.input_shape = tuple(int(v) for v in input_shape)
+        shape = (ctypes.c_size_t * 4)()
+        rank = ctypes.c_size_t()
+        _check(lib().ppocr_hip_output_shape(handle, shape, ctypes.byref(rank)))
+        self.output_shape = [int(shape[i]) for i in range(rank.value)]
+        self.output_len = int(np.prod(self.output_shape))
+        gpu._children.append(self)
+
+    def forward(self, nchw):
+        """``forward(&[f32]) -> ModelOutput`` (src/gpu/model.rs:95-114, :222-237)."""
+        x, xp = _f32(nchw)
+        out = np.empty(self.output_len, dtype=np.float32)
+        _check(lib().ppocr_hip_forward(self.handle, xp, x.size, out.ctypes.data_as(_F), out.size))
+        return ModelOutput(list(self.output_shape), out)
+
+    def forward_image(self, image, corners, content_widths=None):
+        """``forward_image`` with per-item quads [N, 4, 2] and content widths [N]."""
+        c, cp = _f32(np.asarray(corners, dtype=np.float32).reshape(-1, 8))
+        n = c.shape[0]
+        widths = None if content_widths is None else _sizes(content_widths)
+        out = np.empty(self.output_len, dtype=np.float32)
+        _check(lib().ppocr_hip_forward_image(self.handle, image.handle, cp, widths, n, out.ctypes.data_as(_F),
+                                             out.size))
+        return ModelOutput(list(self.output_shape), out)
+
+    def benchmark(self, nchw, warmup=5, runs=30):
+        """Per-run milliseconds, device-only like ``benchmark_nchw`` (src/gpu/runtime.rs:1798-1830)."""
+        x, xp = _f32(nchw)
+        samples = (ctypes.c_double * runs)()
+        _check(lib().ppocr_hip_benchmark(self.handle, xp, x.size, warmup, runs, samples))
+        return list(samples)
+
+    def benchmark_stream(self, nchw, warmup, runs):
+        """Total milliseconds of ``runs`` back-to-back passes (inputs resident in HBM)."""
+        x, xp = _f32(nchw)
+        total = ctypes.c_double()
+        _check(lib().ppocr_hip_benchmark_stream(self.handle, xp, x.size, warmup, runs, ctypes.byref(total)))
+        return total.value
+
+    def profile(self, nchw, runs=10):
+        x, xp = _f32(nchw)
+        count = ctypes.c_size_t()
+        _check(lib().ppocr_hip_profile(self.handle, xp, x.size, 1, None, 0, ctypes.byref(count)))
+        stats = (KernelStat * count.value)()
+        _check(lib().ppocr_hip_profile(self.handle, xp, x.size, runs, stats, count.value, ctypes.byref(count)))
+        return [dict(name=s.name.decode(), kernel=s.kernel.decode(), avg_ms=s.avg_ms, flops=s.flops, bytes=s.bytes,
+                     bound=("mfma" if s.bound else "hbm")) for s in stats]
+
+    def memory_report(self):
+        a, u, w = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+        _check(lib().ppocr_hip_memory_report(self.handle, ctypes.byref(a), ctypes.byref(u), ctypes.byref(w)))
+        return {"arena_bytes": a.value, "unplanned_bytes": u.value, "weight_bytes": w.value}
+
+    def close(self):
+        if self.handle:
+            lib().ppocr_hip_model_free(self.handle)
+            self.handle = None
+
+
+class Detector(_Model):
+    """``gpu::Detector`` (src/gpu/model.rs:44-148)."""
+
+    @classmethod
+    def load(cls, gpu, path, size, input_shape, precision="f32"):
+        h = _VP()
+        _check(lib().ppocr_hip_detector_load(gpu.handle, str(path).encode(), SIZE_CODE[size], _sizes(input_shape),
+                                             PRECISION[precision], ctypes.byref(h)))
+        return cls(gpu, h, input_shape)
+
+
+class Recognizer(_Model):
+    """``gpu::Recognizer`` (src/gpu/model.rs:150-266)."""
+
+    @classmethod
+    def load(cls, gpu, path, size, input_shape, precision="f32", share_weights=None):
+        h = _VP()
+        _check(lib().ppocr_hip_recognizer_load(gpu.handle, str(path).encode(), SIZE_CODE[size], _sizes(input_shape),
+                                               PRECISION[precision],
+                                               share_weights.handle if share_weights is not None else None,
+                                               ctypes.byref(h)))
+        return cls(gpu, h, input_shape)

@@ -1,0 +1,74 @@
+"""Shared helpers of the test suite: seeded model files, comparison rules and
+the CPU-side reference decoders used for the exact-output checks."""
+
+from __future__ import annotations
+
+import pathlib
+import tempfile
+
+import numpy as np
+
+import seeded
+
+_CACHE = pathlib.Path(tempfile.gettempdir()) / "ppocr_hip_test_models"
+
+
+def model_path(kind, size, seed=None):
+    """Seeded safetensors file for (kind, size), generated once per machine."""
+    seed = (1 if kind == "det" else 2) if seed is None else seed
+    _CACHE.mkdir(parents=True, exist_ok=True)
+    path = _CACHE / f"{kind}_{size}_s{seed}.safetensors"
+    if not path.exists():
+        tmp = path.with_suffix(".tmp")
+        seeded.write_weights(tmp, kind, size, seed=seed)
+        tmp.replace(path)
+    return path
+
+
+def band_mismatches(actual, expected, threshold, eps=1e-5):
+    """Binarisation mismatches at `threshold` outside the ambiguity band.
+
+    Values within `eps` of the threshold may legitimately round to either
+    side; everything else must agree exactly.  Returns (mismatches, band).
+    """
+    a = actual >= threshold
+    e = expected >= threshold
+    band = np.abs(expected - threshold) <= eps
+    return int(np.count_nonzero((a != e) & ~band)), int(np.count_nonzero(band))
+
+
+def argmax_last(rows):
+    """Argmax with ties resolved to the last index, as Rust's
+    ``max_by(total_cmp)`` (src/bin/benchmark.rs:287-293, src/ocr.rs:1171-1177)."""
+    rows = np.asarray(rows)
+    flipped = rows[..., ::-1]
+    return rows.shape[-1] - 1 - np.argmax(flipped, axis=-1)
+
+
+def ctc_greedy(probs, dictionary, content_width, input_width):
+    """``decode_ctc_greedy_for_input`` (src/ocr.rs:800-853) for one [T, V] item."""
+    t, classes = probs.shape
+    implicit_space = classes == len(dictionary) + 2
+    valid = min(max(-(-content_width * t // input_width), 1), t)
+    text = []
+    previous = 0
+    log_score = 0.0
+    emitted = 0
+    for step in range(valid):
+        row = probs[step]
+        cls = int(argmax_last(row))
+        if cls != 0 and cls != previous:
+            text.append(" " if implicit_space and cls == classes - 1 else dictionary[cls - 1])
+            log_score += float(np.log(max(float(row[cls]), 1e-8)))
+            emitted += 1
+        previous = cls
+    return "".join(text), (float(np.exp(log_score / emitted)) if emitted else 0.0)
+
+
+def synthetic_dictionary(classes):
+    """Dictionary of `classes - 1` distinct tokens (blank is class 0)."""
+    return [f"<{i}>" for i in range(1, classes)]
+
+
+def quad_corners(x0, y0, x1, y1):
+    return np.array([[x0, y0], [x1, y0], [x1, y1], [x0, y1]], dtype=np.float32)

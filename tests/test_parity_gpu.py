@@ -1,0 +1,215 @@
+"""Parity of the HIP backend against the CPU oracle on identical seeded
+inputs and weights (run on an MI355X: ``pytest -m gpu``).
+
+Bars:
+* detector probability maps: max |diff| <= 1e-3 (fp32 accumulate), and the
+  DB binarisation at 0.2 / 0.5 identical outside a 1e-5 ambiguity band;
+* recognizer softmax probabilities: max |diff| <= 1e-3, argmax identical
+  where the top-2 gap exceeds 1e-4, greedy-CTC strings identical;
+* preprocessing: bit-exact (integer rounding of the bilinear sample).
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+import ppocr_hip
+import seeded
+from helpers import (argmax_last, band_mismatches, ctc_greedy, model_path, quad_corners,
+                     synthetic_dictionary)
+
+pytestmark = pytest.mark.gpu
+
+DET_TOL = 1e-3
+REC_TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    g = ppocr_hip.Gpu(0)
+    yield g
+    g.close()
+
+
+_oracles = {}
+
+
+def oracle_model(kind, size):
+    key = (kind, size)
+    if key not in _oracles:
+        _oracles[key] = oracle.Model(kind, model_path(kind, size), size)
+    return _oracles[key]
+
+
+def check_detector(actual, expected):
+    assert actual.shape == expected.shape
+    err = float(np.max(np.abs(actual - expected)))
+    assert err <= DET_TOL, f"max abs diff {err}"
+    for thr in (0.2, 0.5):
+        mism, band = band_mismatches(actual, expected, thr)
+        assert mism == 0, f"{mism} mask mismatches at {thr} (band {band})"
+    return err
+
+
+def check_recognizer(actual, expected):
+    assert actual.shape == expected.shape
+    err = float(np.max(np.abs(actual - expected)))
+    assert err <= REC_TOL, f"max abs diff {err}"
+    srt = np.sort(expected, axis=-1)
+    clear = (srt[..., -1] - srt[..., -2]) > 1e-4
+    am_a, am_e = argmax_last(actual), argmax_last(expected)
+    assert np.all(am_a[clear] == am_e[clear])
+    return err
+
+
+@pytest.mark.parametrize("size,shape,seed,pattern", [
+    ("tiny", (1, 3, 416, 736), 7, "uniform"),
+    ("tiny", (2, 3, 64, 96), 3, "uniform"),
+    ("tiny", (1, 3, 832, 1472), 5, "blocks"),
+    ("small", (1, 3, 416, 736), 7, "uniform"),
+    ("small", (8, 3, 416, 736), 11, "uniform"),
+    ("medium", (1, 3, 416, 736), 7, "uniform"),
+    ("medium", (2, 3, 128, 160), 9, "uniform"),
+])
+def test_detector_matches_oracle(gpu, size, shape, seed, pattern):
+    x = seeded.seeded_batch(shape[0], shape[2], shape[3], seed, detector=True, pattern=pattern)
+    det = ppocr_hip.Detector.load(gpu, model_path("det", size), size, shape)
+    try:
+        out = det.forward(x)
+        assert out.shape == [shape[0], 1, shape[2], shape[3]]
+        expected = oracle_model("det", size).forward(x)
+        err = check_detector(out.array(), expected)
+        print(f"det {size} {shape}: max abs {err:.2e}")
+    finally:
+        det.close()
+
+
+@pytest.mark.parametrize("size,batch,width", [
+    ("tiny", 4, 320),
+    ("tiny", 64, 320),
+    ("tiny", 3, 100),
+    ("small", 4, 320),
+    ("medium", 4, 320),
+    ("medium", 2, 648),
+])
+def test_recognizer_matches_oracle(gpu, size, batch, width):
+    x = seeded.seeded_batch(batch, 48, width, 100 + batch, detector=False)
+    shape = (batch, 3, 48, width)
+    rec = ppocr_hip.Recognizer.load(gpu, model_path("rec", size), size, shape)
+    try:
+        out = rec.forward(x).array()
+        expected = oracle_model("rec", size).forward(x)
+        err = check_recognizer(out, expected)
+        dictionary = synthetic_dictionary(expected.shape[-1])
+        for i in range(batch):
+            assert ctc_greedy(out[i], dictionary, width, width)[0] == ctc_greedy(expected[i], dictionary, width,
+                                                                               width)[0]
+        print(f"rec {size} {shape}: max abs {err:.2e}")
+    finally:
+        rec.close()
+
+
+def test_preprocess_is_bit_exact(gpu):
+    rng = np.random.default_rng(5)
+    img = rng.integers(0, 256, size=(97, 211, 3), dtype=np.uint8)
+    image = gpu.upload_rgb(img)
+    cases = [
+        (quad_corners(0, 0, 211, 97), 160, 64, 160, True),
+        (np.array([[2.25, 1.75], [190.5, 3.0], [182.75, 90.0], [1.0, 85.5]], np.float32), 320, 48, 201, False),
+        (np.array([[10.0, 80.0], [200.0, 5.0], [205.0, 30.0], [12.0, 96.0]], np.float32), 128, 48, 128, False),
+    ]
+    for corners, cw, ch, content, det in cases:
+        got = gpu.preprocess(image, corners, cw, ch, content, det)
+        want = oracle.preprocess(img, corners, cw, ch, content, det)
+        assert np.array_equal(got, want), f"max diff {np.max(np.abs(got - want))}"
+    image.close()
+
+
+def test_detector_forward_image_matches_host_preprocess(gpu):
+    img = seeded.seeded_rgb(540, 960, 21)
+    h, w = 416, 736
+    det = ppocr_hip.Detector.load(gpu, model_path("det", "tiny"), "tiny", (1, 3, h, w))
+    image = gpu.upload_rgb(img)
+    try:
+        corners = quad_corners(0, 0, 960, 540)
+        out = det.forward_image(image, corners[None]).array()
+        x = oracle.preprocess(img, corners, w, h, w, True)[None]
+        expected = oracle_model("det", "tiny").forward(x)
+        check_detector(out, expected)
+    finally:
+        image.close()
+        det.close()
+
+
+def test_recognizer_forward_image_batched_crops(gpu):
+    img = seeded.seeded_rgb(300, 500, 33, pattern="blocks")
+    quads = np.stack([quad_corners(10, 20, 210, 60), quad_corners(100, 100, 180, 120),
+                      np.array([[300, 200], [480, 210], [478, 250], [298, 240]], np.float32)])
+    widths = [240, 192, 216]
+    n, width = len(quads), 320
+    rec = ppocr_hip.Recognizer.load(gpu, model_path("rec", "tiny"), "tiny", (n, 3, 48, width))
+    image = gpu.upload_rgb(img)
+    try:
+        out = rec.forward_image(image, quads, widths).array()
+        x = np.stack([oracle.preprocess(img, q, width, 48, cw, False) for q, cw in zip(quads, widths)])
+        expected = oracle_model("rec", "tiny").forward(x)
+        check_recognizer(out, expected)
+    finally:
+        image.close()
+        rec.close()
+
+
+def test_recognizers_share_device_weights(gpu):
+    path = model_path("rec", "tiny")
+    a = ppocr_hip.Recognizer.load(gpu, path, "tiny", (2, 3, 48, 320))
+    b = ppocr_hip.Recognizer.load(gpu, path, "tiny", (1, 3, 48, 160), share_weights=a)
+    try:
+        x = seeded.seeded_batch(1, 48, 160, 77, detector=False)
+        check_recognizer(b.forward(x).array(), oracle_model("rec", "tiny").forward(x))
+        assert b.memory_report()["weight_bytes"] == a.memory_report()["weight_bytes"]
+    finally:
+        b.close()
+        a.close()
+
+
+def test_invalid_inputs_are_rejected(gpu):
+    path = model_path("det", "tiny")
+    with pytest.raises(ppocr_hip.GpuError) as e:
+        ppocr_hip.Detector.load(gpu, path, "tiny", (1, 3, 100, 96))
+    assert e.value.kind == "InvalidInput"
+    with pytest.raises(ppocr_hip.GpuError) as e:
+        ppocr_hip.Detector.load(gpu, path, "medium", (1, 3, 64, 64))
+    assert e.value.kind == "InvalidModel"
+    with pytest.raises(ppocr_hip.GpuError) as e:
+        ppocr_hip.Detector.load(gpu, "/nonexistent/weights.safetensors", "tiny", (1, 3, 64, 64))
+    assert e.value.kind == "ReadFile"
+    det = ppocr_hip.Detector.load(gpu, path, "tiny", (1, 3, 64, 64))
+    try:
+        with pytest.raises(ppocr_hip.GpuError) as e:
+            det.forward(np.zeros((1, 3, 64, 32), np.float32))
+        assert e.value.kind == "InvalidInput"
+        bad = np.zeros((1, 3, 64, 64), np.float32)
+        bad[0, 1, 5, 5] = np.nan
+        with pytest.raises(ppocr_hip.GpuError) as e:
+            det.forward(bad)
+        assert e.value.kind == "InvalidInput"
+        good = seeded.seeded_batch(1, 64, 64, 1)
+        check_detector(det.forward(good).array(), oracle_model("det", "tiny").forward(good))
+    finally:
+        det.close()
+
+
+def test_benchmark_and_profile_report(gpu):
+    x = seeded.seeded_batch(1, 416, 736, 7)
+    det = ppocr_hip.Detector.load(gpu, model_path("det", "tiny"), "tiny", x.shape)
+    try:
+        samples = det.benchmark(x, warmup=2, runs=5)
+        assert len(samples) == 5 and all(s > 0 for s in samples)
+        stats = det.profile(x, runs=3)
+        assert stats and all(s["avg_ms"] >= 0 for s in stats)
+        total = det.benchmark_stream(x, 2, 10)
+        assert total > 0
+        # The pass after profiling still matches the oracle (no stale state).
+        check_detector(det.forward(x).array(), oracle_model("det", "tiny").forward(x))
+    finally:
+        det.close()
