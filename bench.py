@@ -42,7 +42,8 @@ TMP = pathlib.Path(tempfile.gettempdir()) / "ppocr_bench_models"
 
 def weights(kind, size):
     TMP.mkdir(parents=True, exist_ok=True)
-    path = TMP / f"{kind}_{size}.safetensors"
+    gain, head_gain = seeded.DEFAULT_GAINS[(kind, size)]
+    path = TMP / f"{kind}_{size}_g{gain}_{head_gain}.safetensors"
     if not path.exists():
         seeded.write_weights(path, kind, size, seed=1 if kind == "det" else 2)
     return path

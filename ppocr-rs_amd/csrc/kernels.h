@@ -68,19 +68,22 @@ struct SeParams {
   int N, HW, C, in_ps;
   float* partial;  // [N][P][C] partial sums
   int P;           // pixel chunks per image
-  const float* w1;  // [Cr][C]
+  const float* w1;  // [Cr][C] reduce weight
   const float* b1;
-  const float* w2;  // [C][Cr]
+  const float* w2;  // [C][Cr] expand weight
   const float* b2;
   int Cr;
   int gate_act;
-  float* gate;  // [N][C]
+  float* hidden;  // [N][Cr]
+  float* gate;    // [N][C]
 };
 
 void launch_conv(const ConvParams& p, hipStream_t s);
 // Name of the tile instance launch_conv picks for M rows x `cols` columns.
 const char* conv_tile_name(int M, int cols);
 void launch_depthwise(const DwParams& p, hipStream_t s);
+// Name of the kernel instance launch_depthwise picks.
+const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho);
 void launch_se(const SeParams& p, hipStream_t s);
 
 // NCHW (3 planes) -> NHWC with 4 channels (fourth channel zero).

@@ -65,9 +65,131 @@ __global__ __launch_bounds__(256) void depthwise_kernel(DwParams p) {
   *reinterpret_cast<float4*>(p.out + (size_t)pix * p.out_ps + c) = acc;
 }
 
+// LDS-tiled stride-1 depthwise.  A block computes a TY x TX output tile of 32
+// channels (8 float4 lanes per pixel, 128 B contiguous per pixel).  The input
+// tile with its halo and the taps are staged once in LDS; each lane then
+// slides a register window of XR + KW - 1 pixels along x to produce XR = 4
+// outputs, so every staged value is reused KW x KH times from registers/LDS
+// instead of being re-read from the caches.  Taps accumulate in (ky, kx)
+// order as the generic kernel does.
+template <int KH, int KW, int TY>
+__global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
+  constexpr int C4B = 8;                  // float4 lanes per pixel (32 channels)
+  constexpr int XR = 4;                   // outputs per lane along x
+  constexpr int XG = 256 / (C4B * TY);    // lane groups along x
+  constexpr int TX = XG * XR;
+  constexpr int IH = TY + KH - 1, IW = TX + KW - 1;
+  __shared__ float4 tile[IH * IW * C4B];
+  __shared__ float4 taps[KH * KW * C4B];
+
+  const int cblocks = (p.C + 31) / 32;
+  const int n = blockIdx.z / cblocks;
+  const int ch0 = (blockIdx.z - n * cblocks) * 32;
+  const int oy0 = blockIdx.y * TY, ox0 = blockIdx.x * TX;
+  const int tid = threadIdx.x;
+
+  for (int i = tid; i < IH * IW * C4B; i += 256) {
+    int c4 = i % C4B;
+    int px = i / C4B;
+    int ix = px % IW, iy = px / IW;
+    int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
+    int c = ch0 + c4 * 4;
+    float4 v = f4_zero();
+    if (c < p.C && gy >= 0 && gy < p.H && gx >= 0 && gx < p.W)
+      v = *reinterpret_cast<const float4*>(p.in + ((size_t)(n * p.H + gy) * p.W + gx) * p.in_ps + c);
+    tile[i] = v;
+  }
+  for (int i = tid; i < KH * KW * C4B; i += 256) {
+    int c = ch0 + (i % C4B) * 4;
+    int t = i / C4B;
+    taps[i] = c < p.C ? *reinterpret_cast<const float4*>(p.wt + (size_t)t * p.C + c) : f4_zero();
+  }
+  __syncthreads();
+
+  const int c4 = tid % C4B;
+  const int xg = (tid / C4B) % XG;
+  const int ty = tid / (C4B * XG);
+  float4 acc[XR];
+#pragma unroll
+  for (int r = 0; r < XR; ++r) acc[r] = f4_zero();
+  // One row window live at a time keeps the kernel free of register spills.
+#pragma unroll 1
+  for (int ky = 0; ky < KH; ++ky) {
+    float4 win[XR + KW - 1];
+#pragma unroll
+    for (int j = 0; j < XR + KW - 1; ++j) win[j] = tile[((ty + ky) * IW + xg * XR + j) * C4B + c4];
+#pragma unroll
+    for (int kx = 0; kx < KW; ++kx) {
+      float4 w = taps[(ky * KW + kx) * C4B + c4];
+#pragma unroll
+      for (int r = 0; r < XR; ++r) {
+        acc[r].x = fmaf(win[r + kx].x, w.x, acc[r].x);
+        acc[r].y = fmaf(win[r + kx].y, w.y, acc[r].y);
+        acc[r].z = fmaf(win[r + kx].z, w.z, acc[r].z);
+        acc[r].w = fmaf(win[r + kx].w, w.w, acc[r].w);
+      }
+    }
+  }
+  const int c = ch0 + c4 * 4;
+  const int oy = oy0 + ty;
+  if (c >= p.C || oy >= p.Ho) return;
+  float4 b = p.bias ? *reinterpret_cast<const float4*>(p.bias + c) : f4_zero();
+#pragma unroll
+  for (int r = 0; r < XR; ++r) {
+    int ox = ox0 + xg * XR + r;
+    if (ox >= p.Wo) break;
+    float4 v = acc[r];
+    if (p.bias) {
+      v.x += b.x;
+      v.y += b.y;
+      v.z += b.z;
+      v.w += b.w;
+    }
+    v.x = act_apply(p.act, v.x);
+    v.y = act_apply(p.act, v.y);
+    v.z = act_apply(p.act, v.z);
+    v.w = act_apply(p.act, v.w);
+    size_t pix = (size_t)(n * p.Ho + oy) * p.Wo + ox;
+    if (p.res) {
+      float4 rr = *reinterpret_cast<const float4*>(p.res + pix * p.res_ps + c);
+      v.x = rr.x + v.x;
+      v.y = rr.y + v.y;
+      v.z = rr.z + v.z;
+      v.w = rr.w + v.w;
+    }
+    *reinterpret_cast<float4*>(p.out + pix * p.out_ps + c) = v;
+  }
+}
+
+template <int KH, int KW, int TY>
+static void launch_dw_tiled(const DwParams& p, hipStream_t s) {
+  constexpr int TX = 256 / (8 * TY) * 4;
+  dim3 grid((p.Wo + TX - 1) / TX, (p.Ho + TY - 1) / TY, p.N * ((p.C + 31) / 32));
+  hipLaunchKernelGGL((depthwise_tiled_kernel<KH, KW, TY>), grid, dim3(256), 0, s, p);
+}
+
 void launch_depthwise(const DwParams& p, hipStream_t s) {
+  if (p.sh == 1 && p.sw == 1) {
+    const bool tall = p.Ho >= 16;
+    if (p.kh == 3 && p.kw == 3) return tall ? launch_dw_tiled<3, 3, 8>(p, s) : launch_dw_tiled<3, 3, 2>(p, s);
+    if (p.kh == 5 && p.kw == 5) return launch_dw_tiled<5, 5, 8>(p, s);
+    if (p.kh == 7 && p.kw == 7) return launch_dw_tiled<7, 7, 8>(p, s);
+    if (p.kh == 9 && p.kw == 9) return launch_dw_tiled<9, 9, 8>(p, s);
+    if (p.kh == 1 && p.kw == 5 && p.Ho == 1) return launch_dw_tiled<1, 5, 1>(p, s);
+    if (p.kh == 1 && p.kw == 7 && p.Ho == 1) return launch_dw_tiled<1, 7, 1>(p, s);
+  }
   long total = (long)p.N * p.Ho * p.Wo * (p.C / 4);
   hipLaunchKernelGGL(depthwise_kernel, dim3(blocks_for(total)), dim3(256), 0, s, p);
+}
+
+const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho) {
+  if (sh == 1 && sw == 1) {
+    if (kh == 3 && kw == 3) return Ho >= 16 ? "depthwise_tiled<3x3>" : "depthwise_tiled<3x3,short>";
+    if (kh == kw && (kh == 5 || kh == 7 || kh == 9))
+      return kh == 5 ? "depthwise_tiled<5x5>" : kh == 7 ? "depthwise_tiled<7x7>" : "depthwise_tiled<9x9>";
+    if (kh == 1 && (kw == 5 || kw == 7) && Ho == 1) return kw == 5 ? "depthwise_tiled<1x5>" : "depthwise_tiled<1x7>";
+  }
+  return "depthwise";
 }
 
 // ----------------------------------------------------------------- SE gate
@@ -112,38 +234,86 @@ __global__ __launch_bounds__(256) void se_partial_kernel(SeParams p, int chunk) 
   }
 }
 
-__global__ __launch_bounds__(256) void se_gate_kernel(SeParams p) {
+// Wave-per-output matrix-vector product: out[j] = sum_i W[j][i] v[i] with
+// the 64 lanes striding i (coalesced weight rows) and a wave reduction.
+__device__ __forceinline__ float wave_dot(const float* __restrict__ w, const float* v, int n, int lane) {
+  float acc = 0.0f;
+  for (int i = lane; i < n; i += 64) acc = fmaf(w[i], v[i], acc);
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  return acc;
+}
+
+// Stage 2: one block per (image, 16 reduced channels).  The block finishes
+// the mean from the partial sums, then each wave computes four outputs of
+// the reducing 1x1 conv + bias + ReLU.
+__global__ __launch_bounds__(256) void se_reduce_kernel(SeParams p) {
   extern __shared__ float sm[];
-  float* mean = sm;           // [C]
-  float* hidden = sm + p.C;   // [Cr]
+  float* mean = sm;                                       // [C]
+  float4* red = reinterpret_cast<float4*>(sm + p.C);     // [256]
   const int n = blockIdx.x;
   const int tid = threadIdx.x;
-  for (int c = tid; c < p.C; c += 256) {
-    float s = 0.0f;
-    for (int k = 0; k < p.P; ++k) s += p.partial[((size_t)n * p.P + k) * p.C + c];
-    mean[c] = s / (float)p.HW;
+  const int C4 = p.C >> 2;
+  const int lanes_p = 256 / C4;
+  const int cq = tid % C4, pl = tid / C4;
+  float4 s = f4_zero();
+  if (pl < lanes_p) {
+    for (int k = pl; k < p.P; k += lanes_p) {
+      float4 v = *reinterpret_cast<const float4*>(p.partial + ((size_t)n * p.P + k) * p.C + cq * 4);
+      s.x += v.x;
+      s.y += v.y;
+      s.z += v.z;
+      s.w += v.w;
+    }
+  }
+  red[tid] = s;
+  __syncthreads();
+  if (tid < C4) {
+    float4 t = red[tid];
+    for (int k = 1; k < lanes_p; ++k) {
+      float4 v = red[k * C4 + tid];
+      t.x += v.x;
+      t.y += v.y;
+      t.z += v.z;
+      t.w += v.w;
+    }
+    const float count = (float)p.HW;
+    mean[tid * 4 + 0] = t.x / count;
+    mean[tid * 4 + 1] = t.y / count;
+    mean[tid * 4 + 2] = t.z / count;
+    mean[tid * 4 + 3] = t.w / count;
   }
   __syncthreads();
-  for (int j = tid; j < p.Cr; j += 256) {
-    const float* w = p.w1 + (size_t)j * p.C;
-    float acc = 0.0f;
-    for (int c = 0; c < p.C; ++c) acc = fmaf(w[c], mean[c], acc);
-    hidden[j] = fmaxf(acc + p.b1[j], 0.0f);
+  const int wave = tid >> 6, lane = tid & 63;
+  for (int q = 0; q < 4; ++q) {
+    int j = blockIdx.y * 16 + wave * 4 + q;
+    if (j >= p.Cr) break;
+    float acc = wave_dot(p.w1 + (size_t)j * p.C, mean, p.C, lane);
+    if (lane == 0) p.hidden[(size_t)n * p.Cr + j] = fmaxf(acc + p.b1[j], 0.0f);
   }
+}
+
+// Stage 3: one block per (image, 16 channels): expanding 1x1 conv + bias and
+// the gate activation.
+__global__ __launch_bounds__(256) void se_expand_kernel(SeParams p) {
+  extern __shared__ float hid[];  // [Cr]
+  const int n = blockIdx.x;
+  for (int j = threadIdx.x; j < p.Cr; j += 256) hid[j] = p.hidden[(size_t)n * p.Cr + j];
   __syncthreads();
-  for (int c = tid; c < p.C; c += 256) {
-    const float* w = p.w2 + (size_t)c * p.Cr;
-    float acc = 0.0f;
-    for (int j = 0; j < p.Cr; ++j) acc = fmaf(w[j], hidden[j], acc);
-    p.gate[(size_t)n * p.C + c] = act_apply(p.gate_act, acc + p.b2[c]);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int q = 0; q < 4; ++q) {
+    int c = blockIdx.y * 16 + wave * 4 + q;
+    if (c >= p.C) break;
+    float acc = wave_dot(p.w2 + (size_t)c * p.Cr, hid, p.Cr, lane);
+    if (lane == 0) p.gate[(size_t)n * p.C + c] = act_apply(p.gate_act, acc + p.b2[c]);
   }
 }
 
 void launch_se(const SeParams& p, hipStream_t s) {
   int chunk = (p.HW + p.P - 1) / p.P;
   hipLaunchKernelGGL(se_partial_kernel, dim3(p.P, p.N), dim3(256), 0, s, p, chunk);
-  size_t lds = (size_t)(p.C + p.Cr) * sizeof(float);
-  hipLaunchKernelGGL(se_gate_kernel, dim3(p.N), dim3(256), lds, s, p);
+  size_t lds = (size_t)p.C * sizeof(float) + 256 * sizeof(float4);
+  hipLaunchKernelGGL(se_reduce_kernel, dim3(p.N, (p.Cr + 15) / 16), dim3(256), lds, s, p);
+  hipLaunchKernelGGL(se_expand_kernel, dim3(p.N, (p.C + 15) / 16), dim3(256), (size_t)p.Cr * sizeof(float), s, p);
 }
 
 // ----------------------------------------------------------------- layout

@@ -307,7 +307,7 @@ class Builder {
     size_t wo = w.w, bo = w.b;
     Op op;
     op.name = name;
-    op.kernel = "depthwise";
+    op.kernel = depthwise_kernel_name(w.kh, w.kw, w.sh, w.sw, Ho);
     op.flops = 2.0 * out.pixels() * w.c * w.kh * w.kw;
     op.bytes = 4.0 * ((double)x.pixels() * w.c + (double)out.pixels() * w.c * (has_res ? 2 : 1) + w.kh * w.kw * w.c);
     op.reads = {x.buf};
@@ -332,6 +332,7 @@ class Builder {
     int HW = x.h * x.w;
     int P = std::max(1, std::min(HW / 64, std::max(1, 1024 / x.n)));
     View part = alloc(x.n, P, 1, x.c, name + ".partial");
+    View hid = alloc(x.n, 1, 1, (int)round_up(w.cr, 4), name + ".hidden");
     View gate = alloc(x.n, 1, 1, x.c, name);
     SeParams base{};
     base.N = x.n, base.HW = HW, base.C = x.c, base.in_ps = x.ps, base.P = P, base.Cr = w.cr, base.gate_act = w.act;
@@ -343,7 +344,7 @@ class Builder {
     op.flops = 2.0 * x.n * ((double)HW * x.c + 2.0 * x.c * w.cr);
     op.bytes = 4.0 * ((double)x.pixels() * x.c + 2.0 * x.c * w.cr + x.n * x.c);
     op.reads = {x.buf};
-    op.writes = {part.buf, gate.buf};
+    op.writes = {part.buf, hid.buf, gate.buf};
     op.launch = [=](const Exec& ex, hipStream_t s) {
       SeParams p = base;
       p.in = ex.ptr(in);
@@ -352,6 +353,7 @@ class Builder {
       p.b1 = ex.w(ww.b1);
       p.w2 = ex.w(ww.w2);
       p.b2 = ex.w(ww.b2);
+      p.hidden = ex.ptr(hid);
       p.gate = ex.ptr(gate);
       launch_se(p, s);
     };

@@ -260,10 +260,14 @@ def seeded_weights(kind, size, seed=0, gain=1.0, head_gain=None):
 
 # Per-model gains keep the seeded networks away from both collapse (a flat
 # probability map / uniform softmax) and saturation (probabilities stuck at
-# 0 or 1), so parity checks compare informative outputs.
+# 0 or 1), so parity checks compare informative outputs.  They also keep the
+# networks well conditioned: a 1e-7 relative perturbation of the input moves
+# every output by at most ~1e-4 (tests/test_seeded_models.py), so the 1e-3
+# parity tolerance measures kernel error rather than the amplification of
+# fp32 rounding noise by an exploding network.
 DEFAULT_GAINS = {
     ("det", "tiny"): (1.2, None), ("det", "small"): (1.16, None), ("det", "medium"): (1.12, None),
-    ("rec", "tiny"): (1.3, 4.0), ("rec", "small"): (1.3, 1.0), ("rec", "medium"): (1.4, 0.5),
+    ("rec", "tiny"): (1.3, 4.0), ("rec", "small"): (1.3, 1.0), ("rec", "medium"): (1.3, 0.5),
 }
 
 

@@ -17,7 +17,8 @@ def model_path(kind, size, seed=None):
     """Seeded safetensors file for (kind, size), generated once per machine."""
     seed = (1 if kind == "det" else 2) if seed is None else seed
     _CACHE.mkdir(parents=True, exist_ok=True)
-    path = _CACHE / f"{kind}_{size}_s{seed}.safetensors"
+    gain, head_gain = seeded.DEFAULT_GAINS[(kind, size)]
+    path = _CACHE / f"{kind}_{size}_s{seed}_g{gain}_{head_gain}.safetensors"
     if not path.exists():
         tmp = path.with_suffix(".tmp")
         seeded.write_weights(tmp, kind, size, seed=seed)
