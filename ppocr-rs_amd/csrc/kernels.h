@@ -32,8 +32,8 @@ struct ConvParams {
   int N, H, W, C, in_ps;
   float* out;
   int Ho, Wo, Co, out_ps;
-  const float* wt;  // packed [K][ldw], zero beyond Co
-  int ldw;
+  const float* wt;  // packed [Co][ldw], k = (ky*kw + kx)*C + c contiguous
+  int ldw;          // = K (a multiple of 4)
   const float* bias;  // [Co] or null
   int kh, kw, sh, sw, pt, pl;
   int act;
@@ -43,9 +43,8 @@ struct ConvParams {
   const float* res_gate;  // [N][Co]: residual term is res * g
   const float* up;        // nearest-upsample-add source [N, Ho/up_s, Wo/up_s, Co]
   int up_s, up_ps;
-  int rep;   // write each output pixel as a rep x rep block (upsample on write)
-  int mode;  // 0: conv; 1: 2x2 stride-2 transposed conv (columns j = tap*Co + o)
-  int out_h, out_w;  // dims of the tensor `out` points into (rep / mode 1)
+  int rep;           // write each output pixel as a rep x rep block (upsample on write)
+  int out_h, out_w;  // dims of the tensor `out` points into (Ho*rep, Wo*rep)
 };
 
 // Depthwise k x k convolution (groups == C), 4 channels per lane.

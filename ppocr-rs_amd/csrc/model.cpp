@@ -28,7 +28,6 @@ struct ConvW {
   size_t w = NOW, b = NOW;
   int ldw = 0;
   int ci = 0, ci_pad = 0, co = 0, kh = 1, kw = 1, sh = 1, sw = 1, pt = 0, pl = 0, pb = 0, pr = 0;
-  bool deconv = false;
 };
 
 struct DwW {
@@ -98,7 +97,8 @@ class Builder {
     return off;
   }
 
-  // OIHW [co][ci][kh][kw] -> [k = (ky*kw + kx)*ci_pad + c][ldw].
+  // OIHW [co][ci][kh][kw] -> [co][k = (ky*kw + kx)*ci_pad + c]; the padded
+  // input channels get zero weights.
   ConvW pack_conv(const std::vector<float>& W, const std::vector<float>& b, int ci, int co, int kh, int kw, int sh,
                   int sw, std::vector<int> pads, int ci_pad = 0) {
     ConvW c;
@@ -107,30 +107,15 @@ class Builder {
     c.co = co;
     c.kh = kh, c.kw = kw, c.sh = sh, c.sw = sw;
     c.pt = pads[0], c.pl = pads[1], c.pb = pads[2], c.pr = pads[3];
-    c.ldw = (int)round_up(co, 4);
+    if (c.ci_pad % 4) raise(PPOCR_ERR_INVALID_MODEL, "conv input channels must be padded to a multiple of 4");
     size_t K = (size_t)kh * kw * c.ci_pad;
-    std::vector<float> packed(K * c.ldw, 0.0f);
+    c.ldw = (int)K;
+    std::vector<float> packed((size_t)co * K, 0.0f);
     for (int o = 0; o < co; ++o)
       for (int i = 0; i < ci; ++i)
         for (int ky = 0; ky < kh; ++ky)
           for (int kx = 0; kx < kw; ++kx)
-            packed[((size_t)(ky * kw + kx) * c.ci_pad + i) * c.ldw + o] = W[(((size_t)o * ci + i) * kh + ky) * kw + kx];
-    c.w = put(packed);
-    if (!b.empty()) c.b = put(b);
-    return c;
-  }
-
-  // IOHW [ci][co][2][2] transposed conv -> [k = c][j = tap*co + o].
-  ConvW pack_deconv(const std::vector<float>& W, const std::vector<float>& b, int ci, int co) {
-    ConvW c;
-    c.ci = c.ci_pad = ci;
-    c.co = co;
-    c.deconv = true;
-    c.ldw = (int)round_up(4 * co, 4);
-    std::vector<float> packed((size_t)ci * c.ldw, 0.0f);
-    for (int i = 0; i < ci; ++i)
-      for (int o = 0; o < co; ++o)
-        for (int t = 0; t < 4; ++t) packed[(size_t)i * c.ldw + t * co + o] = W[((size_t)i * co + o) * 4 + t];
+            packed[(size_t)o * K + (size_t)(ky * kw + kx) * c.ci_pad + i] = W[(((size_t)o * ci + i) * kh + ky) * kw + kx];
     c.w = put(packed);
     if (!b.empty()) c.b = put(b);
     return c;
@@ -223,14 +208,11 @@ class Builder {
   // ------------------------------------------------------------ ops
   View conv(const View& x, const ConvW& w, const Epi& e, const std::string& name) {
     if (x.c != w.ci_pad) raise(PPOCR_ERR_INVALID_MODEL, name + ": input has " + std::to_string(x.c) + " channels");
-    int Ho, Wo;
-    if (w.deconv) {
-      Ho = x.h, Wo = x.w;
-    } else {
-      Ho = (x.h + w.pt + w.pb - w.kh) / w.sh + 1;
-      Wo = (x.w + w.pl + w.pr - w.kw) / w.sw + 1;
-    }
-    int oh = w.deconv ? 2 * Ho : Ho * e.rep, ow = w.deconv ? 2 * Wo : Wo * e.rep;
+    const int Ho = (x.h + w.pt + w.pb - w.kh) / w.sh + 1;
+    const int Wo = (x.w + w.pl + w.pr - w.kw) / w.sw + 1;
+    const int oh = Ho * e.rep, ow = Wo * e.rep;
+    if ((e.res || e.res_gate || e.up || e.rep != 1) && w.co % 4)
+      raise(PPOCR_ERR_INVALID_MODEL, name + ": fused epilogue terms need a multiple of 4 output channels");
     View out;
     if (e.dst) {
       out = *e.dst;
@@ -255,16 +237,15 @@ class Builder {
     base.up_s = e.up_s;
     base.up_ps = has_up ? up.ps : 0;
     base.rep = e.rep;
-    base.mode = w.deconv ? 1 : 0;
     base.out_h = oh, base.out_w = ow;
     size_t wo = w.w, bo = w.b;
     Op op;
     op.name = name;
-    op.kernel = conv_tile_name(x.n * Ho * Wo, w.deconv ? 4 * w.co : w.co);
+    op.kernel = conv_tile_name(x.n * Ho * Wo, w.co);
     op.bound = 1;
     double M = (double)x.n * Ho * Wo;
     double K = (double)w.kh * w.kw * w.ci;
-    double cols = w.deconv ? 4.0 * w.co : w.co;
+    double cols = w.co;
     op.flops = 2.0 * M * cols * K;
     op.bytes = 4.0 * ((double)x.pixels() * w.ci + K * cols + (double)out.pixels() * w.co +
                       (has_res ? M * w.co : 0.0) + (has_up ? (double)up.pixels() * w.co : 0.0));
