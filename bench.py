@@ -49,9 +49,9 @@ def weights(kind, size):
     return path
 
 
-def load(gpu, kind, size, shape):
+def load(gpu, kind, size, shape, precision="f32"):
     cls = ppocr_hip.Detector if kind == "det" else ppocr_hip.Recognizer
-    return cls.load(gpu, weights(kind, size), size, shape)
+    return cls.load(gpu, weights(kind, size), size, shape, precision=precision)
 
 
 def inputs(kind, shape, seed=7):
@@ -123,19 +123,22 @@ def cpu_baseline(kind, size, shape, budget_s=12.0):
 def also(gpu, warmup, steps):
     out = {}
     configs = [
-        ("det", "tiny", (1, 3, 416, 736)),
-        ("det", "small", (1, 3, 416, 736)),
-        ("det", "small", (8, 3, 416, 736)),
-        ("det", "medium", (1, 3, 416, 736)),
-        ("det", "tiny", (1, 3, 832, 1472)),
-        ("rec", "tiny", (64, 3, 48, 320)),
-        ("rec", "small", (64, 3, 48, 320)),
-        ("rec", "medium", (256, 3, 48, 320)),
+        ("det", "tiny", (1, 3, 416, 736), "f32"),
+        ("det", "small", (1, 3, 416, 736), "f32"),
+        ("det", "small", (8, 3, 416, 736), "f32"),
+        ("det", "medium", (1, 3, 416, 736), "f32"),
+        ("det", "tiny", (1, 3, 832, 1472), "f32"),
+        ("rec", "tiny", (64, 3, 48, 320), "f32"),
+        ("rec", "small", (64, 3, 48, 320), "f32"),
+        ("rec", "medium", (256, 3, 48, 320), "f32"),
+        ("det", "medium", (1, 3, 416, 736), "bf16"),
+        ("det", "medium", (8, 3, 416, 736), "bf16"),
+        ("rec", "medium", (256, 3, 48, 320), "bf16"),
     ]
-    for kind, size, shape in configs:
-        key = f"{size}_{kind}_{shape[0]}x{shape[2]}x{shape[3]}"
+    for kind, size, shape, precision in configs:
+        key = f"{size}_{kind}_{shape[0]}x{shape[2]}x{shape[3]}_{precision}"
         try:
-            m = load(gpu, kind, size, shape)
+            m = load(gpu, kind, size, shape, precision)
             x = inputs(kind, shape)
             ms = throughput(m, x, warmup, steps)
             m.close()

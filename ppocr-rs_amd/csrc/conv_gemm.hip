@@ -1,21 +1,23 @@
-// Implicit-GEMM convolution on the CDNA4 fp32 matrix cores.
+// Implicit-GEMM convolution on the CDNA4 matrix cores, fp32 or bf16 storage.
 //
 // Replaces the reference's WGSL `conv`, `conv_medium_linear`,
 // `conv_single_row`, `conv_spatial_m32`, `conv_2x2_direct`,
 // `conv_3x3_stride2_direct`, `conv_3x3_direct` (src/gpu/shaders/*.wgsl;
 // kernel selection src/gpu/runtime.rs:699-949) with one tiled kernel:
 //   * M = output pixels (NHWC rows), N = output channels, K = kh*kw*C.
-//   * A tiles are gathered straight from the NHWC activation (float4 along
-//     the channel axis, padding taps read as zero); B tiles come from weights
-//     packed [Co][K] at load time.  Both are stored k-contiguous in LDS, so
-//     each lane fetches the operands of four consecutive MFMA k-steps with
-//     one 16-byte LDS read.
-//   * Each wave64 owns a TM x TN grid of 16x16 accumulators and issues
-//     v_mfma_f32_16x16x4f32.  LDS is double-buffered: the next K slice is
-//     fetched into registers during the MFMAs and written to the other
-//     buffer, one barrier per slice.
-//   * The epilogue stages the tile through LDS and finishes it with 16-byte
-//     row-contiguous accesses: bias, activation, SE gate on the input
+//   * A tiles are gathered straight from the NHWC activation (four channels
+//     per load, padding taps read as zero); B tiles come from weights packed
+//     [Co][K] at load time.  Both are stored k-contiguous in LDS with 80-byte
+//     rows, so each lane fetches its MFMA operands for one K slice with one
+//     conflict-free 16-byte LDS read per 16x16 tile.
+//   * fp32: v_mfma_f32_16x16x4f32, four per tile per 16-deep K slice.
+//     bf16: v_mfma_f32_16x16x32_bf16, one per tile per 32-deep K slice, fp32
+//     accumulation.
+//   * Each wave64 owns a TM x TN grid of 16x16 accumulators.  LDS is
+//     double-buffered: the next K slice is fetched into registers during the
+//     MFMAs and written to the other buffer, one barrier per slice.
+//   * The epilogue stages the fp32 tile through LDS and finishes it with
+//     row-contiguous vector accesses: bias, activation, SE gate on the input
 //     (applied while gathering A), a (gated) residual add, a
 //     nearest-upsample add and an upsample-on-write.
 #include "device_math.h"
@@ -23,27 +25,66 @@
 namespace ppocr {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+template <typename T>
+struct GemmTraits;
+template <>
+struct GemmTraits<float> {
+  static constexpr int BK = 16;  // K slice: 16 fp32 = 64 B per row
+  using Quad = float4;           // four k values
+};
+template <>
+struct GemmTraits<bf16> {
+  static constexpr int BK = 32;  // K slice: 32 bf16 = 64 B per row
+  using Quad = uint2;
+};
 
 __device__ __forceinline__ float4 f4_add(float4 a, float4 b) {
   return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 
-template <int BM, int BN, int WM, int WN>
+template <typename T>
+__device__ __forceinline__ typename GemmTraits<T>::Quad gate_quad(typename GemmTraits<T>::Quad v, float4 g);
+template <>
+__device__ __forceinline__ float4 gate_quad<float>(float4 v, float4 g) {
+  return f4_mul(v, g);
+}
+template <>
+__device__ __forceinline__ uint2 gate_quad<bf16>(uint2 v, float4 g) {
+  float4 f = f4_mul(make_float4(bf16_bits_to_f32(v.x & 0xFFFFu), bf16_bits_to_f32(v.x >> 16),
+                                bf16_bits_to_f32(v.y & 0xFFFFu), bf16_bits_to_f32(v.y >> 16)),
+                    g);
+  uint2 u;
+  u.x = f32_to_bf16_bits(f.x) | (f32_to_bf16_bits(f.y) << 16);
+  u.y = f32_to_bf16_bits(f.z) | (f32_to_bf16_bits(f.w) << 16);
+  return u;
+}
+
+template <typename T, int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
-  constexpr int BK = 16, KQ = BK / 4, LDA = BK + 4;
+  using Quad = typename GemmTraits<T>::Quad;
+  constexpr int BK = GemmTraits<T>::BK;
+  constexpr int KQ = BK / 4;                 // quads per row of a K slice
+  constexpr int PADE = 16 / sizeof(T);       // 16 B of padding per LDS row
+  constexpr int LDA = BK + PADE;             // 80-byte rows
+  constexpr int OPE = 16 / sizeof(T);        // elements per 16-byte operand read
   constexpr int TM = BM / (WM * 16);
   constexpr int TN = BN / (WN * 16);
   static_assert(WM * WN == 4, "four waves per block");
   static_assert(TM >= 1 && TN >= 1, "tile too small");
-  constexpr int A_PER = BM * KQ / 256;  // float4 loads of A per thread
-  constexpr int B_Q = BN * KQ;          // float4 count of a B tile
+  constexpr int A_PER = BM * KQ / 256;
+  constexpr int B_Q = BN * KQ;
   constexpr int B_PER = (B_Q + 255) / 256;
-  static_assert(A_PER >= 1, "BM must be a multiple of 64");
-  constexpr int STAGE = (BM + BN) * LDA;
-  constexpr int LDE = BN + 4;
-  constexpr int SMEM = 2 * STAGE > BM * LDE ? 2 * STAGE : BM * LDE;
-  __shared__ __attribute__((aligned(16))) float smem[SMEM];
+  static_assert((BM * KQ) % 256 == 0, "A tile must split evenly over the block");
+  constexpr int STAGE = (BM + BN) * LDA;     // elements of T
+  constexpr int LDE = BN + 4;                // fp32 epilogue staging
+  constexpr int SMEM_BYTES = 2 * STAGE * (int)sizeof(T) > BM * LDE * 4 ? 2 * STAGE * (int)sizeof(T) : BM * LDE * 4;
+  __shared__ __attribute__((aligned(16))) char smem_raw[SMEM_BYTES];
+  T* smem = reinterpret_cast<T*>(smem_raw);
 
+  const T* in = static_cast<const T*>(p.in);
+  const T* wt = static_cast<const T*>(p.wt);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -56,7 +97,6 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
   const int n0 = blockIdx.y * BN;
   const int kq = tid % KQ;  // this lane's k-quad in every A and B load
 
-  // Per-thread A-row geometry, fixed for the whole K loop.
   int a_img[A_PER], a_iy0[A_PER], a_ix0[A_PER];
   bool a_ok[A_PER];
 #pragma unroll
@@ -73,8 +113,8 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
     a_ix0[i] = ox * p.sw - p.pl;
   }
 
-  float4 ra[A_PER];
-  float4 rb[B_PER];
+  Quad ra[A_PER];
+  Quad rb[B_PER];
 
   auto load_tile = [&](int k0) {
     const int k = k0 + kq * 4;
@@ -85,18 +125,13 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
     const int kx = tap - ky * p.kw;
 #pragma unroll
     for (int i = 0; i < A_PER; ++i) {
-      float4 v = f4_zero();
+      Quad v{};
       int iy = a_iy0[i] + ky;
       int ix = a_ix0[i] + kx;
       if (kin && a_ok[i] && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W) {
-        v = *reinterpret_cast<const float4*>(p.in + ((size_t)(a_img[i] * p.H + iy) * p.W + ix) * p.in_ps + c);
-        if (p.in_gate) {
-          float4 g = *reinterpret_cast<const float4*>(p.in_gate + (size_t)a_img[i] * p.C + c);
-          v.x *= g.x;
-          v.y *= g.y;
-          v.z *= g.z;
-          v.w *= g.w;
-        }
+        v = *reinterpret_cast<const Quad*>(in + ((size_t)(a_img[i] * p.H + iy) * p.W + ix) * p.in_ps + c);
+        if (p.in_gate)
+          v = gate_quad<T>(v, *reinterpret_cast<const float4*>(p.in_gate + (size_t)a_img[i] * p.C + c));
       }
       ra[i] = v;
     }
@@ -104,22 +139,21 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
     for (int i = 0; i < B_PER; ++i) {
       int q = tid + i * 256;
       int n = n0 + q / KQ;
-      float4 v = f4_zero();
-      if (q < B_Q && kin && n < p.Co) v = *reinterpret_cast<const float4*>(p.wt + (size_t)n * p.ldw + k);
+      Quad v{};
+      if (q < B_Q && kin && n < p.Co) v = *reinterpret_cast<const Quad*>(wt + (size_t)n * p.ldw + k);
       rb[i] = v;
     }
   };
 
   auto store_tile = [&](int buf) {
-    float* As = smem + buf * STAGE;
-    float* Bs = As + BM * LDA;
+    T* As = smem + buf * STAGE;
+    T* Bs = As + BM * LDA;
 #pragma unroll
-    for (int i = 0; i < A_PER; ++i)
-      *reinterpret_cast<float4*>(As + ((tid + i * 256) / KQ) * LDA + kq * 4) = ra[i];
+    for (int i = 0; i < A_PER; ++i) *reinterpret_cast<Quad*>(As + ((tid + i * 256) / KQ) * LDA + kq * 4) = ra[i];
 #pragma unroll
     for (int i = 0; i < B_PER; ++i) {
       int q = tid + i * 256;
-      if (q < B_Q) *reinterpret_cast<float4*>(Bs + (q / KQ) * LDA + kq * 4) = rb[i];
+      if (q < B_Q) *reinterpret_cast<Quad*>(Bs + (q / KQ) * LDA + kq * 4) = rb[i];
     }
   };
 
@@ -129,10 +163,10 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // MFMA operand mapping: lane l supplies A[m = l%16][k] and B[k][n = l%16];
-  // over four MFMA steps lane group g = l/16 covers k = 4g .. 4g+3, read as
-  // one float4 (the k order within a slice is permuted identically for A and
-  // B, so the products pair up unchanged).
+  // MFMA operand mapping: lane l supplies A[m = l%16][k] and B[k][n = l%16]
+  // for the k values of its lane group g = l/16 (fp32: k = 4g..4g+3 over
+  // four MFMAs; bf16: k = 8g..8g+7 in one MFMA).  The k order inside a slice
+  // is the same for A and B, so the products pair up unchanged.
   const int lrow = lane & 15;
   const int g = lane >> 4;
   const int nk = (K + BK - 1) / BK;
@@ -143,46 +177,68 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
   for (int s = 0; s < nk; ++s) {
     const int buf = s & 1;
     if (s + 1 < nk) load_tile((s + 1) * BK);
-    const float* As = smem + buf * STAGE;
-    const float* Bs = As + BM * LDA;
-    float4 a[TM], b[TN];
+    const T* As = smem + buf * STAGE;
+    const T* Bs = As + BM * LDA;
+    if constexpr (sizeof(T) == 4) {
+      float4 a[TM], b[TN];
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-      a[i] = *reinterpret_cast<const float4*>(As + (wm * TM * 16 + i * 16 + lrow) * LDA + g * 4);
+      for (int i = 0; i < TM; ++i)
+        a[i] = *reinterpret_cast<const float4*>(As + (wm * TM * 16 + i * 16 + lrow) * LDA + g * OPE);
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
-      b[j] = *reinterpret_cast<const float4*>(Bs + (wn * TN * 16 + j * 16 + lrow) * LDA + g * 4);
+      for (int j = 0; j < TN; ++j)
+        b[j] = *reinterpret_cast<const float4*>(Bs + (wn * TN * 16 + j * 16 + lrow) * LDA + g * OPE);
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
+    } else {
+      bf16x8 a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        a[i] = *reinterpret_cast<const bf16x8*>(As + (wm * TM * 16 + i * 16 + lrow) * LDA + g * OPE);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        b[j] = *reinterpret_cast<const bf16x8*>(Bs + (wn * TN * 16 + j * 16 + lrow) * LDA + g * OPE);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
     if (s + 1 < nk) store_tile(buf ^ 1);
     __syncthreads();
   }
 
-  // Stage the tile in LDS as [m][n].  Accumulator element e of lane l in
-  // tile (i, j) is row 4*(l/16) + e, column l%16 of that 16x16 tile.
+  // Stage the fp32 tile in LDS as [m][n].  Accumulator element e of lane l
+  // in tile (i, j) is row 4*(l/16) + e, column l%16 of that 16x16 tile.
+  float* stage = reinterpret_cast<float*>(smem_raw);
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        smem[(wm * TM * 16 + i * 16 + g * 4 + e) * LDE + wn * TN * 16 + j * 16 + lrow] = acc[i][j][e];
+        stage[(wm * TM * 16 + i * 16 + g * 4 + e) * LDE + wn * TN * 16 + j * 16 + lrow] = acc[i][j][e];
   __syncthreads();
 
+  const T* res = static_cast<const T*>(p.res);
+  const T* up = static_cast<const T*>(p.up);
   const bool vec_out = (p.out_ps & 3) == 0 && (p.Co & 3) == 0;
   const bool need_coords = p.up != nullptr || p.rep != 1;
   constexpr int NQ = BN / 4;
@@ -192,7 +248,7 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
     const int m = m0 + row;
     const int col = n0 + cq * 4;
     if (m >= M || col >= p.Co) continue;
-    float4 v = *reinterpret_cast<const float4*>(smem + row * LDE + cq * 4);
+    float4 v = *reinterpret_cast<const float4*>(stage + row * LDE + cq * 4);
     int img = m / HoWo, oy = 0, ox = 0;
     if (need_coords) {
       int r = m - img * HoWo;
@@ -205,26 +261,28 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
       v.y = act_apply(p.act, v.y);
       v.z = act_apply(p.act, v.z);
       v.w = act_apply(p.act, v.w);
-      if (p.res) {
-        float4 r = *reinterpret_cast<const float4*>(p.res + (size_t)m * p.res_ps + col);
+      if (res) {
+        float4 r = ld4<T>(res + (size_t)m * p.res_ps + col);
         if (p.res_gate) {
           float4 gt = *reinterpret_cast<const float4*>(p.res_gate + (size_t)img * p.Co + col);
           r = make_float4(__fmul_rn(r.x, gt.x), __fmul_rn(r.y, gt.y), __fmul_rn(r.z, gt.z), __fmul_rn(r.w, gt.w));
         }
         v = f4_add(r, v);
       }
-      if (p.up) {
+      if (up) {
         int uh = p.Ho / p.up_s, uw = p.Wo / p.up_s;
-        v = f4_add(v, *reinterpret_cast<const float4*>(
-                          p.up + ((size_t)(img * uh + oy / p.up_s) * uw + ox / p.up_s) * p.up_ps + col));
+        v = f4_add(v, ld4<T>(up + ((size_t)(img * uh + oy / p.up_s) * uw + ox / p.up_s) * p.up_ps + col));
       }
-      if (p.rep == 1) {
-        *reinterpret_cast<float4*>(p.out + (size_t)m * p.out_ps + col) = v;
+      if (p.out_f32) {
+        *reinterpret_cast<float4*>(static_cast<float*>(p.out) + (size_t)m * p.out_ps + col) = v;
+      } else if (p.rep == 1) {
+        st4<T>(static_cast<T*>(p.out) + (size_t)m * p.out_ps + col, v);
       } else {
         for (int dy = 0; dy < p.rep; ++dy)
           for (int dx = 0; dx < p.rep; ++dx)
-            *reinterpret_cast<float4*>(
-                p.out + ((size_t)(img * p.out_h + oy * p.rep + dy) * p.out_w + ox * p.rep + dx) * p.out_ps + col) = v;
+            st4<T>(static_cast<T*>(p.out) +
+                       ((size_t)(img * p.out_h + oy * p.rep + dy) * p.out_w + ox * p.rep + dx) * p.out_ps + col,
+                   v);
       }
     } else {
       // Channel counts that are not a multiple of 4 (the recognizer
@@ -234,16 +292,21 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
       for (int e = 0; e < 4 && col + e < p.Co; ++e) {
         float t = vv[e];
         if (p.bias) t = t + p.bias[col + e];
-        p.out[(size_t)m * p.out_ps + col + e] = act_apply(p.act, t);
+        t = act_apply(p.act, t);
+        size_t o = (size_t)m * p.out_ps + col + e;
+        if (p.out_f32)
+          static_cast<float*>(p.out)[o] = t;
+        else
+          st1<T>(static_cast<T*>(p.out) + o, t);
       }
     }
   }
 }
 
-template <int BM, int BN, int WM, int WN>
+template <typename T, int BM, int BN, int WM, int WN>
 static void launch_tile(const ConvParams& p, int M, hipStream_t s) {
   dim3 grid((M + BM - 1) / BM, (p.Co + BN - 1) / BN);
-  hipLaunchKernelGGL((conv_gemm_kernel<BM, BN, WM, WN>), grid, dim3(256), 0, s, p);
+  hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN>), grid, dim3(256), 0, s, p);
 }
 
 // Tile choice: narrow output channel counts get tall tiles so no MFMA
@@ -256,19 +319,29 @@ static int pick_tile(int M, int cols) {
   return 3;
 }
 
-const char* conv_tile_name(int M, int cols) {
-  static const char* names[] = {"conv_gemm<256x16>", "conv_gemm<128x32>", "conv_gemm<128x64>", "conv_gemm<64x64>"};
-  return names[pick_tile(M, cols)];
+const char* conv_tile_name(int M, int cols, int dt) {
+  static const char* f32[] = {"conv_gemm<256x16>", "conv_gemm<128x32>", "conv_gemm<128x64>", "conv_gemm<64x64>"};
+  static const char* b16[] = {"conv_gemm_bf16<256x16>", "conv_gemm_bf16<128x32>", "conv_gemm_bf16<128x64>",
+                              "conv_gemm_bf16<64x64>"};
+  return (dt == DT_BF16 ? b16 : f32)[pick_tile(M, cols)];
+}
+
+template <typename T>
+static void launch_typed(const ConvParams& p, hipStream_t s) {
+  int M = p.N * p.Ho * p.Wo;
+  switch (pick_tile(M, p.Co)) {
+    case 0: launch_tile<T, 256, 16, 4, 1>(p, M, s); break;
+    case 1: launch_tile<T, 128, 32, 4, 1>(p, M, s); break;
+    case 2: launch_tile<T, 128, 64, 2, 2>(p, M, s); break;
+    default: launch_tile<T, 64, 64, 2, 2>(p, M, s); break;
+  }
 }
 
 void launch_conv(const ConvParams& p, hipStream_t s) {
-  int M = p.N * p.Ho * p.Wo;
-  switch (pick_tile(M, p.Co)) {
-    case 0: launch_tile<256, 16, 4, 1>(p, M, s); break;
-    case 1: launch_tile<128, 32, 4, 1>(p, M, s); break;
-    case 2: launch_tile<128, 64, 2, 2>(p, M, s); break;
-    default: launch_tile<64, 64, 2, 2>(p, M, s); break;
-  }
+  if (p.dt == DT_BF16)
+    launch_typed<bf16>(p, s);
+  else
+    launch_typed<float>(p, s);
 }
 
 }  // namespace ppocr

@@ -44,4 +44,68 @@ __device__ __forceinline__ float residual_mul(float x, float g) { return __fadd_
 
 __device__ __forceinline__ float4 f4_zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
 
+// ---- activation storage: fp32 or bf16 (round-to-nearest-even on store).
+typedef __bf16 bf16;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Four consecutive values (16 B as fp32, 8 B as bf16).
+template <typename T>
+__device__ __forceinline__ float4 ld4(const T* p);
+template <>
+__device__ __forceinline__ float4 ld4<float>(const float* p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+template <>
+__device__ __forceinline__ float4 ld4<bf16>(const bf16* p) {
+  uint2 u = *reinterpret_cast<const uint2*>(p);
+  return make_float4(bf16_bits_to_f32(u.x & 0xFFFFu), bf16_bits_to_f32(u.x >> 16), bf16_bits_to_f32(u.y & 0xFFFFu),
+                     bf16_bits_to_f32(u.y >> 16));
+}
+
+template <typename T>
+__device__ __forceinline__ void st4(T* p, float4 v);
+template <>
+__device__ __forceinline__ void st4<float>(float* p, float4 v) {
+  *reinterpret_cast<float4*>(p) = v;
+}
+template <>
+__device__ __forceinline__ void st4<bf16>(bf16* p, float4 v) {
+  uint2 u;
+  u.x = f32_to_bf16_bits(v.x) | (f32_to_bf16_bits(v.y) << 16);
+  u.y = f32_to_bf16_bits(v.z) | (f32_to_bf16_bits(v.w) << 16);
+  *reinterpret_cast<uint2*>(p) = u;
+}
+
+template <typename T>
+__device__ __forceinline__ float ld1(const T* p);
+template <>
+__device__ __forceinline__ float ld1<float>(const float* p) {
+  return *p;
+}
+template <>
+__device__ __forceinline__ float ld1<bf16>(const bf16* p) {
+  return bf16_bits_to_f32(*reinterpret_cast<const unsigned short*>(p));
+}
+
+template <typename T>
+__device__ __forceinline__ void st1(T* p, float v);
+template <>
+__device__ __forceinline__ void st1<float>(float* p, float v) {
+  *p = v;
+}
+template <>
+__device__ __forceinline__ void st1<bf16>(bf16* p, float v) {
+  *reinterpret_cast<unsigned short*>(p) = (unsigned short)f32_to_bf16_bits(v);
+}
+
+__device__ __forceinline__ float4 f4_mul(float4 a, float4 b) {
+  return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
+}
+
 }  // namespace ppocr

@@ -4,12 +4,17 @@
 // (pointer to channel 0 of pixel 0, N, H, W, C, pixel stride).  A pixel
 // stride larger than C lets a producer write one channel slice of a wider
 // tensor (the channel concats of the stem and the FPN are never copied).
+// Activations are stored as fp32 or bf16 (`dt`); arithmetic is always fp32
+// (bf16 MFMA products accumulate in fp32).  Small parameter tensors (biases,
+// depthwise taps, SE and LayerNorm weights) stay fp32 in both precisions.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <cstdint>
 
 namespace ppocr {
+
+enum DType : int { DT_F32 = 0, DT_BF16 = 1 };
 
 // Activation codes: the epilogue set of the reference
 // (src/gpu/runtime.rs:302-311, src/cpu/kernels/mod.rs:2376-2390).
@@ -24,46 +29,49 @@ enum Act : int {
   ACT_SIGMOID = 7,
 };
 
-// Implicit-GEMM convolution on the fp32 matrix cores.
-//   out[m, n] = act(sum_k A[m, k] * Wt[k, n] + bias[n])  (+ epilogue terms)
+// Implicit-GEMM convolution on the matrix cores.
+//   out[m, n] = act(sum_k A[m, k] * Wt[n, k] + bias[n])  (+ epilogue terms)
 // m: output pixel (n_img, oy, ox); n: output channel; k = (ky*kw + kx)*C + c.
 struct ConvParams {
-  const float* in;
+  const void* in;
   int N, H, W, C, in_ps;
-  float* out;
+  void* out;
+  int out_f32;  // store the output as fp32 whatever the activation type
   int Ho, Wo, Co, out_ps;
-  const float* wt;  // packed [Co][ldw], k = (ky*kw + kx)*C + c contiguous
-  int ldw;          // = K (a multiple of 4)
+  const void* wt;  // packed [Co][ldw] in the activation type
+  int ldw;         // = K (a multiple of 4)
   const float* bias;  // [Co] or null
   int kh, kw, sh, sw, pt, pl;
   int act;
   const float* in_gate;   // [N][C]: A[m, k] = x * g[n_img, c] (SE prologue)
-  const float* res;       // residual added after the activation
+  const void* res;        // residual added after the activation
   int res_ps;
   const float* res_gate;  // [N][Co]: residual term is res * g
-  const float* up;        // nearest-upsample-add source [N, Ho/up_s, Wo/up_s, Co]
+  const void* up;         // nearest-upsample-add source [N, Ho/up_s, Wo/up_s, Co]
   int up_s, up_ps;
   int rep;           // write each output pixel as a rep x rep block (upsample on write)
   int out_h, out_w;  // dims of the tensor `out` points into (Ho*rep, Wo*rep)
+  int dt;            // activation type of in / res / up / out
 };
 
 // Depthwise k x k convolution (groups == C), 4 channels per lane.
 struct DwParams {
-  const float* in;
+  const void* in;
   int N, H, W, C, in_ps;
-  float* out;
+  void* out;
   int Ho, Wo, out_ps;
   const float* wt;  // [kh*kw][C]
   const float* bias;
   int kh, kw, sh, sw, pt, pl;
   int act;
-  const float* res;  // out = res + act(dw(x) + b)
+  const void* res;  // out = res + act(dw(x) + b)
   int res_ps;
+  int dt;
 };
 
 // Squeeze-excitation gate: g[n, c] = gate_act(W2 relu(W1 mean(x) + b1) + b2).
 struct SeParams {
-  const float* in;
+  const void* in;
   int N, HW, C, in_ps;
   float* partial;  // [N][P][C] partial sums
   int P;           // pixel chunks per image
@@ -75,50 +83,50 @@ struct SeParams {
   int gate_act;
   float* hidden;  // [N][Cr]
   float* gate;    // [N][C]
+  int dt;
 };
 
 void launch_conv(const ConvParams& p, hipStream_t s);
-// Name of the tile instance launch_conv picks for M rows x `cols` columns.
-const char* conv_tile_name(int M, int cols);
+// Name of the kernel instance launch_conv picks for M rows x `cols` columns.
+const char* conv_tile_name(int M, int cols, int dt);
 void launch_depthwise(const DwParams& p, hipStream_t s);
 // Name of the kernel instance launch_depthwise picks.
 const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho);
 void launch_se(const SeParams& p, hipStream_t s);
 
-// NCHW (3 planes) -> NHWC with 4 channels (fourth channel zero).
-void launch_nchw_to_nhwc4(const float* in, float* out, int N, int H, int W, hipStream_t s);
+// NCHW fp32 (3 planes) -> NHWC with 4 channels (fourth channel zero).
+void launch_nchw_to_nhwc4(const float* in, void* out, int N, int H, int W, int dt, hipStream_t s);
 
 // Max pool 2x2, stride 1, pads (0,0,1,1) into a channel slice.
-void launch_maxpool_same(const float* in, int N, int H, int W, int C, int in_ps, float* out, int out_ps,
+void launch_maxpool_same(const void* in, int N, int H, int W, int C, int in_ps, void* out, int out_ps, int dt,
                          hipStream_t s);
 
 // out = x + x*g[n,c] (two roundings) [+ upper[y/2, x/2]], written as
 // rep x rep blocks (rep = 1: plain) into a tensor of pixel stride out_ps.
-void launch_gate_residual(const float* in, int N, int H, int W, int C, int in_ps, const float* gate,
-                          const float* upper, int up_ps, float* out, int out_ps, int rep, hipStream_t s);
+void launch_gate_residual(const void* in, int N, int H, int W, int C, int in_ps, const float* gate,
+                          const void* upper, int up_ps, void* out, int out_ps, int rep, int dt, hipStream_t s);
 
 // Average pool, kernel [3,2], stride [3,2], count_include_pad = false.
-void launch_avgpool32(const float* in, int N, int H, int W, int C, int in_ps, float* out, int Ho, int Wo,
+void launch_avgpool32(const void* in, int N, int H, int W, int C, int in_ps, void* out, int Ho, int Wo, int dt,
                       hipStream_t s);
 
 // Fused detector head tail: 2x2 s2 deconv (+bias, ReLU) then 2x2 s2 deconv to
-// one channel (+bias) and sigmoid; in [N, H, W, Ch] -> out [N, 4H, 4W].
-void launch_db_head_up(const float* in, int N, int H, int W, int Ch, int in_ps, const float* wu, const float* bu,
-                       const float* wf, float bf, float* out, hipStream_t s);
+// one channel (+bias) and sigmoid; in [N, H, W, Ch] -> fp32 out [N, 4H, 4W].
+void launch_db_head_up(const void* in, int N, int H, int W, int Ch, int in_ps, const float* wu, const float* bu,
+                       const float* wf, float bf, float* out, int dt, hipStream_t s);
 
 // Row LayerNorm over C (eps), optional residual added after: out = LN(x) + r.
-void launch_layer_norm(const float* in, int rows, int C, const float* w, const float* b, float eps,
-                       const float* res, float* out, hipStream_t s);
+void launch_layer_norm(const void* in, int rows, int C, const float* w, const float* b, float eps, const void* res,
+                       void* out, int dt, hipStream_t s);
 
 // Multi-head attention core on qkv [B, T, 3*hidden] -> ctx [B, T, hidden].
-void launch_attention(const float* qkv, int B, int T, int hidden, int heads, float* out, hipStream_t s);
+void launch_attention(const void* qkv, int B, int T, int hidden, int heads, void* out, int dt, hipStream_t s);
 
-// In-place row softmax over `cols` columns.
+// In-place fp32 row softmax over `cols` columns.
 void launch_softmax_rows(float* x, long rows, int cols, hipStream_t s);
 
-// Quad-bilinear RGB8 sampling -> rounded -> normalised, written either as
-// NHWC4 (nhwc = 1, channel 3 zero) or NCHW planes.  One geometry per image:
-// corners [N][8], content widths [N].
+// Quad-bilinear RGB8 sampling -> rounded -> normalised NCHW fp32 planes.  One
+// geometry per image: corners [N][8], content widths [N].
 struct PreParams {
   const uint32_t* rgb;  // packed RGB8 bytes, 4-byte aligned
   int sw, sh;
@@ -127,7 +135,6 @@ struct PreParams {
   int N, cw, ch;
   float scale[3], bias[3];
   float* out;
-  int nhwc;
 };
 void launch_preprocess(const PreParams& p, hipStream_t s);
 

@@ -2,20 +2,43 @@
 // squeeze-excitation, FPN gate/upsample/concat, pools, the fused DB head
 // tail, LayerNorm, attention, row softmax and image preprocessing.
 //
-// All activations are NHWC with C % 4 == 0, so one lane moves one float4
-// (16 B) along the channel axis and consecutive lanes touch consecutive
-// 16 B segments: every global access of these kernels is fully coalesced.
+// All activations are NHWC with C % 4 == 0, so one lane moves four channels
+// (16 B as fp32, 8 B as bf16) and consecutive lanes touch consecutive
+// segments: every global access of these kernels is coalesced.  Arithmetic
+// is fp32 for both storage types.
 #include "device_math.h"
 
 namespace ppocr {
 
 static inline unsigned blocks_for(long n, int per = 256) { return (unsigned)((n + per - 1) / per); }
 
+#define DISPATCH_DT(dt, ...)            \
+  do {                                  \
+    if ((dt) == DT_BF16) {              \
+      using T = bf16;                   \
+      __VA_ARGS__;                      \
+    } else {                            \
+      using T = float;                  \
+      __VA_ARGS__;                      \
+    }                                   \
+  } while (0)
+
+__device__ __forceinline__ float4 f4_act(int act, float4 v) {
+  return make_float4(act_apply(act, v.x), act_apply(act, v.y), act_apply(act, v.z), act_apply(act, v.w));
+}
+
+__device__ __forceinline__ float4 f4_sum(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
 // ----------------------------------------------------------------- depthwise
 // Replaces WGSL `depthwise` (src/gpu/shaders/depthwise.wgsl:77); semantics of
 // the reference CPU depthwise (src/cpu/ops.rs:385-826): zero padding, bias,
-// activation, then optional residual add (x + act(dw(x) + b)).
+// activation, then optional residual add (x + act(dw(x) + b)).  This generic
+// form serves the stride-2 layers.
+template <typename T>
 __global__ __launch_bounds__(256) void depthwise_kernel(DwParams p) {
+  const T* in = static_cast<const T*>(p.in);
   const int C4 = p.C >> 2;
   long idx = (long)blockIdx.x * 256 + threadIdx.x;
   long total = (long)p.N * p.Ho * p.Wo * C4;
@@ -31,12 +54,12 @@ __global__ __launch_bounds__(256) void depthwise_kernel(DwParams p) {
   for (int ky = 0; ky < p.kh; ++ky) {
     int iy = oy * p.sh - p.pt + ky;
     if (iy < 0 || iy >= p.H) continue;
-    const float* row = p.in + (size_t)(n * p.H + iy) * p.W * p.in_ps + c;
+    const T* row = in + (size_t)(n * p.H + iy) * p.W * p.in_ps + c;
     const float* wrow = p.wt + (size_t)ky * p.kw * p.C + c;
     for (int kx = 0; kx < p.kw; ++kx) {
       int ix = ox * p.sw - p.pl + kx;
       if (ix < 0 || ix >= p.W) continue;
-      float4 x = *reinterpret_cast<const float4*>(row + (size_t)ix * p.in_ps);
+      float4 x = ld4<T>(row + (size_t)ix * p.in_ps);
       float4 w = *reinterpret_cast<const float4*>(wrow + (size_t)kx * p.C);
       acc.x = fmaf(x.x, w.x, acc.x);
       acc.y = fmaf(x.y, w.y, acc.y);
@@ -44,43 +67,28 @@ __global__ __launch_bounds__(256) void depthwise_kernel(DwParams p) {
       acc.w = fmaf(x.w, w.w, acc.w);
     }
   }
-  if (p.bias) {
-    float4 b = *reinterpret_cast<const float4*>(p.bias + c);
-    acc.x += b.x;
-    acc.y += b.y;
-    acc.z += b.z;
-    acc.w += b.w;
-  }
-  acc.x = act_apply(p.act, acc.x);
-  acc.y = act_apply(p.act, acc.y);
-  acc.z = act_apply(p.act, acc.z);
-  acc.w = act_apply(p.act, acc.w);
-  if (p.res) {
-    float4 r = *reinterpret_cast<const float4*>(p.res + (size_t)pix * p.res_ps + c);
-    acc.x = r.x + acc.x;
-    acc.y = r.y + acc.y;
-    acc.z = r.z + acc.z;
-    acc.w = r.w + acc.w;
-  }
-  *reinterpret_cast<float4*>(p.out + (size_t)pix * p.out_ps + c) = acc;
+  if (p.bias) acc = f4_sum(acc, *reinterpret_cast<const float4*>(p.bias + c));
+  acc = f4_act(p.act, acc);
+  if (p.res) acc = f4_sum(ld4<T>(static_cast<const T*>(p.res) + (size_t)pix * p.res_ps + c), acc);
+  st4<T>(static_cast<T*>(p.out) + (size_t)pix * p.out_ps + c, acc);
 }
 
 // LDS-tiled stride-1 depthwise.  A block computes a TY x TX output tile of 32
-// channels (8 float4 lanes per pixel, 128 B contiguous per pixel).  The input
-// tile with its halo and the taps are staged once in LDS; each lane then
-// slides a register window of XR + KW - 1 pixels along x to produce XR = 4
-// outputs, so every staged value is reused KW x KH times from registers/LDS
-// instead of being re-read from the caches.  Taps accumulate in (ky, kx)
-// order as the generic kernel does.
-template <int KH, int KW, int TY>
+// channels (8 lanes per pixel).  The input tile with its halo and the taps
+// are staged once in LDS as fp32; each lane then slides a register window of
+// XR + KW - 1 pixels along x to produce XR = 4 outputs, so every staged value
+// is reused KW x KH times from registers/LDS instead of being re-read from
+// the caches.  Taps accumulate in (ky, kx) order as the generic kernel does.
+template <typename T, int KH, int KW, int TY>
 __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
-  constexpr int C4B = 8;                  // float4 lanes per pixel (32 channels)
+  constexpr int C4B = 8;                  // four-channel lanes per pixel (32 channels)
   constexpr int XR = 4;                   // outputs per lane along x
   constexpr int XG = 256 / (C4B * TY);    // lane groups along x
   constexpr int TX = XG * XR;
   constexpr int IH = TY + KH - 1, IW = TX + KW - 1;
   __shared__ float4 tile[IH * IW * C4B];
   __shared__ float4 taps[KH * KW * C4B];
+  const T* in = static_cast<const T*>(p.in);
 
   const int cblocks = (p.C + 31) / 32;
   const int n = blockIdx.z / cblocks;
@@ -96,7 +104,7 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
     int c = ch0 + c4 * 4;
     float4 v = f4_zero();
     if (c < p.C && gy >= 0 && gy < p.H && gx >= 0 && gx < p.W)
-      v = *reinterpret_cast<const float4*>(p.in + ((size_t)(n * p.H + gy) * p.W + gx) * p.in_ps + c);
+      v = ld4<T>(in + ((size_t)(n * p.H + gy) * p.W + gx) * p.in_ps + c);
     tile[i] = v;
   }
   for (int i = tid; i < KH * KW * C4B; i += 256) {
@@ -139,48 +147,37 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
     int ox = ox0 + xg * XR + r;
     if (ox >= p.Wo) break;
     float4 v = acc[r];
-    if (p.bias) {
-      v.x += b.x;
-      v.y += b.y;
-      v.z += b.z;
-      v.w += b.w;
-    }
-    v.x = act_apply(p.act, v.x);
-    v.y = act_apply(p.act, v.y);
-    v.z = act_apply(p.act, v.z);
-    v.w = act_apply(p.act, v.w);
+    if (p.bias) v = f4_sum(v, b);
+    v = f4_act(p.act, v);
     size_t pix = (size_t)(n * p.Ho + oy) * p.Wo + ox;
-    if (p.res) {
-      float4 rr = *reinterpret_cast<const float4*>(p.res + pix * p.res_ps + c);
-      v.x = rr.x + v.x;
-      v.y = rr.y + v.y;
-      v.z = rr.z + v.z;
-      v.w = rr.w + v.w;
-    }
-    *reinterpret_cast<float4*>(p.out + pix * p.out_ps + c) = v;
+    if (p.res) v = f4_sum(ld4<T>(static_cast<const T*>(p.res) + pix * p.res_ps + c), v);
+    st4<T>(static_cast<T*>(p.out) + pix * p.out_ps + c, v);
   }
 }
 
-template <int KH, int KW, int TY>
+template <typename T, int KH, int KW, int TY>
 static void launch_dw_tiled(const DwParams& p, hipStream_t s) {
   constexpr int TX = 256 / (8 * TY) * 4;
   dim3 grid((p.Wo + TX - 1) / TX, (p.Ho + TY - 1) / TY, p.N * ((p.C + 31) / 32));
-  hipLaunchKernelGGL((depthwise_tiled_kernel<KH, KW, TY>), grid, dim3(256), 0, s, p);
+  hipLaunchKernelGGL((depthwise_tiled_kernel<T, KH, KW, TY>), grid, dim3(256), 0, s, p);
 }
 
-void launch_depthwise(const DwParams& p, hipStream_t s) {
+template <typename T>
+static void launch_dw_typed(const DwParams& p, hipStream_t s) {
   if (p.sh == 1 && p.sw == 1) {
     const bool tall = p.Ho >= 16;
-    if (p.kh == 3 && p.kw == 3) return tall ? launch_dw_tiled<3, 3, 8>(p, s) : launch_dw_tiled<3, 3, 2>(p, s);
-    if (p.kh == 5 && p.kw == 5) return launch_dw_tiled<5, 5, 8>(p, s);
-    if (p.kh == 7 && p.kw == 7) return launch_dw_tiled<7, 7, 8>(p, s);
-    if (p.kh == 9 && p.kw == 9) return launch_dw_tiled<9, 9, 8>(p, s);
-    if (p.kh == 1 && p.kw == 5 && p.Ho == 1) return launch_dw_tiled<1, 5, 1>(p, s);
-    if (p.kh == 1 && p.kw == 7 && p.Ho == 1) return launch_dw_tiled<1, 7, 1>(p, s);
+    if (p.kh == 3 && p.kw == 3) return tall ? launch_dw_tiled<T, 3, 3, 8>(p, s) : launch_dw_tiled<T, 3, 3, 2>(p, s);
+    if (p.kh == 5 && p.kw == 5) return launch_dw_tiled<T, 5, 5, 8>(p, s);
+    if (p.kh == 7 && p.kw == 7) return launch_dw_tiled<T, 7, 7, 8>(p, s);
+    if (p.kh == 9 && p.kw == 9) return launch_dw_tiled<T, 9, 9, 8>(p, s);
+    if (p.kh == 1 && p.kw == 5 && p.Ho == 1) return launch_dw_tiled<T, 1, 5, 1>(p, s);
+    if (p.kh == 1 && p.kw == 7 && p.Ho == 1) return launch_dw_tiled<T, 1, 7, 1>(p, s);
   }
   long total = (long)p.N * p.Ho * p.Wo * (p.C / 4);
-  hipLaunchKernelGGL(depthwise_kernel, dim3(blocks_for(total)), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(depthwise_kernel<T>, dim3(blocks_for(total)), dim3(256), 0, s, p);
 }
+
+void launch_depthwise(const DwParams& p, hipStream_t s) { DISPATCH_DT(p.dt, launch_dw_typed<T>(p, s)); }
 
 const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho) {
   if (sh == 1 && sw == 1) {
@@ -196,10 +193,12 @@ const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho) {
 // Replaces WGSL `global_mean` + two `conv_single_row` + activation
 // (src/gpu/shaders/pool.wgsl:183, conv_single_row.wgsl:84).  Stage 1: each
 // block sums a chunk of pixels for all channels (lanes split channels x
-// pixel phases, fixed-order LDS reduction).  Stage 2: one block per image
-// finishes the mean and runs both 1x1 convs of the squeeze-excitation.
+// pixel phases, fixed-order LDS reduction).  Stages 2 and 3: the two 1x1
+// convs of the squeeze-excitation as wave-per-output products.
+template <typename T>
 __global__ __launch_bounds__(256) void se_partial_kernel(SeParams p, int chunk) {
   __shared__ float4 red[256];
+  const T* in = static_cast<const T*>(p.in);
   const int C4 = p.C >> 2;
   const int lanes_p = 256 / C4;
   const int tid = threadIdx.x;
@@ -210,26 +209,14 @@ __global__ __launch_bounds__(256) void se_partial_kernel(SeParams p, int chunk) 
   const int end = min(start + chunk, p.HW);
   float4 s = f4_zero();
   if (pl < lanes_p) {
-    const float* base = p.in + (size_t)n * p.HW * p.in_ps + cq * 4;
-    for (int px = start + pl; px < end; px += lanes_p) {
-      float4 v = *reinterpret_cast<const float4*>(base + (size_t)px * p.in_ps);
-      s.x += v.x;
-      s.y += v.y;
-      s.z += v.z;
-      s.w += v.w;
-    }
+    const T* base = in + (size_t)n * p.HW * p.in_ps + cq * 4;
+    for (int px = start + pl; px < end; px += lanes_p) s = f4_sum(s, ld4<T>(base + (size_t)px * p.in_ps));
   }
   red[tid] = s;
   __syncthreads();
   if (tid < C4) {
     float4 t = red[tid];
-    for (int k = 1; k < lanes_p; ++k) {
-      float4 v = red[k * C4 + tid];
-      t.x += v.x;
-      t.y += v.y;
-      t.z += v.z;
-      t.w += v.w;
-    }
+    for (int k = 1; k < lanes_p; ++k) t = f4_sum(t, red[k * C4 + tid]);
     *reinterpret_cast<float4*>(p.partial + ((size_t)n * p.P + blockIdx.x) * p.C + tid * 4) = t;
   }
 }
@@ -248,8 +235,8 @@ __device__ __forceinline__ float wave_dot(const float* __restrict__ w, const flo
 // the reducing 1x1 conv + bias + ReLU.
 __global__ __launch_bounds__(256) void se_reduce_kernel(SeParams p) {
   extern __shared__ float sm[];
-  float* mean = sm;                                       // [C]
-  float4* red = reinterpret_cast<float4*>(sm + p.C);     // [256]
+  float* mean = sm;                                    // [C]
+  float4* red = reinterpret_cast<float4*>(sm + p.C);  // [256]
   const int n = blockIdx.x;
   const int tid = threadIdx.x;
   const int C4 = p.C >> 2;
@@ -257,25 +244,14 @@ __global__ __launch_bounds__(256) void se_reduce_kernel(SeParams p) {
   const int cq = tid % C4, pl = tid / C4;
   float4 s = f4_zero();
   if (pl < lanes_p) {
-    for (int k = pl; k < p.P; k += lanes_p) {
-      float4 v = *reinterpret_cast<const float4*>(p.partial + ((size_t)n * p.P + k) * p.C + cq * 4);
-      s.x += v.x;
-      s.y += v.y;
-      s.z += v.z;
-      s.w += v.w;
-    }
+    for (int k = pl; k < p.P; k += lanes_p)
+      s = f4_sum(s, *reinterpret_cast<const float4*>(p.partial + ((size_t)n * p.P + k) * p.C + cq * 4));
   }
   red[tid] = s;
   __syncthreads();
   if (tid < C4) {
     float4 t = red[tid];
-    for (int k = 1; k < lanes_p; ++k) {
-      float4 v = red[k * C4 + tid];
-      t.x += v.x;
-      t.y += v.y;
-      t.z += v.z;
-      t.w += v.w;
-    }
+    for (int k = 1; k < lanes_p; ++k) t = f4_sum(t, red[k * C4 + tid]);
     const float count = (float)p.HW;
     mean[tid * 4 + 0] = t.x / count;
     mean[tid * 4 + 1] = t.y / count;
@@ -310,32 +286,35 @@ __global__ __launch_bounds__(256) void se_expand_kernel(SeParams p) {
 
 void launch_se(const SeParams& p, hipStream_t s) {
   int chunk = (p.HW + p.P - 1) / p.P;
-  hipLaunchKernelGGL(se_partial_kernel, dim3(p.P, p.N), dim3(256), 0, s, p, chunk);
+  DISPATCH_DT(p.dt, hipLaunchKernelGGL(se_partial_kernel<T>, dim3(p.P, p.N), dim3(256), 0, s, p, chunk));
   size_t lds = (size_t)p.C * sizeof(float) + 256 * sizeof(float4);
   hipLaunchKernelGGL(se_reduce_kernel, dim3(p.N, (p.Cr + 15) / 16), dim3(256), lds, s, p);
   hipLaunchKernelGGL(se_expand_kernel, dim3(p.N, (p.C + 15) / 16), dim3(256), (size_t)p.Cr * sizeof(float), s, p);
 }
 
 // ----------------------------------------------------------------- layout
-__global__ void nchw_to_nhwc4_kernel(const float* in, float* out, int N, int H, int W) {
+template <typename T>
+__global__ void nchw_to_nhwc4_kernel(const float* in, T* out, int N, int H, int W) {
   long idx = (long)blockIdx.x * 256 + threadIdx.x;
   long plane = (long)H * W;
   if (idx >= (long)N * plane) return;
   int n = (int)(idx / plane);
   long i = idx - n * plane;
   const float* src = in + (size_t)n * 3 * plane + i;
-  *reinterpret_cast<float4*>(out + (size_t)idx * 4) = make_float4(src[0], src[plane], src[2 * plane], 0.0f);
+  st4<T>(out + (size_t)idx * 4, make_float4(src[0], src[plane], src[2 * plane], 0.0f));
 }
 
-void launch_nchw_to_nhwc4(const float* in, float* out, int N, int H, int W, hipStream_t s) {
-  hipLaunchKernelGGL(nchw_to_nhwc4_kernel, dim3(blocks_for((long)N * H * W)), dim3(256), 0, s, in, out, N, H, W);
+void launch_nchw_to_nhwc4(const float* in, void* out, int N, int H, int W, int dt, hipStream_t s) {
+  DISPATCH_DT(dt, hipLaunchKernelGGL(nchw_to_nhwc4_kernel<T>, dim3(blocks_for((long)N * H * W)), dim3(256), 0, s, in,
+                                     static_cast<T*>(out), N, H, W));
 }
 
 // ----------------------------------------------------------------- pools
 // Max pool 2x2 / stride 1 / pads (0,0,1,1) of the large stem
 // (src/cpu/model.rs:689, src/cpu/ops.rs:1520-1535); fmaxf ignores NaN like
 // f32::max.
-__global__ void maxpool_same_kernel(const float* in, int N, int H, int W, int C, int in_ps, float* out, int out_ps) {
+template <typename T>
+__global__ void maxpool_same_kernel(const T* in, int N, int H, int W, int C, int in_ps, T* out, int out_ps) {
   const int C4 = C >> 2;
   long idx = (long)blockIdx.x * 256 + threadIdx.x;
   long total = (long)N * H * W * C4;
@@ -351,26 +330,26 @@ __global__ void maxpool_same_kernel(const float* in, int N, int H, int W, int C,
     for (int dx = 0; dx < 2; ++dx) {
       int iy = y + dy, ix = x + dx;
       if (iy >= H || ix >= W) continue;
-      float4 v = *reinterpret_cast<const float4*>(in + ((size_t)(n * H + iy) * W + ix) * in_ps + c);
+      float4 v = ld4<T>(in + ((size_t)(n * H + iy) * W + ix) * in_ps + c);
       m.x = fmaxf(m.x, v.x);
       m.y = fmaxf(m.y, v.y);
       m.z = fmaxf(m.z, v.z);
       m.w = fmaxf(m.w, v.w);
     }
-  *reinterpret_cast<float4*>(out + (size_t)pix * out_ps + c) = m;
+  st4<T>(out + (size_t)pix * out_ps + c, m);
 }
 
-void launch_maxpool_same(const float* in, int N, int H, int W, int C, int in_ps, float* out, int out_ps,
+void launch_maxpool_same(const void* in, int N, int H, int W, int C, int in_ps, void* out, int out_ps, int dt,
                          hipStream_t s) {
   long total = (long)N * H * W * (C / 4);
-  hipLaunchKernelGGL(maxpool_same_kernel, dim3(blocks_for(total)), dim3(256), 0, s, in, N, H, W, C, in_ps, out,
-                     out_ps);
+  DISPATCH_DT(dt, hipLaunchKernelGGL(maxpool_same_kernel<T>, dim3(blocks_for(total)), dim3(256), 0, s,
+                                     static_cast<const T*>(in), N, H, W, C, in_ps, static_cast<T*>(out), out_ps));
 }
 
 // Average pool [3,2] / [3,2], no padding, count_include_pad = false
 // (src/cpu/ops.rs:1537-1604): the six taps are summed in row-major order.
-__global__ void avgpool32_kernel(const float* in, int N, int H, int W, int C, int in_ps, float* out, int Ho,
-                                 int Wo) {
+template <typename T>
+__global__ void avgpool32_kernel(const T* in, int N, int H, int W, int C, int in_ps, T* out, int Ho, int Wo) {
   const int C4 = C >> 2;
   long idx = (long)blockIdx.x * 256 + threadIdx.x;
   long total = (long)N * Ho * Wo * C4;
@@ -383,22 +362,16 @@ __global__ void avgpool32_kernel(const float* in, int N, int H, int W, int C, in
   int n = (int)(t / Ho);
   float4 s = f4_zero();
   for (int ky = 0; ky < 3; ++ky)
-    for (int kx = 0; kx < 2; ++kx) {
-      float4 v =
-          *reinterpret_cast<const float4*>(in + ((size_t)(n * H + oy * 3 + ky) * W + ox * 2 + kx) * in_ps + c);
-      s.x = s.x + v.x;
-      s.y = s.y + v.y;
-      s.z = s.z + v.z;
-      s.w = s.w + v.w;
-    }
-  *reinterpret_cast<float4*>(out + (size_t)pix * C + c) =
-      make_float4(s.x / 6.0f, s.y / 6.0f, s.z / 6.0f, s.w / 6.0f);
+    for (int kx = 0; kx < 2; ++kx)
+      s = f4_sum(s, ld4<T>(in + ((size_t)(n * H + oy * 3 + ky) * W + ox * 2 + kx) * in_ps + c));
+  st4<T>(out + (size_t)pix * C + c, make_float4(s.x / 6.0f, s.y / 6.0f, s.z / 6.0f, s.w / 6.0f));
 }
 
-void launch_avgpool32(const float* in, int N, int H, int W, int C, int in_ps, float* out, int Ho, int Wo,
+void launch_avgpool32(const void* in, int N, int H, int W, int C, int in_ps, void* out, int Ho, int Wo, int dt,
                       hipStream_t s) {
   long total = (long)N * Ho * Wo * (C / 4);
-  hipLaunchKernelGGL(avgpool32_kernel, dim3(blocks_for(total)), dim3(256), 0, s, in, N, H, W, C, in_ps, out, Ho, Wo);
+  DISPATCH_DT(dt, hipLaunchKernelGGL(avgpool32_kernel<T>, dim3(blocks_for(total)), dim3(256), 0, s,
+                                     static_cast<const T*>(in), N, H, W, C, in_ps, static_cast<T*>(out), Ho, Wo));
 }
 
 // ----------------------------------------------------------------- FPN
@@ -407,8 +380,9 @@ void launch_avgpool32(const float* in, int N, int H, int W, int C, int in_ps, fl
 // (upsample_add_nchw, :1265-1320) or with the upsample-and-concat write
 // (upsample_and_cat_nchw, :1322-1417): each input pixel is written as a
 // rep x rep block into its channel slice of the concat tensor.
-__global__ void gate_residual_kernel(const float* in, int N, int H, int W, int C, int in_ps, const float* gate,
-                                     const float* upper, int up_ps, float* out, int out_ps, int rep) {
+template <typename T>
+__global__ void gate_residual_kernel(const T* in, int N, int H, int W, int C, int in_ps, const float* gate,
+                                     const T* upper, int up_ps, T* out, int out_ps, int rep) {
   const int C4 = C >> 2;
   long idx = (long)blockIdx.x * 256 + threadIdx.x;
   long total = (long)N * H * W * C4;
@@ -419,36 +393,30 @@ __global__ void gate_residual_kernel(const float* in, int N, int H, int W, int C
   long t = pix / W;
   int y = (int)(t % H);
   int n = (int)(t / H);
-  float4 v = *reinterpret_cast<const float4*>(in + (size_t)pix * in_ps + c);
+  float4 v = ld4<T>(in + (size_t)pix * in_ps + c);
   float4 g = *reinterpret_cast<const float4*>(gate + (size_t)n * C + c);
-  v.x = residual_mul(v.x, g.x);
-  v.y = residual_mul(v.y, g.y);
-  v.z = residual_mul(v.z, g.z);
-  v.w = residual_mul(v.w, g.w);
+  v = make_float4(residual_mul(v.x, g.x), residual_mul(v.y, g.y), residual_mul(v.z, g.z), residual_mul(v.w, g.w));
   if (upper) {
     int uh = H / 2, uw = W / 2;
-    float4 u = *reinterpret_cast<const float4*>(upper + ((size_t)(n * uh + y / 2) * uw + x / 2) * up_ps + c);
-    v.x = v.x + u.x;
-    v.y = v.y + u.y;
-    v.z = v.z + u.z;
-    v.w = v.w + u.w;
+    v = f4_sum(v, ld4<T>(upper + ((size_t)(n * uh + y / 2) * uw + x / 2) * up_ps + c));
   }
   if (rep == 1) {
-    *reinterpret_cast<float4*>(out + (size_t)pix * out_ps + c) = v;
+    st4<T>(out + (size_t)pix * out_ps + c, v);
   } else {
     int OW = W * rep;
     for (int dy = 0; dy < rep; ++dy) {
-      float* row = out + ((size_t)(n * H * rep + y * rep + dy) * OW + (size_t)x * rep) * out_ps + c;
-      for (int dx = 0; dx < rep; ++dx) *reinterpret_cast<float4*>(row + (size_t)dx * out_ps) = v;
+      T* row = out + ((size_t)(n * H * rep + y * rep + dy) * OW + (size_t)x * rep) * out_ps + c;
+      for (int dx = 0; dx < rep; ++dx) st4<T>(row + (size_t)dx * out_ps, v);
     }
   }
 }
 
-void launch_gate_residual(const float* in, int N, int H, int W, int C, int in_ps, const float* gate,
-                          const float* upper, int up_ps, float* out, int out_ps, int rep, hipStream_t s) {
+void launch_gate_residual(const void* in, int N, int H, int W, int C, int in_ps, const float* gate,
+                          const void* upper, int up_ps, void* out, int out_ps, int rep, int dt, hipStream_t s) {
   long total = (long)N * H * W * (C / 4);
-  hipLaunchKernelGGL(gate_residual_kernel, dim3(blocks_for(total)), dim3(256), 0, s, in, N, H, W, C, in_ps, gate,
-                     upper, up_ps, out, out_ps, rep);
+  DISPATCH_DT(dt, hipLaunchKernelGGL(gate_residual_kernel<T>, dim3(blocks_for(total)), dim3(256), 0, s,
+                                     static_cast<const T*>(in), N, H, W, C, in_ps, gate,
+                                     static_cast<const T*>(upper), up_ps, static_cast<T*>(out), out_ps, rep));
 }
 
 // ----------------------------------------------------------------- DB head
@@ -458,8 +426,8 @@ void launch_gate_residual(const float* in, int N, int H, int W, int C, int in_ps
 // BN folded, +bias, ReLU) then conv_final (2x2 s2 to one channel, +bias)
 // and sigmoid (src/cpu/model.rs:1516-1520), 16 probabilities per lane.
 // Weights: wu [c][o][4] (IOHW, folded), bu [o], wf [o][4].
-template <int CH>
-__global__ __launch_bounds__(256) void db_head_up_kernel(const float* in, int N, int H, int W, int in_ps,
+template <typename T, int CH>
+__global__ __launch_bounds__(256) void db_head_up_kernel(const T* in, int N, int H, int W, int in_ps,
                                                          const float* wu, const float* bu, const float* wf, float bf,
                                                          float* out) {
   __shared__ float s_wu[CH * CH * 4];
@@ -476,19 +444,22 @@ __global__ __launch_bounds__(256) void db_head_up_kernel(const float* in, int N,
   int y = (int)(t % H);
   int n = (int)(t / H);
   float xin[CH];
-  const float* src = in + (size_t)idx * in_ps;
+  const T* src = in + (size_t)idx * in_ps;
 #pragma unroll
   for (int c = 0; c < CH; c += 4) {
-    float4 v = *reinterpret_cast<const float4*>(src + c);
+    float4 v = ld4<T>(src + c);
     xin[c] = v.x;
     xin[c + 1] = v.y;
     xin[c + 2] = v.z;
     xin[c + 3] = v.w;
   }
   const int OW = 4 * W;
-#pragma unroll
+#pragma unroll 1
   for (int tap = 0; tap < 4; ++tap) {
     float f[4] = {0.f, 0.f, 0.f, 0.f};
+    // Rolled over the hidden channels: only the input pixel and one hidden
+    // value are live, which keeps the kernel free of spills for every CH.
+#pragma unroll 1
     for (int o = 0; o < CH; ++o) {
       float acc = 0.0f;
 #pragma unroll
@@ -500,57 +471,67 @@ __global__ __launch_bounds__(256) void db_head_up_kernel(const float* in, int N,
     int yy = 4 * y + 2 * (tap >> 1);
     int xx = 4 * x + 2 * (tap & 1);
     float* o0 = out + ((size_t)n * 4 * H + yy) * OW + xx;
-    float2 top = make_float2(1.0f / (1.0f + expf(-(f[0] + bf))), 1.0f / (1.0f + expf(-(f[1] + bf))));
-    float2 bot = make_float2(1.0f / (1.0f + expf(-(f[2] + bf))), 1.0f / (1.0f + expf(-(f[3] + bf))));
+    float2 top = make_float2(act_apply(ACT_SIGMOID, f[0] + bf), act_apply(ACT_SIGMOID, f[1] + bf));
+    float2 bot = make_float2(act_apply(ACT_SIGMOID, f[2] + bf), act_apply(ACT_SIGMOID, f[3] + bf));
     *reinterpret_cast<float2*>(o0) = top;
     *reinterpret_cast<float2*>(o0 + OW) = bot;
   }
 }
 
-void launch_db_head_up(const float* in, int N, int H, int W, int Ch, int in_ps, const float* wu, const float* bu,
-                       const float* wf, float bf, float* out, hipStream_t s) {
+template <typename T>
+static void launch_db_typed(const void* in, int N, int H, int W, int Ch, int in_ps, const float* wu, const float* bu,
+                            const float* wf, float bf, float* out, hipStream_t s) {
   dim3 grid(blocks_for((long)N * H * W));
+  const T* x = static_cast<const T*>(in);
   switch (Ch) {
-    case 16: hipLaunchKernelGGL(db_head_up_kernel<16>, grid, dim3(256), 0, s, in, N, H, W, in_ps, wu, bu, wf, bf, out); break;
-    case 24: hipLaunchKernelGGL(db_head_up_kernel<24>, grid, dim3(256), 0, s, in, N, H, W, in_ps, wu, bu, wf, bf, out); break;
-    case 64: hipLaunchKernelGGL(db_head_up_kernel<64>, grid, dim3(256), 0, s, in, N, H, W, in_ps, wu, bu, wf, bf, out); break;
+    case 16: hipLaunchKernelGGL((db_head_up_kernel<T, 16>), grid, dim3(256), 0, s, x, N, H, W, in_ps, wu, bu, wf, bf, out); break;
+    case 24: hipLaunchKernelGGL((db_head_up_kernel<T, 24>), grid, dim3(256), 0, s, x, N, H, W, in_ps, wu, bu, wf, bf, out); break;
+    case 64: hipLaunchKernelGGL((db_head_up_kernel<T, 64>), grid, dim3(256), 0, s, x, N, H, W, in_ps, wu, bu, wf, bf, out); break;
     default: break;  // rejected by the planner
   }
+}
+
+void launch_db_head_up(const void* in, int N, int H, int W, int Ch, int in_ps, const float* wu, const float* bu,
+                       const float* wf, float bf, float* out, int dt, hipStream_t s) {
+  DISPATCH_DT(dt, launch_db_typed<T>(in, N, H, W, Ch, in_ps, wu, bu, wf, bf, out, s));
 }
 
 // ----------------------------------------------------------------- LayerNorm
 // Replaces WGSL `layer_norm` (src/gpu/shaders/layer_norm.wgsl:55); formula
 // of layer_norm_in_place (src/cpu/kernels/mod.rs:2288-2313): two-pass mean
 // and variance, out = (x - mean) * (inv_std * w) + b; one wave per row.
-__global__ __launch_bounds__(256) void layer_norm_kernel(const float* in, int rows, int C, const float* w,
-                                                         const float* b, float eps, const float* res, float* out) {
+template <typename T>
+__global__ __launch_bounds__(256) void layer_norm_kernel(const T* in, int rows, int C, const float* w, const float* b,
+                                                         float eps, const T* res, T* out) {
   int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   int lane = threadIdx.x & 63;
   if (row >= rows) return;
-  const float* x = in + (size_t)row * C;
+  const T* x = in + (size_t)row * C;
   float s = 0.0f;
-  for (int c = lane; c < C; c += 64) s += x[c];
+  for (int c = lane; c < C; c += 64) s += ld1<T>(x + c);
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
   float mean = s / (float)C;
   float v = 0.0f;
   for (int c = lane; c < C; c += 64) {
-    float d = x[c] - mean;
+    float d = ld1<T>(x + c) - mean;
     v = fmaf(d, d, v);
   }
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
   float var = v / (float)C;
   float inv = 1.0f / sqrtf(var + eps);
-  float* y = out + (size_t)row * C;
+  T* y = out + (size_t)row * C;
   for (int c = lane; c < C; c += 64) {
-    float r = fmaf(x[c] - mean, inv * w[c], b[c]);
-    if (res) r = r + res[(size_t)row * C + c];
-    y[c] = r;
+    float r = fmaf(ld1<T>(x + c) - mean, inv * w[c], b[c]);
+    if (res) r = r + ld1<T>(res + (size_t)row * C + c);
+    st1<T>(y + c, r);
   }
 }
 
-void launch_layer_norm(const float* in, int rows, int C, const float* w, const float* b, float eps, const float* res,
-                       float* out, hipStream_t s) {
-  hipLaunchKernelGGL(layer_norm_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, s, in, rows, C, w, b, eps, res, out);
+void launch_layer_norm(const void* in, int rows, int C, const float* w, const float* b, float eps, const void* res,
+                       void* out, int dt, hipStream_t s) {
+  DISPATCH_DT(dt, hipLaunchKernelGGL(layer_norm_kernel<T>, dim3(blocks_for(rows, 4)), dim3(256), 0, s,
+                                     static_cast<const T*>(in), rows, C, w, b, eps, static_cast<const T*>(res),
+                                     static_cast<T*>(out)));
 }
 
 // ----------------------------------------------------------------- attention
@@ -561,57 +542,59 @@ void launch_layer_norm(const float* in, int rows, int C, const float* w, const f
 // One block per (image, head, 16 query rows); the score rows stay in LDS.
 constexpr int ATT_Q = 16;
 
-__global__ __launch_bounds__(256) void attention_kernel(const float* qkv, int B, int T, int hidden, int heads,
-                                                        float scale, float* out) {
+template <typename T>
+__global__ __launch_bounds__(256) void attention_kernel(const T* qkv, int B, int T_, int hidden, int heads,
+                                                        float scale, T* out) {
   extern __shared__ float sc[];  // [ATT_Q][T]
   const int bh = blockIdx.x;
   const int b = bh / heads, h = bh - (bh / heads) * heads;
   const int t0 = blockIdx.y * ATT_Q;
   const int hd = hidden / heads;
-  const int rows = min(ATT_Q, T - t0);
+  const int rows = min(ATT_Q, T_ - t0);
   const size_t stride = (size_t)3 * hidden;
-  const float* base = qkv + (size_t)b * T * stride + h * hd;
-  for (int i = threadIdx.x; i < rows * T; i += 256) {
-    int r = i / T, u = i - (i / T) * T;
-    const float* q = base + (size_t)(t0 + r) * stride;
-    const float* k = base + (size_t)u * stride + hidden;
+  const T* base = qkv + (size_t)b * T_ * stride + h * hd;
+  for (int i = threadIdx.x; i < rows * T_; i += 256) {
+    int r = i / T_, u = i - (i / T_) * T_;
+    const T* q = base + (size_t)(t0 + r) * stride;
+    const T* k = base + (size_t)u * stride + hidden;
     float acc = 0.0f;
-    for (int d = 0; d < hd; ++d) acc = fmaf(q[d], k[d], acc);
-    sc[r * T + u] = __fmul_rn(acc, scale);
+    for (int d = 0; d < hd; ++d) acc = fmaf(ld1<T>(q + d), ld1<T>(k + d), acc);
+    sc[r * T_ + u] = __fmul_rn(acc, scale);
   }
   __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   for (int r = wave; r < rows; r += 4) {
-    float* s = sc + r * T;
+    float* s = sc + r * T_;
     float m = -INFINITY;
-    for (int u = lane; u < T; u += 64) m = fmaxf(m, s[u]);
+    for (int u = lane; u < T_; u += 64) m = fmaxf(m, s[u]);
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     float sum = 0.0f;
-    for (int u = lane; u < T; u += 64) {
-      float e = expf(s[u] - m);
+    for (int u = lane; u < T_; u += 64) {
+      float e = fast_exp(s[u] - m);
       s[u] = e;
       sum += e;
     }
     for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
     float rcp = 1.0f / sum;
-    for (int u = lane; u < T; u += 64) s[u] *= rcp;
+    for (int u = lane; u < T_; u += 64) s[u] *= rcp;
   }
   __syncthreads();
   for (int i = threadIdx.x; i < rows * hd; i += 256) {
     int r = i / hd, d = i - (i / hd) * hd;
-    const float* s = sc + r * T;
-    const float* v = base + 2 * hidden + d;
+    const float* s = sc + r * T_;
+    const T* v = base + 2 * hidden + d;
     float acc = 0.0f;
-    for (int u = 0; u < T; ++u) acc = fmaf(s[u], v[(size_t)u * stride], acc);
-    out[((size_t)b * T + t0 + r) * hidden + h * hd + d] = acc;
+    for (int u = 0; u < T_; ++u) acc = fmaf(s[u], ld1<T>(v + (size_t)u * stride), acc);
+    st1<T>(out + ((size_t)b * T_ + t0 + r) * hidden + h * hd + d, acc);
   }
 }
 
-void launch_attention(const float* qkv, int B, int T, int hidden, int heads, float* out, hipStream_t s) {
+void launch_attention(const void* qkv, int B, int T_, int hidden, int heads, void* out, int dt, hipStream_t s) {
   float scale = powf((float)(hidden / heads), -0.5f);
-  dim3 grid(B * heads, (T + ATT_Q - 1) / ATT_Q);
-  size_t lds = (size_t)ATT_Q * T * sizeof(float);
-  hipLaunchKernelGGL(attention_kernel, grid, dim3(256), lds, s, qkv, B, T, hidden, heads, scale, out);
+  dim3 grid(B * heads, (T_ + ATT_Q - 1) / ATT_Q);
+  size_t lds = (size_t)ATT_Q * T_ * sizeof(float);
+  DISPATCH_DT(dt, hipLaunchKernelGGL(attention_kernel<T>, grid, dim3(256), lds, s, static_cast<const T*>(qkv), B, T_,
+                                     hidden, heads, scale, static_cast<T*>(out)));
 }
 
 // ----------------------------------------------------------------- softmax
@@ -639,10 +622,10 @@ __global__ __launch_bounds__(1024) void softmax_rows_kernel(float* x, int cols) 
   for (int i = threadIdx.x; i < cols; i += blockDim.x) m = fmaxf(m, row[i]);
   m = block_reduce(m, red, true);
   float s = 0.0f;
-  for (int i = threadIdx.x; i < cols; i += blockDim.x) s += expf(row[i] - m);
+  for (int i = threadIdx.x; i < cols; i += blockDim.x) s += fast_exp(row[i] - m);
   s = block_reduce(s, red, false);
   float rcp = 1.0f / s;
-  for (int i = threadIdx.x; i < cols; i += blockDim.x) row[i] = expf(row[i] - m) * rcp;
+  for (int i = threadIdx.x; i < cols; i += blockDim.x) row[i] = fast_exp(row[i] - m) * rcp;
 }
 
 void launch_softmax_rows(float* x, long rows, int cols, hipStream_t s) {
@@ -652,8 +635,9 @@ void launch_softmax_rows(float* x, long rows, int cols, hipStream_t s) {
 // ----------------------------------------------------------------- preprocess
 // The reference CPU preprocessing (src/preprocess/kernels.rs:94-170): quad
 // bilinear source point, clamped; bilinear RGB rounded to an integer and
-// clamped; v * (1/(255 std)) - mean/std as BGR; zero past content_width.
-// Contraction is off so every product and sum rounds as in the reference.
+// clamped; v * (1/(255 std)) - mean/std as BGR planes; zero past
+// content_width.  Contraction is off so every product and sum rounds as in
+// the reference.
 __global__ void preprocess_kernel(PreParams p) {
 #pragma clang fp contract(off)
   long idx = (long)blockIdx.x * 256 + threadIdx.x;
@@ -694,14 +678,10 @@ __global__ void preprocess_kernel(PreParams p) {
     g = rgb[1] * p.scale[1] + p.bias[1];
     rr = rgb[0] * p.scale[2] + p.bias[2];
   }
-  if (p.nhwc) {
-    *reinterpret_cast<float4*>(p.out + (size_t)idx * 4) = make_float4(b, g, rr, 0.0f);
-  } else {
-    float* o = p.out + (size_t)n * 3 * plane + r;
-    o[0] = b;
-    o[plane] = g;
-    o[2 * plane] = rr;
-  }
+  float* o = p.out + (size_t)n * 3 * plane + r;
+  o[0] = b;
+  o[plane] = g;
+  o[2 * plane] = rr;
 }
 
 void launch_preprocess(const PreParams& p, hipStream_t s) {

@@ -24,8 +24,14 @@ constexpr size_t NOW = SIZE_MAX;
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+uint16_t to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
 struct ConvW {
-  size_t w = NOW, b = NOW;
+  size_t w = NOW, b = NOW;  // byte offsets into the weight blob
   int ldw = 0;
   int ci = 0, ci_pad = 0, co = 0, kh = 1, kw = 1, sh = 1, sw = 1, pt = 0, pl = 0, pb = 0, pr = 0;
 };
@@ -58,15 +64,17 @@ struct BlockSpec {
 
 class Builder {
  public:
-  Builder(const SafeTensors& st, Plan& plan) : st_(st), plan_(plan) {}
+  Builder(const SafeTensors& st, Plan& plan, int dt) : st_(st), plan_(plan), dt_(dt) { plan_.dt = dt; }
+
+  int dt() const { return dt_; }
 
   // ------------------------------------------------------------ weights
   HostTensor get(const std::string& name, const std::vector<int>& shape) { return st_.get(name, shape); }
 
   // s = gamma / sqrt(var + 1e-5); W' = W s per output channel;
-  // b' = (b - mean) s + beta (src/cpu/model.rs:371-407).  `out_stride`
-  // and `inner` describe where output channel o's weights live:
-  // W[o * out_stride + i * inner_stride + j] for the transposed layout.
+  // b' = (b - mean) s + beta (src/cpu/model.rs:371-407).  With `transposed`
+  // the weight is IOHW [ci][co][k] and the scale applies along its second
+  // axis (fold_transpose_batch_norm, src/cpu/model.rs:1440-1477).
   void fold_bn(std::vector<float>& W, std::vector<float>& b, const std::string& norm, int co, bool transposed = false,
                int ci = 0) {
     HostTensor g = get(norm + ".weight", {co}), be = get(norm + ".bias", {co});
@@ -79,7 +87,7 @@ class Builder {
         for (size_t i = 0; i < row; ++i) W[o * row + i] *= s;
         b[o] = (b[o] - mu.v[o]) * s + be.v[o];
       }
-    } else {  // IOHW [ci][co][k]
+    } else {
       size_t k = W.size() / ((size_t)ci * co);
       for (int o = 0; o < co; ++o) {
         float s = g.v[o] / std::sqrt(var.v[o] + 1e-5f);
@@ -90,10 +98,22 @@ class Builder {
     }
   }
 
+  // Appends fp32 values to the weight blob (256-byte aligned); returns the
+  // byte offset.
   size_t put(const std::vector<float>& v) {
-    size_t off = round_up(plan_.weights.size(), 64);
-    plan_.weights.resize(off + v.size(), 0.0f);
-    std::copy(v.begin(), v.end(), plan_.weights.begin() + off);
+    size_t off = round_up(plan_.weights.size(), 256);
+    plan_.weights.resize(off + v.size() * 4, 0);
+    memcpy(plan_.weights.data() + off, v.data(), v.size() * 4);
+    return off;
+  }
+
+  // Appends values in the activation storage type (matrix-core operands).
+  size_t put_act(const std::vector<float>& v) {
+    if (dt_ == DT_F32) return put(v);
+    size_t off = round_up(plan_.weights.size(), 256);
+    plan_.weights.resize(off + v.size() * 2, 0);
+    uint16_t* dst = reinterpret_cast<uint16_t*>(plan_.weights.data() + off);
+    for (size_t i = 0; i < v.size(); ++i) dst[i] = to_bf16(v[i]);
     return off;
   }
 
@@ -116,7 +136,7 @@ class Builder {
         for (int ky = 0; ky < kh; ++ky)
           for (int kx = 0; kx < kw; ++kx)
             packed[(size_t)o * K + (size_t)(ky * kw + kx) * c.ci_pad + i] = W[(((size_t)o * ci + i) * kh + ky) * kw + kx];
-    c.w = put(packed);
+    c.w = put_act(packed);
     if (!b.empty()) c.b = put(b);
     return c;
   }
@@ -175,14 +195,16 @@ class Builder {
   }
 
   // ------------------------------------------------------------ values
-  View alloc(int n, int h, int w, int c, const std::string& name, int ps = 0) {
+  // A new buffer in the activation storage type (or `dt` when given).
+  View alloc(int n, int h, int w, int c, const std::string& name, int dt = -1, int ps = 0) {
+    View v;
+    v.n = n, v.h = h, v.w = w, v.c = c, v.ps = ps ? ps : c;
+    v.dt = dt < 0 ? dt_ : dt;
     Buffer b;
-    b.elems = (size_t)n * h * w * (ps ? ps : c);
+    b.bytes = (size_t)n * h * w * v.ps * dtype_size(v.dt);
     b.name = name;
     plan_.bufs.push_back(b);
-    View v;
     v.buf = (int)plan_.bufs.size() - 1;
-    v.n = n, v.h = h, v.w = w, v.c = c, v.ps = ps ? ps : c;
     return v;
   }
 
@@ -221,6 +243,8 @@ class Builder {
     } else {
       out = alloc(x.n, oh, ow, w.co, name);
     }
+    if (out.dt != x.dt && (e.res || e.up || e.rep != 1))
+      raise(PPOCR_ERR_INVALID_MODEL, name + ": mixed-type epilogue is limited to plain stores");
     View in = x;
     View res = e.res ? *e.res : View();
     View rg = e.res_gate ? *e.res_gate : View();
@@ -230,6 +254,7 @@ class Builder {
     ConvParams base{};
     base.N = x.n, base.H = x.h, base.W = x.w, base.C = x.c, base.in_ps = x.ps;
     base.Ho = Ho, base.Wo = Wo, base.Co = w.co, base.out_ps = out.ps;
+    base.out_f32 = out.dt == DT_F32 && x.dt != DT_F32;
     base.ldw = w.ldw;
     base.kh = w.kh, base.kw = w.kw, base.sh = w.sh, base.sw = w.sw, base.pt = w.pt, base.pl = w.pl;
     base.act = e.act;
@@ -238,17 +263,20 @@ class Builder {
     base.up_ps = has_up ? up.ps : 0;
     base.rep = e.rep;
     base.out_h = oh, base.out_w = ow;
+    base.dt = x.dt;
     size_t wo = w.w, bo = w.b;
     Op op;
     op.name = name;
-    op.kernel = conv_tile_name(x.n * Ho * Wo, w.co);
+    op.kernel = conv_tile_name(x.n * Ho * Wo, w.co, x.dt);
     op.bound = 1;
+    const double es = (double)dtype_size(x.dt);
     double M = (double)x.n * Ho * Wo;
     double K = (double)w.kh * w.kw * w.ci;
     double cols = w.co;
     op.flops = 2.0 * M * cols * K;
-    op.bytes = 4.0 * ((double)x.pixels() * w.ci + K * cols + (double)out.pixels() * w.co +
-                      (has_res ? M * w.co : 0.0) + (has_up ? (double)up.pixels() * w.co : 0.0));
+    op.bytes = es * ((double)x.pixels() * w.ci + K * cols + (has_res ? M * w.co : 0.0) +
+                     (has_up ? (double)up.pixels() * w.co : 0.0)) +
+               (double)dtype_size(out.dt) * (double)out.pixels() * w.co;
     op.reads = {x.buf};
     if (has_res) op.reads.push_back(res.buf);
     if (has_rg) op.reads.push_back(rg.buf);
@@ -259,11 +287,11 @@ class Builder {
       ConvParams p = base;
       p.in = ex.ptr(in);
       p.out = ex.ptr(out);
-      p.wt = ex.w(wo);
+      p.wt = ex.wv(wo);
       p.bias = ex.w(bo);
-      p.in_gate = has_ig ? ex.ptr(ig) : nullptr;
+      p.in_gate = has_ig ? ex.fptr(ig) : nullptr;
       p.res = has_res ? ex.ptr(res) : nullptr;
-      p.res_gate = has_rg ? ex.ptr(rg) : nullptr;
+      p.res_gate = has_rg ? ex.fptr(rg) : nullptr;
       p.up = has_up ? ex.ptr(up) : nullptr;
       launch_conv(p, s);
     };
@@ -281,6 +309,7 @@ class Builder {
     base.Ho = Ho, base.Wo = Wo, base.out_ps = out.ps;
     base.kh = w.kh, base.kw = w.kw, base.sh = w.sh, base.sw = w.sw, base.pt = w.pt, base.pl = w.pl;
     base.act = act;
+    base.dt = x.dt;
     View in = x;
     View r = res ? *res : View();
     bool has_res = res;
@@ -290,7 +319,8 @@ class Builder {
     op.name = name;
     op.kernel = depthwise_kernel_name(w.kh, w.kw, w.sh, w.sw, Ho);
     op.flops = 2.0 * out.pixels() * w.c * w.kh * w.kw;
-    op.bytes = 4.0 * ((double)x.pixels() * w.c + (double)out.pixels() * w.c * (has_res ? 2 : 1) + w.kh * w.kw * w.c);
+    op.bytes = (double)dtype_size(x.dt) * ((double)x.pixels() * w.c + (double)out.pixels() * w.c * (has_res ? 2 : 1)) +
+               4.0 * w.kh * w.kw * w.c;
     op.reads = {x.buf};
     if (has_res) op.reads.push_back(r.buf);
     op.writes = {out.buf};
@@ -307,35 +337,36 @@ class Builder {
     return out;
   }
 
-  // Squeeze-excitation gate [N,1,1,C] of x (src/cpu/model.rs:456-493,
+  // Squeeze-excitation gate [N,1,1,C] (fp32) of x (src/cpu/model.rs:456-493,
   // :1069-1105).
   View se(const View& x, const SeW& w, const std::string& name) {
     int HW = x.h * x.w;
     int P = std::max(1, std::min(HW / 64, std::max(1, 1024 / x.n)));
-    View part = alloc(x.n, P, 1, x.c, name + ".partial");
-    View hid = alloc(x.n, 1, 1, (int)round_up(w.cr, 4), name + ".hidden");
-    View gate = alloc(x.n, 1, 1, x.c, name);
+    View part = alloc(x.n, P, 1, x.c, name + ".partial", DT_F32);
+    View hid = alloc(x.n, 1, 1, (int)round_up(w.cr, 4), name + ".hidden", DT_F32);
+    View gate = alloc(x.n, 1, 1, x.c, name, DT_F32);
     SeParams base{};
     base.N = x.n, base.HW = HW, base.C = x.c, base.in_ps = x.ps, base.P = P, base.Cr = w.cr, base.gate_act = w.act;
+    base.dt = x.dt;
     View in = x;
     SeW ww = w;
     Op op;
     op.name = name;
     op.kernel = "se_gate";
     op.flops = 2.0 * x.n * ((double)HW * x.c + 2.0 * x.c * w.cr);
-    op.bytes = 4.0 * ((double)x.pixels() * x.c + 2.0 * x.c * w.cr + x.n * x.c);
+    op.bytes = (double)dtype_size(x.dt) * x.pixels() * x.c + 4.0 * (2.0 * x.c * w.cr + x.n * x.c);
     op.reads = {x.buf};
     op.writes = {part.buf, hid.buf, gate.buf};
     op.launch = [=](const Exec& ex, hipStream_t s) {
       SeParams p = base;
       p.in = ex.ptr(in);
-      p.partial = ex.ptr(part);
+      p.partial = ex.fptr(part);
       p.w1 = ex.w(ww.w1);
       p.b1 = ex.w(ww.b1);
       p.w2 = ex.w(ww.w2);
       p.b2 = ex.w(ww.b2);
-      p.hidden = ex.ptr(hid);
-      p.gate = ex.ptr(gate);
+      p.hidden = ex.fptr(hid);
+      p.gate = ex.fptr(gate);
       launch_se(p, s);
     };
     add_op(std::move(op));
@@ -351,13 +382,14 @@ class Builder {
     Op op;
     op.name = name;
     op.kernel = "gate_residual";
-    op.bytes = 4.0 * ((double)x.pixels() * x.c * (1 + rep * rep) + (has_up ? (double)up.pixels() * x.c : 0.0));
+    op.bytes = (double)dtype_size(x.dt) *
+               ((double)x.pixels() * x.c * (1 + rep * rep) + (has_up ? (double)up.pixels() * x.c : 0.0));
     op.reads = {x.buf, g.buf};
     if (has_up) op.reads.push_back(up.buf);
     op.writes = {dst.buf};
     op.launch = [=](const Exec& ex, hipStream_t s) {
-      launch_gate_residual(ex.ptr(in), in.n, in.h, in.w, in.c, in.ps, ex.ptr(gate), has_up ? ex.ptr(up) : nullptr,
-                           has_up ? up.ps : 0, ex.ptr(out), out.ps, rep, s);
+      launch_gate_residual(ex.ptr(in), in.n, in.h, in.w, in.c, in.ps, ex.fptr(gate), has_up ? ex.ptr(up) : nullptr,
+                           has_up ? up.ps : 0, ex.ptr(out), out.ps, rep, in.dt, s);
     };
     add_op(std::move(op));
   }
@@ -367,11 +399,11 @@ class Builder {
     Op op;
     op.name = name;
     op.kernel = "maxpool_same";
-    op.bytes = 8.0 * x.pixels() * x.c;
+    op.bytes = 2.0 * dtype_size(x.dt) * x.pixels() * x.c;
     op.reads = {x.buf};
     op.writes = {dst.buf};
     op.launch = [=](const Exec& ex, hipStream_t s) {
-      launch_maxpool_same(ex.ptr(in), in.n, in.h, in.w, in.c, in.ps, ex.ptr(out), out.ps, s);
+      launch_maxpool_same(ex.ptr(in), in.n, in.h, in.w, in.c, in.ps, ex.ptr(out), out.ps, in.dt, s);
     };
     add_op(std::move(op));
   }
@@ -383,11 +415,11 @@ class Builder {
     Op op;
     op.name = name;
     op.kernel = "avgpool";
-    op.bytes = 4.0 * ((double)x.pixels() * x.c + (double)out.pixels() * x.c);
+    op.bytes = (double)dtype_size(x.dt) * ((double)x.pixels() * x.c + (double)out.pixels() * x.c);
     op.reads = {x.buf};
     op.writes = {out.buf};
     op.launch = [=](const Exec& ex, hipStream_t s) {
-      launch_avgpool32(ex.ptr(in), in.n, in.h, in.w, in.c, in.ps, ex.ptr(out), out.h, out.w, s);
+      launch_avgpool32(ex.ptr(in), in.n, in.h, in.w, in.c, in.ps, ex.ptr(out), out.h, out.w, in.dt, s);
     };
     add_op(std::move(op));
     return out;
@@ -403,13 +435,13 @@ class Builder {
     Op op;
     op.name = name;
     op.kernel = "layer_norm";
-    op.bytes = 4.0 * ((double)x.pixels() * C * (has_res ? 3 : 2) + 2 * C);
+    op.bytes = (double)dtype_size(x.dt) * x.pixels() * C * (has_res ? 3 : 2) + 8.0 * C;
     op.reads = {x.buf};
     if (has_res) op.reads.push_back(r.buf);
     op.writes = {out.buf};
     op.launch = [=](const Exec& ex, hipStream_t s) {
       launch_layer_norm(ex.ptr(in), (int)in.pixels(), C, ex.w(wo), ex.w(bo), 1e-6f, has_res ? ex.ptr(r) : nullptr,
-                        ex.ptr(out), s);
+                        ex.ptr(out), in.dt, s);
     };
     add_op(std::move(op));
     return out;
@@ -419,22 +451,23 @@ class Builder {
     View out = alloc(qkv.n, qkv.h, qkv.w, hidden, name);
     View in = qkv;
     int T = qkv.h * qkv.w;
-    if ((size_t)16 * T * 4 > 160 * 1024) raise(PPOCR_ERR_INVALID_INPUT, "recognizer sequence too long for attention");
+    if ((size_t)16 * T * 4 > 64 * 1024) raise(PPOCR_ERR_INVALID_INPUT, "recognizer sequence too long for attention");
     Op op;
     op.name = name;
     op.kernel = "attention";
     op.flops = 2.0 * qkv.n * heads * (double)T * T * (hidden / heads) * 2.0;
-    op.bytes = 4.0 * ((double)qkv.pixels() * 3 * hidden + (double)out.pixels() * hidden);
+    op.bytes = (double)dtype_size(qkv.dt) * ((double)qkv.pixels() * 3 * hidden + (double)out.pixels() * hidden);
     op.reads = {qkv.buf};
     op.writes = {out.buf};
     op.launch = [=](const Exec& ex, hipStream_t s) {
-      launch_attention(ex.ptr(in), in.n, T, hidden, heads, ex.ptr(out), s);
+      launch_attention(ex.ptr(in), in.n, T, hidden, heads, ex.ptr(out), in.dt, s);
     };
     add_op(std::move(op));
     return out;
   }
 
   void softmax(const View& x, const std::string& name) {
+    if (x.dt != DT_F32) raise(PPOCR_ERR_INVALID_MODEL, name + ": softmax runs on fp32 rows");
     View io = x;
     Op op;
     op.name = name;
@@ -442,23 +475,25 @@ class Builder {
     op.bytes = 8.0 * x.pixels() * x.c;
     op.reads = {x.buf};
     op.writes = {x.buf};
-    op.launch = [=](const Exec& ex, hipStream_t s) { launch_softmax_rows(ex.ptr(io), (long)io.pixels(), io.c, s); };
+    op.launch = [=](const Exec& ex, hipStream_t s) { launch_softmax_rows(ex.fptr(io), (long)io.pixels(), io.c, s); };
     add_op(std::move(op));
   }
 
-  // NCHW staging buffer -> NHWC with 4 channels.
+  // fp32 NCHW staging buffer -> NHWC with 4 channels in the activation type.
   View input(const size_t nchw[4]) {
     int n = (int)nchw[0], h = (int)nchw[2], w = (int)nchw[3];
-    View st = alloc(n, 3, h, w, "input.nchw");
+    View st = alloc(n, 3, h, w, "input.nchw", DT_F32);
     plan_.staging = st.buf;
     View x = alloc(n, h, w, 4, "input");
     Op op;
     op.name = "input";
     op.kernel = "nchw_to_nhwc";
-    op.bytes = 4.0 * 7.0 * n * h * w;
+    op.bytes = (12.0 + 4.0 * dtype_size(x.dt)) * n * h * w;
     op.reads = {st.buf};
     op.writes = {x.buf};
-    op.launch = [=](const Exec& ex, hipStream_t s) { launch_nchw_to_nhwc4(ex.ptr(st), ex.ptr(x), n, h, w, s); };
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      launch_nchw_to_nhwc4(ex.fptr(st), ex.ptr(x), n, h, w, x.dt, s);
+    };
     add_op(std::move(op));
     plan_.input = x;
     return x;
@@ -469,6 +504,7 @@ class Builder {
  private:
   const SafeTensors& st_;
   Plan& plan_;
+  int dt_;
 };
 
 // ------------------------------------------------------------------ backbone
@@ -784,7 +820,7 @@ void detector_head(Builder& B, const View& x, int nc) {
   float bf = B.get("head.conv_final.bias", {1}).v[0];
   size_t owu = B.put(wu), obu = B.put(bu), owf = B.put(wf);
   Plan& plan = B.plan();
-  View out = B.alloc(x.n, 4 * d.h, 4 * d.w, 1, "output");
+  View out = B.alloc(x.n, 4 * d.h, 4 * d.w, 1, "output", DT_F32);
   plan.output = out.buf;
   plan.output_elems = out.pixels();
   plan.output_shape = {(size_t)x.n, 1, (size_t)out.h, (size_t)out.w};
@@ -793,11 +829,12 @@ void detector_head(Builder& B, const View& x, int nc) {
   op.name = "head.conv_up+conv_final";
   op.kernel = "db_head_up";
   op.flops = 2.0 * d.pixels() * (4.0 * h * h + 16.0 * h);
-  op.bytes = 4.0 * ((double)d.pixels() * h + (double)out.pixels() + 4.0 * h * h + 4.0 * h);
+  op.bytes = (double)dtype_size(d.dt) * d.pixels() * h + 4.0 * ((double)out.pixels() + 4.0 * h * h + 4.0 * h);
   op.reads = {d.buf};
   op.writes = {out.buf};
   op.launch = [=](const Exec& ex, hipStream_t s) {
-    launch_db_head_up(ex.ptr(in), in.n, in.h, in.w, in.c, in.ps, ex.w(owu), ex.w(obu), ex.w(owf), bf, ex.ptr(out), s);
+    launch_db_head_up(ex.ptr(in), in.n, in.h, in.w, in.c, in.ps, ex.w(owu), ex.w(obu), ex.w(owf), bf, ex.fptr(out),
+                      in.dt, s);
   };
   B.add_op(std::move(op));
 }
@@ -823,7 +860,7 @@ void validate_recognizer_shape(const size_t s[4]) {
 }  // namespace
 
 // Detector::load (src/gpu/model.rs:50-93; architecture src/cpu/model.rs:1546-1609).
-Plan build_detector(const SafeTensors& st, int size, const size_t nchw[4]) {
+Plan build_detector(const SafeTensors& st, int size, const size_t nchw[4], int dt) {
   validate_detector_shape(nchw);
   const size_t expected = size == PPOCR_SIZE_MEDIUM ? 350 : 271;
   const char* tier = size == PPOCR_SIZE_MEDIUM ? "medium" : size == PPOCR_SIZE_SMALL ? "small" : "tiny";
@@ -832,7 +869,7 @@ Plan build_detector(const SafeTensors& st, int size, const size_t nchw[4]) {
                                        " tensors; expected " + std::to_string(expected));
   Plan plan;
   plan.detector = true;
-  Builder B(st, plan);
+  Builder B(st, plan, dt);
   int chans[4], mid, out, nc;
   if (size == PPOCR_SIZE_MEDIUM) {
     const int c[4] = {128, 256, 512, 896};
@@ -858,7 +895,7 @@ Plan build_detector(const SafeTensors& st, int size, const size_t nchw[4]) {
 
 // Recognizer::load (src/gpu/model.rs:156-220; architecture
 // src/cpu/model.rs:1961-2039).
-Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4]) {
+Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4], int dt) {
   validate_recognizer_shape(nchw);
   const size_t expected = size == PPOCR_SIZE_MEDIUM ? 269 : size == PPOCR_SIZE_SMALL ? 250 : 150;
   const char* tier = size == PPOCR_SIZE_MEDIUM ? "medium" : size == PPOCR_SIZE_SMALL ? "small" : "tiny";
@@ -867,7 +904,7 @@ Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4]) {
                                        " tensors; expected " + std::to_string(expected));
   Plan plan;
   plan.detector = false;
-  Builder B(st, plan);
+  Builder B(st, plan, dt);
   View x = B.input(nchw);
   bool tiny = size == PPOCR_SIZE_TINY;
   int mid = size == PPOCR_SIZE_MEDIUM ? 64 : size == PPOCR_SIZE_SMALL ? 48 : 24;
@@ -876,7 +913,7 @@ Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4]) {
   View pooled = B.avgpool32(stages.back(), "pool");
   if (pooled.h != 1) raise(PPOCR_ERR_INVALID_MODEL, "recognizer pooling must produce height 1");
   const int classes = tiny ? 6906 : 18710;
-  View logits_dst = B.alloc(pooled.n, 1, pooled.w, classes, "output");
+  View logits_dst = B.alloc(pooled.n, 1, pooled.w, classes, "output", DT_F32);
   plan.output = logits_dst.buf;
   plan.output_elems = logits_dst.pixels() * classes;
   plan.output_shape = {(size_t)pooled.n, (size_t)pooled.w, (size_t)classes};
@@ -944,19 +981,19 @@ void plan_arena(Plan& plan) {
   std::vector<int> order(plan.bufs.size());
   for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
   std::sort(order.begin(), order.end(), [&](int a, int b) {
-    if (plan.bufs[a].elems != plan.bufs[b].elems) return plan.bufs[a].elems > plan.bufs[b].elems;
+    if (plan.bufs[a].bytes != plan.bufs[b].bytes) return plan.bufs[a].bytes > plan.bufs[b].bytes;
     return a < b;
   });
   std::vector<int> placed;
   size_t total = 0, unplanned = 0;
   for (int id : order) {
     Buffer& b = plan.bufs[id];
-    size_t size = round_up(b.elems, 64);
+    size_t size = round_up(b.bytes, 256);
     unplanned += size;
     std::vector<std::pair<size_t, size_t>> busy;
     for (int o : placed) {
       const Buffer& q = plan.bufs[o];
-      if (q.first <= b.last && b.first <= q.last) busy.push_back({q.arena_off, q.arena_off + round_up(q.elems, 64)});
+      if (q.first <= b.last && b.first <= q.last) busy.push_back({q.arena_off, q.arena_off + round_up(q.bytes, 256)});
     }
     std::sort(busy.begin(), busy.end());
     size_t off = 0;
@@ -968,8 +1005,8 @@ void plan_arena(Plan& plan) {
     total = std::max(total, off + size);
     placed.push_back(id);
   }
-  plan.arena_elems = total;
-  plan.unplanned_elems = unplanned;
+  plan.arena_bytes = total;
+  plan.unplanned_bytes = unplanned;
 }
 
 }  // namespace ppocr

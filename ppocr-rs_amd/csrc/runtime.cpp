@@ -42,7 +42,7 @@ struct ppocr_hip_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   std::mutex mu;
-  float* arena = nullptr;
+  char* arena = nullptr;
   size_t arena_bytes = 0;
   uint64_t generation = 0;  // bumped whenever the arena moves
   ~ppocr_hip_ctx() {
@@ -58,6 +58,7 @@ struct ppocr_hip_model {
   ppocr::Plan plan;
   size_t in_shape[4] = {0, 0, 0, 0};
   std::shared_ptr<ppocr::DeviceBuffer> weights;
+  size_t weight_blob_bytes = 0;
   std::string weights_path;
   int size = 0;
   hipGraphExec_t graph = nullptr;
@@ -102,15 +103,14 @@ std::shared_ptr<DeviceBuffer> device_alloc(int device, size_t bytes) {
   return b;
 }
 
-// Grows the shared arena to `elems` floats (caller holds ctx->mu).
-void ensure_arena(ppocr_hip_ctx* ctx, size_t elems) {
-  size_t bytes = elems * sizeof(float);
+// Grows the shared arena to `bytes` (caller holds ctx->mu).
+void ensure_arena(ppocr_hip_ctx* ctx, size_t bytes) {
   if (bytes <= ctx->arena_bytes) return;
   HIP_OK(hipStreamSynchronize(ctx->stream));
   if (ctx->arena) HIP_OK(hipFree(ctx->arena));
   ctx->arena = nullptr;
   ctx->arena_bytes = 0;
-  HIP_OK(hipMalloc(&ctx->arena, bytes));
+  HIP_OK(hipMalloc(reinterpret_cast<void**>(&ctx->arena), bytes));
   ctx->arena_bytes = bytes;
   ++ctx->generation;
 }
@@ -118,7 +118,7 @@ void ensure_arena(ppocr_hip_ctx* ctx, size_t elems) {
 Exec exec_of(ppocr_hip_model* m) {
   Exec ex;
   ex.arena = m->ctx->arena;
-  ex.weights = static_cast<const float*>(m->weights->ptr);
+  ex.weights = static_cast<const char*>(m->weights->ptr);
   ex.bufs = &m->plan.bufs;
   return ex;
 }
@@ -162,8 +162,12 @@ void check_input(ppocr_hip_model* m, const float* nchw, size_t len) {
 }
 
 // Device pointer of the plan's NCHW staging buffer / output buffer.
-float* staging_ptr(ppocr_hip_model* m) { return m->ctx->arena + m->plan.bufs[m->plan.staging].arena_off; }
-float* output_ptr(ppocr_hip_model* m) { return m->ctx->arena + m->plan.bufs[m->plan.output].arena_off; }
+float* staging_ptr(ppocr_hip_model* m) {
+  return reinterpret_cast<float*>(m->ctx->arena + m->plan.bufs[m->plan.staging].arena_off);
+}
+float* output_ptr(ppocr_hip_model* m) {
+  return reinterpret_cast<float*>(m->ctx->arena + m->plan.bufs[m->plan.output].arena_off);
+}
 
 void upload_input(ppocr_hip_model* m, const float* nchw, size_t len) {
   HIP_OK(hipMemcpyAsync(staging_ptr(m), nchw, len * sizeof(float), hipMemcpyHostToDevice, m->ctx->stream));
@@ -187,27 +191,29 @@ ppocr_hip_model* load_model(ppocr_hip_ctx* ctx, const char* path, ppocr_model_si
   if (!path) raise(PPOCR_ERR_INVALID_INPUT, "weights path is null");
   if (!nchw) raise(PPOCR_ERR_INVALID_INPUT, "input shape is null");
   if (size < PPOCR_SIZE_MEDIUM || size > PPOCR_SIZE_TINY) raise(PPOCR_ERR_INVALID_INPUT, "unknown model size");
-  if (precision != PPOCR_F32) raise(PPOCR_ERR_INVALID_INPUT, "only F32 precision is available in this build");
+  if (precision != PPOCR_F32 && precision != PPOCR_BF16) raise(PPOCR_ERR_INVALID_INPUT, "unknown precision");
+  const int dt = precision == PPOCR_BF16 ? DT_BF16 : DT_F32;
   SafeTensors st = SafeTensors::load(path);
   auto m = std::make_unique<ppocr_hip_model>();
   m->ctx = ctx;
   m->size = size;
   m->weights_path = path;
   std::copy(nchw, nchw + 4, m->in_shape);
-  m->plan = detector ? build_detector(st, size, nchw) : build_recognizer(st, size, nchw);
+  m->plan = detector ? build_detector(st, size, nchw, dt) : build_recognizer(st, size, nchw, dt);
+  m->weight_blob_bytes = m->plan.weights.size();
   std::lock_guard<std::mutex> lock(ctx->mu);
   HIP_OK(hipSetDevice(ctx->device));
+  // The weight blob depends only on (file, tier, precision): the plan packs
+  // the same tensors in the same order whatever the input shape.
   if (share && share->weights && share->size == size && share->weights_path == m->weights_path &&
-      share->plan.weights.size() == m->plan.weights.size()) {
+      share->plan.dt == m->plan.dt && share->weight_blob_bytes == m->weight_blob_bytes) {
     m->weights = share->weights;
   } else {
-    m->weights = device_alloc(ctx->device, m->plan.weights.size() * sizeof(float));
-    HIP_OK(hipMemcpy(m->weights->ptr, m->plan.weights.data(), m->plan.weights.size() * sizeof(float),
-                     hipMemcpyHostToDevice));
+    m->weights = device_alloc(ctx->device, m->weight_blob_bytes);
+    HIP_OK(hipMemcpy(m->weights->ptr, m->plan.weights.data(), m->weight_blob_bytes, hipMemcpyHostToDevice));
   }
-  std::vector<float>().swap(m->plan.weights);
-  m->plan.weights.shrink_to_fit();
-  ensure_arena(ctx, m->plan.arena_elems);
+  std::vector<uint8_t>().swap(m->plan.weights);
+  ensure_arena(ctx, m->plan.arena_bytes);
   return m.release();
 }
 
@@ -280,7 +286,7 @@ ppocr_status ppocr_hip_forward(ppocr_hip_model* model, const float* nchw, size_t
     check_input(model, nchw, len);
     std::lock_guard<std::mutex> lock(model->ctx->mu);
     HIP_OK(hipSetDevice(model->ctx->device));
-    ensure_arena(model->ctx, model->plan.arena_elems);
+    ensure_arena(model->ctx, model->plan.arena_bytes);
     ensure_graph(model);
     upload_input(model, nchw, len);
     run_graph(model);
@@ -316,10 +322,10 @@ void ppocr_hip_image_free(ppocr_hip_image* image) { delete image; }
 namespace ppocr {
 namespace {
 
-// Runs the device preprocessing of `n` geometries into `dst` (NHWC4 when
-// nhwc, else NCHW planes).  Caller holds ctx->mu.
+// Runs the device preprocessing of `n` geometries into `dst` (fp32 NCHW
+// planes).  Caller holds ctx->mu.
 void run_preprocess(ppocr_hip_ctx* ctx, const ppocr_hip_image* image, const float* corners, const int* content_w,
-                    int n, int cw, int ch, bool detector, float* dst, bool nhwc) {
+                    int n, int cw, int ch, bool detector, float* dst) {
   static const float det_mean[3] = {0.485f, 0.456f, 0.406f}, det_std[3] = {0.229f, 0.224f, 0.225f};
   static const float rec_mean[3] = {0.5f, 0.5f, 0.5f}, rec_std[3] = {0.5f, 0.5f, 0.5f};
   const float* mean = detector ? det_mean : rec_mean;
@@ -345,7 +351,6 @@ void run_preprocess(ppocr_hip_ctx* ctx, const ppocr_hip_image* image, const floa
     p.bias[c] = -mean[c] / stdv[c];
   }
   p.out = dst;
-  p.nhwc = nhwc ? 1 : 0;
   launch_preprocess(p, ctx->stream);
   HIP_OK(hipGetLastError());
   HIP_OK(hipStreamSynchronize(ctx->stream));
@@ -383,11 +388,11 @@ ppocr_status ppocr_hip_forward_image(ppocr_hip_model* model, const ppocr_hip_ima
     std::vector<int> cw = content_widths(content_w, n, model->in_shape[3]);
     std::lock_guard<std::mutex> lock(model->ctx->mu);
     HIP_OK(hipSetDevice(model->ctx->device));
-    ensure_arena(model->ctx, model->plan.arena_elems);
+    ensure_arena(model->ctx, model->plan.arena_bytes);
     ensure_graph(model);
     // Preprocess straight into the NCHW staging buffer the graph starts from.
     run_preprocess(model->ctx, image, corners, cw.data(), (int)n, (int)model->in_shape[3], (int)model->in_shape[2],
-                   model->plan.detector, staging_ptr(model), false);
+                   model->plan.detector, staging_ptr(model));
     run_graph(model);
     read_output(model, out, out_cap);
   });
@@ -407,7 +412,7 @@ ppocr_status ppocr_hip_preprocess(ppocr_hip_ctx* ctx, const ppocr_hip_image* ima
     size_t elems = 3 * canvas_w * canvas_h;
     auto dst = device_alloc(ctx->device, elems * sizeof(float));
     run_preprocess(ctx, image, corners, cw.data(), 1, (int)canvas_w, (int)canvas_h, detector != 0,
-                   static_cast<float*>(dst->ptr), false);
+                   static_cast<float*>(dst->ptr));
     HIP_OK(hipMemcpy(out_nchw, dst->ptr, elems * sizeof(float), hipMemcpyDeviceToHost));
   });
 }
@@ -420,7 +425,7 @@ ppocr_status ppocr_hip_benchmark(ppocr_hip_model* model, const float* nchw, size
     check_input(model, nchw, len);
     std::lock_guard<std::mutex> lock(model->ctx->mu);
     HIP_OK(hipSetDevice(model->ctx->device));
-    ensure_arena(model->ctx, model->plan.arena_elems);
+    ensure_arena(model->ctx, model->plan.arena_bytes);
     ensure_graph(model);
     upload_input(model, nchw, len);
     HIP_OK(hipStreamSynchronize(model->ctx->stream));
@@ -444,7 +449,7 @@ ppocr_status ppocr_hip_benchmark_stream(ppocr_hip_model* model, const float* nch
     check_input(model, nchw, len);
     std::lock_guard<std::mutex> lock(model->ctx->mu);
     HIP_OK(hipSetDevice(model->ctx->device));
-    ensure_arena(model->ctx, model->plan.arena_elems);
+    ensure_arena(model->ctx, model->plan.arena_bytes);
     ensure_graph(model);
     upload_input(model, nchw, len);
     for (size_t i = 0; i < warmup; ++i) run_graph(model);
@@ -465,7 +470,7 @@ ppocr_status ppocr_hip_profile(ppocr_hip_model* model, const float* nchw, size_t
     check_input(model, nchw, len);
     std::lock_guard<std::mutex> lock(model->ctx->mu);
     HIP_OK(hipSetDevice(model->ctx->device));
-    ensure_arena(model->ctx, model->plan.arena_elems);
+    ensure_arena(model->ctx, model->plan.arena_bytes);
     hipStream_t s = model->ctx->stream;
     upload_input(model, nchw, len);
     const auto& ops = model->plan.ops;
@@ -510,8 +515,8 @@ ppocr_status ppocr_hip_memory_report(const ppocr_hip_model* model, size_t* arena
                                      size_t* weight_bytes) {
   return guarded([&] {
     if (!model) raise(PPOCR_ERR_INVALID_INPUT, "model is null");
-    if (arena_bytes) *arena_bytes = model->plan.arena_elems * sizeof(float);
-    if (unplanned_bytes) *unplanned_bytes = model->plan.unplanned_elems * sizeof(float);
+    if (arena_bytes) *arena_bytes = model->plan.arena_bytes;
+    if (unplanned_bytes) *unplanned_bytes = model->plan.unplanned_bytes;
     if (weight_bytes) *weight_bytes = model->weights ? model->weights->bytes : 0;
   });
 }

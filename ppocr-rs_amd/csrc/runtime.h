@@ -59,30 +59,36 @@ class SafeTensors {
 
 // ------------------------------------------------------------------ plans
 
+inline size_t dtype_size(int dt) { return dt == DT_BF16 ? 2 : 4; }
+
 // A view of an NHWC activation inside one planned buffer.  `off` is the
 // element offset of channel 0 of pixel 0 (a channel slice of a wider tensor
-// has off = first channel and ps = the wide tensor's channel count).
+// has off = first channel and ps = the wide tensor's channel count); `dt`
+// is the storage type of the buffer's elements.
 struct View {
   int buf = -1;
   size_t off = 0;
   int n = 0, h = 0, w = 0, c = 0, ps = 0;
+  int dt = DT_F32;
   size_t pixels() const { return (size_t)n * h * w; }
 };
 
 struct Buffer {
-  size_t elems = 0;
-  size_t arena_off = 0;  // elements
+  size_t bytes = 0;
+  size_t arena_off = 0;  // bytes
   int first = -1, last = -1;
   std::string name;
 };
 
 struct Exec {
-  float* arena = nullptr;
-  const float* weights = nullptr;
+  char* arena = nullptr;
+  const char* weights = nullptr;
   const std::vector<Buffer>* bufs = nullptr;
-  float* ptr(const View& v) const { return arena + (*bufs)[v.buf].arena_off + v.off; }
-  float* buf(int id) const { return arena + (*bufs)[id].arena_off; }
-  const float* w(size_t off) const { return off == SIZE_MAX ? nullptr : weights + off; }
+  void* ptr(const View& v) const { return arena + (*bufs)[v.buf].arena_off + v.off * dtype_size(v.dt); }
+  float* fptr(const View& v) const { return static_cast<float*>(ptr(v)); }
+  // Weight blob offsets are in bytes; SIZE_MAX means "absent".
+  const void* wv(size_t off) const { return off == SIZE_MAX ? nullptr : weights + off; }
+  const float* w(size_t off) const { return static_cast<const float*>(wv(off)); }
 };
 
 struct Op {
@@ -97,19 +103,21 @@ struct Op {
 struct Plan {
   std::vector<Buffer> bufs;
   std::vector<Op> ops;
-  std::vector<float> weights;  // packed host weights (uploaded once)
-  int staging = -1;            // NCHW input buffer (written by the host copy)
-  View input;                  // NHWC4 model input
-  int output = -1;             // output buffer
+  std::vector<uint8_t> weights;  // packed host weights, byte blob (uploaded once)
+  int staging = -1;              // fp32 NCHW input buffer (written by the host copy)
+  View input;                    // NHWC4 model input
+  int output = -1;               // fp32 output buffer
   size_t output_elems = 0;
   std::vector<size_t> output_shape;
-  size_t arena_elems = 0, unplanned_elems = 0;
+  size_t arena_bytes = 0, unplanned_bytes = 0;
   bool detector = true;
+  int dt = DT_F32;  // activation storage type
 };
 
-// Builds the plan of one model for a fixed input shape.
-Plan build_detector(const SafeTensors& st, int size, const size_t nchw[4]);
-Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4]);
+// Builds the plan of one model for a fixed input shape; `dt` selects fp32 or
+// bf16 activation storage.
+Plan build_detector(const SafeTensors& st, int size, const size_t nchw[4], int dt);
+Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4], int dt);
 
 // Lifetime-based offset packing of the plan's buffers into one arena
 // (the reference's ArenaAllocator::compact_layout, src/gpu/runtime.rs:414-557).

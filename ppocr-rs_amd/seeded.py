@@ -267,7 +267,7 @@ def seeded_weights(kind, size, seed=0, gain=1.0, head_gain=None):
 # fp32 rounding noise by an exploding network.
 DEFAULT_GAINS = {
     ("det", "tiny"): (1.2, None), ("det", "small"): (1.16, None), ("det", "medium"): (1.12, None),
-    ("rec", "tiny"): (1.3, 4.0), ("rec", "small"): (1.3, 1.0), ("rec", "medium"): (1.3, 0.5),
+    ("rec", "tiny"): (1.3, 4.0), ("rec", "small"): (1.22, 1.0), ("rec", "medium"): (1.3, 0.5),
 }
 
 

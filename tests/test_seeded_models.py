@@ -35,7 +35,7 @@ def test_seeded_detector_is_informative_and_conditioned(size):
 @pytest.mark.parametrize("size", ["tiny", "small", "medium"])
 def test_seeded_recognizer_is_informative_and_conditioned(size):
     m = oracle.Model("rec", model_path("rec", size), size)
-    x = seeded.seeded_batch(2, 48, 320, 104, detector=False)
+    x = seeded.seeded_batch(8, 48, 320, 31, detector=False)
     y = m.forward(x)
     assert np.abs(m.forward(perturbed(x)) - y).max() < TOL / 10
     am = y.argmax(-1)
