@@ -87,7 +87,7 @@ def roofline(stats):
         "peak": peak,
         "unit": unit,
         "frac": round(achieved / peak, 4),
-        "traffic": None,
+        "traffic": traffic_for(name),
         "kernel": name,
         "launches_per_step": g["launches"],
         "avg_launch_ms": round(g["ms"] / g["launches"], 5),
@@ -95,6 +95,46 @@ def roofline(stats):
         "bytes_per_launch": g["bytes"] / g["launches"],
         "share_of_device_time": round(g["ms"] / total_ms, 3) if total_ms else None,
     }
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "dominant_kernel_traffic.txt"
+
+
+def traffic_for(kernel):
+    """HBM bytes per launch of `kernel` from the committed counter summary.
+
+    The summary is written from two rocprofv3 --pmc runs of this benchmark
+    (FETCH_SIZE, WRITE_SIZE, KiB per dispatch), each scaled by the same
+    counter's reading for a copy kernel of known size (``--copy-calibration``).
+    Returns None when the summary covers a different kernel.
+    """
+    if not TRAFFIC_FILE.exists():
+        return None
+    fields = {}
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if ":" in line and not line.startswith("#"):
+            k, v = line.split(":", 1)
+            fields[k.strip()] = v.strip()
+    if fields.get("kernel") != kernel:
+        return None
+    try:
+        return float(fields["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def copy_calibration(mib=256, reps=5):
+    """A plain device copy of known size (y = -x over `mib` MiB of fp32),
+    run under rocprofv3 --pmc to scale FETCH_SIZE / WRITE_SIZE to bytes."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    x = torch.ones(n, device="cuda", dtype=torch.float32)
+    y = torch.empty_like(x)
+    for _ in range(reps):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration": {"bytes_read": n * 4, "bytes_written": n * 4, "launches": reps}}))
 
 
 def cpu_baseline(kind, size, shape, budget_s=12.0):
@@ -157,7 +197,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true", help="skip the other configurations")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a known-size copy kernel (for rocprofv3 counter scaling)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: the detector/recognizer path has no multi-GPU form in this build "
               "(independent images shard across GPUs without communication); run with --gpus 1.",

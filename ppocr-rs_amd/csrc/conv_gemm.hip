@@ -93,8 +93,20 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
   const int HoWo = p.Ho * p.Wo;
   const int M = p.N * HoWo;
   const int K = p.kh * p.kw * p.C;
-  const int m0 = blockIdx.x * BM;
-  const int n0 = blockIdx.y * BN;
+
+  // XCD-aware tile order.  Workgroups are dealt round-robin to the 8 XCDs,
+  // each with its own L2.  Workgroup w runs on XCD w % 8 and is given tile
+  // (w % 8) * per_xcd + w / 8 of the (M-tile, N-tile) list in M-major
+  // order, so every XCD walks a contiguous run of M tiles with all their N
+  // tiles back to back: an activation tile is fetched into one L2 once and
+  // reused by every N tile instead of being re-fetched per N tile.
+  const int n_tiles = (p.Co + BN - 1) / BN;
+  const int m_tiles = (M + BM - 1) / BM;
+  const int per_xcd = gridDim.x / 8;
+  const int t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (t >= m_tiles * n_tiles) return;
+  const int m0 = (t / n_tiles) * BM;
+  const int n0 = (t % n_tiles) * BN;
   const int kq = tid % KQ;  // this lane's k-quad in every A and B load
 
   int a_img[A_PER], a_iy0[A_PER], a_ix0[A_PER];
@@ -305,7 +317,10 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
 
 template <typename T, int BM, int BN, int WM, int WN>
 static void launch_tile(const ConvParams& p, int M, hipStream_t s) {
-  dim3 grid((M + BM - 1) / BM, (p.Co + BN - 1) / BN);
+  // One-dimensional grid rounded up to a multiple of the 8 XCDs; surplus
+  // workgroups exit before touching memory (see the tile order above).
+  long tiles = (long)((M + BM - 1) / BM) * ((p.Co + BN - 1) / BN);
+  dim3 grid((unsigned)((tiles + 7) / 8 * 8));
   hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN>), grid, dim3(256), 0, s, p);
 }
 
