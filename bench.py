@@ -49,9 +49,10 @@ def weights(kind, size):
     return path
 
 
-def load(gpu, kind, size, shape, precision="f32"):
-    cls = ppocr_hip.Detector if kind == "det" else ppocr_hip.Recognizer
-    return cls.load(gpu, weights(kind, size), size, shape, precision=precision)
+def load(gpu, kind, size, shape, precision="f32", greedy=False):
+    if kind == "det":
+        return ppocr_hip.Detector.load(gpu, weights(kind, size), size, shape, precision=precision)
+    return ppocr_hip.Recognizer.load(gpu, weights(kind, size), size, shape, precision=precision, greedy=greedy)
 
 
 def inputs(kind, shape, seed=7):
@@ -174,11 +175,17 @@ def also(gpu, warmup, steps):
         ("det", "medium", (1, 3, 416, 736), "bf16"),
         ("det", "medium", (8, 3, 416, 736), "bf16"),
         ("rec", "medium", (256, 3, 48, 320), "bf16"),
+        # Recognizers with the classifier fused with greedy CTC step decoding
+        # (per-step class + probability instead of [N, T, V] probabilities).
+        ("rec", "tiny", (64, 3, 48, 320), "f32", "greedy"),
+        ("rec", "medium", (256, 3, 48, 320), "f32", "greedy"),
+        ("rec", "medium", (256, 3, 48, 320), "bf16", "greedy"),
     ]
-    for kind, size, shape, precision in configs:
-        key = f"{size}_{kind}_{shape[0]}x{shape[2]}x{shape[3]}_{precision}"
+    for kind, size, shape, precision, *mode in configs:
+        greedy = mode == ["greedy"]
+        key = f"{size}_{kind}_{shape[0]}x{shape[2]}x{shape[3]}_{precision}" + ("_greedy" if greedy else "")
         try:
-            m = load(gpu, kind, size, shape, precision)
+            m = load(gpu, kind, size, shape, precision, greedy)
             x = inputs(kind, shape)
             ms = throughput(m, x, warmup, steps)
             m.close()

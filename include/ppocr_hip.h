@@ -76,6 +76,19 @@ ppocr_status ppocr_hip_recognizer_load(ppocr_hip_ctx* ctx, const char* safetenso
                                        const size_t nchw[4], ppocr_precision precision,
                                        const ppocr_hip_model* share_weights, ppocr_hip_model** out);
 
+/* A recognizer whose classifier is fused with the per-step half of greedy
+ * CTC decoding (`decode_ctc_greedy_for_input`, src/ocr.rs:800-853, which
+ * takes each time step's argmax class, ties to the last index, and that
+ * class's softmax probability).  Loaded like ppocr_hip_recognizer_load; its
+ * output is [N, T, 2] floats, (class index, probability) per time step, in
+ * place of the [N, T, V] probabilities, so the probability tensor is never
+ * written to HBM or copied to the host.  `share_weights` may be either form
+ * of recognizer loaded from the same file.  No counterpart in the reference,
+ * whose recognizer always returns the full probabilities (src/gpu/model.rs:222-237). */
+ppocr_status ppocr_hip_recognizer_load_greedy(ppocr_hip_ctx* ctx, const char* safetensors_path,
+                                              ppocr_model_size size, const size_t nchw[4], ppocr_precision precision,
+                                              const ppocr_hip_model* share_weights, ppocr_hip_model** out);
+
 void ppocr_hip_model_free(ppocr_hip_model* model);
 
 /* Output shape of `ModelOutput` (src/gpu/model.rs:37-41): detector
@@ -154,6 +167,40 @@ ppocr_status ppocr_hip_profile(ppocr_hip_model* model, const float* nchw, size_t
  * without reuse, and device weight bytes. */
 ppocr_status ppocr_hip_memory_report(const ppocr_hip_model* model, size_t* arena_bytes, size_t* unplanned_bytes,
                                      size_t* weight_bytes);
+
+/* ---- Host-side geometry and decoding around the device path (no GPU).
+ * Errors are PPOCR_ERR_INVALID_INPUT with the message in
+ * ppocr_hip_last_error(). */
+
+/* Detector input size for a `width` x `height` image: `DetectorInputPlan::new`
+ * (src/ocr.rs:86-101) with `default_detector_ratio` (:173-184) when
+ * `max_side` is NULL and min(max_side / max(w, h), 1) otherwise, each side
+ * then rounded by `aligned_dimension` (:186-195) to the nearest multiple of
+ * 32 (at least 32).  1920 x 1080 with max_side 736 gives 736 x 416. */
+ppocr_status ppocr_detector_input_plan(uint32_t width, uint32_t height, const uint32_t* max_side,
+                                       uint32_t* input_width, uint32_t* input_height);
+
+/* Canvas width of a recognizer batch: `recognizer_batch_width`
+ * (src/ocr.rs:206-219) over `n` quads (corners [n][4][2]): the largest
+ * content width, at least 320, rounded up to a multiple of 4. */
+ppocr_status ppocr_recognizer_batch_width(const float* corners, size_t n, size_t* width);
+
+/* Content width of one crop on a canvas of `input_width`:
+ * `recognition_input_plan` (src/ocr.rs:154-171) with
+ * `bounded_crop_dimensions` (:1145-1156) and `scaled_recognizer_width`
+ * (:197-204), i.e. ceil(48 w / h) of the bounded crop size. */
+ppocr_status ppocr_recognition_input_plan(const float corners[8], size_t input_width, size_t* content_width);
+
+/* The sequential half of `decode_ctc_greedy_for_input` (src/ocr.rs:800-853)
+ * on one item's `steps` ([T][2], as written by a greedy recognizer):
+ * collapses repeats and blanks over the first ceil(content_width T /
+ * input_width) steps and writes the emitted class indices (1..classes-1;
+ * with an implicit space class, classes - 1 is the space) to `tokens`
+ * (capacity T), their count, and the score exp(mean ln p) (0 when nothing is
+ * emitted).  `classes` must be dictionary_len + 1 or + 2. */
+ppocr_status ppocr_ctc_greedy_decode(const float* steps, size_t time_steps, size_t classes, size_t dictionary_len,
+                                     size_t content_width, size_t input_width, int32_t* tokens, size_t* n_tokens,
+                                     float* score);
 
 #ifdef __cplusplus
 }

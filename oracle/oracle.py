@@ -242,3 +242,56 @@ def fuse_intraclass(sym, sb, vert, vb, hor, hb):
                                         _f(np.ascontiguousarray(hor, np.float32)),
                                         _f(np.ascontiguousarray(hb, np.float32)), co, ci, k))
     return sym, sb
+
+
+# ------------------------------------------------------------ greedy CTC
+PROBABILITY_EPSILON = np.float32(1e-8)  # src/ocr.rs:23
+
+
+def _argmax_last(row):
+    """``argmax`` (src/ocr.rs:1171-1177): ``max_by(total_cmp)`` keeps the last
+    of equal maxima.  Rows are finite (checked by the caller), so the only
+    place ``total_cmp`` differs from ``>=`` is -0.0 against +0.0, which a
+    probability row cannot hold as its maximum."""
+    return int(row.shape[0] - 1 - np.argmax(row[::-1]))
+
+
+def _row_probability(row, value):
+    """``row_probability`` (src/ocr.rs:1158-1169): the value itself when the
+    row is already a distribution (all >= 0, sum within 0.01 of 1), else its
+    max-subtracted softmax probability.  The sum is taken in float32
+    (pairwise rather than sequential: a difference of order 1e-6 against the
+    0.01 test)."""
+    total = float(np.sum(row, dtype=np.float32))
+    if np.all(row >= 0) and abs(total - 1.0) <= 0.01:
+        return float(np.clip(np.float32(value), 0.0, 1.0))
+    m = np.float32(np.max(row))
+    den = np.sum(np.exp((row - m).astype(np.float32)), dtype=np.float32)
+    return float(np.clip(np.float32(np.exp(np.float32(value - m)) / den), 0.0, 1.0))
+
+
+def ctc_greedy_decode(values, dictionary_len, content_width, input_width):
+    """``decode_ctc_greedy_for_input`` (src/ocr.rs:800-853) on one item's
+    [T, V] rows.  Returns (emitted class indices, score); the caller maps
+    class c to dictionary[c - 1], or to a space for the implicit last class
+    when V == len(dictionary) + 2."""
+    values = np.asarray(values, dtype=np.float32)
+    t, classes = values.shape
+    if classes != dictionary_len + 1 and classes != dictionary_len + 2:
+        raise ValueError("class count does not match the dictionary")
+    if content_width == 0 or content_width > input_width:
+        raise ValueError("content width outside 1..=input width")
+    if not np.all(np.isfinite(values)):
+        raise ValueError("non-finite recognizer output")
+    valid = min(max(-(-content_width * t // input_width), 1), t)
+    tokens, log_score, previous = [], 0.0, 0
+    for step in range(valid):
+        row = values[step]
+        cls = _argmax_last(row)
+        if cls != 0 and cls != previous:
+            tokens.append(cls)
+            p = max(np.float32(_row_probability(row, row[cls])), PROBABILITY_EPSILON)
+            log_score += float(np.log(np.float64(p)))
+        previous = cls
+    score = float(np.float32(np.exp(log_score / len(tokens)))) if tokens else 0.0
+    return tokens, score

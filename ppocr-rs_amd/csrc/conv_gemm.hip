@@ -249,6 +249,49 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
         stage[(wm * TM * 16 + i * 16 + g * 4 + e) * LDE + wn * TN * 16 + j * 16 + lrow] = acc[i][j][e];
   __syncthreads();
 
+  // Greedy-CTC classifier epilogue: each row's (max logit, sum of
+  // exp(logit - max), last column holding the max) over this tile's columns.
+  // TPR consecutive lanes share a row, each scanning CPT columns in order, so
+  // ">=" keeps the last maximal column; lanes merge with xor shuffles.
+  if (p.ctc_part) {
+    constexpr int TPR = 256 / BM;
+    constexpr int CPT = BN / TPR;
+    const int row = tid / TPR, sub = tid % TPR;
+    const int c0 = sub * CPT;
+    const int nc = min(CPT, p.Co - (n0 + c0));  // valid columns of this lane
+    const float* srow = stage + row * LDE + c0;
+    const float* brow = p.bias + n0 + c0;
+    float mx = -INFINITY, sum = 0.0f;
+    int idx = -1;
+    // Two passes over the staged row (LDS reads are cheap; holding the
+    // logits in registers would cost the GEMM's occupancy).
+#pragma unroll 4
+    for (int c = 0; c < nc; ++c) {
+      const float v = srow[c] + brow[c];
+      if (v >= mx) {
+        mx = v;
+        idx = n0 + c0 + c;
+      }
+    }
+#pragma unroll 4
+    for (int c = 0; c < nc; ++c) sum += fast_exp(srow[c] + brow[c] - mx);
+#pragma unroll
+    for (int o = 1; o < TPR; o <<= 1) {
+      const float om = __shfl_xor(mx, o), os = __shfl_xor(sum, o);
+      const int oi = __shfl_xor(idx, o);
+      lse_merge(mx, sum, idx, om, os, oi);
+    }
+    const int m = m0 + row;
+    if (sub == 0 && m < M) {
+      const size_t plane = (size_t)n_tiles * M;
+      const size_t at = (size_t)(n0 / BN) * M + m;
+      p.ctc_part[at] = mx;
+      p.ctc_part[plane + at] = sum;
+      p.ctc_part[2 * plane + at] = (float)idx;
+    }
+    return;
+  }
+
   const T* res = static_cast<const T*>(p.res);
   const T* up = static_cast<const T*>(p.up);
   const bool vec_out = (p.out_ps & 3) == 0 && (p.Co & 3) == 0;
@@ -339,6 +382,11 @@ const char* conv_tile_name(int M, int cols, int dt) {
   static const char* b16[] = {"conv_gemm_bf16<256x16>", "conv_gemm_bf16<128x32>", "conv_gemm_bf16<128x64>",
                               "conv_gemm_bf16<64x64>"};
   return (dt == DT_BF16 ? b16 : f32)[pick_tile(M, cols)];
+}
+
+int conv_tile_cols(int M, int cols) {
+  static const int bn[] = {16, 32, 64, 64};
+  return bn[pick_tile(M, cols)];
 }
 
 template <typename T>

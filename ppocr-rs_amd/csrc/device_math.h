@@ -18,6 +18,18 @@ namespace ppocr {
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
+// Merges two partial softmax reductions (max m, sum of exp(x - m), last index
+// of the max) into (m, s, i).  Empty partials (s == 0, m = -inf) contribute
+// nothing; equal maxima keep the larger index.
+__device__ __forceinline__ void lse_merge(float& m, float& s, int& i, float om, float os, int oi) {
+  const float nm = fmaxf(m, om);
+  const float a = s == 0.0f ? 0.0f : s * fast_exp(m - nm);
+  const float b = os == 0.0f ? 0.0f : os * fast_exp(om - nm);
+  i = om > m ? oi : (om < m ? i : max(i, oi));
+  m = nm;
+  s = a + b;
+}
+
 __device__ __forceinline__ float erf_as(float value) {
   float sign = value < 0.0f ? -1.0f : 1.0f;
   float x = fabsf(value);

@@ -52,6 +52,11 @@ struct ConvParams {
   int rep;           // write each output pixel as a rep x rep block (upsample on write)
   int out_h, out_w;  // dims of the tensor `out` points into (Ho*rep, Wo*rep)
   int dt;            // activation type of in / res / up / out
+  // Greedy-CTC epilogue (classifier only; `out` unused, no other epilogue
+  // terms): per row m and column tile j of conv_tile_cols() columns, the
+  // tile's max logit, sum of exp(logit - max) and the last column holding the
+  // max, stored as three planes [3][n_tiles][M] of floats.
+  float* ctc_part;
 };
 
 // Depthwise k x k convolution (groups == C), 4 channels per lane.
@@ -89,6 +94,11 @@ struct SeParams {
 void launch_conv(const ConvParams& p, hipStream_t s);
 // Name of the kernel instance launch_conv picks for M rows x `cols` columns.
 const char* conv_tile_name(int M, int cols, int dt);
+// Column width of that instance's tiles.
+int conv_tile_cols(int M, int cols);
+// Merges the greedy-CTC partials of launch_conv into one (class, probability)
+// pair per row: out[m] = {argmax (ties -> last index), softmax value of it}.
+void launch_ctc_merge(const float* part, int M, int n_tiles, float* out, hipStream_t s);
 void launch_depthwise(const DwParams& p, hipStream_t s);
 // Name of the kernel instance launch_depthwise picks.
 const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho);

@@ -632,6 +632,42 @@ void launch_softmax_rows(float* x, long rows, int cols, hipStream_t s) {
   hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(1024), 0, s, x, cols);
 }
 
+// ------------------------------------------------------------ greedy CTC merge
+// Second half of the classifier's greedy-CTC epilogue.  Partials are planes
+// [3][n_tiles][M] (max, sum exp, last argmax).  A block covers 64 rows with
+// four lanes per row, each folding every fourth column tile (a wave reads 64
+// consecutive rows of one tile: coalesced); the four are merged through LDS.
+// The argmax's softmax value is exp(0) / sum = 1 / sum.
+__global__ __launch_bounds__(256) void ctc_merge_kernel(const float* part, int M, int n_tiles, float* out) {
+  __shared__ float sm[4][64], ss[4][64];
+  __shared__ int si[4][64];
+  const int r = threadIdx.x & 63, split = threadIdx.x >> 6;
+  const int m = blockIdx.x * 64 + r;
+  float mx = -INFINITY, sum = 0.0f;
+  int idx = -1;
+  if (m < M) {
+    const size_t plane = (size_t)n_tiles * M;
+    for (int j = split; j < n_tiles; j += 4) {
+      const size_t at = (size_t)j * M + m;
+      lse_merge(mx, sum, idx, part[at], part[plane + at], (int)part[2 * plane + at]);
+    }
+  }
+  sm[split][r] = mx;
+  ss[split][r] = sum;
+  si[split][r] = idx;
+  __syncthreads();
+  if (split == 0 && m < M) {
+#pragma unroll
+    for (int k = 1; k < 4; ++k) lse_merge(mx, sum, idx, sm[k][r], ss[k][r], si[k][r]);
+    out[2 * (size_t)m] = (float)idx;
+    out[2 * (size_t)m + 1] = 1.0f / sum;
+  }
+}
+
+void launch_ctc_merge(const float* part, int M, int n_tiles, float* out, hipStream_t s) {
+  hipLaunchKernelGGL(ctc_merge_kernel, dim3((unsigned)((M + 63) / 64)), dim3(256), 0, s, part, M, n_tiles, out);
+}
+
 // ----------------------------------------------------------------- preprocess
 // The reference CPU preprocessing (src/preprocess/kernels.rs:94-170): quad
 // bilinear source point, clamped; bilinear RGB rounded to an integer and

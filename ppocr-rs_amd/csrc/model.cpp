@@ -479,6 +479,62 @@ class Builder {
     add_op(std::move(op));
   }
 
+  // Classifier fused with the per-step half of greedy CTC decoding: for each
+  // time step, the argmax class (ties -> last index) and its softmax
+  // probability, the two values src/ocr.rs:800-853 takes from each row of
+  // probabilities.  The logits are reduced inside the GEMM epilogue and never
+  // stored.  Output [N, 1, T, 2] fp32: (class index, probability).
+  View greedy_classifier(const View& x, const ConvW& w, const std::string& name) {
+    if (x.c != w.ci_pad || w.kh != 1 || w.kw != 1 || x.h != 1)
+      raise(PPOCR_ERR_INVALID_MODEL, name + ": greedy classifier takes [N, 1, T, C] rows");
+    if (w.b == NOW) raise(PPOCR_ERR_INVALID_MODEL, name + ": classifier needs a bias");
+    const int M = x.n * x.w;
+    const int tiles = (w.co + conv_tile_cols(M, w.co) - 1) / conv_tile_cols(M, w.co);
+    if ((size_t)3 * tiles * M > (size_t)INT32_MAX) raise(PPOCR_ERR_INVALID_INPUT, name + ": batch too large");
+    View part = alloc(1, 1, 1, 3 * tiles * M, name + ".partials", DT_F32);
+    View out = alloc(x.n, 1, x.w, 2, "output", DT_F32);
+    ConvParams base{};
+    base.N = x.n, base.H = 1, base.W = x.w, base.C = x.c, base.in_ps = x.ps;
+    base.Ho = 1, base.Wo = x.w, base.Co = w.co, base.out_ps = 0;
+    base.ldw = w.ldw;
+    base.kh = base.kw = base.sh = base.sw = 1;
+    base.act = ACT_NONE;
+    base.up_s = 2;
+    base.rep = 1;
+    base.out_h = 1, base.out_w = x.w;
+    base.dt = x.dt;
+    const View in = x;
+    const size_t wo = w.w, bo = w.b;
+    const double es = (double)dtype_size(x.dt), part_bytes = 12.0 * tiles * M;
+    Op op;
+    op.name = name;
+    op.kernel = conv_tile_name(M, w.co, x.dt);
+    op.bound = 1;
+    op.flops = 2.0 * M * w.co * w.ci;
+    op.bytes = es * ((double)M * w.ci + (double)w.ci * w.co) + 4.0 * w.co + part_bytes;
+    op.reads = {x.buf};
+    op.writes = {part.buf};
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      ConvParams p = base;
+      p.in = ex.ptr(in);
+      p.out = nullptr;
+      p.wt = ex.wv(wo);
+      p.bias = ex.w(bo);
+      p.ctc_part = ex.fptr(part);
+      launch_conv(p, s);
+    };
+    add_op(std::move(op));
+    Op merge;
+    merge.name = name + ".ctc_merge";
+    merge.kernel = "ctc_merge";
+    merge.bytes = part_bytes + 8.0 * M;
+    merge.reads = {part.buf};
+    merge.writes = {out.buf};
+    merge.launch = [=](const Exec& ex, hipStream_t s) { launch_ctc_merge(ex.fptr(part), M, tiles, ex.fptr(out), s); };
+    add_op(std::move(merge));
+    return out;
+  }
+
   // fp32 NCHW staging buffer -> NHWC with 4 channels in the activation type.
   View input(const size_t nchw[4]) {
     int n = (int)nchw[0], h = (int)nchw[2], w = (int)nchw[3];
@@ -895,7 +951,7 @@ Plan build_detector(const SafeTensors& st, int size, const size_t nchw[4], int d
 
 // Recognizer::load (src/gpu/model.rs:156-220; architecture
 // src/cpu/model.rs:1961-2039).
-Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4], int dt) {
+Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4], int dt, bool greedy) {
   validate_recognizer_shape(nchw);
   const size_t expected = size == PPOCR_SIZE_MEDIUM ? 269 : size == PPOCR_SIZE_SMALL ? 250 : 150;
   const char* tier = size == PPOCR_SIZE_MEDIUM ? "medium" : size == PPOCR_SIZE_SMALL ? "small" : "tiny";
@@ -913,12 +969,9 @@ Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4], int
   View pooled = B.avgpool32(stages.back(), "pool");
   if (pooled.h != 1) raise(PPOCR_ERR_INVALID_MODEL, "recognizer pooling must produce height 1");
   const int classes = tiny ? 6906 : 18710;
-  View logits_dst = B.alloc(pooled.n, 1, pooled.w, classes, "output", DT_F32);
-  plan.output = logits_dst.buf;
-  plan.output_elems = logits_dst.pixels() * classes;
-  plan.output_shape = {(size_t)pooled.n, (size_t)pooled.w, (size_t)classes};
-  Epi into;
-  into.dst = &logits_dst;
+  View feat;  // classifier input [N, 1, T, C]
+  ConvW cls;
+  std::string cls_name;
   if (tiny) {
     // TinyRecognizerHead (src/cpu/model.rs:1913-1936) with Conv1dBn (:1877-1911).
     std::vector<float> w1 = B.get("head.conv1.weight", {160, 1, 5}).v, b1;
@@ -931,8 +984,9 @@ Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4], int
     Epi hs;
     hs.act = ACT_HSWISH;
     h = B.conv(h, c2, hs, "head.conv2");
-    h = B.conv(h, B.linear_w("head.fc1", 160, 80), Epi{}, "head.fc1");
-    B.conv(h, B.linear_w("head.fc2", 80, classes), into, "head.fc2");
+    feat = B.conv(h, B.linear_w("head.fc1", 160, 80), Epi{}, "head.fc1");
+    cls = B.linear_w("head.fc2", 80, classes);
+    cls_name = "head.fc2";
   } else {
     // LightSvtrRecognizerHead / RecEncoder (src/cpu/model.rs:1686-1875).
     int ci = size == PPOCR_SIZE_MEDIUM ? 768 : 384;
@@ -961,10 +1015,26 @@ Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4], int
       r2.res = &h1;
       h = B.conv(m, B.linear_w(p + ".mlp.fc2", mlp, hid), r2, p + ".mlp.fc2");
     }
-    View y = B.layer_norm(h, e + ".norm", &skip, e + ".norm");
-    B.conv(y, B.linear_w("head.head", hid, classes), into, "head.head");
+    feat = B.layer_norm(h, e + ".norm", &skip, e + ".norm");
+    cls = B.linear_w("head.head", hid, classes);
+    cls_name = "head.head";
   }
-  B.softmax(logits_dst, "softmax");
+  const size_t n = (size_t)pooled.n, steps = (size_t)pooled.w;
+  if (greedy) {
+    View out = B.greedy_classifier(feat, cls, cls_name);
+    plan.output = out.buf;
+    plan.output_elems = n * steps * 2;
+    plan.output_shape = {n, steps, 2};
+  } else {
+    View logits = B.alloc(pooled.n, 1, pooled.w, classes, "output", DT_F32);
+    plan.output = logits.buf;
+    plan.output_elems = n * steps * classes;
+    plan.output_shape = {n, steps, (size_t)classes};
+    Epi into;
+    into.dst = &logits;
+    B.conv(feat, cls, into, cls_name);
+    B.softmax(logits, "softmax");
+  }
   plan_arena(plan);
   return plan;
 }

@@ -13,9 +13,13 @@
 #include "runtime.h"
 
 namespace ppocr {
-namespace {
 
-thread_local std::string g_last_error;
+std::string& last_error() {
+  static thread_local std::string message;
+  return message;
+}
+
+namespace {
 
 struct DeviceBuffer {
   void* ptr = nullptr;
@@ -76,24 +80,6 @@ struct ppocr_hip_image {
 
 namespace ppocr {
 namespace {
-
-template <typename F>
-ppocr_status guarded(F&& f) {
-  try {
-    f();
-    g_last_error.clear();
-    return PPOCR_OK;
-  } catch (const Error& e) {
-    g_last_error = e.what();
-    return e.code;
-  } catch (const std::bad_alloc&) {
-    g_last_error = "host allocation failed";
-    return PPOCR_ERR_GPU;
-  } catch (const std::exception& e) {
-    g_last_error = e.what();
-    return PPOCR_ERR_GPU;
-  }
-}
 
 std::shared_ptr<DeviceBuffer> device_alloc(int device, size_t bytes) {
   auto b = std::make_shared<DeviceBuffer>();
@@ -186,7 +172,8 @@ void read_output(ppocr_hip_model* m, float* out, size_t cap) {
 }
 
 ppocr_hip_model* load_model(ppocr_hip_ctx* ctx, const char* path, ppocr_model_size size, const size_t nchw[4],
-                            ppocr_precision precision, const ppocr_hip_model* share, bool detector) {
+                            ppocr_precision precision, const ppocr_hip_model* share, bool detector,
+                            bool greedy = false) {
   if (!ctx) raise(PPOCR_ERR_INVALID_INPUT, "context is null");
   if (!path) raise(PPOCR_ERR_INVALID_INPUT, "weights path is null");
   if (!nchw) raise(PPOCR_ERR_INVALID_INPUT, "input shape is null");
@@ -199,7 +186,7 @@ ppocr_hip_model* load_model(ppocr_hip_ctx* ctx, const char* path, ppocr_model_si
   m->size = size;
   m->weights_path = path;
   std::copy(nchw, nchw + 4, m->in_shape);
-  m->plan = detector ? build_detector(st, size, nchw, dt) : build_recognizer(st, size, nchw, dt);
+  m->plan = detector ? build_detector(st, size, nchw, dt) : build_recognizer(st, size, nchw, dt, greedy);
   m->weight_blob_bytes = m->plan.weights.size();
   std::lock_guard<std::mutex> lock(ctx->mu);
   HIP_OK(hipSetDevice(ctx->device));
@@ -224,7 +211,7 @@ using namespace ppocr;
 
 extern "C" {
 
-const char* ppocr_hip_last_error(void) { return g_last_error.c_str(); }
+const char* ppocr_hip_last_error(void) { return last_error().c_str(); }
 
 ppocr_status ppocr_hip_create(int device, ppocr_hip_ctx** out) {
   return guarded([&] {
@@ -262,6 +249,18 @@ ppocr_status ppocr_hip_recognizer_load(ppocr_hip_ctx* ctx, const char* path, ppo
     if (share_weights && share_weights->plan.detector)
       raise(PPOCR_ERR_INVALID_INPUT, "shared weights must come from a recognizer");
     *out = load_model(ctx, path, size, nchw, precision, share_weights, false);
+  });
+}
+
+ppocr_status ppocr_hip_recognizer_load_greedy(ppocr_hip_ctx* ctx, const char* path, ppocr_model_size size,
+                                              const size_t nchw[4], ppocr_precision precision,
+                                              const ppocr_hip_model* share_weights, ppocr_hip_model** out) {
+  return guarded([&] {
+    if (!out) raise(PPOCR_ERR_INVALID_INPUT, "output handle pointer is null");
+    *out = nullptr;
+    if (share_weights && share_weights->plan.detector)
+      raise(PPOCR_ERR_INVALID_INPUT, "shared weights must come from a recognizer");
+    *out = load_model(ctx, path, size, nchw, precision, share_weights, false, true);
   });
 }
 

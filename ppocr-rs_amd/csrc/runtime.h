@@ -26,6 +26,29 @@ struct Error : std::runtime_error {
 
 [[noreturn]] inline void raise(ppocr_status code, const std::string& msg) { throw Error(code, msg); }
 
+// Thread-local message of the last failed C-ABI call (ppocr_hip_last_error).
+std::string& last_error();
+
+// Runs `f` as the body of a C-ABI entry point: no exception crosses the ABI;
+// errors become their status code and the thread's last-error message.
+template <typename F>
+ppocr_status guarded(F&& f) {
+  try {
+    f();
+    last_error().clear();
+    return PPOCR_OK;
+  } catch (const Error& e) {
+    last_error() = e.what();
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    last_error() = "host allocation failed";
+    return PPOCR_ERR_GPU;
+  } catch (const std::exception& e) {
+    last_error() = e.what();
+    return PPOCR_ERR_GPU;
+  }
+}
+
 #define HIP_OK(expr)                                                                                 \
   do {                                                                                               \
     hipError_t e_ = (expr);                                                                          \
@@ -115,9 +138,12 @@ struct Plan {
 };
 
 // Builds the plan of one model for a fixed input shape; `dt` selects fp32 or
-// bf16 activation storage.
+// bf16 activation storage.  A `greedy` recognizer ends in the classifier
+// fused with per-step greedy CTC decoding (output [N, T, 2]: class index,
+// probability) instead of the softmax probabilities [N, T, V].  Both forms
+// pack the same weight blob.
 Plan build_detector(const SafeTensors& st, int size, const size_t nchw[4], int dt);
-Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4], int dt);
+Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4], int dt, bool greedy);
 
 // Lifetime-based offset packing of the plan's buffers into one arena
 // (the reference's ArenaAllocator::compact_layout, src/gpu/runtime.rs:414-557).

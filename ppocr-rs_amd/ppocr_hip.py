@@ -37,6 +37,8 @@ EXPORTS = (
     "ppocr_hip_recognizer_load", "ppocr_hip_model_free", "ppocr_hip_output_shape", "ppocr_hip_forward",
     "ppocr_hip_upload_rgb", "ppocr_hip_image_free", "ppocr_hip_forward_image", "ppocr_hip_preprocess",
     "ppocr_hip_benchmark", "ppocr_hip_benchmark_stream", "ppocr_hip_profile", "ppocr_hip_memory_report",
+    "ppocr_hip_recognizer_load_greedy", "ppocr_detector_input_plan", "ppocr_recognizer_batch_width",
+    "ppocr_recognition_input_plan", "ppocr_ctc_greedy_decode",
 )
 
 
@@ -89,6 +91,14 @@ def lib():
         L.ppocr_hip_profile.argtypes = [_VP, _F, ctypes.c_size_t, ctypes.c_size_t, ctypes.POINTER(KernelStat),
                                         ctypes.c_size_t, _SZ]
         L.ppocr_hip_memory_report.argtypes = [_VP, _SZ, _SZ, _SZ]
+        L.ppocr_hip_recognizer_load_greedy.argtypes = L.ppocr_hip_recognizer_load.argtypes
+        _U32 = ctypes.POINTER(ctypes.c_uint32)
+        L.ppocr_detector_input_plan.argtypes = [ctypes.c_uint32, ctypes.c_uint32, _U32, _U32, _U32]
+        L.ppocr_recognizer_batch_width.argtypes = [_F, ctypes.c_size_t, _SZ]
+        L.ppocr_recognition_input_plan.argtypes = [_F, ctypes.c_size_t, _SZ]
+        L.ppocr_ctc_greedy_decode.argtypes = [_F, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
+                                              ctypes.c_size_t, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int32),
+                                              _SZ, _F]
         _lib = L
     return _lib
 
@@ -256,10 +266,62 @@ class Recognizer(_Model):
     """``gpu::Recognizer`` (src/gpu/model.rs:150-266)."""
 
     @classmethod
-    def load(cls, gpu, path, size, input_shape, precision="f32", share_weights=None):
+    def load(cls, gpu, path, size, input_shape, precision="f32", share_weights=None, greedy=False):
+        """``Recognizer::load`` / ``load_with_shared_weights``.  With ``greedy``
+        the classifier is fused with per-step greedy CTC decoding and the
+        output is [N, T, 2] (class index, probability) per time step."""
         h = _VP()
-        _check(lib().ppocr_hip_recognizer_load(gpu.handle, str(path).encode(), SIZE_CODE[size], _sizes(input_shape),
-                                               PRECISION[precision],
-                                               share_weights.handle if share_weights is not None else None,
-                                               ctypes.byref(h)))
+        entry = lib().ppocr_hip_recognizer_load_greedy if greedy else lib().ppocr_hip_recognizer_load
+        _check(entry(gpu.handle, str(path).encode(), SIZE_CODE[size], _sizes(input_shape), PRECISION[precision],
+                     share_weights.handle if share_weights is not None else None, ctypes.byref(h)))
         return cls(gpu, h, input_shape)
+
+
+# ------------------------------------------------------------ host geometry
+
+def detector_input_plan(width, height, max_side=736):
+    """``DetectorInputPlan::new`` (src/ocr.rs:86-101): (input_width, input_height)
+    for an image; ``max_side=None`` applies ``default_detector_ratio``."""
+    w, h = ctypes.c_uint32(), ctypes.c_uint32()
+    ms = None if max_side is None else ctypes.byref(ctypes.c_uint32(int(max_side)))
+    _check(lib().ppocr_detector_input_plan(int(width), int(height), ms, ctypes.byref(w), ctypes.byref(h)))
+    return w.value, h.value
+
+
+def recognizer_batch_width(polygons):
+    """``recognizer_batch_width`` (src/ocr.rs:206-219) over quads [n, 4, 2]."""
+    c, cp = _f32(np.asarray(polygons, dtype=np.float32).reshape(-1, 8))
+    out = ctypes.c_size_t()
+    _check(lib().ppocr_recognizer_batch_width(cp, c.shape[0], ctypes.byref(out)))
+    return out.value
+
+
+def recognition_input_plan(polygon, input_width):
+    """``recognition_input_plan`` (src/ocr.rs:154-171): the crop's content width."""
+    c, cp = _f32(np.asarray(polygon, dtype=np.float32).reshape(8))
+    out = ctypes.c_size_t()
+    _check(lib().ppocr_recognition_input_plan(cp, int(input_width), ctypes.byref(out)))
+    return out.value
+
+
+@dataclass
+class DecodedText:
+    """``DecodedText`` (src/ocr.rs:268-272)."""
+
+    text: str
+    score: float
+
+
+def ctc_greedy_decode(steps, dictionary, classes, content_width, input_width):
+    """``decode_ctc_greedy_for_input`` (src/ocr.rs:800-853) for one item of a
+    greedy recognizer's output ([T, 2]: class index, probability)."""
+    s, sp = _f32(np.asarray(steps, dtype=np.float32).reshape(-1, 2))
+    t = s.shape[0]
+    tokens = (ctypes.c_int32 * max(t, 1))()
+    n = ctypes.c_size_t()
+    score = ctypes.c_float()
+    _check(lib().ppocr_ctc_greedy_decode(sp, t, int(classes), len(dictionary), int(content_width), int(input_width),
+                                         tokens, ctypes.byref(n), ctypes.byref(score)))
+    space = classes == len(dictionary) + 2
+    text = "".join(" " if space and tokens[i] == classes - 1 else dictionary[tokens[i] - 1] for i in range(n.value))
+    return DecodedText(text, score.value)

@@ -8,6 +8,7 @@ import tempfile
 
 import numpy as np
 
+import oracle
 import seeded
 
 _CACHE = pathlib.Path(tempfile.gettempdir()) / "ppocr_hip_test_models"
@@ -47,23 +48,12 @@ def argmax_last(rows):
 
 
 def ctc_greedy(probs, dictionary, content_width, input_width):
-    """``decode_ctc_greedy_for_input`` (src/ocr.rs:800-853) for one [T, V] item."""
-    t, classes = probs.shape
-    implicit_space = classes == len(dictionary) + 2
-    valid = min(max(-(-content_width * t // input_width), 1), t)
-    text = []
-    previous = 0
-    log_score = 0.0
-    emitted = 0
-    for step in range(valid):
-        row = probs[step]
-        cls = int(argmax_last(row))
-        if cls != 0 and cls != previous:
-            text.append(" " if implicit_space and cls == classes - 1 else dictionary[cls - 1])
-            log_score += float(np.log(max(float(row[cls]), 1e-8)))
-            emitted += 1
-        previous = cls
-    return "".join(text), (float(np.exp(log_score / emitted)) if emitted else 0.0)
+    """The oracle's ``decode_ctc_greedy_for_input`` (src/ocr.rs:800-853) for one
+    [T, V] item, with the tokens mapped through `dictionary`."""
+    classes = probs.shape[1]
+    tokens, score = oracle.ctc_greedy_decode(probs, len(dictionary), content_width, input_width)
+    space = classes == len(dictionary) + 2
+    return "".join(" " if space and c == classes - 1 else dictionary[c - 1] for c in tokens), score
 
 
 def synthetic_dictionary(classes):

@@ -14,7 +14,7 @@ ROOT = pathlib.Path(__file__).resolve().parents[1]
 
 def declared_symbols():
     text = (ROOT / "include" / "ppocr_hip.h").read_text()
-    return sorted(set(re.findall(r"\b(ppocr_hip_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(ppocr_\w+)\s*\(", text)))
 
 
 def test_header_and_binding_agree():

@@ -255,3 +255,90 @@ def test_benchmark_and_profile_report(gpu):
         check_detector(det.forward(x).array(), oracle_model("det", "tiny").forward(x))
     finally:
         det.close()
+
+
+# Greedy recognizer: the classifier fused with per-step greedy CTC decoding
+# (src/ocr.rs:800-853).  Bars: the step class equals the oracle's argmax
+# (ties -> last) wherever the oracle's top-2 probability gap exceeds 1e-4,
+# the step probability is within 1e-3 of the oracle's, and the decoded
+# strings are identical.
+def check_greedy(steps, expected, width, content_widths=None):
+    n, t, v = expected.shape
+    assert steps.shape == (n, t, 2)
+    cls = steps[..., 0]
+    assert np.all(cls == np.round(cls)) and cls.min() >= 0 and cls.max() < v
+    srt = np.sort(expected, axis=-1)
+    clear = (srt[..., -1] - srt[..., -2]) > 1e-4
+    am = argmax_last(expected)
+    assert np.all(cls.astype(np.int64)[clear] == am[clear])
+    err = float(np.max(np.abs(steps[..., 1] - srt[..., -1])))
+    assert err <= REC_TOL, f"probability max abs diff {err}"
+    dictionary = synthetic_dictionary(v)
+    for i in range(n):
+        cw = width if content_widths is None else content_widths[i]
+        got = ppocr_hip.ctc_greedy_decode(steps[i], dictionary, v, cw, width)
+        want_text, want_score = ctc_greedy(expected[i], dictionary, cw, width)
+        assert got.text == want_text
+        assert abs(got.score - want_score) <= 1e-3
+    return err
+
+
+@pytest.mark.parametrize("size,batch,width", [
+    ("tiny", 4, 320),
+    ("tiny", 3, 100),
+    ("small", 4, 320),
+    ("medium", 4, 320),
+    ("medium", 64, 320),
+])
+def test_greedy_recognizer_matches_oracle(gpu, size, batch, width):
+    x = seeded.seeded_batch(batch, 48, width, 200 + batch, detector=False)
+    shape = (batch, 3, 48, width)
+    rec = ppocr_hip.Recognizer.load(gpu, model_path("rec", size), size, shape, greedy=True)
+    try:
+        steps = rec.forward(x).array()
+    finally:
+        rec.close()
+    expected = oracle_model("rec", size).forward(x)
+    err = check_greedy(steps, expected, width)
+    print(f"greedy rec {size} {shape}: prob max abs {err:.2e}")
+
+
+def test_greedy_recognizer_agrees_with_probability_output(gpu):
+    # Same device arithmetic up to the classifier: the fused reduction must
+    # reproduce the argmax and probability of the stored softmax rows.
+    for precision in ("f32", "bf16"):
+        shape = (16, 3, 48, 320)
+        x = seeded.seeded_batch(16, 48, 320, 41, detector=False)
+        path = model_path("rec", "medium")
+        probs_model = ppocr_hip.Recognizer.load(gpu, path, "medium", shape, precision=precision)
+        greedy = ppocr_hip.Recognizer.load(gpu, path, "medium", shape, precision=precision,
+                                           share_weights=probs_model, greedy=True)
+        try:
+            probs = probs_model.forward(x).array()
+            steps = greedy.forward(x).array()
+            assert greedy.memory_report()["weight_bytes"] == probs_model.memory_report()["weight_bytes"]
+        finally:
+            greedy.close()
+            probs_model.close()
+        srt = np.sort(probs, axis=-1)
+        clear = (srt[..., -1] - srt[..., -2]) > 1e-5
+        assert np.all(steps[..., 0].astype(np.int64)[clear] == argmax_last(probs)[clear]), precision
+        assert np.max(np.abs(steps[..., 1] - srt[..., -1])) <= 1e-5, precision
+
+
+def test_greedy_recognizer_forward_image(gpu):
+    img = seeded.seeded_rgb(300, 500, 35, pattern="blocks")
+    quads = np.stack([quad_corners(10, 20, 210, 60), quad_corners(100, 100, 180, 120),
+                      np.array([[300, 200], [480, 210], [478, 250], [298, 240]], np.float32)])
+    width = ppocr_hip.recognizer_batch_width(quads)
+    widths = [ppocr_hip.recognition_input_plan(q, width) for q in quads]
+    n = len(quads)
+    rec = ppocr_hip.Recognizer.load(gpu, model_path("rec", "tiny"), "tiny", (n, 3, 48, width), greedy=True)
+    image = gpu.upload_rgb(img)
+    try:
+        steps = rec.forward_image(image, quads, widths).array()
+    finally:
+        image.close()
+        rec.close()
+    x = np.stack([oracle.preprocess(img, q, width, 48, cw, False) for q, cw in zip(quads, widths)])
+    check_greedy(steps, oracle_model("rec", "tiny").forward(x), width, widths)
