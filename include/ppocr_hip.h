@@ -168,6 +168,62 @@ ppocr_status ppocr_hip_profile(ppocr_hip_model* model, const float* nchw, size_t
 ppocr_status ppocr_hip_memory_report(const ppocr_hip_model* model, size_t* arena_bytes, size_t* unplanned_bytes,
                                      size_t* weight_bytes);
 
+/* ---- DB detector postprocess on the device. */
+
+/* `DetectorPostprocessOptions` (src/ocr.rs:231-269); defaults 0.2, 0.4, 3,
+ * 1.4, 1000 (ppocr_db_default_options).  Thresholds must lie in [0, 1],
+ * min_area and max_boxes be at least 1, unclip_ratio be finite and > 0. */
+typedef struct ppocr_db_options {
+  float binary_threshold;
+  float box_threshold;
+  size_t min_area;
+  float unclip_ratio;
+  size_t max_boxes;
+} ppocr_db_options;
+
+/* `DetectorTransform` (src/ocr.rs:32-74): the source image size and the
+ * content size it was resized to inside the detector canvas.  All non-zero. */
+typedef struct ppocr_detector_transform {
+  uint32_t source_width, source_height, content_width, content_height;
+} ppocr_detector_transform;
+
+/* `Detection` (src/ocr.rs:225-229): four (x, y) corners in source pixels,
+ * and the mean probability of the component. */
+typedef struct ppocr_detection {
+  float polygon[8];
+  float score;
+} ppocr_detection;
+
+void ppocr_db_default_options(ppocr_db_options* options);
+
+/* `extract_detections` (src/ocr.rs:723-790) over `n` host probability maps
+ * [n][height][width], computed on the device: pixels >= binary_threshold
+ * inside each content rectangle, 8-connected components with at least
+ * min_area pixels and mean probability >= box_threshold, the rotated box of
+ * each (principal axis, extents, unclip), mapped to source coordinates,
+ * sorted by centre y, x, score (`sort_detections`, :1120-1131) and cut to
+ * max_boxes by score.  `counts[i]` receives image i's detection count and
+ * `total` their sum; up to `cap` detections are written to `out`, image by
+ * image.  `options` NULL means the defaults. */
+ppocr_status ppocr_hip_db_postprocess(ppocr_hip_ctx* ctx, const float* prob, size_t n, size_t height, size_t width,
+                                      const ppocr_detector_transform* transforms, const ppocr_db_options* options,
+                                      ppocr_detection* out, size_t cap, size_t* counts, size_t* total);
+
+/* Detector forward followed by the device postprocess on its output, which
+ * never leaves the device: `GpuOcrRuntime::run_detector` +
+ * `extract_detections` (src/ocr.rs:608-646, :723-790).  One transform per
+ * image of the planned batch; outputs as ppocr_hip_db_postprocess. */
+ppocr_status ppocr_hip_detect(ppocr_hip_model* detector, const float* nchw, size_t len,
+                              const ppocr_detector_transform* transforms, const ppocr_db_options* options,
+                              ppocr_detection* out, size_t cap, size_t* counts, size_t* total);
+
+/* As ppocr_hip_detect, with the input rectified from a device image (one
+ * quad per image of the batch, as ppocr_hip_forward_image). */
+ppocr_status ppocr_hip_detect_image(ppocr_hip_model* detector, const ppocr_hip_image* image, const float* corners,
+                                    size_t n, const ppocr_detector_transform* transforms,
+                                    const ppocr_db_options* options, ppocr_detection* out, size_t cap,
+                                    size_t* counts, size_t* total);
+
 /* ---- Host-side geometry and decoding around the device path (no GPU).
  * Errors are PPOCR_ERR_INVALID_INPUT with the message in
  * ppocr_hip_last_error(). */

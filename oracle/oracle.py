@@ -295,3 +295,34 @@ def ctc_greedy_decode(values, dictionary_len, content_width, input_width):
         previous = cls
     score = float(np.float32(np.exp(log_score / len(tokens)))) if tokens else 0.0
     return tokens, score
+
+
+# ------------------------------------------------------------ DB postprocess
+DB_DEFAULTS = dict(binary_threshold=0.2, box_threshold=0.4, min_area=3, unclip_ratio=1.4, max_boxes=1000)
+
+
+def extract_detections(values, transform, binary_threshold=0.2, box_threshold=0.4, min_area=3, unclip_ratio=1.4,
+                       max_boxes=1000):
+    """``extract_detections`` (src/ocr.rs:723-790) on one [H, W] probability map.
+
+    ``transform`` = (source_width, source_height, content_width,
+    content_height) of ``DetectorTransform`` (src/ocr.rs:32-74).  Returns
+    (polygons [n, 4, 2], scores [n], anisotropy [n]); anisotropy is a
+    diagnostic of how well the component's principal axis is determined.
+    """
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    h, w = v.shape
+    tr = (ctypes.c_uint32 * 4)(*[int(t) for t in transform])
+    count = ctypes.c_size_t()
+    L = lib()
+    fn = L.oracle_extract_detections
+    fn.argtypes = [_F, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_uint32), ctypes.c_float, ctypes.c_float,
+                   ctypes.c_size_t, ctypes.c_float, ctypes.c_size_t, _F, ctypes.c_size_t,
+                   ctypes.POINTER(ctypes.c_size_t)]
+    args = (v.ctypes.data_as(_F), h, w, tr, binary_threshold, box_threshold, min_area, unclip_ratio, max_boxes)
+    if fn(*args, None, 0, ctypes.byref(count)) != 0:
+        raise ValueError("invalid postprocess arguments or non-finite map")
+    out = np.zeros((max(count.value, 1), 10), dtype=np.float32)
+    fn(*args, out.ctypes.data_as(_F), out.shape[0], ctypes.byref(count))
+    out = out[:count.value]
+    return out[:, :8].reshape(-1, 4, 2), out[:, 8].copy(), out[:, 9].copy()

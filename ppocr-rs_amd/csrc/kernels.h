@@ -135,6 +135,35 @@ void launch_attention(const void* qkv, int B, int T, int hidden, int heads, void
 // In-place fp32 row softmax over `cols` columns.
 void launch_softmax_rows(float* x, long rows, int cols, hipStream_t s);
 
+// DB postprocess over N probability maps [N][H][W] (pixel index
+// n*H*W + y*W + x < 2^31).  Work arrays: label/slot per pixel; per
+// component slot (at most max_comp): count, root, keep, moments [6] (fp64),
+// geom [8], extent [4]; out [max_comp][12] = polygon (8), score, image and
+// root pixel (int bits), pad.  counters[0] = components, counters[1] =
+// detections written.
+struct DbParams {
+  const float* prob;
+  int N, H, W;
+  long total;
+  const int* content;        // [N][2] region examined: min(content, map) width, height
+  const int* source;         // [N][2] source image width, height
+  const int* content_scale;  // [N][2] content width, height of the transform
+  float threshold, box_threshold, unclip;
+  int min_area;
+  int max_comp;
+  int* label;
+  int* slot;
+  int* counters;
+  int* count;
+  int* root;
+  int* keep;
+  double* moments;
+  float* geom;
+  int* extent;
+  float* out;
+};
+void launch_db_postprocess(const DbParams& p, hipStream_t s);
+
 // Quad-bilinear RGB8 sampling -> rounded -> normalised NCHW fp32 planes.  One
 // geometry per image: corners [N][8], content widths [N].
 struct PreParams {

@@ -67,6 +67,7 @@ struct ppocr_hip_model {
   int size = 0;
   hipGraphExec_t graph = nullptr;
   uint64_t graph_generation = UINT64_MAX;
+  std::shared_ptr<ppocr::DeviceBuffer> db_work;  // postprocess work arrays, grown on demand
   ~ppocr_hip_model() {
     if (graph) (void)hipGraphExecDestroy(graph);
   }
@@ -517,6 +518,259 @@ ppocr_status ppocr_hip_memory_report(const ppocr_hip_model* model, size_t* arena
     if (arena_bytes) *arena_bytes = model->plan.arena_bytes;
     if (unplanned_bytes) *unplanned_bytes = model->plan.unplanned_bytes;
     if (weight_bytes) *weight_bytes = model->weights ? model->weights->bytes : 0;
+  });
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------ DB postprocess
+namespace ppocr {
+namespace {
+
+struct HostDetection {
+  ppocr_detection det;
+  int image;
+  int root;
+};
+
+ppocr_db_options db_options(const ppocr_db_options* o) {
+  ppocr_db_options v;
+  ppocr_db_default_options(&v);
+  if (o) v = *o;
+  // DetectorPostprocessOptions::validate (src/ocr.rs:250-268).
+  auto prob = [](float x) { return std::isfinite(x) && x >= 0.0f && x <= 1.0f; };
+  if (!prob(v.binary_threshold)) raise(PPOCR_ERR_INVALID_INPUT, "detector binary threshold must be a finite value between zero and one");
+  if (!prob(v.box_threshold)) raise(PPOCR_ERR_INVALID_INPUT, "detector box threshold must be a finite value between zero and one");
+  if (v.min_area == 0) raise(PPOCR_ERR_INVALID_INPUT, "detector minimum area must be at least one pixel");
+  if (v.max_boxes == 0) raise(PPOCR_ERR_INVALID_INPUT, "detector maximum box count must be at least one");
+  if (!std::isfinite(v.unclip_ratio) || v.unclip_ratio <= 0.0f)
+    raise(PPOCR_ERR_INVALID_INPUT, "detector unclip ratio must be a finite value greater than zero");
+  return v;
+}
+
+// polygon_center (src/ocr.rs:1133-1138) in f32.
+void polygon_center(const ppocr_detection& d, float* cx, float* cy) {
+  float sx = 0.0f, sy = 0.0f;
+  for (int k = 0; k < 4; ++k) sx += d.polygon[2 * k];
+  for (int k = 0; k < 4; ++k) sy += d.polygon[2 * k + 1];
+  *cx = sx / 4.0f;
+  *cy = sy / 4.0f;
+}
+
+// f32::total_cmp for finite values.
+int total_cmp(float a, float b) {
+  if (a < b) return -1;
+  if (a > b) return 1;
+  return (int)std::signbit(b) - (int)std::signbit(a);
+}
+
+// sort_detections (src/ocr.rs:1120-1131): centre y, centre x, score; the
+// reference's stable sort keeps raster order (root pixel) among equals.
+bool detection_before(const HostDetection& l, const HostDetection& r) {
+  float lx, ly, rx, ry;
+  polygon_center(l.det, &lx, &ly);
+  polygon_center(r.det, &rx, &ry);
+  if (int c = total_cmp(ly, ry)) return c < 0;
+  if (int c = total_cmp(lx, rx)) return c < 0;
+  if (int c = total_cmp(l.det.score, r.det.score)) return c < 0;
+  return l.root < r.root;
+}
+
+// Runs the device postprocess over N maps already in device memory and
+// returns the per-image sorted, truncated detections.  Caller holds ctx->mu.
+std::vector<std::vector<HostDetection>> run_db(ppocr_hip_ctx* ctx, const float* prob, int N, int H, int W,
+                                               const ppocr_detector_transform* tr, const ppocr_db_options& o,
+                                               std::shared_ptr<DeviceBuffer>& work) {
+  if (!tr) raise(PPOCR_ERR_INVALID_INPUT, "transforms pointer is null");
+  const long total = (long)N * H * W;
+  if (total >= (long)INT32_MAX) raise(PPOCR_ERR_INVALID_INPUT, "probability maps too large for the postprocess");
+  std::vector<int> tables(6 * (size_t)N);
+  for (int n = 0; n < N; ++n) {
+    const ppocr_detector_transform& t = tr[n];
+    if (!t.source_width || !t.source_height || !t.content_width || !t.content_height)
+      raise(PPOCR_ERR_INVALID_INPUT, "detector transform dimensions must be non-zero");
+    tables[2 * n] = (int)std::min<uint32_t>(t.content_width, (uint32_t)W);
+    tables[2 * n + 1] = (int)std::min<uint32_t>(t.content_height, (uint32_t)H);
+    tables[2 * N + 2 * n] = (int)std::min<uint32_t>(t.source_width, INT32_MAX);
+    tables[2 * N + 2 * n + 1] = (int)std::min<uint32_t>(t.source_height, INT32_MAX);
+    tables[4 * N + 2 * n] = (int)std::min<uint32_t>(t.content_width, INT32_MAX);
+    tables[4 * N + 2 * n + 1] = (int)std::min<uint32_t>(t.content_height, INT32_MAX);
+  }
+  // At most one component per 2x2 pixel block: two pixels of one block are
+  // 8-neighbours, so they cannot start different components.
+  const long max_comp = (long)N * ((H + 1) / 2) * ((W + 1) / 2);
+  auto carve = [](size_t& off, size_t bytes) {
+    size_t at = off;
+    off += (bytes + 255) / 256 * 256;
+    return at;
+  };
+  size_t off = 0;
+  const size_t o_label = carve(off, 4 * (size_t)total), o_slot = carve(off, 4 * (size_t)total);
+  const size_t o_counters = carve(off, 8), o_tables = carve(off, 4 * tables.size());
+  const size_t o_count = carve(off, 4 * (size_t)max_comp), o_root = carve(off, 4 * (size_t)max_comp);
+  const size_t o_keep = carve(off, 4 * (size_t)max_comp), o_mom = carve(off, 48 * (size_t)max_comp);
+  const size_t o_geom = carve(off, 32 * (size_t)max_comp), o_ext = carve(off, 16 * (size_t)max_comp);
+  const size_t o_out = carve(off, 48 * (size_t)max_comp);
+  if (!work || work->bytes < off) work = device_alloc(ctx->device, off);
+  char* base = static_cast<char*>(work->ptr);
+  HIP_OK(hipMemcpyAsync(base + o_tables, tables.data(), 4 * tables.size(), hipMemcpyHostToDevice, ctx->stream));
+  DbParams p{};
+  p.prob = prob;
+  p.N = N, p.H = H, p.W = W;
+  p.total = total;
+  p.content = reinterpret_cast<const int*>(base + o_tables);
+  p.source = p.content + 2 * N;
+  p.content_scale = p.content + 4 * N;
+  p.threshold = o.binary_threshold;
+  p.box_threshold = o.box_threshold;
+  p.unclip = o.unclip_ratio;
+  p.min_area = (int)std::min<size_t>(o.min_area, (size_t)INT32_MAX);
+  p.max_comp = (int)max_comp;
+  p.label = reinterpret_cast<int*>(base + o_label);
+  p.slot = reinterpret_cast<int*>(base + o_slot);
+  p.counters = reinterpret_cast<int*>(base + o_counters);
+  p.count = reinterpret_cast<int*>(base + o_count);
+  p.root = reinterpret_cast<int*>(base + o_root);
+  p.keep = reinterpret_cast<int*>(base + o_keep);
+  p.moments = reinterpret_cast<double*>(base + o_mom);
+  p.geom = reinterpret_cast<float*>(base + o_geom);
+  p.extent = reinterpret_cast<int*>(base + o_ext);
+  p.out = reinterpret_cast<float*>(base + o_out);
+  launch_db_postprocess(p, ctx->stream);
+  HIP_OK(hipGetLastError());
+  int counters[2] = {0, 0};
+  HIP_OK(hipMemcpyAsync(counters, p.counters, sizeof counters, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_OK(hipStreamSynchronize(ctx->stream));
+  const int n_det = std::max(0, std::min(counters[1], p.max_comp));
+  std::vector<float> rec(12 * (size_t)n_det);
+  if (n_det) {
+    HIP_OK(hipMemcpyAsync(rec.data(), p.out, rec.size() * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_OK(hipStreamSynchronize(ctx->stream));
+  }
+  std::vector<std::vector<HostDetection>> per(N);
+  for (int i = 0; i < n_det; ++i) {
+    const float* r = rec.data() + 12 * (size_t)i;
+    HostDetection d;
+    memcpy(d.det.polygon, r, 8 * sizeof(float));
+    d.det.score = r[8];
+    memcpy(&d.image, r + 9, 4);
+    memcpy(&d.root, r + 10, 4);
+    if (d.image < 0 || d.image >= N) raise(PPOCR_ERR_GPU, "postprocess produced an invalid image index");
+    per[d.image].push_back(d);
+  }
+  for (auto& v : per) {
+    std::sort(v.begin(), v.end(), detection_before);
+    if (v.size() > o.max_boxes) {
+      // Keep the highest scores (ties: centre y, then x), then restore the
+      // positional order (src/ocr.rs:775-788).
+      std::sort(v.begin(), v.end(), [](const HostDetection& l, const HostDetection& r) {
+        if (int c = total_cmp(r.det.score, l.det.score)) return c < 0;
+        float lx, ly, rx, ry;
+        polygon_center(l.det, &lx, &ly);
+        polygon_center(r.det, &rx, &ry);
+        if (int c = total_cmp(ly, ry)) return c < 0;
+        if (int c = total_cmp(lx, rx)) return c < 0;
+        return l.root < r.root;
+      });
+      v.resize(o.max_boxes);
+      std::sort(v.begin(), v.end(), detection_before);
+    }
+  }
+  return per;
+}
+
+void write_detections(const std::vector<std::vector<HostDetection>>& per, ppocr_detection* out, size_t cap,
+                      size_t* counts, size_t* total) {
+  size_t k = 0;
+  for (size_t n = 0; n < per.size(); ++n) {
+    if (counts) counts[n] = per[n].size();
+    for (const HostDetection& d : per[n]) {
+      if (out && k < cap) out[k] = d.det;
+      ++k;
+    }
+  }
+  if (total) *total = k;
+}
+
+}  // namespace
+}  // namespace ppocr
+
+extern "C" {
+
+void ppocr_db_default_options(ppocr_db_options* o) {
+  if (!o) return;
+  o->binary_threshold = 0.2f;
+  o->box_threshold = 0.4f;
+  o->min_area = 3;
+  o->unclip_ratio = 1.4f;
+  o->max_boxes = 1000;
+}
+
+ppocr_status ppocr_hip_db_postprocess(ppocr_hip_ctx* ctx, const float* prob, size_t n, size_t height, size_t width,
+                                      const ppocr_detector_transform* transforms, const ppocr_db_options* options,
+                                      ppocr_detection* out, size_t cap, size_t* counts, size_t* total) {
+  return guarded([&] {
+    if (!ctx || !prob) raise(PPOCR_ERR_INVALID_INPUT, "null argument");
+    if (n == 0 || height == 0 || width == 0) raise(PPOCR_ERR_INVALID_INPUT, "probability maps must be non-empty");
+    if (n * height * width >= (size_t)INT32_MAX)
+      raise(PPOCR_ERR_INVALID_INPUT, "probability maps too large for the postprocess");
+    const ppocr_db_options o = db_options(options);
+    const size_t elems = n * height * width;
+    for (size_t i = 0; i < elems; ++i)
+      if (!std::isfinite(prob[i])) raise(PPOCR_ERR_INVALID_INPUT, "detector output contains non-finite values");
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    HIP_OK(hipSetDevice(ctx->device));
+    auto maps = device_alloc(ctx->device, elems * sizeof(float));
+    HIP_OK(hipMemcpyAsync(maps->ptr, prob, elems * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    std::shared_ptr<DeviceBuffer> work;
+    auto per = run_db(ctx, static_cast<const float*>(maps->ptr), (int)n, (int)height, (int)width, transforms, o, work);
+    write_detections(per, out, cap, counts, total);
+  });
+}
+
+ppocr_status ppocr_hip_detect(ppocr_hip_model* model, const float* nchw, size_t len,
+                              const ppocr_detector_transform* transforms, const ppocr_db_options* options,
+                              ppocr_detection* out, size_t cap, size_t* counts, size_t* total) {
+  return guarded([&] {
+    if (!model) raise(PPOCR_ERR_INVALID_INPUT, "model is null");
+    if (!model->plan.detector) raise(PPOCR_ERR_INVALID_INPUT, "detection needs a detector model");
+    const ppocr_db_options o = db_options(options);
+    check_input(model, nchw, len);
+    std::lock_guard<std::mutex> lock(model->ctx->mu);
+    HIP_OK(hipSetDevice(model->ctx->device));
+    ensure_arena(model->ctx, model->plan.arena_bytes);
+    ensure_graph(model);
+    upload_input(model, nchw, len);
+    run_graph(model);
+    const auto& s = model->plan.output_shape;
+    auto per = run_db(model->ctx, output_ptr(model), (int)s[0], (int)s[2], (int)s[3], transforms, o, model->db_work);
+    write_detections(per, out, cap, counts, total);
+  });
+}
+
+ppocr_status ppocr_hip_detect_image(ppocr_hip_model* model, const ppocr_hip_image* image, const float* corners,
+                                    size_t n, const ppocr_detector_transform* transforms,
+                                    const ppocr_db_options* options, ppocr_detection* out, size_t cap,
+                                    size_t* counts, size_t* total) {
+  return guarded([&] {
+    if (!model || !image) raise(PPOCR_ERR_INVALID_INPUT, "null argument");
+    if (!model->plan.detector) raise(PPOCR_ERR_INVALID_INPUT, "detection needs a detector model");
+    if (image->ctx != model->ctx) raise(PPOCR_ERR_INVALID_INPUT, "image and model belong to different contexts");
+    if (n != model->in_shape[0])
+      raise(PPOCR_ERR_INVALID_INPUT, "geometry count " + std::to_string(n) + " differs from the planned batch");
+    check_corners(corners, n);
+    const ppocr_db_options o = db_options(options);
+    std::vector<int> cw = content_widths(nullptr, n, model->in_shape[3]);
+    std::lock_guard<std::mutex> lock(model->ctx->mu);
+    HIP_OK(hipSetDevice(model->ctx->device));
+    ensure_arena(model->ctx, model->plan.arena_bytes);
+    ensure_graph(model);
+    run_preprocess(model->ctx, image, corners, cw.data(), (int)n, (int)model->in_shape[3], (int)model->in_shape[2],
+                   true, staging_ptr(model));
+    run_graph(model);
+    const auto& s = model->plan.output_shape;
+    auto per = run_db(model->ctx, output_ptr(model), (int)s[0], (int)s[2], (int)s[3], transforms, o, model->db_work);
+    write_detections(per, out, cap, counts, total);
   });
 }
 

@@ -38,7 +38,8 @@ EXPORTS = (
     "ppocr_hip_upload_rgb", "ppocr_hip_image_free", "ppocr_hip_forward_image", "ppocr_hip_preprocess",
     "ppocr_hip_benchmark", "ppocr_hip_benchmark_stream", "ppocr_hip_profile", "ppocr_hip_memory_report",
     "ppocr_hip_recognizer_load_greedy", "ppocr_detector_input_plan", "ppocr_recognizer_batch_width",
-    "ppocr_recognition_input_plan", "ppocr_ctc_greedy_decode",
+    "ppocr_recognition_input_plan", "ppocr_ctc_greedy_decode", "ppocr_db_default_options",
+    "ppocr_hip_db_postprocess", "ppocr_hip_detect", "ppocr_hip_detect_image",
 )
 
 
@@ -49,6 +50,62 @@ class GpuError(RuntimeError):
         super().__init__(f"{STATUS.get(code, code)}: {message}")
         self.code = code
         self.kind = STATUS.get(code, str(code))
+
+
+class DbOptions(ctypes.Structure):
+    """``DetectorPostprocessOptions`` (src/ocr.rs:231-269)."""
+
+    _fields_ = [("binary_threshold", ctypes.c_float), ("box_threshold", ctypes.c_float),
+                ("min_area", ctypes.c_size_t), ("unclip_ratio", ctypes.c_float), ("max_boxes", ctypes.c_size_t)]
+
+
+class DetectorTransform(ctypes.Structure):
+    """``DetectorTransform`` (src/ocr.rs:32-74)."""
+
+    _fields_ = [("source_width", ctypes.c_uint32), ("source_height", ctypes.c_uint32),
+                ("content_width", ctypes.c_uint32), ("content_height", ctypes.c_uint32)]
+
+
+class _Detection(ctypes.Structure):
+    _fields_ = [("polygon", ctypes.c_float * 8), ("score", ctypes.c_float)]
+
+
+@dataclass
+class Detection:
+    """``Detection`` (src/ocr.rs:225-229): corners [4, 2] in source pixels, score."""
+
+    polygon: np.ndarray
+    score: float
+
+
+def db_options(**kw):
+    o = DbOptions(0.2, 0.4, 3, 1.4, 1000)
+    for k, v in kw.items():
+        setattr(o, k, v)
+    return o
+
+
+def _transforms(transforms):
+    ts = [tuple(int(v) for v in t) for t in transforms]
+    return (DetectorTransform * len(ts))(*[DetectorTransform(*t) for t in ts]), len(ts)
+
+
+def _collect(call, n, max_boxes):
+    """Runs a postprocess entry point with room for max_boxes detections per
+    image (the most it can return); one list of Detection per image."""
+    counts = (ctypes.c_size_t * n)()
+    total = ctypes.c_size_t()
+    buf = (_Detection * (n * max_boxes))()
+    _check(call(buf, n * max_boxes, counts, ctypes.byref(total)))
+    out, k = [], 0
+    for i in range(n):
+        items = []
+        for _ in range(counts[i]):
+            d = buf[k]
+            items.append(Detection(np.array(d.polygon[:], np.float32).reshape(4, 2), float(d.score)))
+            k += 1
+        out.append(items)
+    return out
 
 
 class KernelStat(ctypes.Structure):
@@ -99,6 +156,16 @@ def lib():
         L.ppocr_ctc_greedy_decode.argtypes = [_F, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
                                               ctypes.c_size_t, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int32),
                                               _SZ, _F]
+        _T = ctypes.POINTER(DetectorTransform)
+        _O = ctypes.POINTER(DbOptions)
+        _D8 = ctypes.POINTER(_Detection)
+        L.ppocr_db_default_options.argtypes = [_O]
+        L.ppocr_db_default_options.restype = None
+        L.ppocr_hip_db_postprocess.argtypes = [_VP, _F, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _T, _O,
+                                               _D8, ctypes.c_size_t, _SZ, _SZ]
+        L.ppocr_hip_detect.argtypes = [_VP, _F, ctypes.c_size_t, _T, _O, _D8, ctypes.c_size_t, _SZ, _SZ]
+        L.ppocr_hip_detect_image.argtypes = [_VP, _VP, _F, ctypes.c_size_t, _T, _O, _D8, ctypes.c_size_t, _SZ,
+                                             _SZ]
         _lib = L
     return _lib
 
@@ -156,6 +223,20 @@ class Gpu:
                                           canvas_w if content_width is None else content_width, int(detector),
                                           out.ctypes.data_as(_F)))
         return out
+
+    def db_postprocess(self, prob, transforms, **options):
+        """``extract_detections`` (src/ocr.rs:723-790) on the device for host
+        maps [N, H, W] (or [H, W]); one list of Detection per map."""
+        p = np.ascontiguousarray(prob, dtype=np.float32)
+        if p.ndim == 2:
+            p = p[None]
+        n, h, w = p.shape
+        tr, nt = _transforms(transforms)
+        if nt != n:
+            raise ValueError("one transform per map")
+        o = db_options(**options)
+        return _collect(lambda buf, cap, counts, total: lib().ppocr_hip_db_postprocess(
+            self.handle, p.ctypes.data_as(_F), n, h, w, tr, ctypes.byref(o), buf, cap, counts, total), n, o.max_boxes)
 
     def close(self):
         for child in self._children:
@@ -260,6 +341,23 @@ class Detector(_Model):
         _check(lib().ppocr_hip_detector_load(gpu.handle, str(path).encode(), SIZE_CODE[size], _sizes(input_shape),
                                              PRECISION[precision], ctypes.byref(h)))
         return cls(gpu, h, input_shape)
+
+    def detect(self, nchw, transforms, **options):
+        """Forward + device DB postprocess; one list of Detection per image."""
+        x, xp = _f32(nchw)
+        tr, n = _transforms(transforms)
+        o = db_options(**options)
+        return _collect(lambda buf, cap, counts, total: lib().ppocr_hip_detect(
+            self.handle, xp, x.size, tr, ctypes.byref(o), buf, cap, counts, total), n, o.max_boxes)
+
+    def detect_image(self, image, corners, transforms, **options):
+        """``forward_image`` + device DB postprocess (quads [N, 4, 2])."""
+        c, cp = _f32(np.asarray(corners, dtype=np.float32).reshape(-1, 8))
+        tr, n = _transforms(transforms)
+        o = db_options(**options)
+        return _collect(lambda buf, cap, counts, total: lib().ppocr_hip_detect_image(
+            self.handle, image.handle, cp, c.shape[0], tr, ctypes.byref(o), buf, cap, counts, total), n,
+            o.max_boxes)
 
 
 class Recognizer(_Model):
