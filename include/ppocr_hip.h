@@ -224,6 +224,62 @@ ppocr_status ppocr_hip_detect_image(ppocr_hip_model* detector, const ppocr_hip_i
                                     const ppocr_db_options* options, ppocr_detection* out, size_t cap,
                                     size_t* counts, size_t* total);
 
+/* ---- End-to-end OCR engine (the `OcrBackend` arm, src/ocr.rs:276-281). */
+
+typedef struct ppocr_hip_engine ppocr_hip_engine; /* `OcrEngine` with its GPU runtime */
+typedef struct ppocr_ocr_result ppocr_ocr_result; /* `OcrResult` (src/ocr.rs:343-351) */
+
+/* `OcrOptions` (src/ocr.rs:285-299) for this backend.  detector_max_side 0
+ * means `None` (the model's own resize policy); greedy != 0 runs the
+ * recognizer with the fused greedy-CTC classifier (only per-step class and
+ * probability leave the device), 0 with the full probabilities. */
+typedef struct ppocr_engine_options {
+  ppocr_model_size detector_size;
+  ppocr_model_size recognizer_size;
+  ppocr_precision precision;
+  ppocr_db_options postprocess;
+  uint32_t detector_max_side;
+  int greedy;
+} ppocr_engine_options;
+
+/* `OcrLine` (src/ocr.rs:331-341): polygon in source pixels, detector score,
+ * the recognised text as `token_count` class indices starting at
+ * `token_offset` of the result's token array (class c is dictionary entry
+ * c - 1, or a space for the implicit last class), recognition score. */
+typedef struct ppocr_ocr_line {
+  float polygon[8];
+  float detection_score;
+  float recognition_score;
+  size_t token_offset;
+  size_t token_count;
+} ppocr_ocr_line;
+
+/* Defaults of `OcrOptions::default` (src/ocr.rs:300-314): tiny / tiny,
+ * default postprocess, max side 736; plus F32 and greedy decoding. */
+void ppocr_engine_default_options(ppocr_engine_options* options);
+
+/* `OcrEngine::load` (src/ocr.rs:416-494) with the GPU runtime: validates the
+ * options and that the recognizer's class count is dictionary_len + 1 or + 2
+ * (`validate_recognizer_dictionary`, :691-700).  Models are loaded lazily per
+ * input shape and cached: 2 detector and 4 recognizer plans, oldest evicted
+ * first, all recognizer plans sharing one copy of the weights
+ * (`GpuOcrRuntime`, :608-689).  `options` NULL means the defaults. */
+ppocr_status ppocr_hip_engine_load(ppocr_hip_ctx* ctx, const char* detector_path, const char* recognizer_path,
+                                   size_t dictionary_len, const ppocr_engine_options* options,
+                                   ppocr_hip_engine** out);
+void ppocr_hip_engine_free(ppocr_hip_engine* engine);
+
+/* `OcrEngine::recognize` / `recognize_with` (src/ocr.rs:497-600) on an RGB8
+ * image (row-major HWC, width * height * 3 bytes).  The result is read with
+ * the accessors below and released with ppocr_ocr_result_free. */
+ppocr_status ppocr_hip_engine_recognize(ppocr_hip_engine* engine, const uint8_t* rgb, uint32_t width,
+                                        uint32_t height, ppocr_ocr_result** out);
+const ppocr_ocr_line* ppocr_ocr_result_lines(const ppocr_ocr_result* result, size_t* count);
+const int32_t* ppocr_ocr_result_tokens(const ppocr_ocr_result* result, size_t* count);
+void ppocr_ocr_result_sizes(const ppocr_ocr_result* result, uint32_t source_size[2],
+                            uint32_t detector_input_size[2]);
+void ppocr_ocr_result_free(ppocr_ocr_result* result);
+
 /* ---- Host-side geometry and decoding around the device path (no GPU).
  * Errors are PPOCR_ERR_INVALID_INPUT with the message in
  * ppocr_hip_last_error(). */

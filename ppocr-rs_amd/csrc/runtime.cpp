@@ -525,13 +525,6 @@ ppocr_status ppocr_hip_memory_report(const ppocr_hip_model* model, size_t* arena
 
 // ------------------------------------------------------------ DB postprocess
 namespace ppocr {
-namespace {
-
-struct HostDetection {
-  ppocr_detection det;
-  int image;
-  int root;
-};
 
 ppocr_db_options db_options(const ppocr_db_options* o) {
   ppocr_db_options v;
@@ -547,6 +540,14 @@ ppocr_db_options db_options(const ppocr_db_options* o) {
     raise(PPOCR_ERR_INVALID_INPUT, "detector unclip ratio must be a finite value greater than zero");
   return v;
 }
+
+namespace {
+
+struct HostDetection {
+  ppocr_detection det;
+  int image;
+  int root;
+};
 
 // polygon_center (src/ocr.rs:1133-1138) in f32.
 void polygon_center(const ppocr_detection& d, float* cx, float* cy) {

@@ -145,6 +145,10 @@ struct Plan {
 Plan build_detector(const SafeTensors& st, int size, const size_t nchw[4], int dt);
 Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4], int dt, bool greedy);
 
+// Postprocess options (defaults when null) after
+// DetectorPostprocessOptions::validate (src/ocr.rs:250-268).
+ppocr_db_options db_options(const ppocr_db_options* o);
+
 // Lifetime-based offset packing of the plan's buffers into one arena
 // (the reference's ArenaAllocator::compact_layout, src/gpu/runtime.rs:414-557).
 void plan_arena(Plan& plan);

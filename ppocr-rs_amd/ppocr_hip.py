@@ -39,7 +39,9 @@ EXPORTS = (
     "ppocr_hip_benchmark", "ppocr_hip_benchmark_stream", "ppocr_hip_profile", "ppocr_hip_memory_report",
     "ppocr_hip_recognizer_load_greedy", "ppocr_detector_input_plan", "ppocr_recognizer_batch_width",
     "ppocr_recognition_input_plan", "ppocr_ctc_greedy_decode", "ppocr_db_default_options",
-    "ppocr_hip_db_postprocess", "ppocr_hip_detect", "ppocr_hip_detect_image",
+    "ppocr_hip_db_postprocess", "ppocr_hip_detect", "ppocr_hip_detect_image", "ppocr_engine_default_options",
+    "ppocr_hip_engine_load", "ppocr_hip_engine_free", "ppocr_hip_engine_recognize", "ppocr_ocr_result_lines",
+    "ppocr_ocr_result_tokens", "ppocr_ocr_result_sizes", "ppocr_ocr_result_free",
 )
 
 
@@ -423,3 +425,120 @@ def ctc_greedy_decode(steps, dictionary, classes, content_width, input_width):
     space = classes == len(dictionary) + 2
     text = "".join(" " if space and tokens[i] == classes - 1 else dictionary[tokens[i] - 1] for i in range(n.value))
     return DecodedText(text, score.value)
+
+
+# ------------------------------------------------------------ OCR engine
+
+class EngineOptions(ctypes.Structure):
+    """``OcrOptions`` (src/ocr.rs:285-299) for this backend."""
+
+    _fields_ = [("detector_size", ctypes.c_int), ("recognizer_size", ctypes.c_int), ("precision", ctypes.c_int),
+                ("postprocess", DbOptions), ("detector_max_side", ctypes.c_uint32), ("greedy", ctypes.c_int)]
+
+
+class _OcrLine(ctypes.Structure):
+    _fields_ = [("polygon", ctypes.c_float * 8), ("detection_score", ctypes.c_float),
+                ("recognition_score", ctypes.c_float), ("token_offset", ctypes.c_size_t),
+                ("token_count", ctypes.c_size_t)]
+
+
+@dataclass
+class OcrLine:
+    """``OcrLine`` (src/ocr.rs:330-341)."""
+
+    polygon: np.ndarray
+    detection_score: float
+    text: str
+    recognition_score: float
+    tokens: list
+
+
+@dataclass
+class OcrResult:
+    """``OcrResult`` (src/ocr.rs:343-368)."""
+
+    source_size: tuple
+    detector_input_size: tuple
+    lines: list
+
+    def text(self):
+        return "\n".join(line.text for line in self.lines if line.text)
+
+
+def _engine_lib():
+    L = lib()
+    if not getattr(L, "_engine_ready", False):
+        L.ppocr_engine_default_options.argtypes = [ctypes.POINTER(EngineOptions)]
+        L.ppocr_engine_default_options.restype = None
+        L.ppocr_hip_engine_load.argtypes = [_VP, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t,
+                                            ctypes.POINTER(EngineOptions), ctypes.POINTER(_VP)]
+        L.ppocr_hip_engine_free.argtypes = [_VP]
+        L.ppocr_hip_engine_recognize.argtypes = [_VP, _VP, ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(_VP)]
+        L.ppocr_ocr_result_lines.argtypes = [_VP, _SZ]
+        L.ppocr_ocr_result_lines.restype = ctypes.POINTER(_OcrLine)
+        L.ppocr_ocr_result_tokens.argtypes = [_VP, _SZ]
+        L.ppocr_ocr_result_tokens.restype = ctypes.POINTER(ctypes.c_int32)
+        L.ppocr_ocr_result_sizes.argtypes = [_VP, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32)]
+        L.ppocr_ocr_result_sizes.restype = None
+        L.ppocr_ocr_result_free.argtypes = [_VP]
+        L._engine_ready = True
+    return L
+
+
+class OcrEngine:
+    """``OcrEngine`` (src/ocr.rs:354-600) running on this backend."""
+
+    def __init__(self, gpu, handle, dictionary, classes):
+        self.gpu, self.handle, self.dictionary, self.classes = gpu, handle, list(dictionary), classes
+        gpu._children.append(self)
+
+    @classmethod
+    def load(cls, gpu, detector_model, recognizer_model, dictionary, detector_size="tiny", recognizer_size="tiny",
+             precision="f32", detector_max_side=736, greedy=True, **postprocess):
+        """``OcrEngine::load`` (src/ocr.rs:416-494); ``dictionary`` is the list of
+        entries (``load_dictionary``, src/ocr.rs:792-798)."""
+        L = _engine_lib()
+        o = EngineOptions()
+        L.ppocr_engine_default_options(ctypes.byref(o))
+        o.detector_size, o.recognizer_size = SIZE_CODE[detector_size], SIZE_CODE[recognizer_size]
+        o.precision = PRECISION[precision]
+        o.detector_max_side = 0 if detector_max_side is None else int(detector_max_side)
+        o.greedy = int(bool(greedy))
+        for k, v in postprocess.items():
+            setattr(o.postprocess, k, v)
+        h = _VP()
+        _check(L.ppocr_hip_engine_load(gpu.handle, str(detector_model).encode(), str(recognizer_model).encode(),
+                                       len(dictionary), ctypes.byref(o), ctypes.byref(h)))
+        return cls(gpu, h, dictionary, 6906 if recognizer_size == "tiny" else 18710)
+
+    def recognize(self, rgb):
+        """``OcrEngine::recognize`` (src/ocr.rs:497-522) on an HxWx3 uint8 image."""
+        L = _engine_lib()
+        rgb = np.ascontiguousarray(rgb, dtype=np.uint8)
+        if rgb.ndim != 3 or rgb.shape[2] != 3:
+            raise ValueError("expected an HxWx3 uint8 image")
+        r = _VP()
+        _check(L.ppocr_hip_engine_recognize(self.handle, rgb.ctypes.data_as(_VP), rgb.shape[1], rgb.shape[0],
+                                            ctypes.byref(r)))
+        try:
+            n, nt = ctypes.c_size_t(), ctypes.c_size_t()
+            lines = L.ppocr_ocr_result_lines(r, ctypes.byref(n))
+            toks = L.ppocr_ocr_result_tokens(r, ctypes.byref(nt))
+            src, det = (ctypes.c_uint32 * 2)(), (ctypes.c_uint32 * 2)()
+            L.ppocr_ocr_result_sizes(r, src, det)
+            space = self.classes == len(self.dictionary) + 2
+            out = []
+            for i in range(n.value):
+                ln = lines[i]
+                ids = [int(toks[ln.token_offset + k]) for k in range(ln.token_count)]
+                text = "".join(" " if space and c == self.classes - 1 else self.dictionary[c - 1] for c in ids)
+                out.append(OcrLine(np.array(ln.polygon[:], np.float32).reshape(4, 2), float(ln.detection_score),
+                                   text, float(ln.recognition_score), ids))
+            return OcrResult((src[0], src[1]), (det[0], det[1]), out)
+        finally:
+            L.ppocr_ocr_result_free(r)
+
+    def close(self):
+        if self.handle:
+            _engine_lib().ppocr_hip_engine_free(self.handle)
+            self.handle = None
