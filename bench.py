@@ -197,6 +197,42 @@ def also(gpu, warmup, steps):
     return out
 
 
+def pipeline(gpu, reps=20):
+    """End-to-end calls with host buffers (wall clock, PCIe included): the
+    detector with the device DB postprocess against the detector returning its
+    probability map, and the OCR engine on a 960x540 synthetic page."""
+    out = {}
+    shape = (1, 3, 416, 736)
+    det = load(gpu, "det", "tiny", shape)
+    x = inputs("det", shape)
+    transforms = [(736, 416, 736, 416)]
+    det.forward(x)
+    det.detect(x, transforms, binary_threshold=0.62, box_threshold=0.0)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        det.forward(x)
+    t1 = time.perf_counter()
+    for _ in range(reps):
+        n = len(det.detect(x, transforms, binary_threshold=0.62, box_threshold=0.0)[0])
+    t2 = time.perf_counter()
+    det.close()
+    out["tiny_det_1x416x736_forward_map_to_host_ms"] = round((t1 - t0) / reps * 1e3, 3)
+    out["tiny_det_1x416x736_detect_on_device_ms"] = round((t2 - t1) / reps * 1e3, 3)
+    out["tiny_det_1x416x736_detections"] = n
+    dictionary = [f"<{i}>" for i in range(1, 6906)]
+    img = seeded.seeded_rgb(540, 960, 23, pattern="blocks")
+    for label, opts in [("default", {}), ("thr0.62", dict(binary_threshold=0.62, box_threshold=0.0))]:
+        engine = ppocr_hip.OcrEngine.load(gpu, weights("det", "tiny"), weights("rec", "tiny"), dictionary, **opts)
+        r = engine.recognize(img)  # warm: loads and captures every plan
+        t0 = time.perf_counter()
+        for _ in range(5):
+            r = engine.recognize(img)
+        el = (time.perf_counter() - t0) / 5
+        engine.close()
+        out[f"engine_tiny_960x540_{label}"] = {"ms_per_image": round(el * 1e3, 3), "lines": len(r.lines)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -249,6 +285,7 @@ def main():
         line["cpu_baseline"] = cpu_baseline(kind, size, shape)
     if not args.no_extra:
         line["also"] = also(gpu, args.warmup, max(5, args.steps // 2))
+        line["pipeline"] = pipeline(gpu)
     gpu.close()
     print(json.dumps(line), flush=True)
 

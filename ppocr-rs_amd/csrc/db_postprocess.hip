@@ -5,14 +5,17 @@
 //
 // Components are labelled with a union-find over the pixels (each label
 // points at a smaller pixel index; unions link roots with atomicMin, so
-// every loop strictly decreases an index and ends).  The root of a component
-// is its smallest raster index, which is the pixel the reference's raster
-// scan starts its BFS from.  Component moments (count, sum of scores, sums
-// of x, y, x^2, xy, y^2) are reduced within each wave over lanes that share a
-// component before one lane issues the atomics, so a large component costs
-// one atomic per wave, not per pixel.  Moments are accumulated in fp64, so
-// the centre and covariance are at least as accurate as the reference's
-// sequential fp32 sums.  Box extents use order-preserving integer atomics.
+// every loop strictly decreases an index and ends).  Labels start at the
+// first pixel of each horizontal run (a per-row max-scan), so only runs of
+// neighbouring rows are united, one union per touching pair of runs; finds
+// halve their path as they go.  The root of a component is its smallest
+// raster index, which is the pixel the reference's raster scan starts its
+// BFS from.  Component moments (count, sum of scores, sums of x, y, x^2, xy,
+// y^2) are summed per thread over 8 consecutive pixels, then over the lanes
+// of a wave that share a component, before one lane issues the atomics.
+// Moments are accumulated in fp64, so the centre and covariance are at least
+// as accurate as the reference's sequential fp32 sums.  Box extents use
+// order-preserving integer atomics.
 //
 // Pixel p of image n is index n*H*W + y*W + x; only pixels inside the
 // image's content rectangle take part.
@@ -22,14 +25,21 @@ namespace ppocr {
 
 namespace {
 
+constexpr int PPT = 8;  // pixels per thread in the moment and extent passes
+
 __device__ __forceinline__ int load_label(const int* L, int i) {
   return __hip_atomic_load(L + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ int find_root(const int* L, int x) {
+// Root of x with path halving: each visited node is re-pointed at its
+// grandparent (an ancestor, so the forest stays valid under concurrency).
+__device__ __forceinline__ int find_root(int* L, int x) {
   int p = load_label(L, x);
   while (p != x) {
-    x = p;
+    const int gp = load_label(L, p);
+    if (gp == p) return p;
+    atomicMin(L + x, gp);
+    x = gp;
     p = load_label(L, x);
   }
   return x;
@@ -101,30 +111,64 @@ __global__ void db_reset_kernel(int* counters) {
   if (threadIdx.x < 2) counters[threadIdx.x] = 0;
 }
 
-// label = own index for pixels >= threshold inside the content, else -1.
-__global__ __launch_bounds__(256) void db_init_kernel(DbParams p) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= p.total) return;
-  const PixelPos q = locate(p, i);
-  p.label[i] = q.inside && p.prob[i] >= p.threshold ? (int)i : -1;
+// One block per image row: label = index of the first pixel of the pixel's
+// horizontal run of foreground (>= threshold, inside the content), else -1.
+// The run start of a foreground pixel is the largest run start at or before
+// it: a max-scan over the row (per-thread chunks, then across the block).
+__global__ __launch_bounds__(256) void db_runs_kernel(DbParams p) {
+  __shared__ int carry[256];
+  const int row = blockIdx.x;
+  const int n = row / p.H, y = row - n * p.H;
+  const long base = (long)row * p.W;
+  const int cw = y < p.content[2 * n + 1] ? p.content[2 * n] : 0;
+  const int per = (p.W + 255) / 256;
+  const int x0 = min(p.W, (int)threadIdx.x * per), x1 = min(p.W, x0 + per);
+  auto fg = [&](int x) { return x < cw && p.prob[base + x] >= p.threshold; };
+  int last = -1;
+  for (int x = x0; x < x1; ++x)
+    if (fg(x) && (x == 0 || !fg(x - 1))) last = x;
+  carry[threadIdx.x] = last;
+  __syncthreads();
+  for (int o = 1; o < 256; o <<= 1) {  // inclusive max-scan of the chunk maxima
+    const int v = threadIdx.x >= (unsigned)o ? carry[threadIdx.x - o] : -1;
+    __syncthreads();
+    carry[threadIdx.x] = max(carry[threadIdx.x], v);
+    __syncthreads();
+  }
+  int run = threadIdx.x > 0 ? carry[threadIdx.x - 1] : -1;
+  for (int x = x0; x < x1; ++x) {
+    const bool f = fg(x);
+    if (f && (x == 0 || !fg(x - 1))) run = x;
+    p.label[base + x] = f ? (int)(base + run) : -1;
+  }
 }
 
-// Links each foreground pixel with its foreground neighbours to the left,
-// upper-left, up and upper-right; with every pixel doing so, all eight
-// neighbour pairs are covered.
+// Unites each run with the runs of the row above that touch it (8-connected:
+// columns a-1 .. b+1 for a run [a, b]).  A foreground pixel at the start of
+// its run unites with the upper run over column a (or a-1); every pixel x
+// whose upper-right neighbour starts an upper run (up(x) background,
+// up(x+1) foreground) unites with that run.  Together these reach every
+// upper run overlapping a-1 .. b+1, once each.
 __global__ __launch_bounds__(256) void db_union_kernel(DbParams p) {
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= p.total || p.label[i] < 0) return;
+  if (i >= p.total) return;
+  // Foreground is label >= 0, which unions never change; the label values
+  // themselves do change under concurrent unions, so run starts are found
+  // from the mask, not from label == index.
+  if (p.label[i] < 0) return;
   const PixelPos q = locate(p, i);
-  const int cw = p.content[2 * q.n];
+  if (q.y == 0) return;
   const int me = (int)i;
-  if (q.x > 0 && p.label[i - 1] >= 0) unite(p.label, me, me - 1);
-  if (q.y > 0) {
-    const long up = i - p.W;
-    if (q.x > 0 && p.label[up - 1] >= 0) unite(p.label, me, (int)(up - 1));
-    if (p.label[up] >= 0) unite(p.label, me, (int)up);
-    if (q.x + 1 < cw && p.label[up + 1] >= 0) unite(p.label, me, (int)(up + 1));
+  const int cw = p.content[2 * q.n];
+  const long up = i - p.W;
+  const bool up_fg = p.label[up] >= 0;
+  if (q.x == 0 || p.label[i - 1] < 0) {  // run start
+    if (up_fg)
+      unite(p.label, me, (int)up);
+    else if (q.x > 0 && p.label[up - 1] >= 0)
+      unite(p.label, me, (int)(up - 1));
   }
+  if (!up_fg && q.x + 1 < cw && p.label[up + 1] >= 0) unite(p.label, me, (int)(up + 1));
 }
 
 // label = root; each root takes a component slot and clears its moments.
@@ -147,41 +191,53 @@ __global__ __launch_bounds__(256) void db_flatten_kernel(DbParams p) {
 
 // Component moments: count, sum of scores, sums of x, y, x^2, xy, y^2 of the
 // pixel centres (x + 0.5, y + 0.5).
+// Each thread sums PPT consecutive pixels; a change of component inside the
+// chunk flushes the finished part with its own atomics (only at run ends),
+// and the last part goes through the wave-level combine.
+__device__ __forceinline__ void flush_moments(const DbParams& p, int id, int c, const double* v) {
+  atomicAdd(&p.count[id], c);
+#pragma unroll
+  for (int k = 0; k < 6; ++k) atomicAdd(&p.moments[6 * (size_t)id + k], v[k]);
+}
+
 __global__ __launch_bounds__(256) void db_moments_kernel(DbParams p) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  const long i0 = ((long)blockIdx.x * 256 + threadIdx.x) * PPT;
   const int lane = threadIdx.x & 63;
-  int id = -1;
-  if (i < p.total) {
-    const int r = p.label[i];
-    if (r >= 0) id = p.slot[r];
-  }
-  const bool active = id >= 0 && id < p.max_comp;
+  int id = -1, c = 0;
   double v[6] = {0, 0, 0, 0, 0, 0};
-  if (active) {
+  for (long i = i0; i < i0 + PPT && i < p.total; ++i) {
+    const int r = p.label[i];
+    const int pid = r >= 0 ? p.slot[r] : -1;
+    if (pid < 0 || pid >= p.max_comp) continue;
+    if (pid != id) {
+      if (id >= 0) flush_moments(p, id, c, v);
+      id = pid;
+      c = 0;
+#pragma unroll
+      for (int k = 0; k < 6; ++k) v[k] = 0.0;
+    }
     const PixelPos q = locate(p, i);
     const double x = q.x + 0.5, y = q.y + 0.5;
-    v[0] = (double)p.prob[i];
-    v[1] = x;
-    v[2] = y;
-    v[3] = x * x;
-    v[4] = x * y;
-    v[5] = y * y;
+    c += 1;
+    v[0] += (double)p.prob[i];
+    v[1] += x;
+    v[2] += y;
+    v[3] += x * x;
+    v[4] += x * y;
+    v[5] += y * y;
   }
+  const bool active = id >= 0;
   uint64_t pending = __ballot(active);
   while (pending) {
     const int leader = __ffsll((unsigned long long)pending) - 1;
     const int lid = __shfl(id, leader);
     const bool mine = active && id == lid && ((pending >> lane) & 1);
     pending &= ~__ballot(mine);
-    const int c = wave_sum(mine ? 1 : 0);
+    const int cs = wave_sum(mine ? c : 0);
     double s[6];
 #pragma unroll
     for (int k = 0; k < 6; ++k) s[k] = wave_sum(mine ? v[k] : 0.0);
-    if (lane == leader) {
-      atomicAdd(&p.count[lid], c);
-#pragma unroll
-      for (int k = 0; k < 6; ++k) atomicAdd(&p.moments[6 * (size_t)lid + k], s[k]);
-    }
+    if (lane == leader) flush_moments(p, lid, cs, s);
   }
 }
 
@@ -219,39 +275,54 @@ __global__ __launch_bounds__(256) void db_axis_kernel(DbParams p) {
   e[3] = ordered(-INFINITY);
 }
 
-// Extents of each kept component along its axis and normal.
+// Extents of each kept component along its axis and normal (PPT pixels per
+// thread, then the wave-level combine, as the moments).
+__device__ __forceinline__ void flush_extent(const DbParams& p, int id, const float* m) {
+  int* e = p.extent + 4 * (size_t)id;
+  atomicMin(&e[0], ordered(m[0]));
+  atomicMax(&e[1], ordered(m[1]));
+  atomicMin(&e[2], ordered(m[2]));
+  atomicMax(&e[3], ordered(m[3]));
+}
+
 __global__ __launch_bounds__(256) void db_extent_kernel(DbParams p) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  const long i0 = ((long)blockIdx.x * 256 + threadIdx.x) * PPT;
   const int lane = threadIdx.x & 63;
   int id = -1;
-  if (i < p.total) {
+  float m[4] = {INFINITY, -INFINITY, INFINITY, -INFINITY};
+  for (long i = i0; i < i0 + PPT && i < p.total; ++i) {
     const int r = p.label[i];
-    if (r >= 0) id = p.slot[r];
-  }
-  bool active = id >= 0 && id < p.max_comp && p.keep[id];
-  float a = 0.0f, nrm = 0.0f;
-  if (active) {
+    const int pid = r >= 0 ? p.slot[r] : -1;
+    if (pid < 0 || pid >= p.max_comp || !p.keep[pid]) continue;
+    if (pid != id) {
+      if (id >= 0) flush_extent(p, id, m);
+      id = pid;
+      m[0] = m[2] = INFINITY;
+      m[1] = m[3] = -INFINITY;
+    }
     const PixelPos q = locate(p, i);
     const float* g = p.geom + 8 * (size_t)id;
     const float dx = (float)q.x + 0.5f - g[0], dy = (float)q.y + 0.5f - g[1];
-    a = dx * g[2] + dy * g[3];
-    nrm = dx * (-g[3]) + dy * g[2];
+    const float a = dx * g[2] + dy * g[3];
+    const float nrm = dx * (-g[3]) + dy * g[2];
+    m[0] = fminf(m[0], a);
+    m[1] = fmaxf(m[1], a);
+    m[2] = fminf(m[2], nrm);
+    m[3] = fmaxf(m[3], nrm);
   }
+  const bool active = id >= 0;
   uint64_t pending = __ballot(active);
   while (pending) {
     const int leader = __ffsll((unsigned long long)pending) - 1;
     const int lid = __shfl(id, leader);
     const bool mine = active && id == lid && ((pending >> lane) & 1);
     pending &= ~__ballot(mine);
-    const float amin = wave_min(mine ? a : INFINITY), amax = wave_max(mine ? a : -INFINITY);
-    const float nmin = wave_min(mine ? nrm : INFINITY), nmax = wave_max(mine ? nrm : -INFINITY);
-    if (lane == leader) {
-      int* e = p.extent + 4 * (size_t)lid;
-      atomicMin(&e[0], ordered(amin));
-      atomicMax(&e[1], ordered(amax));
-      atomicMin(&e[2], ordered(nmin));
-      atomicMax(&e[3], ordered(nmax));
-    }
+    float s[4];
+    s[0] = wave_min(mine ? m[0] : INFINITY);
+    s[1] = wave_max(mine ? m[1] : -INFINITY);
+    s[2] = wave_min(mine ? m[2] : INFINITY);
+    s[3] = wave_max(mine ? m[3] : -INFINITY);
+    if (lane == leader) flush_extent(p, lid, s);
   }
 }
 
@@ -296,14 +367,15 @@ __global__ __launch_bounds__(256) void db_emit_kernel(DbParams p) {
 
 void launch_db_postprocess(const DbParams& p, hipStream_t s) {
   const unsigned px_blocks = (unsigned)((p.total + 255) / 256);
+  const unsigned chunk_blocks = (unsigned)((p.total + 256L * PPT - 1) / (256L * PPT));
   const unsigned comp_blocks = (unsigned)((p.max_comp + 255) / 256);
   hipLaunchKernelGGL(db_reset_kernel, dim3(1), dim3(64), 0, s, p.counters);
-  hipLaunchKernelGGL(db_init_kernel, dim3(px_blocks), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(db_runs_kernel, dim3((unsigned)(p.N * p.H)), dim3(256), 0, s, p);
   hipLaunchKernelGGL(db_union_kernel, dim3(px_blocks), dim3(256), 0, s, p);
   hipLaunchKernelGGL(db_flatten_kernel, dim3(px_blocks), dim3(256), 0, s, p);
-  hipLaunchKernelGGL(db_moments_kernel, dim3(px_blocks), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(db_moments_kernel, dim3(chunk_blocks), dim3(256), 0, s, p);
   hipLaunchKernelGGL(db_axis_kernel, dim3(comp_blocks), dim3(256), 0, s, p);
-  hipLaunchKernelGGL(db_extent_kernel, dim3(px_blocks), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(db_extent_kernel, dim3(chunk_blocks), dim3(256), 0, s, p);
   hipLaunchKernelGGL(db_emit_kernel, dim3(comp_blocks), dim3(256), 0, s, p);
 }
 

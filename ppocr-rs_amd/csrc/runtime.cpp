@@ -547,6 +547,7 @@ struct HostDetection {
   ppocr_detection det;
   int image;
   int root;
+  float cx, cy;  // polygon_center, computed once for the sorts
 };
 
 // polygon_center (src/ocr.rs:1133-1138) in f32.
@@ -568,11 +569,8 @@ int total_cmp(float a, float b) {
 // sort_detections (src/ocr.rs:1120-1131): centre y, centre x, score; the
 // reference's stable sort keeps raster order (root pixel) among equals.
 bool detection_before(const HostDetection& l, const HostDetection& r) {
-  float lx, ly, rx, ry;
-  polygon_center(l.det, &lx, &ly);
-  polygon_center(r.det, &rx, &ry);
-  if (int c = total_cmp(ly, ry)) return c < 0;
-  if (int c = total_cmp(lx, rx)) return c < 0;
+  if (int c = total_cmp(l.cy, r.cy)) return c < 0;
+  if (int c = total_cmp(l.cx, r.cx)) return c < 0;
   if (int c = total_cmp(l.det.score, r.det.score)) return c < 0;
   return l.root < r.root;
 }
@@ -657,6 +655,7 @@ std::vector<std::vector<HostDetection>> run_db(ppocr_hip_ctx* ctx, const float* 
     memcpy(&d.image, r + 9, 4);
     memcpy(&d.root, r + 10, 4);
     if (d.image < 0 || d.image >= N) raise(PPOCR_ERR_GPU, "postprocess produced an invalid image index");
+    polygon_center(d.det, &d.cx, &d.cy);
     per[d.image].push_back(d);
   }
   for (auto& v : per) {
@@ -666,11 +665,8 @@ std::vector<std::vector<HostDetection>> run_db(ppocr_hip_ctx* ctx, const float* 
       // positional order (src/ocr.rs:775-788).
       std::sort(v.begin(), v.end(), [](const HostDetection& l, const HostDetection& r) {
         if (int c = total_cmp(r.det.score, l.det.score)) return c < 0;
-        float lx, ly, rx, ry;
-        polygon_center(l.det, &lx, &ly);
-        polygon_center(r.det, &rx, &ry);
-        if (int c = total_cmp(ly, ry)) return c < 0;
-        if (int c = total_cmp(lx, rx)) return c < 0;
+        if (int c = total_cmp(l.cy, r.cy)) return c < 0;
+        if (int c = total_cmp(l.cx, r.cx)) return c < 0;
         return l.root < r.root;
       });
       v.resize(o.max_boxes);
