@@ -1,7 +1,7 @@
 """Input plans and the greedy-CTC collapse of the C ABI (host code, no GPU).
 
 Pinned by the reference's own literal tests (src/preprocess.rs:150-179,
-src/ocr.rs:1266-1301) and by what the arithmetic fixes: aligned sides are the
+src/ocr.rs:1254-1301) and by what the arithmetic fixes: aligned sides are the
 nearest multiple of 32, content widths are ceil(48 w / h) of the bounded crop,
 the batch canvas is the largest content width (at least 320) rounded up to a
 multiple of 4, and the decode emits a class on each change away from blank
@@ -63,9 +63,9 @@ def test_detector_plan_rejects_bad_arguments():
 def test_recognizer_plan_matches_reference_literals():
     # src/preprocess.rs:161-179: an 80x20 crop has content width 192 of 320.
     assert ppocr_hip.recognition_input_plan(rect(80, 20), 320) == 192
-    # src/ocr.rs:1285-1301: the widest crop sets the canvas.
+    # src/ocr.rs:1284-1301: the widest crop sets the canvas.
     assert ppocr_hip.recognizer_batch_width([rect(80, 20), rect(300, 20)]) == 720
-    # src/ocr.rs:1266-1283: a 1000x20 crop keeps its whole width.
+    # src/ocr.rs:1269-1282: a 1000x20 crop keeps its whole width.
     wide = rect(1000, 20)
     width = ppocr_hip.recognizer_batch_width([wide])
     assert width == 2400
@@ -125,7 +125,7 @@ def steps_of(rows):
 
 
 def test_ctc_matches_reference_literal():
-    # src/ocr.rs:1239-1252: five steps of "A", only ceil(40 * 5 / 100) = 2 valid.
+    # src/ocr.rs:1254-1266: five steps of "A", only ceil(40 * 5 / 100) = 2 valid.
     rows = np.array([[0.1, 0.9]] * 5, np.float32)
     d = ppocr_hip.ctc_greedy_decode(steps_of(rows), ["A"], 2, 40, 100)
     assert d.text == "A"
