@@ -32,40 +32,63 @@ struct GemmTraits;
 template <>
 struct GemmTraits<float> {
   static constexpr int BK = 16;  // K slice: 16 fp32 = 64 B per row
-  using Quad = float4;           // four k values
 };
 template <>
 struct GemmTraits<bf16> {
   static constexpr int BK = 32;  // K slice: 32 bf16 = 64 B per row
-  using Quad = uint2;
+};
+
+// A global-load vector of VE consecutive k values: 16 bytes (fp32 x4,
+// bf16 x8), or 8 bytes (bf16 x4) for layers whose channel count is not a
+// multiple of 8.
+template <typename T, int VE>
+struct VecT;
+template <>
+struct VecT<float, 4> {
+  using type = float4;
+};
+template <>
+struct VecT<bf16, 8> {
+  using type = uint4;
+};
+template <>
+struct VecT<bf16, 4> {
+  using type = uint2;
 };
 
 __device__ __forceinline__ float4 f4_add(float4 a, float4 b) {
   return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 
-template <typename T>
-__device__ __forceinline__ typename GemmTraits<T>::Quad gate_quad(typename GemmTraits<T>::Quad v, float4 g);
-template <>
-__device__ __forceinline__ float4 gate_quad<float>(float4 v, float4 g) {
-  return f4_mul(v, g);
-}
-template <>
-__device__ __forceinline__ uint2 gate_quad<bf16>(uint2 v, float4 g) {
-  float4 f = f4_mul(make_float4(bf16_bits_to_f32(v.x & 0xFFFFu), bf16_bits_to_f32(v.x >> 16),
-                                bf16_bits_to_f32(v.y & 0xFFFFu), bf16_bits_to_f32(v.y >> 16)),
-                    g);
-  uint2 u;
-  u.x = f32_to_bf16_bits(f.x) | (f32_to_bf16_bits(f.y) << 16);
-  u.y = f32_to_bf16_bits(f.z) | (f32_to_bf16_bits(f.w) << 16);
-  return u;
+__device__ __forceinline__ uint32_t gate_pair(uint32_t v, float g0, float g1) {
+  return f32_to_bf16_bits(bf16_bits_to_f32(v & 0xFFFFu) * g0) |
+         (f32_to_bf16_bits(bf16_bits_to_f32(v >> 16) * g1) << 16);
 }
 
-template <typename T, int BM, int BN, int WM, int WN>
+// v * g elementwise (the SE gate applied while gathering A); g points at the
+// VE gate values of these channels.
+__device__ __forceinline__ float4 gate_vec(float4 v, const float* g) {
+  return f4_mul(v, *reinterpret_cast<const float4*>(g));
+}
+__device__ __forceinline__ uint2 gate_vec(uint2 v, const float* g) {
+  const float4 a = *reinterpret_cast<const float4*>(g);
+  return make_uint2(gate_pair(v.x, a.x, a.y), gate_pair(v.y, a.z, a.w));
+}
+__device__ __forceinline__ uint4 gate_vec(uint4 v, const float* g) {
+  const float4 a = *reinterpret_cast<const float4*>(g), b = *reinterpret_cast<const float4*>(g + 4);
+  return make_uint4(gate_pair(v.x, a.x, a.y), gate_pair(v.y, a.z, a.w), gate_pair(v.z, b.x, b.y),
+                    gate_pair(v.w, b.z, b.w));
+}
+
+// PW: 1x1 convolution with stride 1 and no padding, where an output pixel
+// reads exactly its own input pixel and A rows are plain strided rows.
+// VE: k values per global load (see VecT).
+template <typename T, int BM, int BN, int WM, int WN, bool PW, int VE>
 __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
-  using Quad = typename GemmTraits<T>::Quad;
+  using Vec = typename VecT<T, VE>::type;
   constexpr int BK = GemmTraits<T>::BK;
-  constexpr int KQ = BK / 4;                 // quads per row of a K slice
+  constexpr int KV = BK / VE;                // vectors per row of a K slice
+  constexpr int RPP = 256 / KV;              // tile rows loaded per pass of the block
   constexpr int PADE = 16 / sizeof(T);       // 16 B of padding per LDS row
   constexpr int LDA = BK + PADE;             // 80-byte rows
   constexpr int OPE = 16 / sizeof(T);        // elements per 16-byte operand read
@@ -73,10 +96,9 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
   constexpr int TN = BN / (WN * 16);
   static_assert(WM * WN == 4, "four waves per block");
   static_assert(TM >= 1 && TN >= 1, "tile too small");
-  constexpr int A_PER = BM * KQ / 256;
-  constexpr int B_Q = BN * KQ;
-  constexpr int B_PER = (B_Q + 255) / 256;
-  static_assert((BM * KQ) % 256 == 0, "A tile must split evenly over the block");
+  static_assert(BM % RPP == 0, "A tile must split evenly over the block");
+  constexpr int A_PER = BM / RPP;
+  constexpr int B_PER = (BN + RPP - 1) / RPP;
   constexpr int STAGE = (BM + BN) * LDA;     // elements of T
   constexpr int LDE = BN + 4;                // fp32 epilogue staging
   constexpr int SMEM_BYTES = 2 * STAGE * (int)sizeof(T) > BM * LDE * 4 ? 2 * STAGE * (int)sizeof(T) : BM * LDE * 4;
@@ -107,53 +129,95 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
   if (t >= m_tiles * n_tiles) return;
   const int m0 = (t / n_tiles) * BM;
   const int n0 = (t % n_tiles) * BN;
-  const int kq = tid % KQ;  // this lane's k-quad in every A and B load
+  const int kv = tid % KV;    // this lane's vector within a row of the K slice
+  const int rrow = tid / KV;  // this lane's first tile row; then every RPP rows
 
+  // A rows.  PW: a row is the input pixel itself.  Otherwise: image and the
+  // top-left input coordinate of the output pixel's window.
+  const T* a_ptr[A_PER];
   int a_img[A_PER], a_iy0[A_PER], a_ix0[A_PER];
   bool a_ok[A_PER];
 #pragma unroll
   for (int i = 0; i < A_PER; ++i) {
-    int m = m0 + (tid + i * 256) / KQ;
+    const int m = m0 + rrow + i * RPP;
     a_ok[i] = m < M;
-    int mm = a_ok[i] ? m : 0;
-    int img = mm / HoWo;
-    int r = mm - img * HoWo;
-    int oy = r / p.Wo;
-    int ox = r - oy * p.Wo;
+    const int mm = a_ok[i] ? m : 0;
+    const int img = mm / HoWo;
     a_img[i] = img;
-    a_iy0[i] = oy * p.sh - p.pt;
-    a_ix0[i] = ox * p.sw - p.pl;
+    if constexpr (PW) {
+      a_ptr[i] = in + (size_t)mm * p.in_ps;
+      a_iy0[i] = a_ix0[i] = 0;
+    } else {
+      const int r = mm - img * HoWo;
+      const int oy = r / p.Wo;
+      const int ox = r - oy * p.Wo;
+      a_ptr[i] = in + (size_t)img * p.H * p.W * p.in_ps;
+      a_iy0[i] = oy * p.sh - p.pt;
+      a_ix0[i] = ox * p.sw - p.pl;
+    }
+  }
+  bool b_ok[B_PER];
+  const T* b_ptr[B_PER];
+#pragma unroll
+  for (int i = 0; i < B_PER; ++i) {
+    const int r = rrow + i * RPP;
+    const int n = n0 + r;
+    b_ok[i] = r < BN && n < p.Co;
+    b_ptr[i] = wt + (size_t)(b_ok[i] ? n : 0) * p.ldw;
   }
 
-  Quad ra[A_PER];
-  Quad rb[B_PER];
+  // Decomposition of this lane's k = k0 + kv*VE into (ky, kx, c), kept up to
+  // date as the K slices advance (one division at the start, none in the
+  // loop).  A vector never straddles a tap: C is a multiple of VE.
+  int kc = kv * VE, kx = 0, ky = 0;
+  if constexpr (!PW) {
+    const int tap = kc / p.C;
+    kc -= tap * p.C;
+    ky = tap / p.kw;
+    kx = tap - ky * p.kw;
+  }
 
+  Vec ra[A_PER];
+  Vec rb[B_PER];
+
+  // Loads the K slice starting at k0 (called for k0 = 0, BK, 2 BK, ... in
+  // order) into registers.
   auto load_tile = [&](int k0) {
-    const int k = k0 + kq * 4;
+    const int k = k0 + kv * VE;
     const bool kin = k < K;
-    const int tap = k / p.C;
-    const int c = k - tap * p.C;
-    const int ky = tap / p.kw;
-    const int kx = tap - ky * p.kw;
 #pragma unroll
     for (int i = 0; i < A_PER; ++i) {
-      Quad v{};
-      int iy = a_iy0[i] + ky;
-      int ix = a_ix0[i] + kx;
-      if (kin && a_ok[i] && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W) {
-        v = *reinterpret_cast<const Quad*>(in + ((size_t)(a_img[i] * p.H + iy) * p.W + ix) * p.in_ps + c);
-        if (p.in_gate)
-          v = gate_quad<T>(v, *reinterpret_cast<const float4*>(p.in_gate + (size_t)a_img[i] * p.C + c));
+      Vec v{};
+      if constexpr (PW) {
+        if (kin && a_ok[i]) {
+          v = *reinterpret_cast<const Vec*>(a_ptr[i] + k);
+          if (p.in_gate) v = gate_vec(v, p.in_gate + (size_t)a_img[i] * p.C + k);
+        }
+      } else {
+        const int iy = a_iy0[i] + ky;
+        const int ix = a_ix0[i] + kx;
+        if (kin && a_ok[i] && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W) {
+          v = *reinterpret_cast<const Vec*>(a_ptr[i] + ((size_t)iy * p.W + ix) * p.in_ps + kc);
+          if (p.in_gate) v = gate_vec(v, p.in_gate + (size_t)a_img[i] * p.C + kc);
+        }
       }
       ra[i] = v;
     }
 #pragma unroll
     for (int i = 0; i < B_PER; ++i) {
-      int q = tid + i * 256;
-      int n = n0 + q / KQ;
-      Quad v{};
-      if (q < B_Q && kin && n < p.Co) v = *reinterpret_cast<const Quad*>(wt + (size_t)n * p.ldw + k);
+      Vec v{};
+      if (kin && b_ok[i]) v = *reinterpret_cast<const Vec*>(b_ptr[i] + k);
       rb[i] = v;
+    }
+    if constexpr (!PW) {
+      kc += BK;
+      while (kc >= p.C) {
+        kc -= p.C;
+        if (++kx == p.kw) {
+          kx = 0;
+          ++ky;
+        }
+      }
     }
   };
 
@@ -161,12 +225,10 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
     T* As = smem + buf * STAGE;
     T* Bs = As + BM * LDA;
 #pragma unroll
-    for (int i = 0; i < A_PER; ++i) *reinterpret_cast<Quad*>(As + ((tid + i * 256) / KQ) * LDA + kq * 4) = ra[i];
+    for (int i = 0; i < A_PER; ++i) *reinterpret_cast<Vec*>(As + (rrow + i * RPP) * LDA + kv * VE) = ra[i];
 #pragma unroll
-    for (int i = 0; i < B_PER; ++i) {
-      int q = tid + i * 256;
-      if (q < B_Q) *reinterpret_cast<Quad*>(Bs + (q / KQ) * LDA + kq * 4) = rb[i];
-    }
+    for (int i = 0; i < B_PER; ++i)
+      if (rrow + i * RPP < BN) *reinterpret_cast<Vec*>(Bs + (rrow + i * RPP) * LDA + kv * VE) = rb[i];
   };
 
   floatx4 acc[TM][TN];
@@ -364,7 +426,26 @@ static void launch_tile(const ConvParams& p, int M, hipStream_t s) {
   // workgroups exit before touching memory (see the tile order above).
   long tiles = (long)((M + BM - 1) / BM) * ((p.Co + BN - 1) / BN);
   dim3 grid((unsigned)((tiles + 7) / 8 * 8));
-  hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN>), grid, dim3(256), 0, s, p);
+  const bool pw = p.kh == 1 && p.kw == 1 && p.sh == 1 && p.sw == 1 && p.pt == 0 && p.pl == 0 && p.Ho == p.H &&
+                  p.Wo == p.W;
+  if constexpr (sizeof(T) == 4) {
+    if (pw)
+      hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, true, 4>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, false, 4>), grid, dim3(256), 0, s, p);
+  } else {
+    // 16-byte loads need every 8-channel group 16-byte aligned.
+    const bool v8 = p.C % 8 == 0 && p.in_ps % 8 == 0 && p.ldw % 8 == 0 &&
+                    reinterpret_cast<uintptr_t>(p.in) % 16 == 0 && reinterpret_cast<uintptr_t>(p.wt) % 16 == 0;
+    if (pw && v8)
+      hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, true, 8>), grid, dim3(256), 0, s, p);
+    else if (pw)
+      hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, true, 4>), grid, dim3(256), 0, s, p);
+    else if (v8)
+      hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, false, 8>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, false, 4>), grid, dim3(256), 0, s, p);
+  }
 }
 
 // Tile choice: narrow output channel counts get tall tiles so no MFMA
