@@ -13,9 +13,13 @@
 //   * fp32: v_mfma_f32_16x16x4f32, four per tile per 16-deep K slice.
 //     bf16: v_mfma_f32_16x16x32_bf16, one per tile per 32-deep K slice, fp32
 //     accumulation.
-//   * Each wave64 owns a TM x TN grid of 16x16 accumulators.  LDS is
-//     double-buffered: the next K slice is fetched into registers during the
-//     MFMAs and written to the other buffer, one barrier per slice.
+//   * Each wave64 owns a TM x TN grid of 16x16 accumulators.
+//   * Layers without an SE input gate run conv_gemm_direct_kernel: operand
+//     rows are loaded straight into LDS (global_load_lds_dwordx4) through a
+//     3- or 4-stage pipeline.  Gated layers (the gate multiplies A while it
+//     is gathered) and bf16 layers whose channel count is not a multiple of 8
+//     run conv_gemm_kernel: the next K slice is fetched into registers during
+//     the MFMAs and written to the other of two LDS buffers.
 //   * The epilogue stages the fp32 tile through LDS and finishes it with
 //     row-contiguous vector accesses: bias, activation, SE gate on the input
 //     (applied while gathering A), a (gated) residual add, a
@@ -79,6 +83,10 @@ __device__ __forceinline__ uint4 gate_vec(uint4 v, const float* g) {
   return make_uint4(gate_pair(v.x, a.x, a.y), gate_pair(v.y, a.z, a.w), gate_pair(v.z, b.x, b.y),
                     gate_pair(v.w, b.z, b.w));
 }
+
+template <typename T, int BM, int BN, int WM, int WN, typename RowPtr>
+__device__ __forceinline__ void finish_tile(const ConvParams& p, const floatx4 (&acc)[BM / (WM * 16)][BN / (WN * 16)],
+                                            RowPtr row_ptr, int m0, int n0, int M, int n_tiles);
 
 // PW: 1x1 convolution with stride 1 and no padding, where an output pixel
 // reads exactly its own input pixel and A rows are plain strided rows.
@@ -177,12 +185,11 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
     kx = tap - ky * p.kw;
   }
 
-  Vec ra[A_PER];
-  Vec rb[B_PER];
+  Vec ra[A_PER], rb[B_PER];
 
   // Loads the K slice starting at k0 (called for k0 = 0, BK, 2 BK, ... in
   // order) into registers.
-  auto load_tile = [&](int k0) {
+  auto load_tile = [&](Vec(&ra)[A_PER], Vec(&rb)[B_PER], int k0) {
     const int k = k0 + kv * VE;
     const bool kin = k < K;
 #pragma unroll
@@ -221,7 +228,7 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
     }
   };
 
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](const Vec(&ra)[A_PER], const Vec(&rb)[B_PER], int buf) {
     T* As = smem + buf * STAGE;
     T* Bs = As + BM * LDA;
 #pragma unroll
@@ -245,12 +252,7 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
   const int g = lane >> 4;
   const int nk = (K + BK - 1) / BK;
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  for (int s = 0; s < nk; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < nk) load_tile((s + 1) * BK);
+  auto compute = [&](int buf) {
     const T* As = smem + buf * STAGE;
     const T* Bs = As + BM * LDA;
     if constexpr (sizeof(T) == 4) {
@@ -295,20 +297,52 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
-    if (s + 1 < nk) store_tile(buf ^ 1);
+  };
+
+  // Double-buffered LDS: the next slice's loads are in flight in registers
+  // while this slice is multiplied, then stored to the other buffer.
+  load_tile(ra, rb, 0);
+  store_tile(ra, rb, 0);
+  __syncthreads();
+  for (int s = 0; s < nk; ++s) {
+    if (s + 1 < nk) load_tile(ra, rb, (s + 1) * BK);
+    compute(s & 1);
+    if (s + 1 < nk) store_tile(ra, rb, (s + 1) & 1);
     __syncthreads();
   }
 
+  float* stage = reinterpret_cast<float*>(smem_raw);
+  finish_tile<T, BM, BN, WM, WN>(
+      p, acc, [=](int row) { return stage + row * LDE; }, m0, n0, M, n_tiles);
+}
+
+// Stages the fp32 accumulator tile in LDS and finishes it: the greedy-CTC
+// row reduction, or bias, activation, (gated) residual, upsample-add and the
+// store (plain, fp32, or upsample-on-write).  row_ptr(r) is the LDS address
+// of staged row r (BN + 4 floats).  Caller has passed a barrier after its
+// last read of the LDS operand buffers.
+template <typename T, int BM, int BN, int WM, int WN, typename RowPtr>
+__device__ __forceinline__ void finish_tile(const ConvParams& p, const floatx4 (&acc)[BM / (WM * 16)][BN / (WN * 16)],
+                                            RowPtr row_ptr, int m0, int n0, int M, int n_tiles) {
+  constexpr int TM = BM / (WM * 16);
+  constexpr int TN = BN / (WN * 16);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int lrow = lane & 15;
+  const int g = lane >> 4;
+  const int HoWo = p.Ho * p.Wo;
+
   // Stage the fp32 tile in LDS as [m][n].  Accumulator element e of lane l
   // in tile (i, j) is row 4*(l/16) + e, column l%16 of that 16x16 tile.
-  float* stage = reinterpret_cast<float*>(smem_raw);
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        stage[(wm * TM * 16 + i * 16 + g * 4 + e) * LDE + wn * TN * 16 + j * 16 + lrow] = acc[i][j][e];
+        row_ptr(wm * TM * 16 + i * 16 + g * 4 + e)[wn * TN * 16 + j * 16 + lrow] = acc[i][j][e];
   __syncthreads();
 
   // Greedy-CTC classifier epilogue: each row's (max logit, sum of
@@ -321,7 +355,7 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
     const int row = tid / TPR, sub = tid % TPR;
     const int c0 = sub * CPT;
     const int nc = min(CPT, p.Co - (n0 + c0));  // valid columns of this lane
-    const float* srow = stage + row * LDE + c0;
+    const float* srow = row_ptr(row) + c0;
     const float* brow = p.bias + n0 + c0;
     float mx = -INFINITY, sum = 0.0f;
     int idx = -1;
@@ -365,7 +399,7 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
     const int m = m0 + row;
     const int col = n0 + cq * 4;
     if (m >= M || col >= p.Co) continue;
-    float4 v = *reinterpret_cast<const float4*>(stage + row * LDE + cq * 4);
+    float4 v = *reinterpret_cast<const float4*>(row_ptr(row) + cq * 4);
     int img = m / HoWo, oy = 0, ox = 0;
     if (need_coords) {
       int r = m - img * HoWo;
@@ -420,6 +454,300 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Direct-to-LDS variant (layers without an SE input gate, 16-byte k vectors).
+// global_load_lds_dwordx4 writes each lane's 16 bytes straight into LDS, so
+// the operands never pass through registers and S K slices are in flight at
+// once: slice s is multiplied while slices s+1 .. s+S-1 load.  LDS rows are
+// 64 bytes (one K slice of one tile row) with no padding; the four 16-byte
+// vectors of row r are stored at positions v ^ ((r >> 2) & 3), which makes
+// the MFMA operand reads (16 rows, one vector position) conflict-free.  A
+// lane's LDS destination is fixed (base + 16 * lane), so the swizzle is
+// applied by choosing which global vector each lane fetches.  Masked loads
+// (padding taps, rows past M, k past K) read a 16-byte zero block.  The
+// kernel orders its loads and LDS reads itself: explicit vmcnt waits before
+// each barrier, and operand reads issued as inline assembly, which the
+// compiler's wait insertion does not see (it would otherwise wait for every
+// load in flight before each read).
+
+__device__ __attribute__((aligned(16))) float g_conv_zero[4];
+
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// s_waitcnt with only the vector-memory count bounded (expcnt and lgkmcnt at
+// their maxima): waits until at most N of this wave's loads are in flight.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Execution barrier without the memory fence of __syncthreads(), whose
+// release would wait for every load in flight (vmcnt(0)) and so drain the
+// pipeline.  The operand loads are ordered by the explicit vmcnt waits; the
+// empty asm statements keep the compiler from moving LDS accesses across.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// One 16-byte global -> LDS load per lane (LDS destination base + 16 * lane,
+// base wave-uniform).
+__device__ __forceinline__ void lds_dma16(const void* src, char* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_ptr)lds_base, 16, 0, 0);
+}
+
+// LDS offset of a __shared__ address.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// 16-byte LDS read issued as inline assembly; the value is usable only
+// after lds_wait() on it.
+__device__ __forceinline__ floatx4 lds_read16(unsigned addr) {
+  floatx4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+// Waits for the LDS reads in flight; taking the value as an operand orders
+// its uses after the wait.
+__device__ __forceinline__ void lds_wait(floatx4& v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v)); }
+
+template <typename T, int BM, int BN, int WM, int WN, bool PW, int S>
+__global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
+  constexpr int BK = GemmTraits<T>::BK;  // one 64-byte row per K slice
+  constexpr int VE = 16 / sizeof(T);
+  constexpr int TM = BM / (WM * 16);
+  constexpr int TN = BN / (WN * 16);
+  static_assert(WM * WN == 4, "four waves per block");
+  static_assert(BM % 64 == 0, "A rows load in passes of 64");
+  static_assert(S == 3 || S == 4, "three or four stages");
+  constexpr int A_PASS = BM / 64;
+  constexpr int B_PASS = (BN + 63) / 64;
+  constexpr int STAGE_BYTES = (BM + BN) * 64;
+  constexpr int LDE = BN + 4;
+  constexpr int RPA = (BM + S - 1) / S;  // epilogue rows staged per stage array
+  constexpr int PART = STAGE_BYTES > RPA * LDE * 4 ? STAGE_BYTES : RPA * LDE * 4;
+  __shared__ __attribute__((aligned(16))) char st0[PART];
+  __shared__ __attribute__((aligned(16))) char st1[PART];
+  __shared__ __attribute__((aligned(16))) char st2[PART];
+  __shared__ __attribute__((aligned(16))) char st3[S == 4 ? PART : 16];
+
+  const T* in = static_cast<const T*>(p.in);
+  const T* wt = static_cast<const T*>(p.wt);
+  const T* zero = reinterpret_cast<const T*>(g_conv_zero);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases and wait counts
+  const int wm = wave / WN, wn = wave % WN;
+  const int HoWo = p.Ho * p.Wo;
+  // Stage j's LDS array (j is a constant at every call site once inlined).
+  auto pick = [&](int j) -> char* { return j == 0 ? st0 : j == 1 ? st1 : j == 2 ? st2 : st3; };
+  const int M = p.N * HoWo;
+  const int K = p.kh * p.kw * p.C;
+
+  // XCD-aware tile order (as conv_gemm_kernel).
+  const int n_tiles = (p.Co + BN - 1) / BN;
+  const int m_tiles = (M + BM - 1) / BM;
+  const int per_xcd = gridDim.x / 8;
+  const int t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (t >= m_tiles * n_tiles) return;
+  const int m0 = (t / n_tiles) * BM;
+  const int n0 = (t % n_tiles) * BN;
+
+  // This lane fills LDS row pass*64 + prow, position lane % 4, with k vector
+  // kvec of its source row (the swizzle: (prow >> 2) & 3 == lane >> 4).
+  const int prow = wave * 16 + (lane >> 2);
+  const int kvec = (lane & 3) ^ (lane >> 4);
+
+  const T* a_ptr[A_PASS];
+  int a_iy0[A_PASS], a_ix0[A_PASS];
+  bool a_ok[A_PASS];
+#pragma unroll
+  for (int i = 0; i < A_PASS; ++i) {
+    const int m = m0 + i * 64 + prow;
+    a_ok[i] = m < M;
+    const int mm = a_ok[i] ? m : 0;
+    const int img = mm / HoWo;
+    if constexpr (PW) {
+      a_ptr[i] = in + (size_t)mm * p.in_ps;
+      a_iy0[i] = a_ix0[i] = 0;
+    } else {
+      const int r = mm - img * HoWo;
+      const int oy = r / p.Wo;
+      const int ox = r - oy * p.Wo;
+      a_ptr[i] = in + (size_t)img * p.H * p.W * p.in_ps;
+      a_iy0[i] = oy * p.sh - p.pt;
+      a_ix0[i] = ox * p.sw - p.pl;
+    }
+  }
+  const T* b_ptr[B_PASS];
+  bool b_ok[B_PASS];
+#pragma unroll
+  for (int i = 0; i < B_PASS; ++i) {
+    const int r = i * 64 + prow;
+    const int n = n0 + r;
+    b_ok[i] = r < BN && n < p.Co;
+    b_ptr[i] = wt + (size_t)(b_ok[i] ? n : 0) * p.ldw;
+  }
+
+  int kc = kvec * VE, kx = 0, ky = 0;
+  if constexpr (!PW) {
+    const int tap = kc / p.C;
+    kc -= tap * p.C;
+    ky = tap / p.kw;
+    kx = tap - ky * p.kw;
+  }
+
+  // Issues the loads of the K slice at k0 (in order k0 = 0, BK, ...).
+  auto issue = [&](int j, int k0) {
+    char* stage = pick(j);
+    const int k = k0 + kvec * VE;
+    const bool kin = k < K;
+#pragma unroll
+    for (int i = 0; i < A_PASS; ++i) {
+      const T* src = zero;
+      if constexpr (PW) {
+        if (kin && a_ok[i]) src = a_ptr[i] + k;
+      } else {
+        const int iy = a_iy0[i] + ky;
+        const int ix = a_ix0[i] + kx;
+        if (kin && a_ok[i] && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W)
+          src = a_ptr[i] + ((size_t)iy * p.W + ix) * p.in_ps + kc;
+      }
+      lds_dma16(src, stage + (i * 64 + wave * 16) * 64);
+    }
+#pragma unroll
+    for (int i = 0; i < B_PASS; ++i) {
+      if (i * 64 + wave * 16 < BN) {
+        const T* src = kin && b_ok[i] ? b_ptr[i] + k : zero;
+        lds_dma16(src, stage + (BM + i * 64 + wave * 16) * 64);
+      }
+    }
+    if constexpr (!PW) {
+      kc += BK;
+      while (kc >= p.C) {
+        kc -= p.C;
+        if (++kx == p.kw) {
+          kx = 0;
+          ++ky;
+        }
+      }
+    }
+  };
+
+  floatx4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int lrow = lane & 15;
+  const int g = lane >> 4;
+  const int swz = (g ^ (lrow >> 2)) << 4;  // byte offset of this lane's vector in its row
+
+  // Operand reads go through lds_read16 (outside the compiler's view): the
+  // compiler cannot tell the stage being read from the stages being filled
+  // by the loads in flight and would otherwise wait for all of them before
+  // every LDS read, draining the pipeline.
+  auto compute = [&](int j) {
+    const unsigned stage = lds_addr(pick(j));
+    floatx4 ra[TM], rb[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) ra[i] = lds_read16(stage + (wm * TM * 16 + i * 16 + lrow) * 64 + swz);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) rb[j] = lds_read16(stage + (BM + wn * TN * 16 + j * 16 + lrow) * 64 + swz);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) lds_wait(ra[i]);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) lds_wait(rb[j]);
+    if constexpr (sizeof(T) == 4) {
+      float4 a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = make_float4(ra[i][0], ra[i][1], ra[i][2], ra[i][3]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j] = make_float4(rb[j][0], rb[j][1], rb[j][2], rb[j][3]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
+    } else {
+      bf16x8 a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = __builtin_bit_cast(bf16x8, ra[i]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j] = __builtin_bit_cast(bf16x8, rb[j]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  const int nk = (K + BK - 1) / BK;
+  // One pipeline step: wait for slice s (slices s+1 .. s+S-2 may still be
+  // loading), barrier (all waves' loads of slice s are in LDS and every wave
+  // is done with slice s-1), refill the stage slice s-1 used with slice
+  // s+S-1, multiply slice s.
+  // Loads per wave per slice counted by the waits: the A passes, plus the B
+  // passes when every wave takes part in them (BN >= 64).  With BN < 64 only
+  // some waves load B; counting A alone makes those waves wait a little
+  // longer than needed, never less.
+  constexpr int L = A_PASS + (BN >= 64 ? B_PASS : 0);
+  auto step = [&](int cur, int refill, int s) {
+    const int after = nk - 1 - s;  // slices issued after s (capped at S - 2)
+    if (after >= S - 2)
+      wait_vmcnt<(S - 2) * L>();
+    else if (S == 4 && after == 1)
+      wait_vmcnt<L>();
+    else
+      wait_vmcnt<0>();
+    stage_barrier();
+    if (s + S - 1 < nk) issue(refill, (s + S - 1) * BK);
+    compute(cur);
+  };
+  issue(0, 0);
+  if (nk > 1) issue(1, BK);
+  if (S == 4 && nk > 2) issue(2, 2 * BK);
+  for (int s = 0; s < nk; s += S) {
+    if constexpr (S == 4) {
+      step(0, 3, s);
+      if (s + 1 < nk) step(1, 0, s + 1);
+      if (s + 2 < nk) step(2, 1, s + 2);
+      if (s + 3 < nk) step(3, 2, s + 3);
+    } else {
+      step(0, 2, s);
+      if (s + 1 < nk) step(1, 0, s + 1);
+      if (s + 2 < nk) step(2, 1, s + 2);
+    }
+  }
+  wait_vmcnt<0>();  // every stage load has landed (the compiler does not count them all)
+  __syncthreads();
+
+  finish_tile<T, BM, BN, WM, WN>(
+      p, acc,
+      [&](int row) {
+        const int part = row / RPA;
+        char* base = part == 0 ? st0 : part == 1 ? st1 : part == 2 ? st2 : st3;
+        return reinterpret_cast<float*>(base) + (row - part * RPA) * LDE;
+      },
+      m0, n0, M, n_tiles);
+}
+
 template <typename T, int BM, int BN, int WM, int WN>
 static void launch_tile(const ConvParams& p, int M, hipStream_t s) {
   // One-dimensional grid rounded up to a multiple of the 8 XCDs; surplus
@@ -428,6 +756,17 @@ static void launch_tile(const ConvParams& p, int M, hipStream_t s) {
   dim3 grid((unsigned)((tiles + 7) / 8 * 8));
   const bool pw = p.kh == 1 && p.kw == 1 && p.sh == 1 && p.sw == 1 && p.pt == 0 && p.pl == 0 && p.Ho == p.H &&
                   p.Wo == p.W;
+  constexpr int VE16 = 16 / sizeof(T);
+  const bool v16 = p.C % VE16 == 0 && p.in_ps % VE16 == 0 && p.ldw % VE16 == 0 &&
+                   reinterpret_cast<uintptr_t>(p.in) % 16 == 0 && reinterpret_cast<uintptr_t>(p.wt) % 16 == 0;
+  if (!p.in_gate && v16) {
+    constexpr int S = (BM + BN) * 64 <= 10240 ? 4 : 3;  // stages: about 40 KB of LDS at most
+    if (pw)
+      hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, false, S>), grid, dim3(256), 0, s, p);
+    return;
+  }
   if constexpr (sizeof(T) == 4) {
     if (pw)
       hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, true, 4>), grid, dim3(256), 0, s, p);
