@@ -788,12 +788,14 @@ static void launch_tile(const ConvParams& p, int M, hipStream_t s) {
 }
 
 // Tile choice: narrow output channel counts get tall tiles so no MFMA
-// column is wasted; wide layers take 128x64 when that still gives every CU
-// several blocks.
-static int pick_tile(int M, int cols) {
+// column is wasted.  Wide layers: fp32 takes 64x64 (its MFMA is slow enough
+// that the smaller tile's occupancy wins); bf16 takes 128x64 when that
+// still gives every CU several blocks (its faster MFMA needs the operand
+// reuse of the taller tile).
+static int pick_tile(int M, int cols, int dt) {
   if (cols <= 16) return 0;
   if (cols <= 32) return 1;
-  if ((long)((M + 127) / 128) * ((cols + 63) / 64) >= 2048) return 2;
+  if (dt == DT_BF16 && (long)((M + 127) / 128) * ((cols + 63) / 64) >= 2048) return 2;
   return 3;
 }
 
@@ -801,18 +803,18 @@ const char* conv_tile_name(int M, int cols, int dt) {
   static const char* f32[] = {"conv_gemm<256x16>", "conv_gemm<128x32>", "conv_gemm<128x64>", "conv_gemm<64x64>"};
   static const char* b16[] = {"conv_gemm_bf16<256x16>", "conv_gemm_bf16<128x32>", "conv_gemm_bf16<128x64>",
                               "conv_gemm_bf16<64x64>"};
-  return (dt == DT_BF16 ? b16 : f32)[pick_tile(M, cols)];
+  return (dt == DT_BF16 ? b16 : f32)[pick_tile(M, cols, dt)];
 }
 
-int conv_tile_cols(int M, int cols) {
+int conv_tile_cols(int M, int cols, int dt) {
   static const int bn[] = {16, 32, 64, 64};
-  return bn[pick_tile(M, cols)];
+  return bn[pick_tile(M, cols, dt)];
 }
 
 template <typename T>
 static void launch_typed(const ConvParams& p, hipStream_t s) {
   int M = p.N * p.Ho * p.Wo;
-  switch (pick_tile(M, p.Co)) {
+  switch (pick_tile(M, p.Co, p.dt)) {
     case 0: launch_tile<T, 256, 16, 4, 1>(p, M, s); break;
     case 1: launch_tile<T, 128, 32, 4, 1>(p, M, s); break;
     case 2: launch_tile<T, 128, 64, 2, 2>(p, M, s); break;

@@ -95,7 +95,7 @@ void launch_conv(const ConvParams& p, hipStream_t s);
 // Name of the kernel instance launch_conv picks for M rows x `cols` columns.
 const char* conv_tile_name(int M, int cols, int dt);
 // Column width of that instance's tiles.
-int conv_tile_cols(int M, int cols);
+int conv_tile_cols(int M, int cols, int dt);
 // Merges the greedy-CTC partials of launch_conv into one (class, probability)
 // pair per row: out[m] = {argmax (ties -> last index), softmax value of it}.
 void launch_ctc_merge(const float* part, int M, int n_tiles, float* out, hipStream_t s);

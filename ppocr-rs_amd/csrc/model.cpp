@@ -489,7 +489,8 @@ class Builder {
       raise(PPOCR_ERR_INVALID_MODEL, name + ": greedy classifier takes [N, 1, T, C] rows");
     if (w.b == NOW) raise(PPOCR_ERR_INVALID_MODEL, name + ": classifier needs a bias");
     const int M = x.n * x.w;
-    const int tiles = (w.co + conv_tile_cols(M, w.co) - 1) / conv_tile_cols(M, w.co);
+    const int bn = conv_tile_cols(M, w.co, x.dt);
+    const int tiles = (w.co + bn - 1) / bn;
     if ((size_t)3 * tiles * M > (size_t)INT32_MAX) raise(PPOCR_ERR_INVALID_INPUT, name + ": batch too large");
     View part = alloc(1, 1, 1, 3 * tiles * M, name + ".partials", DT_F32);
     View out = alloc(x.n, 1, x.w, 2, "output", DT_F32);
