@@ -174,10 +174,16 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
     b_ptr[i] = wt + (size_t)(b_ok[i] ? n : 0) * p.ldw;
   }
 
+  // K slices of this workgroup: all of them, or its split's share.
+  const int nk_all = (K + BK - 1) / BK;
+  const int s_begin = (int)((long)blockIdx.y * nk_all / gridDim.y);
+  const int nk = (int)((long)(blockIdx.y + 1) * nk_all / gridDim.y) - s_begin;
+  const int kbase = s_begin * BK;
+
   // Decomposition of this lane's k = k0 + kv*VE into (ky, kx, c), kept up to
   // date as the K slices advance (one division at the start, none in the
   // loop).  A vector never straddles a tap: C is a multiple of VE.
-  int kc = kv * VE, kx = 0, ky = 0;
+  int kc = kbase + kv * VE, kx = 0, ky = 0;
   if constexpr (!PW) {
     const int tap = kc / p.C;
     kc -= tap * p.C;
@@ -187,8 +193,8 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
 
   Vec ra[A_PER], rb[B_PER];
 
-  // Loads the K slice starting at k0 (called for k0 = 0, BK, 2 BK, ... in
-  // order) into registers.
+  // Loads the K slice starting at k0 (called for k0 = kbase, kbase + BK,
+  // ... in order) into registers.
   auto load_tile = [&](Vec(&ra)[A_PER], Vec(&rb)[B_PER], int k0) {
     const int k = k0 + kv * VE;
     const bool kin = k < K;
@@ -250,7 +256,6 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
   // is the same for A and B, so the products pair up unchanged.
   const int lrow = lane & 15;
   const int g = lane >> 4;
-  const int nk = (K + BK - 1) / BK;
 
   auto compute = [&](int buf) {
     const T* As = smem + buf * STAGE;
@@ -301,11 +306,11 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
 
   // Double-buffered LDS: the next slice's loads are in flight in registers
   // while this slice is multiplied, then stored to the other buffer.
-  load_tile(ra, rb, 0);
+  load_tile(ra, rb, kbase);
   store_tile(ra, rb, 0);
   __syncthreads();
   for (int s = 0; s < nk; ++s) {
-    if (s + 1 < nk) load_tile(ra, rb, (s + 1) * BK);
+    if (s + 1 < nk) load_tile(ra, rb, kbase + (s + 1) * BK);
     compute(s & 1);
     if (s + 1 < nk) store_tile(ra, rb, (s + 1) & 1);
     __syncthreads();
@@ -316,10 +321,14 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
       p, acc, [=](int row) { return stage + row * LDE; }, m0, n0, M, n_tiles);
 }
 
-// Stages the fp32 accumulator tile in LDS and finishes it: the greedy-CTC
-// row reduction, or bias, activation, (gated) residual, upsample-add and the
-// store (plain, fp32, or upsample-on-write).  row_ptr(r) is the LDS address
-// of staged row r (BN + 4 floats).  Caller has passed a barrier after its
+template <typename T, int BM, int BN, typename RowPtr>
+__device__ __forceinline__ void finish_staged(const ConvParams& p, RowPtr row_ptr, int m0, int n0, int M,
+                                              int n_tiles);
+
+// Stages the fp32 accumulator tile in LDS as [m][n] (row_ptr(r): LDS
+// address of staged row r, BN + 4 floats) and finishes it: with split K
+// (p.splits > 1) the tile goes to this split's plane of the workspace as is,
+// otherwise through the epilogue.  Caller has passed a barrier after its
 // last read of the LDS operand buffers.
 template <typename T, int BM, int BN, int WM, int WN, typename RowPtr>
 __device__ __forceinline__ void finish_tile(const ConvParams& p, const floatx4 (&acc)[BM / (WM * 16)][BN / (WN * 16)],
@@ -332,10 +341,9 @@ __device__ __forceinline__ void finish_tile(const ConvParams& p, const floatx4 (
   const int wm = wave / WN, wn = wave % WN;
   const int lrow = lane & 15;
   const int g = lane >> 4;
-  const int HoWo = p.Ho * p.Wo;
 
-  // Stage the fp32 tile in LDS as [m][n].  Accumulator element e of lane l
-  // in tile (i, j) is row 4*(l/16) + e, column l%16 of that 16x16 tile.
+  // Accumulator element e of lane l in tile (i, j) is row 4*(l/16) + e,
+  // column l%16 of that 16x16 tile.
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -344,6 +352,31 @@ __device__ __forceinline__ void finish_tile(const ConvParams& p, const floatx4 (
       for (int e = 0; e < 4; ++e)
         row_ptr(wm * TM * 16 + i * 16 + g * 4 + e)[wn * TN * 16 + j * 16 + lrow] = acc[i][j][e];
   __syncthreads();
+  if (p.splits > 1) {
+    // Co is a multiple of 4 for split layers: whole float4 rows.
+    float* ws = p.split_ws + (size_t)blockIdx.y * M * p.Co;
+    constexpr int NQ = BN / 4;
+    for (int q = tid; q < BM * NQ; q += 256) {
+      const int row = q / NQ;
+      const int col = n0 + (q - row * NQ) * 4;
+      const int m = m0 + row;
+      if (m < M && col < p.Co)
+        *reinterpret_cast<float4*>(ws + (size_t)m * p.Co + col) =
+            *reinterpret_cast<const float4*>(row_ptr(row) + (col - n0));
+    }
+    return;
+  }
+  finish_staged<T, BM, BN>(p, row_ptr, m0, n0, M, n_tiles);
+}
+
+// Epilogue of a tile staged in LDS: the greedy-CTC row reduction, or bias,
+// activation, (gated) residual, upsample-add and the store (plain, fp32, or
+// upsample-on-write).
+template <typename T, int BM, int BN, typename RowPtr>
+__device__ __forceinline__ void finish_staged(const ConvParams& p, RowPtr row_ptr, int m0, int n0, int M,
+                                              int n_tiles) {
+  const int tid = threadIdx.x;
+  const int HoWo = p.Ho * p.Wo;
 
   // Greedy-CTC classifier epilogue: each row's (max logit, sum of
   // exp(logit - max), last column holding the max) over this tile's columns.
@@ -593,7 +626,13 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
     b_ptr[i] = wt + (size_t)(b_ok[i] ? n : 0) * p.ldw;
   }
 
-  int kc = kvec * VE, kx = 0, ky = 0;
+  // K slices of this workgroup: all of them, or its split's share.
+  const int nk_all = (K + BK - 1) / BK;
+  const int s_begin = (int)((long)blockIdx.y * nk_all / gridDim.y);
+  const int nk = (int)((long)(blockIdx.y + 1) * nk_all / gridDim.y) - s_begin;
+  const int kbase = s_begin * BK;
+
+  int kc = kbase + kvec * VE, kx = 0, ky = 0;
   if constexpr (!PW) {
     const int tap = kc / p.C;
     kc -= tap * p.C;
@@ -601,7 +640,8 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
     kx = tap - ky * p.kw;
   }
 
-  // Issues the loads of the K slice at k0 (in order k0 = 0, BK, ...).
+  // Issues the loads of the K slice at k0 (in order k0 = kbase,
+  // kbase + BK, ...).
   auto issue = [&](int j, int k0) {
     char* stage = pick(j);
     const int k = k0 + kvec * VE;
@@ -698,7 +738,6 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
     }
   };
 
-  const int nk = (K + BK - 1) / BK;
   // One pipeline step: wait for slice s (slices s+1 .. s+S-2 may still be
   // loading), barrier (all waves' loads of slice s are in LDS and every wave
   // is done with slice s-1), refill the stage slice s-1 used with slice
@@ -717,12 +756,12 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
     else
       wait_vmcnt<0>();
     stage_barrier();
-    if (s + S - 1 < nk) issue(refill, (s + S - 1) * BK);
+    if (s + S - 1 < nk) issue(refill, kbase + (s + S - 1) * BK);
     compute(cur);
   };
-  issue(0, 0);
-  if (nk > 1) issue(1, BK);
-  if (S == 4 && nk > 2) issue(2, 2 * BK);
+  issue(0, kbase);
+  if (nk > 1) issue(1, kbase + BK);
+  if (S == 4 && nk > 2) issue(2, kbase + 2 * BK);
   for (int s = 0; s < nk; s += S) {
     if constexpr (S == 4) {
       step(0, 3, s);
@@ -748,12 +787,46 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
       m0, n0, M, n_tiles);
 }
 
+// Split-K finish: one workgroup per 16x64 output tile, one float4 of it per
+// lane.  A lane issues the loads of all its split partials at once (the
+// reduction is short and latency-bound), adds them in split order, stages
+// the sum in LDS and the tile runs the epilogue.
+constexpr int kMaxSplits = 16;
+constexpr int kFinishBM = 16, kFinishBN = 64;
+
+template <typename T>
+__global__ __launch_bounds__(256) void conv_splitk_finish_kernel(ConvParams p) {
+  constexpr int LDE = kFinishBN + 4;
+  constexpr int NQ = kFinishBN / 4;
+  static_assert(kFinishBM * NQ == 256, "one float4 per lane");
+  __shared__ __attribute__((aligned(16))) float stage[kFinishBM * LDE];
+  const int M = p.N * p.Ho * p.Wo;
+  const int n_tiles = (p.Co + kFinishBN - 1) / kFinishBN;
+  const int m0 = (int)(blockIdx.x / n_tiles) * kFinishBM;
+  const int n0 = (int)(blockIdx.x % n_tiles) * kFinishBN;
+  const size_t plane = (size_t)M * p.Co;
+  const int row = threadIdx.x / NQ;
+  const int c = (threadIdx.x % NQ) * 4;
+  const int m = m0 + row;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (m < M && n0 + c < p.Co) {
+    const float* src = p.split_ws + (size_t)m * p.Co + n0 + c;
+    float4 part[kMaxSplits];
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplits; ++sp)
+      if (sp < p.splits) part[sp] = *reinterpret_cast<const float4*>(src + sp * plane);
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplits; ++sp)
+      if (sp < p.splits) v = f4_add(v, part[sp]);
+  }
+  *reinterpret_cast<float4*>(stage + row * LDE + c) = v;
+  __syncthreads();
+  finish_staged<T, kFinishBM, kFinishBN>(
+      p, [&](int row) { return stage + row * LDE; }, m0, n0, M, n_tiles);
+}
+
 template <typename T, int BM, int BN, int WM, int WN>
-static void launch_tile(const ConvParams& p, int M, hipStream_t s) {
-  // One-dimensional grid rounded up to a multiple of the 8 XCDs; surplus
-  // workgroups exit before touching memory (see the tile order above).
-  long tiles = (long)((M + BM - 1) / BM) * ((p.Co + BN - 1) / BN);
-  dim3 grid((unsigned)((tiles + 7) / 8 * 8));
+static void launch_tile_kernel(const ConvParams& p, dim3 grid, hipStream_t s) {
   const bool pw = p.kh == 1 && p.kw == 1 && p.sh == 1 && p.sw == 1 && p.pt == 0 && p.pl == 0 && p.Ho == p.H &&
                   p.Wo == p.W;
   constexpr int VE16 = 16 / sizeof(T);
@@ -787,6 +860,20 @@ static void launch_tile(const ConvParams& p, int M, hipStream_t s) {
   }
 }
 
+template <typename T, int BM, int BN, int WM, int WN>
+static void launch_tile(const ConvParams& p, int M, hipStream_t s) {
+  // Grid rows of workgroups rounded up to a multiple of the 8 XCDs; surplus
+  // workgroups exit before touching memory (see the tile order above).  With
+  // split K, grid row y takes split y.
+  const long tiles = (long)((M + BM - 1) / BM) * ((p.Co + BN - 1) / BN);
+  const int splits = p.splits > 1 ? p.splits : 1;
+  launch_tile_kernel<T, BM, BN, WM, WN>(p, dim3((unsigned)((tiles + 7) / 8 * 8), (unsigned)splits), s);
+  if (splits > 1) {
+    const long fin = (long)((M + kFinishBM - 1) / kFinishBM) * ((p.Co + kFinishBN - 1) / kFinishBN);
+    hipLaunchKernelGGL(conv_splitk_finish_kernel<T>, dim3((unsigned)fin), dim3(256), 0, s, p);
+  }
+}
+
 // Tile choice: narrow output channel counts get tall tiles so no MFMA
 // column is wasted.  Wide layers: fp32 takes 64x64 (its MFMA is slow enough
 // that the smaller tile's occupancy wins); bf16 takes 128x64 when that
@@ -809,6 +896,23 @@ const char* conv_tile_name(int M, int cols, int dt) {
 int conv_tile_cols(int M, int cols, int dt) {
   static const int bn[] = {16, 32, 64, 64};
   return bn[pick_tile(M, cols, dt)];
+}
+
+// Split K when the tiles fill fewer than 192 of the 256 CUs: enough splits
+// for about two workgroups per CU, each split keeping at least 8 K slices
+// (the load pipeline is 3-4 slices deep), at most 16 splits.
+int conv_split_k(int M, int Co, int K, int dt) {
+  static const int bm[] = {256, 128, 128, 64};
+  static const int bn[] = {16, 32, 64, 64};
+  const int t = pick_tile(M, Co, dt);
+  const long tiles = (long)((M + bm[t] - 1) / bm[t]) * ((Co + bn[t] - 1) / bn[t]);
+  const int bk = dt == DT_BF16 ? GemmTraits<bf16>::BK : GemmTraits<float>::BK;
+  const int nk = (K + bk - 1) / bk;
+  if (Co % 4 != 0 || tiles >= 192) return 1;
+  long s = (512 + tiles - 1) / tiles;
+  s = std::min<long>(s, nk / 8);
+  s = std::min<long>(s, kMaxSplits);
+  return s >= 2 ? (int)s : 1;
 }
 
 template <typename T>

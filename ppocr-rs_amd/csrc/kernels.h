@@ -57,6 +57,13 @@ struct ConvParams {
   // tile's max logit, sum of exp(logit - max) and the last column holding the
   // max, stored as three planes [3][n_tiles][M] of floats.
   float* ctc_part;
+  // Split K (splits > 1, from conv_split_k): workgroup row y of the grid
+  // multiplies K slices [y*nk/splits, (y+1)*nk/splits) of its tile and
+  // stores the raw fp32 sums to split_ws [splits][M][Co]; a second kernel
+  // adds the splits in order and runs the epilogue.  Not combined with the
+  // greedy-CTC epilogue.
+  float* split_ws;
+  int splits;
 };
 
 // Depthwise k x k convolution (groups == C), 4 channels per lane.
@@ -96,6 +103,10 @@ void launch_conv(const ConvParams& p, hipStream_t s);
 const char* conv_tile_name(int M, int cols, int dt);
 // Column width of that instance's tiles.
 int conv_tile_cols(int M, int cols, int dt);
+// K splits for a convolution of M rows, Co columns and reduction depth K:
+// more than 1 when its tiles alone would leave most of the 256 CUs idle and
+// K is deep enough to divide (the workspace is splits * M * Co floats).
+int conv_split_k(int M, int Co, int K, int dt);
 // Merges the greedy-CTC partials of launch_conv into one (class, probability)
 // pair per row: out[m] = {argmax (ties -> last index), softmax value of it}.
 void launch_ctc_merge(const float* part, int M, int n_tiles, float* out, hipStream_t s);

@@ -265,9 +265,15 @@ class Builder {
     base.out_h = oh, base.out_w = ow;
     base.dt = x.dt;
     size_t wo = w.w, bo = w.b;
+    // Split-K workspace [splits][M][Co] fp32, live for this op only.
+    const int splits = conv_split_k(x.n * Ho * Wo, w.co, w.kh * w.kw * x.c, x.dt);
+    View ws;
+    if (splits > 1) ws = alloc(1, splits, x.n * Ho * Wo, w.co, name + ".split_k", DT_F32);
+    base.splits = splits;
     Op op;
     op.name = name;
     op.kernel = conv_tile_name(x.n * Ho * Wo, w.co, x.dt);
+    if (splits > 1) op.kernel += "+split_k" + std::to_string(splits);
     op.bound = 1;
     const double es = (double)dtype_size(x.dt);
     double M = (double)x.n * Ho * Wo;
@@ -283,6 +289,7 @@ class Builder {
     if (has_ig) op.reads.push_back(ig.buf);
     if (has_up) op.reads.push_back(up.buf);
     op.writes = {out.buf};
+    if (splits > 1) op.writes.push_back(ws.buf);
     op.launch = [=](const Exec& ex, hipStream_t s) {
       ConvParams p = base;
       p.in = ex.ptr(in);
@@ -293,6 +300,7 @@ class Builder {
       p.res = has_res ? ex.ptr(res) : nullptr;
       p.res_gate = has_rg ? ex.fptr(rg) : nullptr;
       p.up = has_up ? ex.ptr(up) : nullptr;
+      p.split_ws = splits > 1 ? ex.fptr(ws) : nullptr;
       launch_conv(p, s);
     };
     add_op(std::move(op));
