@@ -35,7 +35,7 @@ __device__ __forceinline__ float4 f4_sum(float4 a, float4 b) {
 // Replaces WGSL `depthwise` (src/gpu/shaders/depthwise.wgsl:77); semantics of
 // the reference CPU depthwise (src/cpu/ops.rs:385-826): zero padding, bias,
 // activation, then optional residual add (x + act(dw(x) + b)).  This generic
-// form serves the stride-2 layers.
+// form serves the shapes the strip and tiled kernels below do not cover.
 template <typename T>
 __global__ __launch_bounds__(256) void depthwise_kernel(DwParams p) {
   const T* in = static_cast<const T*>(p.in);
@@ -155,6 +155,88 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
   }
 }
 
+// Depthwise as vertical strips, no LDS: a lane owns four channels of R
+// consecutive output rows at one x (vertical stride SH, horizontal stride
+// p.sw).  It walks the (R - 1) * SH + KH input rows of its strip once,
+// loading the KW pixels of each row (the neighbouring x lanes load the same
+// pixels, so they come from L1/L2 and HBM sees each input about once), and
+// adds each row into every output row it touches.  The taps stay in
+// registers.  Output row r receives its input rows in increasing ky and
+// each row in increasing kx: the (ky, kx) tap order of the generic kernel.
+// Lanes run channels fastest, then x, so every load and store of a wave is
+// one contiguous run.
+template <typename T, int KH, int KW, int R, int SH>
+__global__ __launch_bounds__(256) void depthwise_strip_kernel(DwParams p) {
+  const T* in = static_cast<const T*>(p.in);
+  const int C4 = p.C >> 2;
+  const int strips = (p.Ho + R - 1) / R;
+  long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  const long total = (long)p.N * strips * p.Wo * C4;
+  if (idx >= total) return;
+  const int c4 = (int)(idx % C4);
+  long t = idx / C4;
+  const int ox = (int)(t % p.Wo);
+  t /= p.Wo;
+  const int strip = (int)(t % strips);
+  const int n = (int)(t / strips);
+  const int c = c4 * 4;
+  const int oy0 = strip * R;
+  const int rows = min(R, p.Ho - oy0);
+
+  float4 w[KH * KW];
+#pragma unroll
+  for (int i = 0; i < KH * KW; ++i) w[i] = *reinterpret_cast<const float4*>(p.wt + (size_t)i * p.C + c);
+  float4 acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = f4_zero();
+
+  const T* img = in + (size_t)n * p.H * p.W * p.in_ps + c;
+  const int ix0 = ox * p.sw - p.pl;
+#pragma unroll
+  for (int j = 0; j < (R - 1) * SH + KH; ++j) {  // input row oy0 * SH - pt + j
+    const int iy = oy0 * SH - p.pt + j;
+    if (iy < 0 || iy >= p.H) continue;
+    float4 x[KW];
+#pragma unroll
+    for (int kx = 0; kx < KW; ++kx) {
+      const int ix = ix0 + kx;
+      x[kx] = ix >= 0 && ix < p.W ? ld4<T>(img + ((size_t)iy * p.W + ix) * p.in_ps) : f4_zero();
+    }
+    // Output row r = (j - ky) / SH takes this row as its tap row ky.
+#pragma unroll
+    for (int ky = KH - 1; ky >= 0; --ky) {
+      if (j < ky || (j - ky) % SH != 0) continue;
+      const int r = (j - ky) / SH;
+      if (r >= R) continue;
+#pragma unroll
+      for (int kx = 0; kx < KW; ++kx) {
+        const float4 wk = w[ky * KW + kx];
+        acc[r].x = fmaf(x[kx].x, wk.x, acc[r].x);
+        acc[r].y = fmaf(x[kx].y, wk.y, acc[r].y);
+        acc[r].z = fmaf(x[kx].z, wk.z, acc[r].z);
+        acc[r].w = fmaf(x[kx].w, wk.w, acc[r].w);
+      }
+    }
+  }
+  const float4 b = p.bias ? *reinterpret_cast<const float4*>(p.bias + c) : f4_zero();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (r >= rows) break;
+    float4 v = acc[r];
+    if (p.bias) v = f4_sum(v, b);
+    v = f4_act(p.act, v);
+    const size_t pix = (size_t)(n * p.Ho + oy0 + r) * p.Wo + ox;
+    if (p.res) v = f4_sum(ld4<T>(static_cast<const T*>(p.res) + pix * p.res_ps + c), v);
+    st4<T>(static_cast<T*>(p.out) + pix * p.out_ps + c, v);
+  }
+}
+
+template <typename T, int KH, int KW, int R, int SH>
+static void launch_dw_strip(const DwParams& p, hipStream_t s) {
+  const long total = (long)p.N * ((p.Ho + R - 1) / R) * p.Wo * (p.C / 4);
+  hipLaunchKernelGGL((depthwise_strip_kernel<T, KH, KW, R, SH>), dim3(blocks_for(total)), dim3(256), 0, s, p);
+}
+
 template <typename T, int KH, int KW, int TY>
 static void launch_dw_tiled(const DwParams& p, hipStream_t s) {
   constexpr int TX = 256 / (8 * TY) * 4;
@@ -164,9 +246,14 @@ static void launch_dw_tiled(const DwParams& p, hipStream_t s) {
 
 template <typename T>
 static void launch_dw_typed(const DwParams& p, hipStream_t s) {
+  // 3x3 with vertical stride 2 (stage entries), and maps of at most 4 rows
+  // (the recognizer's last stage), where the LDS tile would load its halo
+  // rows for only a few output rows: vertical strips.
+  if (p.kh == 3 && p.kw == 3 && p.sh == 2) return launch_dw_strip<T, 3, 3, 3, 2>(p, s);
+  if (p.kh == 3 && p.kw == 3 && p.sh == 1 && p.Ho <= 4)
+    return p.Ho == 3 ? launch_dw_strip<T, 3, 3, 3, 1>(p, s) : launch_dw_strip<T, 3, 3, 4, 1>(p, s);
   if (p.sh == 1 && p.sw == 1) {
-    const bool tall = p.Ho >= 16;
-    if (p.kh == 3 && p.kw == 3) return tall ? launch_dw_tiled<T, 3, 3, 8>(p, s) : launch_dw_tiled<T, 3, 3, 2>(p, s);
+    if (p.kh == 3 && p.kw == 3) return launch_dw_tiled<T, 3, 3, 8>(p, s);
     if (p.kh == 5 && p.kw == 5) return launch_dw_tiled<T, 5, 5, 8>(p, s);
     if (p.kh == 7 && p.kw == 7) return launch_dw_tiled<T, 7, 7, 8>(p, s);
     if (p.kh == 9 && p.kw == 9) return launch_dw_tiled<T, 9, 9, 8>(p, s);
@@ -180,8 +267,10 @@ static void launch_dw_typed(const DwParams& p, hipStream_t s) {
 void launch_depthwise(const DwParams& p, hipStream_t s) { DISPATCH_DT(p.dt, launch_dw_typed<T>(p, s)); }
 
 const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho) {
+  if (kh == 3 && kw == 3 && sh == 2) return "depthwise_strip<3x3,s2>";
+  if (kh == 3 && kw == 3 && sh == 1 && Ho <= 4) return "depthwise_strip<3x3>";
   if (sh == 1 && sw == 1) {
-    if (kh == 3 && kw == 3) return Ho >= 16 ? "depthwise_tiled<3x3>" : "depthwise_tiled<3x3,short>";
+    if (kh == 3 && kw == 3) return "depthwise_tiled<3x3>";
     if (kh == kw && (kh == 5 || kh == 7 || kh == 9))
       return kh == 5 ? "depthwise_tiled<5x5>" : kh == 7 ? "depthwise_tiled<7x7>" : "depthwise_tiled<9x9>";
     if (kh == 1 && (kw == 5 || kw == 7) && Ho == 1) return kw == 5 ? "depthwise_tiled<1x5>" : "depthwise_tiled<1x7>";
