@@ -15,15 +15,17 @@
 //     accumulation.
 //   * Each wave64 owns a TM x TN grid of 16x16 accumulators.
 //   * Layers without an SE input gate run conv_gemm_direct_kernel: operand
-//     rows are loaded straight into LDS (global_load_lds_dwordx4) through a
-//     3- or 4-stage pipeline.  Gated layers (the gate multiplies A while it
-//     is gathered) and bf16 layers whose channel count is not a multiple of 8
-//     run conv_gemm_kernel: the next K slice is fetched into registers during
-//     the MFMAs and written to the other of two LDS buffers.
+//     rows are loaded straight into LDS (buffer_load_dwordx4 ... lds)
+//     through a 3- or 4-stage pipeline.  Gated layers (the gate multiplies A
+//     while it is gathered) and bf16 layers whose channel count is not a
+//     multiple of 8 run conv_gemm_kernel: the next K slice is fetched into
+//     registers during the MFMAs and written to the other of two LDS buffers.
 //   * The epilogue stages the fp32 tile through LDS and finishes it with
 //     row-contiguous vector accesses: bias, activation, SE gate on the input
 //     (applied while gathering A), a (gated) residual add, a
 //     nearest-upsample add and an upsample-on-write.
+#include <type_traits>
+
 #include "device_math.h"
 
 namespace ppocr {
@@ -489,21 +491,60 @@ __device__ __forceinline__ void finish_staged(const ConvParams& p, RowPtr row_pt
 
 // ---------------------------------------------------------------------------
 // Direct-to-LDS variant (layers without an SE input gate, 16-byte k vectors).
-// global_load_lds_dwordx4 writes each lane's 16 bytes straight into LDS, so
-// the operands never pass through registers and S K slices are in flight at
-// once: slice s is multiplied while slices s+1 .. s+S-1 load.  LDS rows are
-// 64 bytes (one K slice of one tile row) with no padding; the four 16-byte
-// vectors of row r are stored at positions v ^ ((r >> 2) & 3), which makes
-// the MFMA operand reads (16 rows, one vector position) conflict-free.  A
-// lane's LDS destination is fixed (base + 16 * lane), so the swizzle is
-// applied by choosing which global vector each lane fetches.  Masked loads
-// (padding taps, rows past M, k past K) read a 16-byte zero block.  The
-// kernel orders its loads and LDS reads itself: explicit vmcnt waits before
-// each barrier, and operand reads issued as inline assembly, which the
-// compiler's wait insertion does not see (it would otherwise wait for every
-// load in flight before each read).
+// buffer_load_dwordx4 ... lds writes each lane's 16 bytes straight into LDS,
+// so the operands never pass through registers and S K slices are in flight
+// at once: slice s is multiplied while slices s+1 .. s+S-1 load.  The loads
+// address the activation and weight tensors through buffer resources: lane
+// offsets are 32-bit, and a masked lane (padding tap, row past M, k past K)
+// gets an offset past the end of the buffer, which the hardware reads as
+// zero.  For 1x1 layers a lane's offset is fixed for the whole K loop and
+// the slice's k moves in the scalar offset, so the loop spends no vector
+// instructions on addresses.  LDS rows are 64 bytes (one K slice of one
+// tile row) with no padding; the four 16-byte vectors of row r are stored
+// at positions v ^ swizzle_key(r), which makes the MFMA operand reads (16
+// rows, one vector position) conflict-free whether the LDS serves 8 or 16
+// lanes of a 16-byte read per cycle.  A lane's LDS destination is fixed
+// (base + 16 * lane), so the swizzle is applied by choosing which global
+// vector each lane fetches.  The kernel orders its loads and LDS reads
+// itself: explicit vmcnt waits before each barrier, and operand reads issued
+// as inline assembly, which the compiler's wait insertion does not see (it
+// would otherwise wait for every load in flight before each read).
 
-__device__ __attribute__((aligned(16))) float g_conv_zero[4];
+typedef int int32x4_t __attribute__((ext_vector_type(4)));
+
+// Offset past the end of every buffer the direct kernel reads (their sizes
+// are checked below 2^31 bytes at launch): loads there return zero.
+constexpr unsigned kOutOfRange = 0x80000000u;
+
+// Raw buffer resource over `bytes` bytes at `base` (stride 0, 32-bit
+// format): the descriptor of the gfx9 family.
+__device__ __forceinline__ int32x4_t buffer_resource(const void* base, unsigned bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  int32x4_t r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu));
+  r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+  r.w = 0x00020000;
+  return r;
+}
+
+__device__ void llvm_raw_buffer_load_lds(int32x4_t rsrc, __attribute__((address_space(3))) uint32_t* lds, int size,
+                                         int voffset, int soffset, int offset,
+                                         int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+
+// One 16-byte buffer -> LDS load per lane from byte voffset + soffset of
+// the resource (LDS destination base + 16 * lane, base wave-uniform).
+__device__ __forceinline__ void lds_load16(int32x4_t rsrc, unsigned voffset, unsigned soffset, char* lds_base) {
+  llvm_raw_buffer_load_lds(rsrc, (__attribute__((address_space(3))) uint32_t*)lds_base, 16, (int)voffset,
+                           (int)soffset, 0, 0);
+}
+
+// Vector-position key of LDS row r (rows of 64 bytes, four 16-byte
+// vectors): bits (b2, b1 ^ b3) of r.  Among any 8 consecutive aligned rows
+// the even rows take distinct keys and so do the odd rows (8 lanes of a
+// read per cycle, 128-byte bank window), and among 16 rows the rows of
+// each residue mod 4 take distinct keys (16 lanes per cycle, 256 bytes).
+__device__ __forceinline__ int swizzle_key(int r) { return (((r >> 2) & 1) << 1) | (((r >> 1) ^ (r >> 3)) & 1); }
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
@@ -523,12 +564,6 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-}
-
-// One 16-byte global -> LDS load per lane (LDS destination base + 16 * lane,
-// base wave-uniform).
-__device__ __forceinline__ void lds_dma16(const void* src, char* lds_base) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void_ptr)lds_base, 16, 0, 0);
 }
 
 // LDS offset of a __shared__ address.
@@ -568,9 +603,6 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   __shared__ __attribute__((aligned(16))) char st2[PART];
   __shared__ __attribute__((aligned(16))) char st3[S == 4 ? PART : 16];
 
-  const T* in = static_cast<const T*>(p.in);
-  const T* wt = static_cast<const T*>(p.wt);
-  const T* zero = reinterpret_cast<const T*>(g_conv_zero);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases and wait counts
@@ -580,6 +612,7 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   auto pick = [&](int j) -> char* { return j == 0 ? st0 : j == 1 ? st1 : j == 2 ? st2 : st3; };
   const int M = p.N * HoWo;
   const int K = p.kh * p.kw * p.C;
+  constexpr int ES = sizeof(T);
 
   // XCD-aware tile order (as conv_gemm_kernel).
   const int n_tiles = (p.Co + BN - 1) / BN;
@@ -590,40 +623,44 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   const int m0 = (t / n_tiles) * BM;
   const int n0 = (t % n_tiles) * BN;
 
-  // This lane fills LDS row pass*64 + prow, position lane % 4, with k vector
-  // kvec of its source row (the swizzle: (prow >> 2) & 3 == lane >> 4).
-  const int prow = wave * 16 + (lane >> 2);
-  const int kvec = (lane & 3) ^ (lane >> 4);
+  const int32x4_t a_rsrc = buffer_resource(p.in, (unsigned)((size_t)p.N * p.H * p.W * p.in_ps * ES));
+  const int32x4_t b_rsrc = buffer_resource(p.wt, (unsigned)((size_t)p.Co * p.ldw * ES));
 
-  const T* a_ptr[A_PASS];
+  // This lane fills LDS row pass*64 + prow, position lane % 4, with k vector
+  // kvec of its source row: position ^ swizzle_key(row), where prow % 16 is
+  // (lane >> 2) & 15.
+  const int prow = wave * 16 + (lane >> 2);
+  const int kvec = (lane & 3) ^ swizzle_key((lane >> 2) & 15);
+
+  // Byte offsets of this lane's rows in the buffers (kOutOfRange for rows
+  // past M or Co).  1x1: the row's k vector kvec, the slice's k0 goes in the
+  // scalar offset.  Otherwise: the row's image; the tap is added per slice.
+  unsigned a_off[A_PASS];
   int a_iy0[A_PASS], a_ix0[A_PASS];
-  bool a_ok[A_PASS];
 #pragma unroll
   for (int i = 0; i < A_PASS; ++i) {
     const int m = m0 + i * 64 + prow;
-    a_ok[i] = m < M;
-    const int mm = a_ok[i] ? m : 0;
+    const bool ok = m < M;
+    const int mm = ok ? m : 0;
     const int img = mm / HoWo;
     if constexpr (PW) {
-      a_ptr[i] = in + (size_t)mm * p.in_ps;
+      a_off[i] = ok ? (unsigned)(((size_t)mm * p.in_ps + kvec * VE) * ES) : kOutOfRange;
       a_iy0[i] = a_ix0[i] = 0;
     } else {
       const int r = mm - img * HoWo;
       const int oy = r / p.Wo;
       const int ox = r - oy * p.Wo;
-      a_ptr[i] = in + (size_t)img * p.H * p.W * p.in_ps;
+      a_off[i] = ok ? (unsigned)((size_t)img * p.H * p.W * p.in_ps * ES) : kOutOfRange;
       a_iy0[i] = oy * p.sh - p.pt;
       a_ix0[i] = ox * p.sw - p.pl;
     }
   }
-  const T* b_ptr[B_PASS];
-  bool b_ok[B_PASS];
+  unsigned b_off[B_PASS];
 #pragma unroll
   for (int i = 0; i < B_PASS; ++i) {
     const int r = i * 64 + prow;
     const int n = n0 + r;
-    b_ok[i] = r < BN && n < p.Co;
-    b_ptr[i] = wt + (size_t)(b_ok[i] ? n : 0) * p.ldw;
+    b_off[i] = r < BN && n < p.Co ? (unsigned)(((size_t)n * p.ldw + kvec * VE) * ES) : kOutOfRange;
   }
 
   // K slices of this workgroup: all of them, or its split's share.
@@ -641,31 +678,35 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   }
 
   // Issues the loads of the K slice at k0 (in order k0 = kbase,
-  // kbase + BK, ...).
-  auto issue = [&](int j, int k0) {
-    char* stage = pick(j);
-    const int k = k0 + kvec * VE;
-    const bool kin = k < K;
+  // kbase + BK, ...).  `tail`: the slice reaches past K, so lanes whose k
+  // is past K are masked (only the last slice of a K that is not a multiple
+  // of BK).
+  auto issue_loads = [&](char* stage, int k0, auto tail) {
+    constexpr bool TAIL = decltype(tail)::value;
+    const unsigned ks = (unsigned)k0 * ES;
+    const bool kin = !TAIL || k0 + kvec * VE < K;
 #pragma unroll
     for (int i = 0; i < A_PASS; ++i) {
-      const T* src = zero;
+      char* dst = stage + (i * 64 + wave * 16) * 64;
       if constexpr (PW) {
-        if (kin && a_ok[i]) src = a_ptr[i] + k;
+        lds_load16(a_rsrc, kin ? a_off[i] : kOutOfRange, ks, dst);
       } else {
         const int iy = a_iy0[i] + ky;
         const int ix = a_ix0[i] + kx;
-        if (kin && a_ok[i] && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W)
-          src = a_ptr[i] + ((size_t)iy * p.W + ix) * p.in_ps + kc;
+        const bool ok = kin && a_off[i] != kOutOfRange && (unsigned)iy < (unsigned)p.H && (unsigned)ix < (unsigned)p.W;
+        lds_load16(a_rsrc, ok ? a_off[i] + (unsigned)(((iy * p.W + ix) * p.in_ps + kc) * ES) : kOutOfRange, 0u,
+                   dst);
       }
-      lds_dma16(src, stage + (i * 64 + wave * 16) * 64);
     }
 #pragma unroll
-    for (int i = 0; i < B_PASS; ++i) {
-      if (i * 64 + wave * 16 < BN) {
-        const T* src = kin && b_ok[i] ? b_ptr[i] + k : zero;
-        lds_dma16(src, stage + (BM + i * 64 + wave * 16) * 64);
-      }
-    }
+    for (int i = 0; i < B_PASS; ++i)
+      if (i * 64 + wave * 16 < BN) lds_load16(b_rsrc, kin ? b_off[i] : kOutOfRange, ks, stage + (BM + i * 64 + wave * 16) * 64);
+  };
+  auto issue = [&](int j, int k0) {
+    if (k0 + BK > K)
+      issue_loads(pick(j), k0, std::true_type{});
+    else
+      issue_loads(pick(j), k0, std::false_type{});
     if constexpr (!PW) {
       kc += BK;
       while (kc >= p.C) {
@@ -686,7 +727,7 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
 
   const int lrow = lane & 15;
   const int g = lane >> 4;
-  const int swz = (g ^ (lrow >> 2)) << 4;  // byte offset of this lane's vector in its row
+  const int swz = (g ^ swizzle_key(lrow)) << 4;  // byte offset of this lane's vector in its row
 
   // Operand reads go through lds_read16 (outside the compiler's view): the
   // compiler cannot tell the stage being read from the stages being filled
@@ -832,7 +873,11 @@ static void launch_tile_kernel(const ConvParams& p, dim3 grid, hipStream_t s) {
   constexpr int VE16 = 16 / sizeof(T);
   const bool v16 = p.C % VE16 == 0 && p.in_ps % VE16 == 0 && p.ldw % VE16 == 0 &&
                    reinterpret_cast<uintptr_t>(p.in) % 16 == 0 && reinterpret_cast<uintptr_t>(p.wt) % 16 == 0;
-  if (!p.in_gate && v16) {
+  // The direct kernel's buffer offsets are 32-bit with kOutOfRange as the
+  // masked offset: both buffers must stay below 2^31 bytes.
+  const bool small = (size_t)p.N * p.H * p.W * p.in_ps * sizeof(T) < kOutOfRange &&
+                     (size_t)p.Co * p.ldw * sizeof(T) < kOutOfRange;
+  if (!p.in_gate && v16 && small) {
     constexpr int S = (BM + BN) * 64 <= 10240 ? 4 : 3;  // stages: about 40 KB of LDS at most
     if (pw)
       hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S>), grid, dim3(256), 0, s, p);
