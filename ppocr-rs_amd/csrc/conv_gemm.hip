@@ -427,6 +427,7 @@ __device__ __forceinline__ void finish_staged(const ConvParams& p, RowPtr row_pt
   const T* up = static_cast<const T*>(p.up);
   const bool vec_out = (p.out_ps & 3) == 0 && (p.Co & 3) == 0;
   const bool need_coords = p.up != nullptr || p.rep != 1;
+  const bool need_img = need_coords || p.res_gate != nullptr;
   constexpr int NQ = BN / 4;
   for (int q = tid; q < BM * NQ; q += 256) {
     const int row = q / NQ;
@@ -435,11 +436,16 @@ __device__ __forceinline__ void finish_staged(const ConvParams& p, RowPtr row_pt
     const int col = n0 + cq * 4;
     if (m >= M || col >= p.Co) continue;
     float4 v = *reinterpret_cast<const float4*>(row_ptr(row) + cq * 4);
-    int img = m / HoWo, oy = 0, ox = 0;
-    if (need_coords) {
-      int r = m - img * HoWo;
-      oy = r / p.Wo;
-      ox = r - oy * p.Wo;
+    // Image and output coordinates only for the terms that use them (the
+    // divisions would otherwise cost more than the rest of the epilogue).
+    int img = 0, oy = 0, ox = 0;
+    if (need_img) {
+      img = m / HoWo;
+      if (need_coords) {
+        const int r = m - img * HoWo;
+        oy = r / p.Wo;
+        ox = r - oy * p.Wo;
+      }
     }
     if (vec_out) {
       if (p.bias) v = f4_add(v, *reinterpret_cast<const float4*>(p.bias + col));
@@ -878,7 +884,10 @@ static void launch_tile_kernel(const ConvParams& p, dim3 grid, hipStream_t s) {
   const bool small = (size_t)p.N * p.H * p.W * p.in_ps * sizeof(T) < kOutOfRange &&
                      (size_t)p.Co * p.ldw * sizeof(T) < kOutOfRange;
   if (!p.in_gate && v16 && small) {
-    constexpr int S = (BM + BN) * 64 <= 10240 ? 4 : 3;  // stages: about 40 KB of LDS at most
+    // Stages: fp32 slices take long enough on the MFMAs that three cover the
+    // load latency (and the smaller LDS footprint fits more workgroups per
+    // CU); bf16 takes four where they fit in about 40 KB.
+    constexpr int S = sizeof(T) == 2 && (BM + BN) * 64 <= 10240 ? 4 : 3;
     if (pw)
       hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S>), grid, dim3(256), 0, s, p);
     else
