@@ -14,12 +14,14 @@
 //     bf16: v_mfma_f32_16x16x32_bf16, one per tile per 32-deep K slice, fp32
 //     accumulation.
 //   * Each wave64 owns a TM x TN grid of 16x16 accumulators.
-//   * Layers without an SE input gate run conv_gemm_direct_kernel: operand
-//     rows are loaded straight into LDS (buffer_load_dwordx4 ... lds)
-//     through a 3- or 4-stage pipeline.  Gated layers (the gate multiplies A
-//     while it is gathered) and bf16 layers whose channel count is not a
-//     multiple of 8 run conv_gemm_kernel: the next K slice is fetched into
-//     registers during the MFMAs and written to the other of two LDS buffers.
+//   * Most layers run conv_gemm_direct_kernel: operand rows are loaded
+//     straight into LDS (buffer_load_dwordx4 ... lds) through a 3- or
+//     4-stage pipeline; fp32 1x1 layers with an SE input gate multiply the A
+//     fragments by gate rows staged in LDS.  The other gated layers (the gate
+//     multiplies A while it is gathered) and bf16 layers whose channel count
+//     is not a multiple of 8 run conv_gemm_kernel: the next K slice is
+//     fetched into registers during the MFMAs and written to the other of
+//     two LDS buffers.
 //   * The epilogue stages the fp32 tile through LDS and finishes it with
 //     row-contiguous vector accesses: bias, activation, SE gate on the input
 //     (applied while gathering A), a (gated) residual add, a
@@ -589,7 +591,11 @@ __device__ __forceinline__ floatx4 lds_read16(unsigned addr) {
 // its uses after the wait.
 __device__ __forceinline__ void lds_wait(floatx4& v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v)); }
 
-template <typename T, int BM, int BN, int WM, int WN, bool PW, int S>
+// GATE (fp32 1x1 layers whose tiles span at most two images): the SE gate
+// rows of those images are staged in LDS once and each A operand fragment is
+// multiplied by its gate values after it is read, x * g rounded to fp32 as
+// when the gate is applied during the gather.
+template <typename T, int BM, int BN, int WM, int WN, bool PW, int S, bool GATE>
 __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   constexpr int BK = GemmTraits<T>::BK;  // one 64-byte row per K slice
   constexpr int VE = 16 / sizeof(T);
@@ -628,6 +634,27 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   if (t >= m_tiles * n_tiles) return;
   const int m0 = (t / n_tiles) * BM;
   const int n0 = (t % n_tiles) * BN;
+
+  const int lrow = lane & 15;
+  const int g = lane >> 4;
+
+  // Gate rows of images img_lo and img_lo + 1: gate_lds[i] = gate of image
+  // img_lo + i / C, channel i % C, zero past the gate array and in the BK
+  // floats after both rows (read by the last slice's lanes past K).
+  extern __shared__ __attribute__((aligned(16))) float gate_lds[];
+  int g_sel[TM];  // first gate float of the image of A fragment i's row
+  if constexpr (GATE) {
+    const int img_lo = m0 / HoWo;
+    const size_t g0 = (size_t)img_lo * p.C, gend = (size_t)p.N * p.C;
+    for (int i = tid; i < 2 * p.C + BK; i += 256)
+      gate_lds[i] = i < 2 * p.C && g0 + i < gend ? p.in_gate[g0 + i] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = min(m0 + wm * TM * 16 + i * 16 + lrow, M - 1);
+      g_sel[i] = (m / HoWo - img_lo) * p.C;
+    }
+    __syncthreads();
+  }
 
   const int32x4_t a_rsrc = buffer_resource(p.in, (unsigned)((size_t)p.N * p.H * p.W * p.in_ps * ES));
   const int32x4_t b_rsrc = buffer_resource(p.wt, (unsigned)((size_t)p.Co * p.ldw * ES));
@@ -731,21 +758,26 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  const int lrow = lane & 15;
-  const int g = lane >> 4;
   const int swz = (g ^ swizzle_key(lrow)) << 4;  // byte offset of this lane's vector in its row
 
   // Operand reads go through lds_read16 (outside the compiler's view): the
   // compiler cannot tell the stage being read from the stages being filled
   // by the loads in flight and would otherwise wait for all of them before
   // every LDS read, draining the pipeline.
-  auto compute = [&](int j) {
+  auto compute = [&](int j, int k0) {
     const unsigned stage = lds_addr(pick(j));
-    floatx4 ra[TM], rb[TN];
+    floatx4 ra[TM], rb[TN], gv[TM];
 #pragma unroll
     for (int i = 0; i < TM; ++i) ra[i] = lds_read16(stage + (wm * TM * 16 + i * 16 + lrow) * 64 + swz);
 #pragma unroll
     for (int j = 0; j < TN; ++j) rb[j] = lds_read16(stage + (BM + wn * TN * 16 + j * 16 + lrow) * 64 + swz);
+    if constexpr (GATE) {
+      // This lane's A values are k0 + 4g .. k0 + 4g + 3 of its row.
+#pragma unroll
+      for (int i = 0; i < TM; ++i) gv[i] = lds_read16(lds_addr(gate_lds) + (g_sel[i] + k0 + 4 * g) * 4);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) lds_wait(gv[i]);
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) lds_wait(ra[i]);
 #pragma unroll
@@ -754,6 +786,12 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
       float4 a[TM], b[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) a[i] = make_float4(ra[i][0], ra[i][1], ra[i][2], ra[i][3]);
+      if constexpr (GATE) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          a[i] = make_float4(__fmul_rn(a[i].x, gv[i][0]), __fmul_rn(a[i].y, gv[i][1]), __fmul_rn(a[i].z, gv[i][2]),
+                             __fmul_rn(a[i].w, gv[i][3]));
+      }
 #pragma unroll
       for (int j = 0; j < TN; ++j) b[j] = make_float4(rb[j][0], rb[j][1], rb[j][2], rb[j][3]);
 #pragma unroll
@@ -804,7 +842,7 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
       wait_vmcnt<0>();
     stage_barrier();
     if (s + S - 1 < nk) issue(refill, kbase + (s + S - 1) * BK);
-    compute(cur);
+    compute(cur, kbase + s * BK);
   };
   issue(0, kbase);
   if (nk > 1) issue(1, kbase + BK);
@@ -883,16 +921,26 @@ static void launch_tile_kernel(const ConvParams& p, dim3 grid, hipStream_t s) {
   // masked offset: both buffers must stay below 2^31 bytes.
   const bool small = (size_t)p.N * p.H * p.W * p.in_ps * sizeof(T) < kOutOfRange &&
                      (size_t)p.Co * p.ldw * sizeof(T) < kOutOfRange;
+  // Stages: fp32 slices take long enough on the MFMAs that three cover the
+  // load latency (and the smaller LDS footprint fits more workgroups per
+  // CU); bf16 takes four where they fit in about 40 KB.
+  constexpr int S = sizeof(T) == 2 && (BM + BN) * 64 <= 10240 ? 4 : 3;
   if (!p.in_gate && v16 && small) {
-    // Stages: fp32 slices take long enough on the MFMAs that three cover the
-    // load latency (and the smaller LDS footprint fits more workgroups per
-    // CU); bf16 takes four where they fit in about 40 KB.
-    constexpr int S = sizeof(T) == 2 && (BM + BN) * 64 <= 10240 ? 4 : 3;
     if (pw)
-      hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, false>), grid, dim3(256), 0, s, p);
     else
-      hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, false, S>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, false, S, false>), grid, dim3(256), 0, s, p);
     return;
+  }
+  // Gated fp32 1x1 layers whose tiles span at most two images (an image has
+  // at least BM pixels) and whose two gate rows fit in 32 KB of LDS.
+  const size_t gate_bytes = (2 * (size_t)p.C + GemmTraits<T>::BK) * sizeof(float);
+  if constexpr (sizeof(T) == 4) {
+    if (p.in_gate && pw && v16 && small && p.Ho * p.Wo >= BM && gate_bytes <= 32768) {
+      hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, true>), grid, dim3(256),
+                         (unsigned)gate_bytes, s, p);
+      return;
+    }
   }
   if constexpr (sizeof(T) == 4) {
     if (pw)
