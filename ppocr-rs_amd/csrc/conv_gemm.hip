@@ -910,55 +910,71 @@ __global__ __launch_bounds__(256) void conv_splitk_finish_kernel(ConvParams p) {
       p, [&](int row) { return stage + row * LDE; }, m0, n0, M, n_tiles);
 }
 
-template <typename T, int BM, int BN, int WM, int WN>
-static void launch_tile_kernel(const ConvParams& p, dim3 grid, hipStream_t s) {
+// Kernel variant launch_conv runs for a layer (pointers are only tested for
+// null and 16-byte alignment).
+enum ConvVariant : int {
+  CV_DIRECT_1X1 = 0,   // conv_gemm_direct_kernel, 1x1
+  CV_DIRECT = 1,       // conv_gemm_direct_kernel, k x k / strided
+  CV_DIRECT_GATE = 2,  // conv_gemm_direct_kernel, gated 1x1 (fp32)
+  CV_REG_1X1 = 3,      // conv_gemm_kernel, 1x1, 16-byte loads
+  CV_REG = 4,          // conv_gemm_kernel, 16-byte loads
+  CV_REG_1X1_V4 = 5,   // conv_gemm_kernel, 1x1, 8-byte bf16 loads
+  CV_REG_V4 = 6,       // conv_gemm_kernel, 8-byte bf16 loads
+};
+
+static int conv_variant(const ConvParams& p, int BM) {
+  const int es = p.dt == DT_BF16 ? 2 : 4;
+  const int ve16 = 16 / es;
   const bool pw = p.kh == 1 && p.kw == 1 && p.sh == 1 && p.sw == 1 && p.pt == 0 && p.pl == 0 && p.Ho == p.H &&
                   p.Wo == p.W;
-  constexpr int VE16 = 16 / sizeof(T);
-  const bool v16 = p.C % VE16 == 0 && p.in_ps % VE16 == 0 && p.ldw % VE16 == 0 &&
-                   reinterpret_cast<uintptr_t>(p.in) % 16 == 0 && reinterpret_cast<uintptr_t>(p.wt) % 16 == 0;
+  const bool aligned = reinterpret_cast<uintptr_t>(p.in) % 16 == 0 && reinterpret_cast<uintptr_t>(p.wt) % 16 == 0;
+  const bool v16 = p.C % ve16 == 0 && p.in_ps % ve16 == 0 && p.ldw % ve16 == 0 && aligned;
   // The direct kernel's buffer offsets are 32-bit with kOutOfRange as the
   // masked offset: both buffers must stay below 2^31 bytes.
-  const bool small = (size_t)p.N * p.H * p.W * p.in_ps * sizeof(T) < kOutOfRange &&
-                     (size_t)p.Co * p.ldw * sizeof(T) < kOutOfRange;
+  const bool small = (size_t)p.N * p.H * p.W * p.in_ps * es < kOutOfRange && (size_t)p.Co * p.ldw * es < kOutOfRange;
+  if (!p.in_gate && v16 && small) return pw ? CV_DIRECT_1X1 : CV_DIRECT;
+  // Gated fp32 1x1 layers whose tiles span at most two images (an image has
+  // at least BM pixels) and whose two gate rows fit in 32 KB of LDS.
+  const size_t gate_bytes = (2 * (size_t)p.C + GemmTraits<float>::BK) * sizeof(float);
+  if (es == 4 && p.in_gate && pw && v16 && small && p.Ho * p.Wo >= BM && gate_bytes <= 32768) return CV_DIRECT_GATE;
+  // Register kernel: 16-byte loads need every vector of VE channels 16-byte
+  // aligned (fp32 layers always have C % 4 == 0).
+  const bool wide = es == 4 || (p.C % 8 == 0 && p.in_ps % 8 == 0 && p.ldw % 8 == 0 && aligned);
+  if (pw) return wide ? CV_REG_1X1 : CV_REG_1X1_V4;
+  return wide ? CV_REG : CV_REG_V4;
+}
+
+template <typename T, int BM, int BN, int WM, int WN>
+static void launch_tile_kernel(const ConvParams& p, dim3 grid, hipStream_t s) {
   // Stages: fp32 slices take long enough on the MFMAs that three cover the
   // load latency (and the smaller LDS footprint fits more workgroups per
   // CU); bf16 takes four where they fit in about 40 KB.
   constexpr int S = sizeof(T) == 2 && (BM + BN) * 64 <= 10240 ? 4 : 3;
-  if (!p.in_gate && v16 && small) {
-    if (pw)
+  constexpr int VW = 16 / sizeof(T);  // k values per 16-byte load
+  switch (conv_variant(p, BM)) {
+    case CV_DIRECT_1X1:
       hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, false>), grid, dim3(256), 0, s, p);
-    else
+      break;
+    case CV_DIRECT:
       hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, false, S, false>), grid, dim3(256), 0, s, p);
-    return;
-  }
-  // Gated fp32 1x1 layers whose tiles span at most two images (an image has
-  // at least BM pixels) and whose two gate rows fit in 32 KB of LDS.
-  const size_t gate_bytes = (2 * (size_t)p.C + GemmTraits<T>::BK) * sizeof(float);
-  if constexpr (sizeof(T) == 4) {
-    if (p.in_gate && pw && v16 && small && p.Ho * p.Wo >= BM && gate_bytes <= 32768) {
-      hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, true>), grid, dim3(256),
-                         (unsigned)gate_bytes, s, p);
-      return;
-    }
-  }
-  if constexpr (sizeof(T) == 4) {
-    if (pw)
+      break;
+    case CV_DIRECT_GATE:
+      if constexpr (sizeof(T) == 4)
+        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, true>), grid, dim3(256),
+                           (unsigned)((2 * (size_t)p.C + GemmTraits<T>::BK) * sizeof(float)), s, p);
+      break;
+    case CV_REG_1X1:
+      hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, true, VW>), grid, dim3(256), 0, s, p);
+      break;
+    case CV_REG:
+      hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, false, VW>), grid, dim3(256), 0, s, p);
+      break;
+    case CV_REG_1X1_V4:
       hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, true, 4>), grid, dim3(256), 0, s, p);
-    else
+      break;
+    default:
       hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, false, 4>), grid, dim3(256), 0, s, p);
-  } else {
-    // 16-byte loads need every 8-channel group 16-byte aligned.
-    const bool v8 = p.C % 8 == 0 && p.in_ps % 8 == 0 && p.ldw % 8 == 0 &&
-                    reinterpret_cast<uintptr_t>(p.in) % 16 == 0 && reinterpret_cast<uintptr_t>(p.wt) % 16 == 0;
-    if (pw && v8)
-      hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, true, 8>), grid, dim3(256), 0, s, p);
-    else if (pw)
-      hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, true, 4>), grid, dim3(256), 0, s, p);
-    else if (v8)
-      hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, false, 8>), grid, dim3(256), 0, s, p);
-    else
-      hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, false, 4>), grid, dim3(256), 0, s, p);
+      break;
   }
 }
 
@@ -988,11 +1004,13 @@ static int pick_tile(int M, int cols, int dt) {
   return 3;
 }
 
-const char* conv_tile_name(int M, int cols, int dt) {
-  static const char* f32[] = {"conv_gemm<256x16>", "conv_gemm<128x32>", "conv_gemm<128x64>", "conv_gemm<64x64>"};
-  static const char* b16[] = {"conv_gemm_bf16<256x16>", "conv_gemm_bf16<128x32>", "conv_gemm_bf16<128x64>",
-                              "conv_gemm_bf16<64x64>"};
-  return (dt == DT_BF16 ? b16 : f32)[pick_tile(M, cols, dt)];
+std::string conv_kernel_name(const ConvParams& p) {
+  static const char* tiles[] = {"256x16", "128x32", "128x64", "64x64"};
+  static const int bm[] = {256, 128, 128, 64};
+  static const char* variants[] = {",1x1", "", ",1x1,gate", ",1x1,reg", ",reg", ",1x1,reg4", ",reg4"};
+  const int t = pick_tile(p.N * p.Ho * p.Wo, p.Co, p.dt);
+  return std::string(p.dt == DT_BF16 ? "conv_gemm_bf16<" : "conv_gemm<") + tiles[t] +
+         variants[conv_variant(p, bm[t])] + ">";
 }
 
 int conv_tile_cols(int M, int cols, int dt) {

@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime.h>
 #include <cstdint>
+#include <string>
 
 namespace ppocr {
 
@@ -99,8 +100,10 @@ struct SeParams {
 };
 
 void launch_conv(const ConvParams& p, hipStream_t s);
-// Name of the kernel instance launch_conv picks for M rows x `cols` columns.
-const char* conv_tile_name(int M, int cols, int dt);
+// Name of the kernel instance launch_conv runs for p (tile, and the variant:
+// 1x1 or k x k, gated, register-staged); the pointers of p are only tested
+// for null and 16-byte alignment.
+std::string conv_kernel_name(const ConvParams& p);
 // Column width of that instance's tiles.
 int conv_tile_cols(int M, int cols, int dt);
 // K splits for a convolution of M rows, Co columns and reduction depth K:

@@ -228,6 +228,18 @@ class Builder {
   }
 
   // ------------------------------------------------------------ ops
+  // Name of the kernel instance launch_conv will run for `base` reading view
+  // x with weights at blob offset wo.  The pointers are stood in for by
+  // their offsets, which decide their alignment: arena buffers and weight
+  // offsets are 256-byte aligned.
+  static std::string conv_kernel(const ConvParams& base, const View& x, size_t wo, bool gated) {
+    ConvParams probe = base;
+    probe.in = reinterpret_cast<const void*>((uintptr_t)(x.off * dtype_size(x.dt)));
+    probe.wt = reinterpret_cast<const void*>((uintptr_t)wo);
+    probe.in_gate = gated ? reinterpret_cast<const float*>((uintptr_t)16) : nullptr;
+    return conv_kernel_name(probe);
+  }
+
   View conv(const View& x, const ConvW& w, const Epi& e, const std::string& name) {
     if (x.c != w.ci_pad) raise(PPOCR_ERR_INVALID_MODEL, name + ": input has " + std::to_string(x.c) + " channels");
     const int Ho = (x.h + w.pt + w.pb - w.kh) / w.sh + 1;
@@ -272,7 +284,7 @@ class Builder {
     base.splits = splits;
     Op op;
     op.name = name;
-    op.kernel = conv_tile_name(x.n * Ho * Wo, w.co, x.dt);
+    op.kernel = conv_kernel(base, x, wo, has_ig);
     if (splits > 1) op.kernel += "+split_k" + std::to_string(splits);
     op.bound = 1;
     const double es = (double)dtype_size(x.dt);
@@ -517,7 +529,7 @@ class Builder {
     const double es = (double)dtype_size(x.dt), part_bytes = 12.0 * tiles * M;
     Op op;
     op.name = name;
-    op.kernel = conv_tile_name(M, w.co, x.dt);
+    op.kernel = conv_kernel(base, x, wo, false);
     op.bound = 1;
     op.flops = 2.0 * M * w.co * w.ci;
     op.bytes = es * ((double)M * w.ci + (double)w.ci * w.co) + 4.0 * w.co + part_bytes;
