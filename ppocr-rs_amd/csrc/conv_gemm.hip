@@ -382,6 +382,67 @@ __device__ __forceinline__ void finish_staged(const ConvParams& p, RowPtr row_pt
   const int tid = threadIdx.x;
   const int HoWo = p.Ho * p.Wo;
 
+  // DB head tail.  Pass 1: u = ReLU(staged + bias) in place.  Pass 2: for
+  // each (row, tap) of the tile, f[q] = sum_o u[o] * wf[o][q] over the
+  // tap's db_ch hidden channels; tpi lanes share an item, each summing a
+  // contiguous quarter or half of o, combined with xor shuffles; then
+  // sigmoid(f + bf) into the 2x2 output block of the tap
+  // (src/cpu/model.rs:1516-1520).
+  if (p.db_ch) {
+    const int ch = p.db_ch;
+    for (int q = tid; q < BM * BN; q += 256) {
+      const int row = q / BN, c = q - row * BN;
+      float* r = row_ptr(row);
+      r[c] = fmaxf(r[c] + p.bias[n0 + c], 0.0f);
+    }
+    __syncthreads();
+    const int taps = BN / ch;
+    const int items = BM * taps;
+    const int tpi = items >= 256 ? 1 : 256 / items;  // 1, 2 or 4 (ch <= 64, BM >= 64)
+    const int per = ch / tpi;
+    const int OW = 4 * p.Wo;
+    float* map = static_cast<float*>(p.out);
+    for (int base = 0; base < items * tpi; base += 256) {
+      const int it = base + tid;
+      const int item = it / tpi, sub = it - item * tpi;
+      const int row = item / taps, tl = item - row * taps;
+      const float* u = row_ptr(min(row, BM - 1)) + tl * ch + sub * per;
+      const float* w = p.db_wf + sub * per * 4;
+      float f0 = 0.f, f1 = 0.f, f2 = 0.f, f3 = 0.f;
+      for (int o = 0; o < per; ++o) {
+        const float4 wq = *reinterpret_cast<const float4*>(w + o * 4);
+        const float v = u[o];
+        f0 = fmaf(v, wq.x, f0);
+        f1 = fmaf(v, wq.y, f1);
+        f2 = fmaf(v, wq.z, f2);
+        f3 = fmaf(v, wq.w, f3);
+      }
+      for (int s = 1; s < tpi; s <<= 1) {
+        f0 += __shfl_xor(f0, s);
+        f1 += __shfl_xor(f1, s);
+        f2 += __shfl_xor(f2, s);
+        f3 += __shfl_xor(f3, s);
+      }
+      const int m = m0 + row;
+      if (item >= items || m >= M) continue;
+      const int img = m / HoWo, r = m - img * HoWo;
+      const int y = r / p.Wo, x = r - y * p.Wo;
+      const int tap = n0 / ch + tl;
+      float* top = map + ((size_t)img * 4 * p.Ho + 4 * y + 2 * (tap >> 1)) * OW + 4 * x + 2 * (tap & 1);
+      const float s0 = act_apply(ACT_SIGMOID, f0 + p.db_bf), s1 = act_apply(ACT_SIGMOID, f1 + p.db_bf);
+      const float s2 = act_apply(ACT_SIGMOID, f2 + p.db_bf), s3 = act_apply(ACT_SIGMOID, f3 + p.db_bf);
+      if (tpi == 1) {
+        *reinterpret_cast<float2*>(top) = make_float2(s0, s1);
+        *reinterpret_cast<float2*>(top + OW) = make_float2(s2, s3);
+      } else if (tpi == 2) {
+        *reinterpret_cast<float2*>(top + sub * OW) = sub ? make_float2(s2, s3) : make_float2(s0, s1);
+      } else {
+        top[(sub >> 1) * OW + (sub & 1)] = sub == 0 ? s0 : sub == 1 ? s1 : sub == 2 ? s2 : s3;
+      }
+    }
+    return;
+  }
+
   // Greedy-CTC classifier epilogue: each row's (max logit, sum of
   // exp(logit - max), last column holding the max) over this tile's columns.
   // TPR consecutive lanes share a row, each scanning CPT columns in order, so

@@ -65,6 +65,15 @@ struct ConvParams {
   // greedy-CTC epilogue.
   float* split_ws;
   int splits;
+  // DB head tail (db_ch > 0): the GEMM is conv_up of the detector head as a
+  // 1x1 conv whose column tap * db_ch + o is hidden channel o of 2x2 tap
+  // `tap`; the epilogue adds the bias, applies ReLU, then conv_final (2x2
+  // stride 2 to one channel: weights db_wf [db_ch][4], bias db_bf) and the
+  // sigmoid, and writes the fp32 map `out` [N][4 Ho][4 Wo].  The tile width
+  // must be a multiple of db_ch; no other epilogue terms.
+  int db_ch;
+  const float* db_wf;
+  float db_bf;
 };
 
 // Depthwise k x k convolution (groups == C), 4 channels per lane.

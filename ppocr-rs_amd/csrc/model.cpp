@@ -904,15 +904,54 @@ void detector_head(Builder& B, const View& x, int nc) {
   View in = d;
   Op op;
   op.name = "head.conv_up+conv_final";
-  op.kernel = "db_head_up";
   op.flops = 2.0 * d.pixels() * (4.0 * h * h + 16.0 * h);
   op.bytes = (double)dtype_size(d.dt) * d.pixels() * h + 4.0 * ((double)out.pixels() + 4.0 * h * h + 4.0 * h);
   op.reads = {d.buf};
   op.writes = {out.buf};
-  op.launch = [=](const Exec& ex, hipStream_t s) {
-    launch_db_head_up(ex.ptr(in), in.n, in.h, in.w, in.c, in.ps, ex.w(owu), ex.w(obu), ex.w(owf), bf, ex.fptr(out),
-                      in.dt, s);
-  };
+  const int M = d.n * d.h * d.w;
+  if (conv_tile_cols(M, 4 * h, d.dt) % h == 0) {
+    // conv_up on the matrix cores as a 1x1 conv with 4h columns (column
+    // tap * h + o, weight wu[c][o][tap], bias bu[o]); conv_final and the
+    // sigmoid run in its epilogue (tiles are whole taps wide).
+    std::vector<float> w1((size_t)4 * h * h), b1((size_t)4 * h);
+    for (int tap = 0; tap < 4; ++tap)
+      for (int o = 0; o < h; ++o) {
+        b1[(size_t)tap * h + o] = bu[o];
+        for (int c = 0; c < h; ++c) w1[((size_t)tap * h + o) * h + c] = wu[((size_t)c * h + o) * 4 + tap];
+      }
+    const ConvW up = B.pack_conv(w1, b1, h, 4 * h, 1, 1, 1, 1, {0, 0, 0, 0});
+    ConvParams base{};
+    base.N = d.n, base.H = d.h, base.W = d.w, base.C = d.c, base.in_ps = d.ps;
+    base.Ho = d.h, base.Wo = d.w, base.Co = 4 * h, base.out_ps = 1;
+    base.out_f32 = 1;
+    base.ldw = up.ldw;
+    base.kh = base.kw = base.sh = base.sw = 1;
+    base.act = ACT_RELU;
+    base.up_s = 2;
+    base.rep = 1;
+    base.out_h = out.h, base.out_w = out.w;
+    base.dt = d.dt;
+    base.db_ch = h;
+    base.db_bf = bf;
+    const size_t uw = up.w, ub = up.b;
+    op.kernel = Builder::conv_kernel(base, d, uw, false) + "+db_head";
+    op.bound = 1;
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      ConvParams p = base;
+      p.in = ex.ptr(in);
+      p.out = ex.fptr(out);
+      p.wt = ex.wv(uw);
+      p.bias = ex.w(ub);
+      p.db_wf = ex.w(owf);
+      launch_conv(p, s);
+    };
+  } else {
+    op.kernel = "db_head_up";
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      launch_db_head_up(ex.ptr(in), in.n, in.h, in.w, in.c, in.ps, ex.w(owu), ex.w(obu), ex.w(owf), bf, ex.fptr(out),
+                        in.dt, s);
+    };
+  }
   B.add_op(std::move(op));
 }
 
