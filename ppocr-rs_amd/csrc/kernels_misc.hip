@@ -283,7 +283,24 @@ const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho) {
 // (src/gpu/shaders/pool.wgsl:183, conv_single_row.wgsl:84).  Stage 1: each
 // block sums a chunk of pixels for all channels (lanes split channels x
 // pixel phases, fixed-order LDS reduction).  Stages 2 and 3: the two 1x1
-// convs of the squeeze-excitation as wave-per-output products.
+// convs of the squeeze-excitation as wave-per-output products.  The work is
+// small and latency-bound: every strided sum issues its loads four at a
+// time (then adds them in the same order), and a wave computes its four
+// outputs together.
+
+// s += v[k] for k = k0, k0 + step, ... < end, in that order, loads issued
+// four at a time.
+template <typename T>
+__device__ __forceinline__ float4 strided_sum4(float4 s, const T* base, size_t stride, int k0, int end, int step) {
+  int k = k0;
+  for (; k + 3 * step < end; k += 4 * step) {
+    const float4 a = ld4<T>(base + (size_t)k * stride), b = ld4<T>(base + (size_t)(k + step) * stride);
+    const float4 c = ld4<T>(base + (size_t)(k + 2 * step) * stride), d = ld4<T>(base + (size_t)(k + 3 * step) * stride);
+    s = f4_sum(f4_sum(f4_sum(f4_sum(s, a), b), c), d);
+  }
+  for (; k < end; k += step) s = f4_sum(s, ld4<T>(base + (size_t)k * stride));
+  return s;
+}
 template <typename T>
 __global__ __launch_bounds__(256) void se_partial_kernel(SeParams p, int chunk) {
   __shared__ float4 red[256];
@@ -297,10 +314,7 @@ __global__ __launch_bounds__(256) void se_partial_kernel(SeParams p, int chunk) 
   const int start = blockIdx.x * chunk;
   const int end = min(start + chunk, p.HW);
   float4 s = f4_zero();
-  if (pl < lanes_p) {
-    const T* base = in + (size_t)n * p.HW * p.in_ps + cq * 4;
-    for (int px = start + pl; px < end; px += lanes_p) s = f4_sum(s, ld4<T>(base + (size_t)px * p.in_ps));
-  }
+  if (pl < lanes_p) s = strided_sum4<T>(s, in + (size_t)n * p.HW * p.in_ps + cq * 4, p.in_ps, start + pl, end, lanes_p);
   red[tid] = s;
   __syncthreads();
   if (tid < C4) {
@@ -310,13 +324,31 @@ __global__ __launch_bounds__(256) void se_partial_kernel(SeParams p, int chunk) 
   }
 }
 
-// Wave-per-output matrix-vector product: out[j] = sum_i W[j][i] v[i] with
-// the 64 lanes striding i (coalesced weight rows) and a wave reduction.
-__device__ __forceinline__ float wave_dot(const float* __restrict__ w, const float* v, int n, int lane) {
-  float acc = 0.0f;
-  for (int i = lane; i < n; i += 64) acc = fmaf(w[i], v[i], acc);
-  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
-  return acc;
+// Four wave-per-output matrix-vector products at once: out[q] = sum_i
+// W[j_q][i] v[i] with the 64 lanes striding i (coalesced weight rows), each
+// lane's terms in increasing i, then a wave reduction.  Rows j_q past
+// `rows` are computed on row 0 and ignored by the caller.
+__device__ __forceinline__ float4 wave_dot4(const float* __restrict__ w, int j0, int rows, const float* v, int n,
+                                            int lane) {
+  const float* r0 = w + (size_t)(j0 < rows ? j0 : 0) * n;
+  const float* r1 = w + (size_t)(j0 + 1 < rows ? j0 + 1 : 0) * n;
+  const float* r2 = w + (size_t)(j0 + 2 < rows ? j0 + 2 : 0) * n;
+  const float* r3 = w + (size_t)(j0 + 3 < rows ? j0 + 3 : 0) * n;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  for (int i = lane; i < n; i += 64) {
+    const float x = v[i];
+    a0 = fmaf(r0[i], x, a0);
+    a1 = fmaf(r1[i], x, a1);
+    a2 = fmaf(r2[i], x, a2);
+    a3 = fmaf(r3[i], x, a3);
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    a0 += __shfl_xor(a0, o);
+    a1 += __shfl_xor(a1, o);
+    a2 += __shfl_xor(a2, o);
+    a3 += __shfl_xor(a3, o);
+  }
+  return make_float4(a0, a1, a2, a3);
 }
 
 // Stage 2: one block per (image, 16 reduced channels).  The block finishes
@@ -332,10 +364,7 @@ __global__ __launch_bounds__(256) void se_reduce_kernel(SeParams p) {
   const int lanes_p = 256 / C4;
   const int cq = tid % C4, pl = tid / C4;
   float4 s = f4_zero();
-  if (pl < lanes_p) {
-    for (int k = pl; k < p.P; k += lanes_p)
-      s = f4_sum(s, *reinterpret_cast<const float4*>(p.partial + ((size_t)n * p.P + k) * p.C + cq * 4));
-  }
+  if (pl < lanes_p) s = strided_sum4<float>(s, p.partial + (size_t)n * p.P * p.C + cq * 4, p.C, pl, p.P, lanes_p);
   red[tid] = s;
   __syncthreads();
   if (tid < C4) {
@@ -349,12 +378,10 @@ __global__ __launch_bounds__(256) void se_reduce_kernel(SeParams p) {
   }
   __syncthreads();
   const int wave = tid >> 6, lane = tid & 63;
-  for (int q = 0; q < 4; ++q) {
-    int j = blockIdx.y * 16 + wave * 4 + q;
-    if (j >= p.Cr) break;
-    float acc = wave_dot(p.w1 + (size_t)j * p.C, mean, p.C, lane);
-    if (lane == 0) p.hidden[(size_t)n * p.Cr + j] = fmaxf(acc + p.b1[j], 0.0f);
-  }
+  const int j0 = blockIdx.y * 16 + wave * 4;
+  const float4 acc = wave_dot4(p.w1, j0, p.Cr, mean, p.C, lane);
+  const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+  if (lane < 4 && j0 + lane < p.Cr) p.hidden[(size_t)n * p.Cr + j0 + lane] = fmaxf(a[lane] + p.b1[j0 + lane], 0.0f);
 }
 
 // Stage 3: one block per (image, 16 channels): expanding 1x1 conv + bias and
@@ -365,12 +392,10 @@ __global__ __launch_bounds__(256) void se_expand_kernel(SeParams p) {
   for (int j = threadIdx.x; j < p.Cr; j += 256) hid[j] = p.hidden[(size_t)n * p.Cr + j];
   __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int q = 0; q < 4; ++q) {
-    int c = blockIdx.y * 16 + wave * 4 + q;
-    if (c >= p.C) break;
-    float acc = wave_dot(p.w2 + (size_t)c * p.Cr, hid, p.Cr, lane);
-    if (lane == 0) p.gate[(size_t)n * p.C + c] = act_apply(p.gate_act, acc + p.b2[c]);
-  }
+  const int c0 = blockIdx.y * 16 + wave * 4;
+  const float4 acc = wave_dot4(p.w2, c0, p.C, hid, p.Cr, lane);
+  const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+  if (lane < 4 && c0 + lane < p.C) p.gate[(size_t)n * p.C + c0 + lane] = act_apply(p.gate_act, a[lane] + p.b2[c0 + lane]);
 }
 
 void launch_se(const SeParams& p, hipStream_t s) {
