@@ -73,16 +73,18 @@ __global__ __launch_bounds__(256) void depthwise_kernel(DwParams p) {
   st4<T>(static_cast<T*>(p.out) + (size_t)pix * p.out_ps + c, acc);
 }
 
-// LDS-tiled stride-1 depthwise.  A block computes a TY x TX output tile of 32
-// channels (8 lanes per pixel).  The input tile with its halo and the taps
-// are staged once in LDS as fp32; each lane then slides a register window of
-// XR + KW - 1 pixels along x to produce XR = 4 outputs, so every staged value
-// is reused KW x KH times from registers/LDS instead of being re-read from
-// the caches.  Taps accumulate in (ky, kx) order as the generic kernel does.
-template <typename T, int KH, int KW, int TY>
+// LDS-tiled stride-1 depthwise.  A block computes a TY x TX output tile of
+// 4 * C4B channels (C4B lanes per pixel).  The input tile with its halo and
+// the taps are staged once in LDS as fp32; each lane then slides a register
+// window of XR + KW - 1 pixels along x to produce XR outputs, so every
+// staged value is reused KW x KH times from registers/LDS instead of being
+// re-read from the caches.  Per tap row a lane reads XR + KW - 1 window and
+// KW tap vectors for KW * XR * 4 FMAs.  The 7x7 and 9x9 layers take 16-row
+// tiles of 16 channels (less halo per output row; measured faster than
+// wider XR, which costs occupancy).  Taps accumulate in (ky, kx) order as
+// the generic kernel does.
+template <typename T, int KH, int KW, int TY, int XR = 4, int C4B = 8>
 __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
-  constexpr int C4B = 8;                  // four-channel lanes per pixel (32 channels)
-  constexpr int XR = 4;                   // outputs per lane along x
   constexpr int XG = 256 / (C4B * TY);    // lane groups along x
   constexpr int TX = XG * XR;
   constexpr int IH = TY + KH - 1, IW = TX + KW - 1;
@@ -90,9 +92,9 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
   __shared__ float4 taps[KH * KW * C4B];
   const T* in = static_cast<const T*>(p.in);
 
-  const int cblocks = (p.C + 31) / 32;
+  const int cblocks = (p.C + 4 * C4B - 1) / (4 * C4B);
   const int n = blockIdx.z / cblocks;
-  const int ch0 = (blockIdx.z - n * cblocks) * 32;
+  const int ch0 = (blockIdx.z - n * cblocks) * 4 * C4B;
   const int oy0 = blockIdx.y * TY, ox0 = blockIdx.x * TX;
   const int tid = threadIdx.x;
 
@@ -237,11 +239,11 @@ static void launch_dw_strip(const DwParams& p, hipStream_t s) {
   hipLaunchKernelGGL((depthwise_strip_kernel<T, KH, KW, R, SH>), dim3(blocks_for(total)), dim3(256), 0, s, p);
 }
 
-template <typename T, int KH, int KW, int TY>
+template <typename T, int KH, int KW, int TY, int XR = 4, int C4B = 8>
 static void launch_dw_tiled(const DwParams& p, hipStream_t s) {
-  constexpr int TX = 256 / (8 * TY) * 4;
-  dim3 grid((p.Wo + TX - 1) / TX, (p.Ho + TY - 1) / TY, p.N * ((p.C + 31) / 32));
-  hipLaunchKernelGGL((depthwise_tiled_kernel<T, KH, KW, TY>), grid, dim3(256), 0, s, p);
+  constexpr int TX = 256 / (C4B * TY) * XR;
+  dim3 grid((p.Wo + TX - 1) / TX, (p.Ho + TY - 1) / TY, p.N * ((p.C + 4 * C4B - 1) / (4 * C4B)));
+  hipLaunchKernelGGL((depthwise_tiled_kernel<T, KH, KW, TY, XR, C4B>), grid, dim3(256), 0, s, p);
 }
 
 template <typename T>
@@ -255,8 +257,10 @@ static void launch_dw_typed(const DwParams& p, hipStream_t s) {
   if (p.sh == 1 && p.sw == 1) {
     if (p.kh == 3 && p.kw == 3) return launch_dw_tiled<T, 3, 3, 8>(p, s);
     if (p.kh == 5 && p.kw == 5) return launch_dw_tiled<T, 5, 5, 8>(p, s);
-    if (p.kh == 7 && p.kw == 7) return launch_dw_tiled<T, 7, 7, 8>(p, s);
-    if (p.kh == 9 && p.kw == 9) return launch_dw_tiled<T, 9, 9, 8>(p, s);
+    // 7x7 and 9x9: 16-row tiles of 16 channels (less halo per output row,
+    // three workgroups per CU).
+    if (p.kh == 7 && p.kw == 7) return launch_dw_tiled<T, 7, 7, 16, 4, 4>(p, s);
+    if (p.kh == 9 && p.kw == 9) return launch_dw_tiled<T, 9, 9, 16, 4, 4>(p, s);
     if (p.kh == 1 && p.kw == 5 && p.Ho == 1) return launch_dw_tiled<T, 1, 5, 1>(p, s);
     if (p.kh == 1 && p.kw == 7 && p.Ho == 1) return launch_dw_tiled<T, 1, 7, 1>(p, s);
   }
