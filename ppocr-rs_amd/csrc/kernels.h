@@ -139,6 +139,11 @@ void launch_maxpool_same(const void* in, int N, int H, int W, int C, int in_ps, 
 void launch_gate_residual(const void* in, int N, int H, int W, int C, int in_ps, const float* gate,
                           const void* upper, int up_ps, void* out, int out_ps, int rep, int dt, hipStream_t s);
 
+// out[n, p, c] = x[n, p, c] * gate[n, c] rounded to the storage type; out is
+// packed (pixel stride C).
+void launch_scale_channels(const void* in, int N, int HW, int C, int in_ps, const float* gate, void* out, int dt,
+                           hipStream_t s);
+
 // Average pool, kernel [3,2], stride [3,2], count_include_pad = false.
 void launch_avgpool32(const void* in, int N, int H, int W, int C, int in_ps, void* out, int Ho, int Wo, int dt,
                       hipStream_t s);

@@ -537,6 +537,28 @@ void launch_gate_residual(const void* in, int N, int H, int W, int C, int in_ps,
                                      static_cast<const T*>(upper), up_ps, static_cast<T*>(out), out_ps, rep));
 }
 
+// SE gate applied to a whole tensor: out = x * g[n, c] rounded to the
+// storage type, the value the consumer conv would otherwise form while
+// gathering A (the SE multiply of src/cpu/model.rs:1138-1142).
+template <typename T>
+__global__ void scale_channels_kernel(const T* in, long pixels, int HW, int C, int in_ps, const float* gate, T* out) {
+  const int C4 = C >> 2;
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= pixels * C4) return;
+  const int c = (int)(idx % C4) * 4;
+  const long pix = idx / C4;
+  const float4 v = ld4<T>(in + (size_t)pix * in_ps + c);
+  const float4 g = *reinterpret_cast<const float4*>(gate + (size_t)(pix / HW) * C + c);
+  st4<T>(out + (size_t)pix * C + c, make_float4(v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w));
+}
+
+void launch_scale_channels(const void* in, int N, int HW, int C, int in_ps, const float* gate, void* out, int dt,
+                           hipStream_t s) {
+  const long pixels = (long)N * HW;
+  DISPATCH_DT(dt, hipLaunchKernelGGL(scale_channels_kernel<T>, dim3(blocks_for(pixels * (C / 4))), dim3(256), 0, s,
+                                     static_cast<const T*>(in), pixels, HW, C, in_ps, gate, static_cast<T*>(out)));
+}
+
 // ----------------------------------------------------------------- DB head
 // Replaces WGSL `detector_head` / `deconv_phase` + `deconv_final`
 // (src/gpu/shaders/detector_head.wgsl:52, deconv_phase.wgsl:105,

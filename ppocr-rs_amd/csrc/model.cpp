@@ -263,8 +263,16 @@ class Builder {
     View ig = e.in_gate ? *e.in_gate : View();
     View up = e.up ? *e.up : View();
     bool has_res = e.res, has_rg = e.res_gate, has_ig = e.in_gate, has_up = e.up;
+    // bf16 layers with an SE input gate: a separate pass writes x * g
+    // (rounded to bf16, the value the gather would form) and the GEMM runs
+    // ungated on the direct kernel; applying the gate per operand fragment
+    // would cost more vector instructions than the bf16 MFMAs take.
+    const bool prescale = has_ig && x.dt == DT_BF16;
+    View xs;
+    if (prescale) xs = alloc(x.n, x.h, x.w, x.c, name + ".gated");
+    const View& a_src = prescale ? xs : x;
     ConvParams base{};
-    base.N = x.n, base.H = x.h, base.W = x.w, base.C = x.c, base.in_ps = x.ps;
+    base.N = x.n, base.H = x.h, base.W = x.w, base.C = x.c, base.in_ps = a_src.ps;
     base.Ho = Ho, base.Wo = Wo, base.Co = w.co, base.out_ps = out.ps;
     base.out_f32 = out.dt == DT_F32 && x.dt != DT_F32;
     base.ldw = w.ldw;
@@ -284,7 +292,8 @@ class Builder {
     base.splits = splits;
     Op op;
     op.name = name;
-    op.kernel = conv_kernel(base, x, wo, has_ig);
+    op.kernel = conv_kernel(base, a_src, wo, has_ig && !prescale);
+    if (prescale) op.kernel += "+gate_pass";
     if (splits > 1) op.kernel += "+split_k" + std::to_string(splits);
     op.bound = 1;
     const double es = (double)dtype_size(x.dt);
@@ -302,13 +311,20 @@ class Builder {
     if (has_up) op.reads.push_back(up.buf);
     op.writes = {out.buf};
     if (splits > 1) op.writes.push_back(ws.buf);
+    if (prescale) op.writes.push_back(xs.buf);
     op.launch = [=](const Exec& ex, hipStream_t s) {
       ConvParams p = base;
-      p.in = ex.ptr(in);
+      if (prescale) {
+        launch_scale_channels(ex.ptr(in), in.n, in.h * in.w, in.c, in.ps, ex.fptr(ig), ex.ptr(xs), in.dt, s);
+        p.in = ex.ptr(xs);
+        p.in_gate = nullptr;
+      } else {
+        p.in = ex.ptr(in);
+        p.in_gate = has_ig ? ex.fptr(ig) : nullptr;
+      }
       p.out = ex.ptr(out);
       p.wt = ex.wv(wo);
       p.bias = ex.w(bo);
-      p.in_gate = has_ig ? ex.fptr(ig) : nullptr;
       p.res = has_res ? ex.ptr(res) : nullptr;
       p.res_gate = has_rg ? ex.fptr(rg) : nullptr;
       p.up = has_up ? ex.ptr(up) : nullptr;
