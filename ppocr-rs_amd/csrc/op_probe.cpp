@@ -1,0 +1,128 @@
+// Test harness for the convolution kernels, built as libppocr_hip_probe.so
+// next to the backend and loaded only by tests/: one launch_conv on host
+// arrays, with the split count, storage type and SE input gate chosen by the
+// caller, so every kernel variant (1x1 / k x k, direct / register-staged,
+// gated, split K, bf16) can be checked against a CPU convolution on shapes
+// that exercise its tails.  Not part of the backend's C ABI.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "kernels.h"
+
+namespace {
+
+uint16_t to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+float from_bf16(uint16_t h) {
+  const uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+// Device copy of n floats, stored as fp32 or (dt = bf16) rounded to bf16.
+void* upload(const float* src, size_t n, int dt) {
+  void* d = nullptr;
+  if (dt == ppocr::DT_BF16) {
+    std::vector<uint16_t> h(n);
+    for (size_t i = 0; i < n; ++i) h[i] = to_bf16(src[i]);
+    if (hipMalloc(&d, n * 2) != hipSuccess) return nullptr;
+    if (hipMemcpy(d, h.data(), n * 2, hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+  } else {
+    if (hipMalloc(&d, n * 4) != hipSuccess) return nullptr;
+    if (hipMemcpy(d, src, n * 4, hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+  }
+  return d;
+}
+
+}  // namespace
+
+extern "C" {
+
+// x [n][h][w][c] (c % 4 == 0), weight [co][c][kh][kw], bias [co] (or null),
+// gate [n][c] (or null): out [n][ho][wo][co] = act(conv(x * gate) + bias),
+// computed with `splits` K splits (1: none) in storage type dt (0 fp32,
+// 1 bf16; bf16 output is returned widened).  Returns 0, or 1 on a HIP error.
+int ppocr_probe_conv(const float* x, int n, int h, int w, int c, const float* weight, const float* bias, int co,
+                     int kh, int kw, int sh, int sw, int pt, int pl, int pb, int pr, int act, const float* gate,
+                     int splits, int dt, float* out) {
+  const int ho = (h + pt + pb - kh) / sh + 1, wo = (w + pl + pr - kw) / sw + 1;
+  const size_t K = (size_t)kh * kw * c, M = (size_t)n * ho * wo;
+  std::vector<float> packed((size_t)co * K);
+  for (int o = 0; o < co; ++o)
+    for (int i = 0; i < c; ++i)
+      for (int ky = 0; ky < kh; ++ky)
+        for (int kx = 0; kx < kw; ++kx)
+          packed[(size_t)o * K + (size_t)(ky * kw + kx) * c + i] = weight[(((size_t)o * c + i) * kh + ky) * kw + kx];
+  void* d_in = upload(x, (size_t)n * h * w * c, dt);
+  void* d_wt = upload(packed.data(), packed.size(), dt);
+  void* d_bias = bias ? upload(bias, co, ppocr::DT_F32) : nullptr;
+  void* d_gate = gate ? upload(gate, (size_t)n * c, ppocr::DT_F32) : nullptr;
+  void *d_out = nullptr, *d_ws = nullptr;
+  int rc = 0;
+  const size_t es = dt == ppocr::DT_BF16 ? 2 : 4;
+  if (!d_in || !d_wt || (bias && !d_bias) || (gate && !d_gate) || hipMalloc(&d_out, M * co * es) != hipSuccess ||
+      (splits > 1 && hipMalloc(&d_ws, (size_t)splits * M * co * 4) != hipSuccess)) {
+    rc = 1;
+  } else {
+    ppocr::ConvParams p{};
+    p.in = d_in;
+    p.N = n, p.H = h, p.W = w, p.C = c, p.in_ps = c;
+    p.out = d_out;
+    p.Ho = ho, p.Wo = wo, p.Co = co, p.out_ps = co;
+    p.wt = d_wt;
+    p.ldw = (int)K;
+    p.bias = static_cast<const float*>(d_bias);
+    p.kh = kh, p.kw = kw, p.sh = sh, p.sw = sw, p.pt = pt, p.pl = pl;
+    p.act = act;
+    p.in_gate = static_cast<const float*>(d_gate);
+    p.up_s = 2;
+    p.rep = 1;
+    p.out_h = ho, p.out_w = wo;
+    p.dt = dt;
+    p.split_ws = static_cast<float*>(d_ws);
+    p.splits = splits;
+    ppocr::launch_conv(p, nullptr);
+    if (hipDeviceSynchronize() != hipSuccess) rc = 1;
+    if (rc == 0) {
+      if (dt == ppocr::DT_BF16) {
+        std::vector<uint16_t> hb(M * co);
+        if (hipMemcpy(hb.data(), d_out, hb.size() * 2, hipMemcpyDeviceToHost) != hipSuccess) rc = 1;
+        for (size_t i = 0; i < hb.size(); ++i) out[i] = from_bf16(hb[i]);
+      } else if (hipMemcpy(out, d_out, M * co * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+        rc = 1;
+      }
+    }
+  }
+  for (void* ptr : {d_in, d_wt, d_bias, d_gate, d_out, static_cast<void*>(d_ws)})
+    if (ptr) (void)hipFree(ptr);
+  return rc;
+}
+
+// The kernel instance ppocr_probe_conv runs for these arguments (pointers
+// stand in by their alignment: the probe's buffers are hipMalloc'd), and the
+// split count the planner would choose for the layer.
+const char* ppocr_probe_conv_kernel(int n, int h, int w, int c, int co, int kh, int kw, int sh, int sw, int pt,
+                                    int pl, int pb, int pr, int gated, int dt, int* planner_splits) {
+  static thread_local std::string name;
+  const int ho = (h + pt + pb - kh) / sh + 1, wo = (w + pl + pr - kw) / sw + 1;
+  ppocr::ConvParams p{};
+  p.N = n, p.H = h, p.W = w, p.C = c, p.in_ps = c;
+  p.Ho = ho, p.Wo = wo, p.Co = co, p.out_ps = co;
+  p.ldw = kh * kw * c;
+  p.kh = kh, p.kw = kw, p.sh = sh, p.sw = sw, p.pt = pt, p.pl = pl;
+  p.in_gate = gated ? reinterpret_cast<const float*>((uintptr_t)256) : nullptr;
+  p.dt = dt;
+  name = ppocr::conv_kernel_name(p);
+  if (planner_splits) *planner_splits = ppocr::conv_split_k(n * ho * wo, co, kh * kw * c, dt);
+  return name.c_str();
+}
+
+}  // extern "C"

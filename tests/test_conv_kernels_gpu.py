@@ -1,0 +1,157 @@
+"""Kernel-level checks of the implicit-GEMM convolution on the GPU.
+
+Every variant launch_conv can pick (1x1 and k x k direct kernels, the gated
+direct kernel, the register-staged kernel with its in-gather gate and its
+8-byte bf16 loads, split K, bf16 storage) runs through the test harness
+libppocr_hip_probe.so on shapes whose M, N and K are not multiples of the
+tiles, and is compared with a float64 convolution of the same operands
+(the reference conv semantics: zero padding, bias, then the activation,
+src/cpu/ops.rs).  Each case first asserts which kernel instance it runs, so
+a change in kernel selection cannot silently drop a variant from the test.
+"""
+import ctypes
+import pathlib
+import zlib
+
+import numpy as np
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+PROBE = ROOT / "ppocr-rs_amd" / "libppocr_hip_probe.so"
+
+ACT_NONE, ACT_RELU, ACT_HSWISH, ACT_SIGMOID = 0, 1, 6, 7
+
+
+def _lib():
+    if not PROBE.exists():
+        raise RuntimeError(f"{PROBE} is not built (make -C ppocr-rs_amd)")
+    lib = ctypes.CDLL(str(PROBE))
+    f = ctypes.POINTER(ctypes.c_float)
+    i = ctypes.c_int
+    lib.ppocr_probe_conv.argtypes = [f, i, i, i, i, f, f, i, i, i, i, i, i, i, i, i, i, f, i, i, f]
+    lib.ppocr_probe_conv.restype = i
+    lib.ppocr_probe_conv_kernel.argtypes = [i] * 15 + [ctypes.POINTER(i)]
+    lib.ppocr_probe_conv_kernel.restype = ctypes.c_char_p
+    return lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def bf16_round(a):
+    """Round float32 values to bfloat16 (nearest even), returned as float32."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32)
+
+
+def act(y, kind):
+    if kind == ACT_RELU:
+        return np.maximum(y, 0.0)
+    if kind == ACT_HSWISH:
+        return y * np.clip(y / 6.0 + 0.5, 0.0, 1.0)
+    if kind == ACT_SIGMOID:
+        return 1.0 / (1.0 + np.exp(-y))
+    return y
+
+
+def conv_ref(x, w, b, stride, pads, kind):
+    """float64 NHWC convolution: x [n][h][w][c], w [co][c][kh][kw]."""
+    n, h, wd, c = x.shape
+    co, _, kh, kw = w.shape
+    pt, pl, pb, pr = pads
+    xp = np.zeros((n, h + pt + pb, wd + pl + pr, c))
+    xp[:, pt:pt + h, pl:pl + wd, :] = x
+    ho = (h + pt + pb - kh) // stride[0] + 1
+    wo = (wd + pl + pr - kw) // stride[1] + 1
+    y = np.zeros((n, ho, wo, co))
+    for ky in range(kh):
+        for kx in range(kw):
+            patch = xp[:, ky:ky + stride[0] * (ho - 1) + 1:stride[0], kx:kx + stride[1] * (wo - 1) + 1:stride[1], :]
+            y += patch @ w[:, :, ky, kx].T.astype(np.float64)
+    if b is not None:
+        y += b
+    return act(y, kind)
+
+
+# (name, n, h, w, c, co, (kh, kw), (sh, sw), (pt, pl, pb, pr), gated, splits, dt, act, expected kernel)
+CASES = [
+    ("1x1 M/N tails", 2, 7, 9, 64, 96, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_RELU, "conv_gemm<64x64,1x1>"),
+    ("3x3 K tail", 1, 11, 13, 20, 24, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 0, ACT_HSWISH, "conv_gemm<128x32>"),
+    ("3x3 stride 2", 2, 12, 10, 16, 64, (3, 3), (2, 2), (1, 1, 1, 1), False, 1, 0, ACT_NONE, "conv_gemm<64x64>"),
+    ("7x1 asymmetric", 1, 9, 6, 8, 24, (7, 1), (1, 1), (3, 0, 3, 0), False, 1, 0, ACT_RELU, "conv_gemm<128x32>"),
+    ("1x1 narrow Co", 1, 5, 6, 12, 10, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_SIGMOID, "conv_gemm<256x16,1x1>"),
+    ("gated 1x1 direct", 3, 8, 10, 64, 64, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 0, ACT_RELU,
+     "conv_gemm<64x64,1x1,gate>"),
+    ("gated 1x1 small images", 5, 3, 5, 64, 64, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 0, ACT_NONE,
+     "conv_gemm<64x64,1x1,reg>"),
+    ("split K 1x1", 1, 5, 7, 256, 64, (1, 1), (1, 1), (0, 0, 0, 0), False, 4, 0, ACT_RELU, "conv_gemm<64x64,1x1>"),
+    ("split K 3x3 uneven", 2, 6, 5, 32, 32, (3, 3), (1, 1), (1, 1, 1, 1), False, 5, 0, ACT_HSWISH,
+     "conv_gemm<128x32>"),
+    ("split K gated", 2, 6, 12, 128, 64, (1, 1), (1, 1), (0, 0, 0, 0), True, 3, 0, ACT_NONE,
+     "conv_gemm<64x64,1x1,gate>"),
+    ("bf16 1x1", 2, 9, 7, 64, 96, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 1, ACT_RELU, "conv_gemm_bf16<64x64,1x1>"),
+    ("bf16 3x3", 1, 10, 12, 32, 64, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 1, ACT_NONE, "conv_gemm_bf16<64x64>"),
+    ("bf16 C % 8 = 4", 1, 8, 9, 12, 48, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 1, ACT_RELU,
+     "conv_gemm_bf16<64x64,reg4>"),
+    ("bf16 gated", 2, 8, 10, 64, 64, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 1, ACT_NONE,
+     "conv_gemm_bf16<64x64,1x1,reg>"),
+    ("bf16 split K", 1, 7, 5, 256, 64, (1, 1), (1, 1), (0, 0, 0, 0), False, 2, 1, ACT_RELU,
+     "conv_gemm_bf16<64x64,1x1>"),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_conv_variant_matches_float64(case):
+    name, n, h, w, c, co, (kh, kw), (sh, sw), pads, gated, splits, dt, kind, want_kernel = case
+    lib = _lib()
+    kernel = lib.ppocr_probe_conv_kernel(n, h, w, c, co, kh, kw, sh, sw, *pads, int(gated), dt, None).decode()
+    assert kernel == want_kernel, f"{name}: runs {kernel}"
+
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    x = rng.standard_normal((n, h, w, c)).astype(np.float32)
+    wt = (rng.standard_normal((co, c, kh, kw)) / np.sqrt(c * kh * kw)).astype(np.float32)
+    b = rng.standard_normal(co).astype(np.float32) * 0.1
+    g = rng.uniform(0.0, 1.0, (n, c)).astype(np.float32) if gated else None
+    ho = (h + pads[0] + pads[2] - kh) // sh + 1
+    wo = (w + pads[1] + pads[3] - kw) // sw + 1
+    out = np.empty((n, ho, wo, co), dtype=np.float32)
+    rc = lib.ppocr_probe_conv(_ptr(x), n, h, w, c, _ptr(wt), _ptr(b), co, kh, kw, sh, sw, *pads, kind, _ptr(g),
+                              splits, dt, _ptr(out))
+    assert rc == 0
+
+    if dt == 1:
+        # The kernel multiplies bf16 operands (and, gated, bf16(x * g)) with
+        # fp32 accumulation and stores the result in bf16.
+        xs = bf16_round(x)
+        if gated:
+            xs = bf16_round(xs * g[:, None, None, :])
+        ref = conv_ref(xs.astype(np.float64), bf16_round(wt).astype(np.float64), b, (sh, sw), pads, kind)
+        tol = 1e-3 + 8e-3 * np.abs(ref)
+    else:
+        xs = x * g[:, None, None, :] if gated else x
+        ref = conv_ref(xs.astype(np.float64), wt.astype(np.float64), b, (sh, sw), pads, kind)
+        tol = 1e-4 + 1e-5 * np.abs(ref)
+    err = np.abs(out - ref)
+    assert np.all(err <= tol), f"{name} ({kernel}): max abs diff {err.max():.3e}"
+
+
+@pytest.mark.gpu
+def test_split_k_agrees_with_unsplit():
+    """The same layer with 1, 2 and 7 K splits: results agree to fp32 rounding."""
+    lib = _lib()
+    rng = np.random.default_rng(3)
+    n, h, w, c, co = 1, 6, 9, 192, 64
+    x = rng.standard_normal((n, h, w, c)).astype(np.float32)
+    wt = (rng.standard_normal((co, c, 3, 3)) / np.sqrt(9 * c)).astype(np.float32)
+    b = rng.standard_normal(co).astype(np.float32)
+    outs = []
+    for splits in (1, 2, 7):
+        out = np.empty((n, h, w, co), dtype=np.float32)
+        assert lib.ppocr_probe_conv(_ptr(x), n, h, w, c, _ptr(wt), _ptr(b), co, 3, 3, 1, 1, 1, 1, 1, 1, ACT_NONE,
+                                    None, splits, 0, _ptr(out)) == 0
+        outs.append(out)
+    for o in outs[1:]:
+        assert np.max(np.abs(o - outs[0])) <= 1e-4
