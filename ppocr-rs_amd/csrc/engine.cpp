@@ -74,6 +74,36 @@ bool total_less(float a, float b) {
   return std::signbit(a) && !std::signbit(b);
 }
 
+// Pinned host staging of the queued recognizer batches of one page: each
+// batch's geometry packet (read by its upload) and its per-step (class,
+// probability) pairs (written by its download), 256-byte aligned slices.
+struct PinnedStage {
+  char* base = nullptr;
+  size_t bytes = 0, used = 0;
+  PinnedStage() = default;
+  PinnedStage(const PinnedStage&) = delete;
+  PinnedStage& operator=(const PinnedStage&) = delete;
+  ~PinnedStage() {
+    if (base) (void)hipHostFree(base);
+  }
+  static size_t round(size_t n) { return (n + 255) / 256 * 256; }
+  char* take(size_t n) {
+    n = round(n);
+    if (used + n > bytes) return nullptr;
+    char* p = base + used;
+    used += n;
+    return p;
+  }
+  // Replaces the area (nothing may be queued on it).
+  void reserve(size_t n) {
+    if (base) HIP_OK(hipHostFree(base));
+    base = nullptr;
+    bytes = used = 0;
+    HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&base), n, hipHostMallocDefault));
+    bytes = n;
+  }
+};
+
 }  // namespace
 
 struct ppocr_hip_engine {
@@ -83,6 +113,15 @@ struct ppocr_hip_engine {
   size_t classes = 0, dictionary_len = 0;
   std::vector<Cached> detectors, recognizers;
   ppocr_hip_model* shared_weights = nullptr;  // any live recognizer plan
+  PinnedStage stage;
+  ~ppocr_hip_engine() {
+    // Queued downloads may still target the staging area and queued graphs
+    // may still run the cached plans.
+    if (ctx) try {
+        ppocr::sync_context(ctx);
+      } catch (const std::exception&) {
+      }
+  }
 };
 
 struct ppocr_ocr_result {
@@ -99,6 +138,7 @@ ppocr_hip_model* cached_model(ppocr_hip_engine* e, std::vector<Cached>& cache, s
   for (Cached& c : cache)
     if (std::equal(shape, shape + 4, c.shape)) return c.model->m;
   if (cache.size() == limit) {
+    ppocr::sync_context(e->ctx);  // queued batches may still run the evicted plan
     if (!detector && e->shared_weights == cache.front().model->m) e->shared_weights = nullptr;
     cache.erase(cache.begin());
     if (!detector && !e->shared_weights && !cache.empty()) e->shared_weights = cache.front().model->m;
@@ -219,6 +259,49 @@ ppocr_status ppocr_hip_engine_recognize(ppocr_hip_engine* e, const uint8_t* rgb,
     });
     std::vector<std::vector<int32_t>> tokens(dets.size());
     std::vector<float> scores(dets.size(), 0.0f);
+    auto decode = [&](const float* steps, size_t start, size_t n, size_t t, const std::vector<size_t>& content,
+                      size_t input_width) {
+      std::vector<int32_t> buf(t);
+      for (size_t i = 0; i < n; ++i) {
+        size_t emitted = 0;
+        float score = 0.0f;
+        check(ppocr_ctc_greedy_decode(&steps[2 * t * i], t, e->classes, e->dictionary_len, content[i], input_width,
+                                      buf.data(), &emitted, &score));
+        tokens[order[start + i]].assign(buf.begin(), buf.begin() + emitted);
+        scores[order[start + i]] = score;
+      }
+    };
+    // Greedy batches are queued back to back on the stream and decoded once
+    // it has drained: one wait per page instead of two per batch.
+    struct Queued {
+      size_t start, n, t, input_width;
+      std::vector<size_t> content;
+      const float* steps;
+    };
+    std::vector<Queued> queued;
+    auto drain = [&] {
+      if (queued.empty()) return;
+      ppocr::sync_context(e->ctx);
+      for (const Queued& q : queued) {
+        for (size_t i = 0; i < q.n * q.t * 2; ++i)
+          if (!std::isfinite(q.steps[i])) ppocr::raise(PPOCR_ERR_GPU, "model output contains non-finite values");
+        decode(q.steps, q.start, q.n, q.t, q.content, q.input_width);
+      }
+      queued.clear();
+      e->stage.used = 0;
+    };
+    // Declared after `image`, so it runs first on every exit: no queued
+    // batch outlives the page, its device image or its staging.
+    struct DrainGuard {
+      ppocr_hip_ctx* ctx;
+      ~DrainGuard() {
+        try {
+          ppocr::sync_context(ctx);
+        } catch (const std::exception&) {
+        }
+      }
+    } guard{e->ctx};
+    e->stage.used = 0;  // the previous page's guard drained the stream
     for (size_t start = 0; start < order.size(); start += RECOGNIZER_BATCH_SIZE) {
       const size_t n = std::min(RECOGNIZER_BATCH_SIZE, order.size() - start);
       std::vector<float> quads(8 * n);
@@ -232,25 +315,25 @@ ppocr_status ppocr_hip_engine_recognize(ppocr_hip_engine* e, const uint8_t* rgb,
       size_t oshape[4], rank = 0;
       check(ppocr_hip_output_shape(rec, oshape, &rank));
       const size_t t = oshape[1];
-      std::vector<float> steps;
       if (e->options.greedy) {
-        steps.resize(n * t * 2);
-        check(ppocr_hip_forward_image(rec, image.p, quads.data(), content.data(), n, steps.data(), steps.size()));
+        const size_t packet = ppocr::packet_bytes(n), out_bytes = n * t * 2 * sizeof(float);
+        const size_t need = PinnedStage::round(packet) + PinnedStage::round(out_bytes);
+        if (e->stage.used + need > e->stage.bytes) {
+          drain();
+          if (need > e->stage.bytes) e->stage.reserve(std::max(need, (size_t)1 << 20));
+        }
+        char* geo = e->stage.take(packet);
+        float* steps = reinterpret_cast<float*>(e->stage.take(out_bytes));
+        ppocr::enqueue_forward_image(rec, image.p, quads.data(), content.data(), n, geo, steps, n * t * 2);
+        queued.push_back(Queued{start, n, t, input_width, content, steps});
       } else {
         std::vector<float> rows(n * t * e->classes);
         check(ppocr_hip_forward_image(rec, image.p, quads.data(), content.data(), n, rows.data(), rows.size()));
-        steps = steps_from_rows(rows, n, t, e->classes);
-      }
-      std::vector<int32_t> buf(t);
-      for (size_t i = 0; i < n; ++i) {
-        size_t emitted = 0;
-        float score = 0.0f;
-        check(ppocr_ctc_greedy_decode(&steps[2 * t * i], t, e->classes, e->dictionary_len, content[i], input_width,
-                                      buf.data(), &emitted, &score));
-        tokens[order[start + i]].assign(buf.begin(), buf.begin() + emitted);
-        scores[order[start + i]] = score;
+        const std::vector<float> steps = steps_from_rows(rows, n, t, e->classes);
+        decode(steps.data(), start, n, t, content, input_width);
       }
     }
+    drain();
     for (size_t i = 0; i < dets.size(); ++i) {
       ppocr_ocr_line line;
       memcpy(line.polygon, dets[i].polygon, sizeof line.polygon);

@@ -49,10 +49,13 @@ struct ppocr_hip_ctx {
   char* arena = nullptr;
   size_t arena_bytes = 0;
   uint64_t generation = 0;  // bumped whenever the arena moves
+  void* geo = nullptr;      // crop geometry of the synchronous image calls, grown on demand
+  size_t geo_bytes = 0;
   ~ppocr_hip_ctx() {
     (void)hipSetDevice(device);
     if (stream) (void)hipStreamSynchronize(stream);
     if (arena) (void)hipFree(arena);
+    if (geo) (void)hipFree(geo);
     if (stream) (void)hipStreamDestroy(stream);
   }
 };
@@ -125,6 +128,9 @@ void ensure_graph(ppocr_hip_model* m) {
     m->graph = nullptr;
   }
   hipGraph_t graph = nullptr;
+  // Queued work of other models may still be pending on the stream (the
+  // engine's batch queue): let it drain so the capture starts from an idle stream.
+  HIP_OK(hipStreamSynchronize(ctx->stream));
   HIP_OK(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
   launch_all(m, ctx->stream);
   hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
@@ -322,27 +328,22 @@ void ppocr_hip_image_free(ppocr_hip_image* image) { delete image; }
 namespace ppocr {
 namespace {
 
-// Runs the device preprocessing of `n` geometries into `dst` (fp32 NCHW
-// planes).  Caller holds ctx->mu.
-void run_preprocess(ppocr_hip_ctx* ctx, const ppocr_hip_image* image, const float* corners, const int* content_w,
-                    int n, int cw, int ch, bool detector, float* dst) {
+// Enqueues the device preprocessing of `n` geometries into `dst` (fp32 NCHW
+// planes) on the context stream; `geo` is the geometry table in device
+// memory: corners [n][8] floats, then content widths [n] ints.  Caller holds
+// ctx->mu.
+void enqueue_preprocess(ppocr_hip_ctx* ctx, const ppocr_hip_image* image, const void* geo, int n, int cw, int ch,
+                        bool detector, float* dst) {
   static const float det_mean[3] = {0.485f, 0.456f, 0.406f}, det_std[3] = {0.229f, 0.224f, 0.225f};
   static const float rec_mean[3] = {0.5f, 0.5f, 0.5f}, rec_std[3] = {0.5f, 0.5f, 0.5f};
   const float* mean = detector ? det_mean : rec_mean;
   const float* stdv = detector ? det_std : rec_std;
-  // Geometry table: corners [n][8] then content widths [n].
-  size_t geo_bytes = (size_t)n * 8 * sizeof(float) + (size_t)n * sizeof(int);
-  auto geo = device_alloc(ctx->device, geo_bytes);
-  std::vector<char> host(geo_bytes);
-  memcpy(host.data(), corners, (size_t)n * 8 * sizeof(float));
-  memcpy(host.data() + (size_t)n * 8 * sizeof(float), content_w, (size_t)n * sizeof(int));
-  HIP_OK(hipMemcpyAsync(geo->ptr, host.data(), geo_bytes, hipMemcpyHostToDevice, ctx->stream));
   PreParams p{};
   p.rgb = static_cast<const uint32_t*>(image->pixels->ptr);
   p.sw = (int)image->width;
   p.sh = (int)image->height;
-  p.corners = static_cast<const float*>(geo->ptr);
-  p.content_w = reinterpret_cast<const int*>(static_cast<const char*>(geo->ptr) + (size_t)n * 8 * sizeof(float));
+  p.corners = static_cast<const float*>(geo);
+  p.content_w = reinterpret_cast<const int*>(static_cast<const char*>(geo) + (size_t)n * 8 * sizeof(float));
   p.N = n;
   p.cw = cw;
   p.ch = ch;
@@ -353,6 +354,38 @@ void run_preprocess(ppocr_hip_ctx* ctx, const ppocr_hip_image* image, const floa
   p.out = dst;
   launch_preprocess(p, ctx->stream);
   HIP_OK(hipGetLastError());
+}
+
+void pack_geometry(char* dst, const float* corners, const int* content_w, size_t n) {
+  memcpy(dst, corners, n * 8 * sizeof(float));
+  memcpy(dst + n * 8 * sizeof(float), content_w, n * sizeof(int));
+}
+
+// Sizes the context's device geometry buffer to at least `bytes`; a move
+// waits for the queued work that may still read the old one.  Caller holds
+// ctx->mu.
+void ensure_geometry(ppocr_hip_ctx* ctx, size_t bytes) {
+  if (bytes <= ctx->geo_bytes) return;
+  HIP_OK(hipStreamSynchronize(ctx->stream));
+  if (ctx->geo) HIP_OK(hipFree(ctx->geo));
+  ctx->geo = nullptr;
+  ctx->geo_bytes = 0;
+  HIP_OK(hipMalloc(&ctx->geo, bytes));
+  ctx->geo_bytes = bytes;
+}
+
+// Runs the device preprocessing of `n` geometries into `dst` and waits for
+// it: the geometry goes through the context's geometry buffer, which the
+// next call may overwrite.  Caller holds ctx->mu.
+void run_preprocess(ppocr_hip_ctx* ctx, const ppocr_hip_image* image, const float* corners, const int* content_w,
+                    int n, int cw, int ch, bool detector, float* dst) {
+  const size_t bytes = packet_bytes((size_t)n);
+  ensure_geometry(ctx, bytes);
+  std::vector<char> host(bytes);
+  pack_geometry(host.data(), corners, content_w, (size_t)n);
+  HIP_OK(hipMemcpyAsync(ctx->geo, host.data(), bytes, hipMemcpyHostToDevice, ctx->stream));
+  enqueue_preprocess(ctx, image, ctx->geo, n, cw, ch, detector, dst);
+  // `host` is pageable and goes out of scope here.
   HIP_OK(hipStreamSynchronize(ctx->stream));
 }
 
@@ -373,6 +406,44 @@ void check_corners(const float* corners, size_t n) {
 }
 
 }  // namespace
+
+// Geometry packet of `n` crops: corners [n][8] floats, then content widths
+// [n] ints.
+size_t packet_bytes(size_t n) { return n * 8 * sizeof(float) + n * sizeof(int); }
+
+void enqueue_forward_image(ppocr_hip_model* model, const ppocr_hip_image* image, const float* corners,
+                           const size_t* content_w, size_t n, char* packet, float* out, size_t out_cap) {
+  if (!model || !image || !packet || !out) raise(PPOCR_ERR_INVALID_INPUT, "null argument");
+  if (image->ctx != model->ctx) raise(PPOCR_ERR_INVALID_INPUT, "image and model belong to different contexts");
+  if (n != model->in_shape[0])
+    raise(PPOCR_ERR_INVALID_INPUT, "geometry count " + std::to_string(n) + " differs from the planned batch");
+  if (out_cap < model->plan.output_elems)
+    raise(PPOCR_ERR_INVALID_INPUT,
+          "output capacity " + std::to_string(out_cap) + " is below " + std::to_string(model->plan.output_elems));
+  check_corners(corners, n);
+  std::vector<int> cw = content_widths(content_w, n, model->in_shape[3]);
+  pack_geometry(packet, corners, cw.data(), n);
+  ppocr_hip_ctx* ctx = model->ctx;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  HIP_OK(hipSetDevice(ctx->device));
+  ensure_arena(ctx, model->plan.arena_bytes);
+  ensure_graph(model);
+  // One geometry buffer serves every queued batch: each batch's upload is
+  // ordered after the previous batch's preprocess on the stream.
+  ensure_geometry(ctx, packet_bytes(n));
+  HIP_OK(hipMemcpyAsync(ctx->geo, packet, packet_bytes(n), hipMemcpyHostToDevice, ctx->stream));
+  enqueue_preprocess(ctx, image, ctx->geo, (int)n, (int)model->in_shape[3], (int)model->in_shape[2],
+                     model->plan.detector, staging_ptr(model));
+  run_graph(model);
+  HIP_OK(hipMemcpyAsync(out, output_ptr(model), model->plan.output_elems * sizeof(float), hipMemcpyDeviceToHost,
+                        ctx->stream));
+}
+
+void sync_context(ppocr_hip_ctx* ctx) {
+  HIP_OK(hipSetDevice(ctx->device));
+  HIP_OK(hipStreamSynchronize(ctx->stream));
+}
+
 }  // namespace ppocr
 
 extern "C" {

@@ -149,6 +149,18 @@ Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4], int
 // DetectorPostprocessOptions::validate (src/ocr.rs:250-268).
 ppocr_db_options db_options(const ppocr_db_options* o);
 
+// Queued image forward for the engine's batch loop (no C-ABI counterpart):
+// the checks and work of ppocr_hip_forward_image, with nothing waited for.
+// `packet` (packet_bytes(n) bytes) and `out` must be pinned host memory
+// (hipHostMalloc) left untouched until sync_context returns: the geometry
+// upload reads `packet` and the output download writes `out` when the stream
+// reaches them.
+size_t packet_bytes(size_t n);
+void enqueue_forward_image(ppocr_hip_model* model, const ppocr_hip_image* image, const float* corners,
+                           const size_t* content_w, size_t n, char* packet, float* out, size_t out_cap);
+// Waits for all work queued on the context's stream.
+void sync_context(ppocr_hip_ctx* ctx);
+
 // Lifetime-based offset packing of the plan's buffers into one arena
 // (the reference's ArenaAllocator::compact_layout, src/gpu/runtime.rs:414-557).
 void plan_arena(Plan& plan);
