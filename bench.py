@@ -12,6 +12,8 @@ Alongside ``value`` the line carries:
   algorithmic FLOPs (2 x MACs) or bytes per step over its HIP-event-timed
   duration (events recorded on the stream the kernels run on), against the
   MI355X peak (fp32 matrix 157.3 TFLOP/s, HBM 8 TB/s);
+* ``kernels``: the same measure for the twelve kernel instances with the
+  most device time (the depthwise and elementwise ones against HBM);
 * ``cpu_baseline``: the C++ restatement of the reference CPU path (the
   parity oracle) timed on this host on a bounded sample of the same workload;
 * ``also``: the other benchmark configurations, measured after the timed
@@ -64,8 +66,8 @@ def throughput(model, x, warmup, steps):
     return total_ms
 
 
-def roofline(stats):
-    """Dominant kernel instance: the one with the most device time per step."""
+def kernel_groups(stats):
+    """Per-step device time and algorithmic work of each kernel instance."""
     groups = {}
     for s in stats:
         g = groups.setdefault(s["kernel"], {"ms": 0.0, "flops": 0.0, "bytes": 0.0, "launches": 0, "bound": s["bound"]})
@@ -73,14 +75,36 @@ def roofline(stats):
         g["flops"] += s["flops"]
         g["bytes"] += s["bytes"]
         g["launches"] += 1
-    name, g = max(groups.items(), key=lambda kv: kv[1]["ms"])
+    return groups
+
+
+def rate(g):
+    """(achieved, peak, unit) of a kernel group against its bound's peak."""
     secs = g["ms"] * 1e-3
     if g["bound"] == "mfma":
-        achieved = g["flops"] / secs / 1e12
-        peak, unit = PEAK_F32_TFLOPS, "TFLOP/s"
-    else:
-        achieved = g["bytes"] / secs / 1e9
-        peak, unit = PEAK_HBM_GBS, "GB/s"
+        return g["flops"] / secs / 1e12, PEAK_F32_TFLOPS, "TFLOP/s"
+    return g["bytes"] / secs / 1e9, PEAK_HBM_GBS, "GB/s"
+
+
+def kernel_table(stats, top=12):
+    """The `top` kernel instances by device time, each against its roofline."""
+    groups = kernel_groups(stats)
+    total_ms = sum(v["ms"] for v in groups.values())
+    rows = []
+    for name, g in sorted(groups.items(), key=lambda kv: -kv[1]["ms"])[:top]:
+        achieved, peak, unit = rate(g)
+        rows.append({"kernel": name, "bound": "mfma" if g["bound"] == "mfma" else "hbm",
+                     "launches_per_step": g["launches"], "ms_per_step": round(g["ms"], 4),
+                     "share_of_device_time": round(g["ms"] / total_ms, 3) if total_ms else None,
+                     "achieved": round(achieved, 2), "unit": unit, "frac": round(achieved / peak, 3)})
+    return rows
+
+
+def roofline(stats):
+    """Dominant kernel instance: the one with the most device time per step."""
+    groups = kernel_groups(stats)
+    name, g = max(groups.items(), key=lambda kv: kv[1]["ms"])
+    achieved, peak, unit = rate(g)
     total_ms = sum(v["ms"] for v in groups.values())
     return {
         "bound": "mfma" if g["bound"] == "mfma" else "hbm",
@@ -280,6 +304,7 @@ def main():
         "config": {"workload": "PP-OCRv6 medium detector, fp32, batch 8, input 8x3x416x736",
                    "model_size": "medium", "batch": shape[0], "height": shape[2], "width": shape[3]},
         "roofline": roof,
+        "kernels": kernel_table(stats),
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(kind, size, shape)

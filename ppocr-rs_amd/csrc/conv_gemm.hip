@@ -322,21 +322,83 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvParams p) {
 
   float* stage = reinterpret_cast<float*>(smem_raw);
   finish_tile<T, BM, BN, WM, WN>(
-      p, acc, [=](int row) { return stage + row * LDE; }, m0, n0, M, n_tiles);
+      p, acc, [=](int row) { return stage + row * LDE; }, m0, n0, M, n_tiles, nullptr);
+}
+
+// Epilogue of four consecutive output columns col..col+3 of row m (Co and
+// out_ps multiples of 4), in two phases so that a tile's loads are all in
+// flight before its first store (the compiler cannot move a load above a
+// store that may alias it, and each load would otherwise cost a full memory
+// latency): epilogue_load reads the memory terms, the (gated) residual r and
+// the upsample-add source u; epilogue_store adds the bias b, applies the
+// activation, adds r then u, and stores (plain, fp32, or upsample-on-write).
+// img, oy, ox: the row's image and output coordinates, read only by the
+// terms that use them.
+struct EpiTerms {
+  float4 r, u;
+};
+
+template <typename T>
+__device__ __forceinline__ EpiTerms epilogue_load(const ConvParams& p, int m, int col, int img, int oy, int ox) {
+  EpiTerms t{};
+  if (p.res) {
+    t.r = ld4<T>(static_cast<const T*>(p.res) + (size_t)m * p.res_ps + col);
+    if (p.res_gate) {
+      const float4 gt = *reinterpret_cast<const float4*>(p.res_gate + (size_t)img * p.Co + col);
+      t.r = make_float4(__fmul_rn(t.r.x, gt.x), __fmul_rn(t.r.y, gt.y), __fmul_rn(t.r.z, gt.z),
+                        __fmul_rn(t.r.w, gt.w));
+    }
+  }
+  if (p.up) {
+    const int uh = p.Ho / p.up_s, uw = p.Wo / p.up_s;
+    t.u = ld4<T>(static_cast<const T*>(p.up) + ((size_t)(img * uh + oy / p.up_s) * uw + ox / p.up_s) * p.up_ps +
+                 col);
+  }
+  return t;
+}
+
+// Bias of columns col..col+3 (zero without a bias or past Co).
+__device__ __forceinline__ float4 bias4(const ConvParams& p, int col) {
+  return p.bias && col + 3 < p.Co ? *reinterpret_cast<const float4*>(p.bias + col) : float4{0.f, 0.f, 0.f, 0.f};
+}
+
+template <typename T>
+__device__ __forceinline__ void epilogue_store(const ConvParams& p, float4 v, float4 b, const EpiTerms& t, int m,
+                                               int col, int img, int oy, int ox) {
+  if (p.bias) v = f4_add(v, b);
+  v.x = act_apply(p.act, v.x);
+  v.y = act_apply(p.act, v.y);
+  v.z = act_apply(p.act, v.z);
+  v.w = act_apply(p.act, v.w);
+  if (p.res) v = f4_add(t.r, v);
+  if (p.up) v = f4_add(v, t.u);
+  if (p.out_f32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(p.out) + (size_t)m * p.out_ps + col) = v;
+  } else if (p.rep == 1) {
+    st4<T>(static_cast<T*>(p.out) + (size_t)m * p.out_ps + col, v);
+  } else {
+    for (int dy = 0; dy < p.rep; ++dy)
+      for (int dx = 0; dx < p.rep; ++dx)
+        st4<T>(static_cast<T*>(p.out) +
+                   ((size_t)(img * p.out_h + oy * p.rep + dy) * p.out_w + ox * p.rep + dx) * p.out_ps + col,
+               v);
+  }
 }
 
 template <typename T, int BM, int BN, typename RowPtr>
 __device__ __forceinline__ void finish_staged(const ConvParams& p, RowPtr row_ptr, int m0, int n0, int M,
-                                              int n_tiles);
+                                              int n_tiles, const float4* bias_pre);
 
 // Stages the fp32 accumulator tile in LDS as [m][n] (row_ptr(r): LDS
 // address of staged row r, BN + 4 floats) and finishes it: with split K
 // (p.splits > 1) the tile goes to this split's plane of the workspace as is,
 // otherwise through the epilogue.  Caller has passed a barrier after its
-// last read of the LDS operand buffers.
+// last read of the LDS operand buffers.  bias_pre: null, or the bias of this
+// thread's staged-epilogue columns (staged_col) loaded ahead.
 template <typename T, int BM, int BN, int WM, int WN, typename RowPtr>
 __device__ __forceinline__ void finish_tile(const ConvParams& p, const floatx4 (&acc)[BM / (WM * 16)][BN / (WN * 16)],
-                                            RowPtr row_ptr, int m0, int n0, int M, int n_tiles) {
+                                            RowPtr row_ptr, int m0, int n0, int M, int n_tiles,
+                                            const float4* bias_pre) {
   constexpr int TM = BM / (WM * 16);
   constexpr int TN = BN / (WN * 16);
   const int tid = threadIdx.x;
@@ -370,7 +432,16 @@ __device__ __forceinline__ void finish_tile(const ConvParams& p, const floatx4 (
     }
     return;
   }
-  finish_staged<T, BM, BN>(p, row_ptr, m0, n0, M, n_tiles);
+  finish_staged<T, BM, BN>(p, row_ptr, m0, n0, M, n_tiles, bias_pre);
+}
+
+// First column of a thread's float4 groups in the staged epilogue: 256
+// threads walk the tile's BN / 4 groups per row, and BN / 4 divides 256, so
+// a thread keeps the same column group in every row it finishes.
+template <int BN>
+__device__ __forceinline__ int staged_col(int n0) {
+  static_assert(256 % (BN / 4) == 0, "fixed column group per thread");
+  return n0 + (threadIdx.x % (BN / 4)) * 4;
 }
 
 // Epilogue of a tile staged in LDS: the greedy-CTC row reduction, or bias,
@@ -378,7 +449,7 @@ __device__ __forceinline__ void finish_tile(const ConvParams& p, const floatx4 (
 // upsample-on-write).
 template <typename T, int BM, int BN, typename RowPtr>
 __device__ __forceinline__ void finish_staged(const ConvParams& p, RowPtr row_ptr, int m0, int n0, int M,
-                                              int n_tiles) {
+                                              int n_tiles, const float4* bias_pre) {
   const int tid = threadIdx.x;
   const int HoWo = p.Ho * p.Wo;
 
@@ -486,21 +557,163 @@ __device__ __forceinline__ void finish_staged(const ConvParams& p, RowPtr row_pt
     return;
   }
 
-  const T* res = static_cast<const T*>(p.res);
-  const T* up = static_cast<const T*>(p.up);
-  const bool vec_out = (p.out_ps & 3) == 0 && (p.Co & 3) == 0;
+  constexpr int NQ = BN / 4;
+  const int col = staged_col<BN>(n0);
+  const int row0 = tid / NQ;
+  if ((p.out_ps & 3) == 0 && (p.Co & 3) == 0) {
+    // Rows row0 + it * (256 / NQ) of column group col, two at a time: the
+    // loads of both rows, then their stores (two rows bound the registers
+    // held across the loads).
+    constexpr int IT = BM * NQ / 256;
+    constexpr int RSTEP = 256 / NQ;
+    constexpr int CH = IT < 2 ? IT : 2;
+    const bool need_coords = p.up != nullptr || p.rep != 1;
+    const bool need_img = need_coords || p.res_gate != nullptr;
+    const float4 b = bias_pre ? *bias_pre : bias4(p, col);
+#pragma unroll
+    for (int c0 = 0; c0 < IT; c0 += CH) {
+      int img[CH], oy[CH], ox[CH];
+      EpiTerms t[CH];
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int m = m0 + row0 + (c0 + c) * RSTEP;
+        img[c] = oy[c] = ox[c] = 0;
+        if (m >= M || col >= p.Co) continue;
+        // Image and output coordinates only for the terms that use them
+        // (the divisions would otherwise cost more than the rest of the
+        // epilogue).
+        if (need_img) {
+          img[c] = m / HoWo;
+          if (need_coords) {
+            const int r = m - img[c] * HoWo;
+            oy[c] = r / p.Wo;
+            ox[c] = r - oy[c] * p.Wo;
+          }
+        }
+        t[c] = epilogue_load<T>(p, m, col, img[c], oy[c], ox[c]);
+      }
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int row = row0 + (c0 + c) * RSTEP;
+        const int m = m0 + row;
+        if (m >= M || col >= p.Co) continue;
+        const float4 v = *reinterpret_cast<const float4*>(row_ptr(row) + (col - n0));
+        epilogue_store<T>(p, v, b, t[c], m, col, img[c], oy[c], ox[c]);
+      }
+    }
+    return;
+  }
+  // Channel counts that are not a multiple of 4 (the recognizer classifiers,
+  // 6906 and 18710) go element by element; they carry no residual, gate or
+  // upsample terms.
+  for (int row = row0; row < BM; row += 256 / NQ) {
+    const int m = m0 + row;
+    if (m >= M || col >= p.Co) continue;
+    const float* v = row_ptr(row) + (col - n0);
+    for (int e = 0; e < 4 && col + e < p.Co; ++e) {
+      float t = v[e];
+      if (p.bias) t = t + p.bias[col + e];
+      t = act_apply(p.act, t);
+      size_t o = (size_t)m * p.out_ps + col + e;
+      if (p.out_f32)
+        static_cast<float*>(p.out)[o] = t;
+      else
+        st1<T>(static_cast<T*>(p.out) + o, t);
+    }
+  }
+}
+
+// Register epilogue (no LDS staging, no barrier).  An MFMA accumulator
+// block holds, in lane l, column l % 16 of rows 4 (l / 16) .. +3; a 4x4
+// transpose inside each quad of lanes (two DPP exchanges) turns that into
+// row 4 (l / 16) + l % 4, columns 4 ((l % 16) / 4) .. +3, so each lane
+// finishes whole float4 column groups and a quad stores 64 contiguous bytes
+// of a row.  (Trading column blocks between lanes l and l ^ 32 so that one
+// store writes whole 32-column rows measured slower.)
+
+// quad_perm patterns of DPP: lane j reads lane j ^ 1, or lane j ^ 2.
+constexpr int kDppXor1 = 0xB1;  // [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;  // [2, 3, 0, 1]
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_swap(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+// Lane j of a quad holds a[e] = D[e][j] of a 4x4 block D; returns D[j][0..3].
+// Every lane of the wave must be active.
+__device__ __forceinline__ floatx4 quad_transpose(floatx4 a, int lane) {
+  const bool odd = lane & 1;
+  // Across lane bit 0: element e of lane j becomes D[e ^ 1][j ^ 1] where
+  // e and j differ in bit 0.
+  const float r0 = dpp_swap<kDppXor1>(odd ? a[0] : a[1]);
+  const float r1 = dpp_swap<kDppXor1>(odd ? a[2] : a[3]);
+  floatx4 b;
+  b[0] = odd ? r0 : a[0];
+  b[1] = odd ? a[1] : r0;
+  b[2] = odd ? r1 : a[2];
+  b[3] = odd ? a[3] : r1;
+  // Across lane bit 1, element pairs (0, 2) and (1, 3).
+  const bool hi = lane & 2;
+  const float q0 = dpp_swap<kDppXor2>(hi ? b[0] : b[2]);
+  const float q1 = dpp_swap<kDppXor2>(hi ? b[1] : b[3]);
+  floatx4 c;
+  c[0] = hi ? q0 : b[0];
+  c[1] = hi ? q1 : b[1];
+  c[2] = hi ? b[2] : q0;
+  c[3] = hi ? b[3] : q1;
+  return c;
+}
+
+// Column group of accumulator block column j of this lane after the quad
+// transpose (finish_regs).
+template <int BN, int WN>
+__device__ __forceinline__ int regs_col(int n0, int j) {
+  constexpr int TN = BN / (WN * 16);
+  const int lane = threadIdx.x & 63;
+  const int wn = (threadIdx.x >> 6) % WN;
+  return n0 + wn * TN * 16 + j * 16 + 4 * ((lane & 15) >> 2);
+}
+
+// finish_tile without LDS: the split-K workspace store or the epilogue
+// straight from the accumulators.  bias[j]: bias of column group
+// regs_col(n0, j), loaded ahead.
+template <typename T, int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void finish_regs(const ConvParams& p, floatx4 (&acc)[BM / (WM * 16)][BN / (WN * 16)],
+                                            int m0, int n0, int M, const float4 (&bias)[BN / (WN * 16)]) {
+  constexpr int TM = BM / (WM * 16);
+  constexpr int TN = BN / (WN * 16);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / WN;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = quad_transpose(acc[i][j], lane);
+  const int rsub = 4 * (lane >> 4) + (lane & 3);
+  if (p.splits > 1) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm * TM * 16 + i * 16 + rsub;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = regs_col<BN, WN>(n0, j);
+        if (m < M && col < p.Co)
+          *reinterpret_cast<float4*>(p.split_ws + ((size_t)blockIdx.y * M + m) * p.Co + col) =
+              make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      }
+    }
+    return;
+  }
+  const int HoWo = p.Ho * p.Wo;
   const bool need_coords = p.up != nullptr || p.rep != 1;
   const bool need_img = need_coords || p.res_gate != nullptr;
-  constexpr int NQ = BN / 4;
-  for (int q = tid; q < BM * NQ; q += 256) {
-    const int row = q / NQ;
-    const int cq = q - row * NQ;
-    const int m = m0 + row;
-    const int col = n0 + cq * 4;
-    if (m >= M || col >= p.Co) continue;
-    float4 v = *reinterpret_cast<const float4*>(row_ptr(row) + cq * 4);
-    // Image and output coordinates only for the terms that use them (the
-    // divisions would otherwise cost more than the rest of the epilogue).
+  // Row block by row block (the memory terms of a whole tile would cost the
+  // main loop its occupancy): loads of the block's columns, then the stores.
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * TM * 16 + i * 16 + rsub;
+    if (m >= M) continue;
     int img = 0, oy = 0, ox = 0;
     if (need_img) {
       img = m / HoWo;
@@ -510,50 +723,18 @@ __device__ __forceinline__ void finish_staged(const ConvParams& p, RowPtr row_pt
         ox = r - oy * p.Wo;
       }
     }
-    if (vec_out) {
-      if (p.bias) v = f4_add(v, *reinterpret_cast<const float4*>(p.bias + col));
-      v.x = act_apply(p.act, v.x);
-      v.y = act_apply(p.act, v.y);
-      v.z = act_apply(p.act, v.z);
-      v.w = act_apply(p.act, v.w);
-      if (res) {
-        float4 r = ld4<T>(res + (size_t)m * p.res_ps + col);
-        if (p.res_gate) {
-          float4 gt = *reinterpret_cast<const float4*>(p.res_gate + (size_t)img * p.Co + col);
-          r = make_float4(__fmul_rn(r.x, gt.x), __fmul_rn(r.y, gt.y), __fmul_rn(r.z, gt.z), __fmul_rn(r.w, gt.w));
-        }
-        v = f4_add(r, v);
-      }
-      if (up) {
-        int uh = p.Ho / p.up_s, uw = p.Wo / p.up_s;
-        v = f4_add(v, ld4<T>(up + ((size_t)(img * uh + oy / p.up_s) * uw + ox / p.up_s) * p.up_ps + col));
-      }
-      if (p.out_f32) {
-        *reinterpret_cast<float4*>(static_cast<float*>(p.out) + (size_t)m * p.out_ps + col) = v;
-      } else if (p.rep == 1) {
-        st4<T>(static_cast<T*>(p.out) + (size_t)m * p.out_ps + col, v);
-      } else {
-        for (int dy = 0; dy < p.rep; ++dy)
-          for (int dx = 0; dx < p.rep; ++dx)
-            st4<T>(static_cast<T*>(p.out) +
-                       ((size_t)(img * p.out_h + oy * p.rep + dy) * p.out_w + ox * p.rep + dx) * p.out_ps + col,
-                   v);
-      }
-    } else {
-      // Channel counts that are not a multiple of 4 (the recognizer
-      // classifiers, 6906 and 18710) go element by element; they carry no
-      // residual, gate or upsample terms.
-      const float vv[4] = {v.x, v.y, v.z, v.w};
-      for (int e = 0; e < 4 && col + e < p.Co; ++e) {
-        float t = vv[e];
-        if (p.bias) t = t + p.bias[col + e];
-        t = act_apply(p.act, t);
-        size_t o = (size_t)m * p.out_ps + col + e;
-        if (p.out_f32)
-          static_cast<float*>(p.out)[o] = t;
-        else
-          st1<T>(static_cast<T*>(p.out) + o, t);
-      }
+    EpiTerms t[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = regs_col<BN, WN>(n0, j);
+      if (col < p.Co) t[j] = epilogue_load<T>(p, m, col, img, oy, ox);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = regs_col<BN, WN>(n0, j);
+      if (col >= p.Co) continue;
+      const float4 v = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      epilogue_store<T>(p, v, bias[j], t[j], m, col, img, oy, ox);
     }
   }
 }
@@ -656,7 +837,7 @@ __device__ __forceinline__ void lds_wait(floatx4& v) { asm volatile("s_waitcnt l
 // rows of those images are staged in LDS once and each A operand fragment is
 // multiplied by its gate values after it is read, x * g rounded to fp32 as
 // when the gate is applied during the gather.
-template <typename T, int BM, int BN, int WM, int WN, bool PW, int S, bool GATE>
+template <typename T, int BM, int BN, int WM, int WN, bool PW, int S, bool GATE, bool REGS>
 __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   constexpr int BK = GemmTraits<T>::BK;  // one 64-byte row per K slice
   constexpr int VE = 16 / sizeof(T);
@@ -905,6 +1086,15 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
     if (s + S - 1 < nk) issue(refill, kbase + (s + S - 1) * BK);
     compute(cur, kbase + s * BK);
   };
+  // Epilogue bias of this thread's column groups, loaded ahead so that its
+  // latency hides behind the main loop.
+  constexpr int NB = REGS ? TN : 1;
+  float4 bias_pre[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+    bias_pre[j] = p.splits > 1 ? float4{0.f, 0.f, 0.f, 0.f}
+                               : bias4(p, REGS ? regs_col<BN, WN>(n0, j) : staged_col<BN>(n0));
+
   issue(0, kbase);
   if (nk > 1) issue(1, kbase + BK);
   if (S == 4 && nk > 2) issue(2, kbase + 2 * BK);
@@ -921,6 +1111,10 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
     }
   }
   wait_vmcnt<0>();  // every stage load has landed (the compiler does not count them all)
+  if constexpr (REGS) {
+    finish_regs<T, BM, BN, WM, WN>(p, acc, m0, n0, M, bias_pre);
+    return;
+  }
   __syncthreads();
 
   finish_tile<T, BM, BN, WM, WN>(
@@ -930,7 +1124,7 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
         char* base = part == 0 ? st0 : part == 1 ? st1 : part == 2 ? st2 : st3;
         return reinterpret_cast<float*>(base) + (row - part * RPA) * LDE;
       },
-      m0, n0, M, n_tiles);
+      m0, n0, M, n_tiles, &bias_pre[0]);
 }
 
 // Split-K finish: one workgroup per 16x64 output tile, one float4 of it per
@@ -968,7 +1162,7 @@ __global__ __launch_bounds__(256) void conv_splitk_finish_kernel(ConvParams p) {
   *reinterpret_cast<float4*>(stage + row * LDE + c) = v;
   __syncthreads();
   finish_staged<T, kFinishBM, kFinishBN>(
-      p, [&](int row) { return stage + row * LDE; }, m0, n0, M, n_tiles);
+      p, [&](int row) { return stage + row * LDE; }, m0, n0, M, n_tiles, nullptr);
 }
 
 // Kernel variant launch_conv runs for a layer (pointers are only tested for
@@ -1005,6 +1199,19 @@ static int conv_variant(const ConvParams& p, int BM) {
   return wide ? CV_REG : CV_REG_V4;
 }
 
+// Whether the direct kernel finishes its tiles from registers (finish_regs)
+// rather than through LDS (finish_tile): it can with whole float4 column
+// groups (Co and out_ps multiples of 4) and none of the tile-wide epilogues
+// (greedy CTC, DB head).  Measured on the detector and recognizer layers:
+// the register epilogue is faster for fp32 and for bf16 up to K = 512; the
+// LDS one writes longer row segments per store, which wins for bf16 layers
+// of deeper K (1-4 %) and for upsample-on-write (2x at 8x8 blocks).
+static bool regs_epilogue(const ConvParams& p) {
+  const int K = p.kh * p.kw * p.C;
+  return !p.db_ch && !p.ctc_part && p.Co % 4 == 0 && p.out_ps % 4 == 0 && p.rep == 1 &&
+         (p.dt == DT_F32 || K <= 512);
+}
+
 template <typename T, int BM, int BN, int WM, int WN>
 static void launch_tile_kernel(const ConvParams& p, dim3 grid, hipStream_t s) {
   // Stages: fp32 slices take long enough on the MFMAs that three cover the
@@ -1012,17 +1219,34 @@ static void launch_tile_kernel(const ConvParams& p, dim3 grid, hipStream_t s) {
   // CU); bf16 takes four where they fit in about 40 KB.
   constexpr int S = sizeof(T) == 2 && (BM + BN) * 64 <= 10240 ? 4 : 3;
   constexpr int VW = 16 / sizeof(T);  // k values per 16-byte load
+  const bool regs = regs_epilogue(p);
   switch (conv_variant(p, BM)) {
     case CV_DIRECT_1X1:
-      hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, false>), grid, dim3(256), 0, s, p);
+      if (regs)
+        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, false, true>), grid, dim3(256), 0, s,
+                           p);
+      else
+        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, false, false>), grid, dim3(256), 0,
+                           s, p);
       break;
     case CV_DIRECT:
-      hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, false, S, false>), grid, dim3(256), 0, s, p);
+      if (regs)
+        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, false, S, false, true>), grid, dim3(256), 0,
+                           s, p);
+      else
+        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, false, S, false, false>), grid, dim3(256), 0,
+                           s, p);
       break;
     case CV_DIRECT_GATE:
-      if constexpr (sizeof(T) == 4)
-        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, true>), grid, dim3(256),
-                           (unsigned)((2 * (size_t)p.C + GemmTraits<T>::BK) * sizeof(float)), s, p);
+      if constexpr (sizeof(T) == 4) {
+        const unsigned lds = (unsigned)((2 * (size_t)p.C + GemmTraits<T>::BK) * sizeof(float));
+        if (regs)
+          hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, true, true>), grid, dim3(256), lds,
+                             s, p);
+        else
+          hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, true, false>), grid, dim3(256),
+                             lds, s, p);
+      }
       break;
     case CV_REG_1X1:
       hipLaunchKernelGGL((conv_gemm_kernel<T, BM, BN, WM, WN, true, VW>), grid, dim3(256), 0, s, p);
