@@ -193,6 +193,9 @@ def also(gpu, warmup, steps):
         ("det", "small", (8, 3, 416, 736), "f32"),
         ("det", "medium", (1, 3, 416, 736), "f32"),
         ("det", "tiny", (1, 3, 832, 1472), "f32"),
+        ("rec", "tiny", (1, 3, 48, 320), "f32"),
+        ("rec", "small", (1, 3, 48, 320), "f32"),
+        ("rec", "medium", (1, 3, 48, 320), "f32"),
         ("rec", "tiny", (64, 3, 48, 320), "f32"),
         ("rec", "small", (64, 3, 48, 320), "f32"),
         ("rec", "medium", (256, 3, 48, 320), "f32"),

@@ -126,6 +126,9 @@ void launch_depthwise(const DwParams& p, hipStream_t s);
 // Name of the kernel instance launch_depthwise picks.
 const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho);
 void launch_se(const SeParams& p, hipStream_t s);
+// Whether launch_se runs the gate as one kernel (small maps and weights; the
+// partial and hidden arrays are then unused).
+bool se_fused(const SeParams& p);
 
 // NCHW fp32 (3 planes) -> NHWC with 4 channels (fourth channel zero).
 void launch_nchw_to_nhwc4(const float* in, void* out, int N, int H, int W, int dt, hipStream_t s);

@@ -402,7 +402,64 @@ __global__ __launch_bounds__(256) void se_expand_kernel(SeParams p) {
   if (lane < 4 && c0 + lane < p.C) p.gate[(size_t)n * p.C + c0 + lane] = act_apply(p.gate_act, a[lane] + p.b2[c0 + lane]);
 }
 
+// The whole gate of one image in one workgroup, for small maps and weights
+// (where three dependent launches cost more than the work): channel means
+// (lanes split channels x pixel phases, fixed-order LDS reduction), then the
+// reducing and expanding 1x1 convs as in stages 2 and 3, 16 waves at a time.
+template <typename T>
+__global__ __launch_bounds__(1024) void se_fused_kernel(SeParams p) {
+  extern __shared__ float sm[];
+  const int cr4 = (p.Cr + 3) & ~3;
+  float* mean = sm;                                          // [C]
+  float* hid = sm + p.C;                                     // [Cr]
+  float4* red = reinterpret_cast<float4*>(sm + p.C + cr4);  // [1024]
+  const T* in = static_cast<const T*>(p.in);
+  const int n = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int C4 = p.C >> 2;
+  const int lanes_p = 1024 / C4;
+  const int cq = tid % C4, pl = tid / C4;
+  float4 s = f4_zero();
+  if (pl < lanes_p) s = strided_sum4<T>(s, in + (size_t)n * p.HW * p.in_ps + cq * 4, p.in_ps, pl, p.HW, lanes_p);
+  red[tid] = s;
+  __syncthreads();
+  if (tid < C4) {
+    float4 t = red[tid];
+    for (int k = 1; k < lanes_p; ++k) t = f4_sum(t, red[k * C4 + tid]);
+    const float count = (float)p.HW;
+    mean[tid * 4 + 0] = t.x / count;
+    mean[tid * 4 + 1] = t.y / count;
+    mean[tid * 4 + 2] = t.z / count;
+    mean[tid * 4 + 3] = t.w / count;
+  }
+  __syncthreads();
+  const int wave = tid >> 6, lane = tid & 63;
+  for (int j0 = wave * 4; j0 < p.Cr; j0 += 64) {
+    const float4 acc = wave_dot4(p.w1, j0, p.Cr, mean, p.C, lane);
+    const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+    if (lane < 4 && j0 + lane < p.Cr) hid[j0 + lane] = fmaxf(a[lane] + p.b1[j0 + lane], 0.0f);
+  }
+  __syncthreads();
+  for (int c0 = wave * 4; c0 < p.C; c0 += 64) {
+    const float4 acc = wave_dot4(p.w2, c0, p.C, hid, p.Cr, lane);
+    const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+    if (lane < 4 && c0 + lane < p.C)
+      p.gate[(size_t)n * p.C + c0 + lane] = act_apply(p.gate_act, a[lane] + p.b2[c0 + lane]);
+  }
+}
+
+bool se_fused(const SeParams& p) {
+  const size_t es = p.dt == DT_BF16 ? 2 : 4;
+  return p.C % 4 == 0 && p.C <= 4096 && (size_t)p.HW * p.C * es <= (256u << 10) &&
+         (size_t)p.C * p.Cr * 2 * sizeof(float) <= (128u << 10);
+}
+
 void launch_se(const SeParams& p, hipStream_t s) {
+  if (se_fused(p)) {
+    const size_t lds = ((size_t)p.C + ((p.Cr + 3) & ~3)) * sizeof(float) + 1024 * sizeof(float4);
+    DISPATCH_DT(p.dt, hipLaunchKernelGGL(se_fused_kernel<T>, dim3(p.N), dim3(1024), lds, s, p));
+    return;
+  }
   int chunk = (p.HW + p.P - 1) / p.P;
   DISPATCH_DT(p.dt, hipLaunchKernelGGL(se_partial_kernel<T>, dim3(p.P, p.N), dim3(256), 0, s, p, chunk));
   size_t lds = (size_t)p.C * sizeof(float) + 256 * sizeof(float4);

@@ -378,30 +378,36 @@ class Builder {
   View se(const View& x, const SeW& w, const std::string& name) {
     int HW = x.h * x.w;
     int P = std::max(1, std::min(HW / 64, std::max(1, 1024 / x.n)));
-    View part = alloc(x.n, P, 1, x.c, name + ".partial", DT_F32);
-    View hid = alloc(x.n, 1, 1, (int)round_up(w.cr, 4), name + ".hidden", DT_F32);
-    View gate = alloc(x.n, 1, 1, x.c, name, DT_F32);
     SeParams base{};
     base.N = x.n, base.HW = HW, base.C = x.c, base.in_ps = x.ps, base.P = P, base.Cr = w.cr, base.gate_act = w.act;
     base.dt = x.dt;
+    // Small gates run in one kernel without the partial and hidden arrays.
+    const bool fused = se_fused(base);
+    View part, hid;
+    if (!fused) {
+      part = alloc(x.n, P, 1, x.c, name + ".partial", DT_F32);
+      hid = alloc(x.n, 1, 1, (int)round_up(w.cr, 4), name + ".hidden", DT_F32);
+    }
+    View gate = alloc(x.n, 1, 1, x.c, name, DT_F32);
     View in = x;
     SeW ww = w;
     Op op;
     op.name = name;
-    op.kernel = "se_gate";
+    op.kernel = fused ? "se_fused" : "se_gate";
     op.flops = 2.0 * x.n * ((double)HW * x.c + 2.0 * x.c * w.cr);
     op.bytes = (double)dtype_size(x.dt) * x.pixels() * x.c + 4.0 * (2.0 * x.c * w.cr + x.n * x.c);
     op.reads = {x.buf};
-    op.writes = {part.buf, hid.buf, gate.buf};
+    op.writes = {gate.buf};
+    if (!fused) op.writes.insert(op.writes.end(), {part.buf, hid.buf});
     op.launch = [=](const Exec& ex, hipStream_t s) {
       SeParams p = base;
       p.in = ex.ptr(in);
-      p.partial = ex.fptr(part);
+      p.partial = fused ? nullptr : ex.fptr(part);
       p.w1 = ex.w(ww.w1);
       p.b1 = ex.w(ww.b1);
       p.w2 = ex.w(ww.w2);
       p.b2 = ex.w(ww.b2);
-      p.hidden = ex.fptr(hid);
+      p.hidden = fused ? nullptr : ex.fptr(hid);
       p.gate = ex.fptr(gate);
       launch_se(p, s);
     };
