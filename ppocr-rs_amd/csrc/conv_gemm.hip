@@ -1304,8 +1304,13 @@ int conv_tile_cols(int M, int cols, int dt) {
 }
 
 // Split K when the tiles fill fewer than 192 of the 256 CUs: enough splits
-// for about two workgroups per CU, each split keeping at least 8 K slices
-// (the load pipeline is 3-4 slices deep), at most 16 splits.
+// for about two workgroups per CU.  Also when they give only one to two
+// workgroups per CU (<= 560 tiles) and K is deep (>= 48 slices), where the
+// CUs holding two tiles set the time: splits for about eight workgroups per
+// CU (measured on the detector's 13x23 and 52x92 layers: 1.2-1.4x faster
+// with the finish pass included; shallower K or more tiles measured
+// slower).  Each split keeps at least 8 K slices (the load pipeline is 3-4
+// slices deep), at most 16 splits.
 int conv_split_k(int M, int Co, int K, int dt) {
   static const int bm[] = {256, 128, 128, 64};
   static const int bn[] = {16, 32, 64, 64};
@@ -1313,8 +1318,14 @@ int conv_split_k(int M, int Co, int K, int dt) {
   const long tiles = (long)((M + bm[t] - 1) / bm[t]) * ((Co + bn[t] - 1) / bn[t]);
   const int bk = dt == DT_BF16 ? GemmTraits<bf16>::BK : GemmTraits<float>::BK;
   const int nk = (K + bk - 1) / bk;
-  if (Co % 4 != 0 || tiles >= 192) return 1;
-  long s = (512 + tiles - 1) / tiles;
+  if (Co % 4 != 0) return 1;
+  long s;
+  if (tiles < 192)
+    s = (512 + tiles - 1) / tiles;
+  else if (tiles <= 560 && nk >= 48)
+    s = (2048 + tiles - 1) / tiles;
+  else
+    return 1;
   s = std::min<long>(s, nk / 8);
   s = std::min<long>(s, kMaxSplits);
   return s >= 2 ? (int)s : 1;
