@@ -739,6 +739,95 @@ __device__ __forceinline__ void finish_regs(const ConvParams& p, floatx4 (&acc)[
   }
 }
 
+// DB head tail from registers (p.db_ch a multiple of 16, tiles whole taps
+// wide).  After the quad transpose a lane holds row r and columns
+// 4 g .. 4 g + 3 of a 16-column block, all in one tap (column tap * db_ch +
+// o): it adds the bias, applies ReLU, multiplies by its four rows of
+// conv_final's weights and adds the block's four column groups with xor
+// shuffles.  The block partials go through LDS (`part`, BM x BN / 16
+// float4, free once every wave has passed the barrier), and each (row, tap)
+// item adds its db_ch / 16 blocks in order, applies the sigmoid and writes
+// its 2x2 block of the map (src/cpu/model.rs:1516-1520).
+template <typename T, int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void finish_db_regs(const ConvParams& p, floatx4 (&acc)[BM / (WM * 16)][BN / (WN * 16)],
+                                               int m0, int n0, int M, const float4 (&bias)[BN / (WN * 16)],
+                                               float4* part) {
+  constexpr int TM = BM / (WM * 16);
+  constexpr int TN = BN / (WN * 16);
+  constexpr int NB = BN / 16;  // column blocks per tile
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int ch = p.db_ch;
+  float4 wq[TN][4];  // conv_final weights of this lane's four hidden channels per block
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int o0 = regs_col<BN, WN>(n0, j) % ch;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wq[j][e] = *reinterpret_cast<const float4*>(p.db_wf + (size_t)(o0 + e) * 4);
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = quad_transpose(acc[i][j], lane);
+  const int rsub = 4 * (lane >> 4) + (lane & 3);
+  float4 f[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const float b[4] = {bias[j].x, bias[j].y, bias[j].z, bias[j].w};
+      float4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float u = fmaxf(acc[i][j][e] + b[e], 0.0f);
+        s.x = fmaf(u, wq[j][e].x, s.x);
+        s.y = fmaf(u, wq[j][e].y, s.y);
+        s.z = fmaf(u, wq[j][e].z, s.z);
+        s.w = fmaf(u, wq[j][e].w, s.w);
+      }
+#pragma unroll
+      for (int x = 4; x <= 8; x <<= 1) {
+        s.x += __shfl_xor(s.x, x);
+        s.y += __shfl_xor(s.y, x);
+        s.z += __shfl_xor(s.z, x);
+        s.w += __shfl_xor(s.w, x);
+      }
+      f[i][j] = s;
+    }
+  __syncthreads();  // every wave is done with the operand stages `part` overlays
+  if (((lane >> 2) & 3) == 0) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) part[(wm * TM * 16 + i * 16 + rsub) * NB + wn * TN + j] = f[i][j];
+  }
+  __syncthreads();
+  const int taps = BN / ch, per = ch / 16;
+  const int HoWo = p.Ho * p.Wo;
+  const int OW = 4 * p.Wo;
+  float* map = static_cast<float*>(p.out);
+  for (int it = tid; it < BM * taps; it += 256) {
+    const int row = it / taps, tl = it - row * taps;
+    const int m = m0 + row;
+    if (m >= M) continue;
+    float4 s = part[row * NB + tl * per];
+    for (int b = 1; b < per; ++b) {
+      const float4 t = part[row * NB + tl * per + b];
+      s = make_float4(s.x + t.x, s.y + t.y, s.z + t.z, s.w + t.w);
+    }
+    const int img = m / HoWo, r = m - img * HoWo;
+    const int y = r / p.Wo, x = r - y * p.Wo;
+    const int tap = n0 / ch + tl;
+    float* top = map + ((size_t)img * 4 * p.Ho + 4 * y + 2 * (tap >> 1)) * OW + 4 * x + 2 * (tap & 1);
+    *reinterpret_cast<float2*>(top) =
+        make_float2(act_apply(ACT_SIGMOID, s.x + p.db_bf), act_apply(ACT_SIGMOID, s.y + p.db_bf));
+    *reinterpret_cast<float2*>(top + OW) =
+        make_float2(act_apply(ACT_SIGMOID, s.z + p.db_bf), act_apply(ACT_SIGMOID, s.w + p.db_bf));
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Direct-to-LDS variant (layers without an SE input gate, 16-byte k vectors).
 // buffer_load_dwordx4 ... lds writes each lane's 16 bytes straight into LDS,
@@ -837,7 +926,15 @@ __device__ __forceinline__ void lds_wait(floatx4& v) { asm volatile("s_waitcnt l
 // rows of those images are staged in LDS once and each A operand fragment is
 // multiplied by its gate values after it is read, x * g rounded to fp32 as
 // when the gate is applied during the gather.
-template <typename T, int BM, int BN, int WM, int WN, bool PW, int S, bool GATE, bool REGS>
+// Epilogue of the direct kernel, fixed per instantiation so each keeps only
+// the registers its own epilogue needs.
+enum DirectEpi : int {
+  EPI_LDS = 0,   // finish_tile: staged through LDS (every epilogue)
+  EPI_REGS = 1,  // finish_regs
+  EPI_DB = 2,    // finish_db_regs (DB head tail)
+};
+
+template <typename T, int BM, int BN, int WM, int WN, bool PW, int S, bool GATE, int EPI>
 __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   constexpr int BK = GemmTraits<T>::BK;  // one 64-byte row per K slice
   constexpr int VE = 16 / sizeof(T);
@@ -1088,6 +1185,7 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   };
   // Epilogue bias of this thread's column groups, loaded ahead so that its
   // latency hides behind the main loop.
+  constexpr bool REGS = EPI != EPI_LDS;
   constexpr int NB = REGS ? TN : 1;
   float4 bias_pre[NB];
 #pragma unroll
@@ -1111,7 +1209,12 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
     }
   }
   wait_vmcnt<0>();  // every stage load has landed (the compiler does not count them all)
-  if constexpr (REGS) {
+  if constexpr (EPI == EPI_DB) {
+    static_assert(BM * (BN / 16) * 16 <= PART, "DB partials fit one stage");
+    finish_db_regs<T, BM, BN, WM, WN>(p, acc, m0, n0, M, bias_pre, reinterpret_cast<float4*>(st0));
+    return;
+  }
+  if constexpr (EPI == EPI_REGS) {
     finish_regs<T, BM, BN, WM, WN>(p, acc, m0, n0, M, bias_pre);
     return;
   }
@@ -1199,17 +1302,18 @@ static int conv_variant(const ConvParams& p, int BM) {
   return wide ? CV_REG : CV_REG_V4;
 }
 
-// Whether the direct kernel finishes its tiles from registers (finish_regs)
-// rather than through LDS (finish_tile): it can with whole float4 column
-// groups (Co and out_ps multiples of 4) and none of the tile-wide epilogues
-// (greedy CTC, DB head).  Measured on the detector and recognizer layers:
+// Whether the direct kernel finishes its tiles from registers (finish_regs,
+// or finish_db_regs for the DB head with 16-column taps) rather than through
+// LDS (finish_tile): it can with whole float4 column groups (Co and out_ps
+// multiples of 4) and without the greedy-CTC epilogue.  Measured on the detector and recognizer layers:
 // the register epilogue is faster for fp32 and for bf16 up to K = 512; the
 // LDS one writes longer row segments per store, which wins for bf16 layers
 // of deeper K (1-4 %) and for upsample-on-write (2x at 8x8 blocks).
 static bool regs_epilogue(const ConvParams& p) {
   const int K = p.kh * p.kw * p.C;
-  return !p.db_ch && !p.ctc_part && p.Co % 4 == 0 && p.out_ps % 4 == 0 && p.rep == 1 &&
-         (p.dt == DT_F32 || K <= 512);
+  if (p.ctc_part) return false;
+  if (p.db_ch) return p.db_ch % 16 == 0;
+  return p.Co % 4 == 0 && p.out_ps % 4 == 0 && p.rep == 1 && (p.dt == DT_F32 || K <= 512);
 }
 
 template <typename T, int BM, int BN, int WM, int WN>
@@ -1222,29 +1326,32 @@ static void launch_tile_kernel(const ConvParams& p, dim3 grid, hipStream_t s) {
   const bool regs = regs_epilogue(p);
   switch (conv_variant(p, BM)) {
     case CV_DIRECT_1X1:
-      if (regs)
-        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, false, true>), grid, dim3(256), 0, s,
-                           p);
+      if (regs && p.db_ch)
+        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, false, EPI_DB>), grid, dim3(256), 0,
+                           s, p);
+      else if (regs)
+        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, false, EPI_REGS>), grid, dim3(256), 0,
+                           s, p);
       else
-        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, false, false>), grid, dim3(256), 0,
+        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, false, EPI_LDS>), grid, dim3(256), 0,
                            s, p);
       break;
     case CV_DIRECT:
-      if (regs)
-        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, false, S, false, true>), grid, dim3(256), 0,
-                           s, p);
+      if (regs && !p.db_ch)
+        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, false, S, false, EPI_REGS>), grid, dim3(256),
+                           0, s, p);
       else
-        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, false, S, false, false>), grid, dim3(256), 0,
+        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, false, S, false, EPI_LDS>), grid, dim3(256), 0,
                            s, p);
       break;
     case CV_DIRECT_GATE:
       if constexpr (sizeof(T) == 4) {
         const unsigned lds = (unsigned)((2 * (size_t)p.C + GemmTraits<T>::BK) * sizeof(float));
-        if (regs)
-          hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, true, true>), grid, dim3(256), lds,
-                             s, p);
+        if (regs && !p.db_ch)
+          hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, true, EPI_REGS>), grid, dim3(256),
+                             lds, s, p);
         else
-          hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, true, false>), grid, dim3(256),
+          hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, true, EPI_LDS>), grid, dim3(256),
                              lds, s, p);
       }
       break;
