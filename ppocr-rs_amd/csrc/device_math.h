@@ -66,6 +66,19 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
+// v rounded to the storage type T (what st4 stores and ld4 reads back).
+template <typename T>
+__device__ __forceinline__ float4 round4(float4 v);
+template <>
+__device__ __forceinline__ float4 round4<float>(float4 v) {
+  return v;
+}
+template <>
+__device__ __forceinline__ float4 round4<bf16>(float4 v) {
+  return make_float4(bf16_bits_to_f32(f32_to_bf16_bits(v.x)), bf16_bits_to_f32(f32_to_bf16_bits(v.y)),
+                     bf16_bits_to_f32(f32_to_bf16_bits(v.z)), bf16_bits_to_f32(f32_to_bf16_bits(v.w)));
+}
+
 // Four consecutive values (16 B as fp32, 8 B as bf16).
 template <typename T>
 __device__ __forceinline__ float4 ld4(const T* p);

@@ -89,6 +89,9 @@ struct DwParams {
   const void* res;  // out = res + act(dw(x) + b)
   int res_ps;
   int dt;
+  // Per-block channel sums of the stored output for a squeeze-excitation
+  // ([N][P][C] fp32, P = depthwise_se_blocks()), or null.
+  float* se_part;
 };
 
 // Squeeze-excitation gate: g[n, c] = gate_act(W2 relu(W1 mean(x) + b1) + b2).
@@ -123,9 +126,15 @@ int conv_split_k(int M, int Co, int K, int dt);
 // pair per row: out[m] = {argmax (ties -> last index), softmax value of it}.
 void launch_ctc_merge(const float* part, int M, int n_tiles, float* out, hipStream_t s);
 void launch_depthwise(const DwParams& p, hipStream_t s);
+// Blocks per image of the depthwise launch when it can leave the channel
+// sums of its output for a squeeze-excitation (p.se_part), else 0.
+int depthwise_se_blocks(const DwParams& p);
 // Name of the kernel instance launch_depthwise picks.
 const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho);
 void launch_se(const SeParams& p, hipStream_t s);
+// Stages 2 and 3 of launch_se from partial sums already in p.partial
+// ([N][P][C], e.g. from the producing depthwise).
+void launch_se_from_partials(const SeParams& p, hipStream_t s);
 // Whether launch_se runs the gate as one kernel (small maps and weights; the
 // partial and hidden arrays are then unused).
 bool se_fused(const SeParams& p);

@@ -142,18 +142,34 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
   }
   const int c = ch0 + c4 * 4;
   const int oy = oy0 + ty;
-  if (c >= p.C || oy >= p.Ho) return;
-  float4 b = p.bias ? *reinterpret_cast<const float4*>(p.bias + c) : f4_zero();
+  const bool cin = c < p.C;
+  float4 b = p.bias && cin ? *reinterpret_cast<const float4*>(p.bias + c) : f4_zero();
+  float4 sum = f4_zero();  // this lane's stored outputs, for the SE partial sums
 #pragma unroll
   for (int r = 0; r < XR; ++r) {
     int ox = ox0 + xg * XR + r;
-    if (ox >= p.Wo) break;
+    if (!cin || oy >= p.Ho || ox >= p.Wo) break;
     float4 v = acc[r];
     if (p.bias) v = f4_sum(v, b);
     v = f4_act(p.act, v);
     size_t pix = (size_t)(n * p.Ho + oy) * p.Wo + ox;
     if (p.res) v = f4_sum(ld4<T>(static_cast<const T*>(p.res) + pix * p.res_ps + c), v);
-    st4<T>(static_cast<T*>(p.out) + pix * p.out_ps + c, v);
+    T* o = static_cast<T*>(p.out) + pix * p.out_ps + c;
+    st4<T>(o, v);
+    if (p.se_part) sum = f4_sum(sum, round4<T>(v));
+  }
+  if (p.se_part) {
+    // Channel sums of the block's outputs (in the storage type, as a later
+    // reader sees them): lanes of one channel group add in a fixed order.
+    __syncthreads();  // every lane is done with the input tile
+    tile[tid] = sum;
+    __syncthreads();
+    if (tid < C4B && ch0 + tid * 4 < p.C) {
+      float4 t = tile[tid];
+      for (int k = 1; k < 256 / C4B; ++k) t = f4_sum(t, tile[k * C4B + tid]);
+      const int blk = blockIdx.y * gridDim.x + blockIdx.x;
+      *reinterpret_cast<float4*>(p.se_part + ((size_t)n * gridDim.x * gridDim.y + blk) * p.C + ch0 + tid * 4) = t;
+    }
   }
 }
 
@@ -345,6 +361,15 @@ static void launch_dw_wave(const DwParams& p, hipStream_t s) {
   hipLaunchKernelGGL((depthwise_wave_kernel<T, KH, KW>), grid, dim3(256), 0, s, p);
 }
 
+// The launch shape of the tiled 3x3 kernel, the one that can leave SE
+// partial sums (stride 1 and more than 4 output rows).
+constexpr int kDw3TY = 8, kDw3C4B = 8, kDw3TX = 256 / (kDw3C4B * kDw3TY) * 4;
+
+int depthwise_se_blocks(const DwParams& p) {
+  if (!(p.kh == 3 && p.kw == 3 && p.sh == 1 && p.sw == 1 && p.Ho > 4)) return 0;
+  return ((p.Wo + kDw3TX - 1) / kDw3TX) * ((p.Ho + kDw3TY - 1) / kDw3TY);
+}
+
 template <typename T>
 static void launch_dw_typed(const DwParams& p, hipStream_t s) {
   // 3x3 with vertical stride 2 (stage entries), and maps of at most 4 rows
@@ -354,7 +379,7 @@ static void launch_dw_typed(const DwParams& p, hipStream_t s) {
   if (p.kh == 3 && p.kw == 3 && p.sh == 1 && p.Ho <= 4)
     return p.Ho == 3 ? launch_dw_strip<T, 3, 3, 3, 1>(p, s) : launch_dw_strip<T, 3, 3, 4, 1>(p, s);
   if (p.sh == 1 && p.sw == 1) {
-    if (p.kh == 3 && p.kw == 3) return launch_dw_tiled<T, 3, 3, 8>(p, s);
+    if (p.kh == 3 && p.kw == 3) return launch_dw_tiled<T, 3, 3, kDw3TY, 4, kDw3C4B>(p, s);
     // 5x5 and 9x9: taps in scalar registers (1.1-1.2x the LDS-tap kernel);
     // 7x7 (32 channels here) measured even: 16-row tiles of 16 channels.
     if (p.kh == 5 && p.kw == 5) return launch_dw_wave<T, 5, 5>(p, s);
@@ -551,6 +576,12 @@ bool se_fused(const SeParams& p) {
   const size_t es = p.dt == DT_BF16 ? 2 : 4;
   return p.C % 4 == 0 && p.C <= 4096 && (size_t)p.HW * p.C * es <= (256u << 10) &&
          (size_t)p.C * p.Cr * 2 * sizeof(float) <= (128u << 10);
+}
+
+void launch_se_from_partials(const SeParams& p, hipStream_t s) {
+  size_t lds = (size_t)p.C * sizeof(float) + 256 * sizeof(float4);
+  hipLaunchKernelGGL(se_reduce_kernel, dim3(p.N, (p.Cr + 15) / 16), dim3(256), lds, s, p);
+  hipLaunchKernelGGL(se_expand_kernel, dim3(p.N, (p.C + 15) / 16), dim3(256), (size_t)p.Cr * sizeof(float), s, p);
 }
 
 void launch_se(const SeParams& p, hipStream_t s) {

@@ -335,7 +335,19 @@ class Builder {
     return out;
   }
 
-  View depthwise(const View& x, const DwW& w, int act, const View* res, const std::string& name) {
+  // Channel sums of a depthwise output left by the depthwise kernel for the
+  // squeeze-excitation that reads it: [N][P][C] fp32.
+  struct SePartial {
+    View part;
+    int P = 0;
+  };
+
+  // Depthwise conv.  With se_cr > 0 a squeeze-excitation of reduction width
+  // se_cr reads the output next; when the kernel can, and the gate is not
+  // small enough for its one-kernel form, it also leaves the gate's channel
+  // sums in *sp (sp->P = 0 otherwise).
+  View depthwise(const View& x, const DwW& w, int act, const View* res, const std::string& name, int se_cr = 0,
+                 SePartial* sp = nullptr) {
     if (x.c != w.c) raise(PPOCR_ERR_INVALID_MODEL, name + ": channel mismatch");
     int Ho = (x.h + w.pt + w.pb - w.kh) / w.sh + 1;
     int Wo = (x.w + w.pl + w.pr - w.kw) / w.sw + 1;
@@ -346,6 +358,20 @@ class Builder {
     base.kh = w.kh, base.kw = w.kw, base.sh = w.sh, base.sw = w.sw, base.pt = w.pt, base.pl = w.pl;
     base.act = act;
     base.dt = x.dt;
+    View part;
+    bool has_part = false;
+    if (sp) {
+      sp->P = 0;
+      SeParams se{};
+      se.N = x.n, se.HW = Ho * Wo, se.C = w.c, se.Cr = se_cr, se.dt = x.dt;
+      const int P = depthwise_se_blocks(base);
+      if (se_cr > 0 && P > 0 && !se_fused(se)) {
+        part = alloc(x.n, P, 1, w.c, name + ".se_partial", DT_F32);
+        has_part = true;
+        sp->part = part;
+        sp->P = P;
+      }
+    }
     View in = x;
     View r = res ? *res : View();
     bool has_res = res;
@@ -360,6 +386,7 @@ class Builder {
     op.reads = {x.buf};
     if (has_res) op.reads.push_back(r.buf);
     op.writes = {out.buf};
+    if (has_part) op.writes.push_back(part.buf);
     op.launch = [=](const Exec& ex, hipStream_t s) {
       DwParams p = base;
       p.in = ex.ptr(in);
@@ -367,6 +394,7 @@ class Builder {
       p.wt = ex.w(wo);
       p.bias = ex.w(bo);
       p.res = has_res ? ex.ptr(r) : nullptr;
+      p.se_part = has_part ? ex.fptr(part) : nullptr;
       launch_depthwise(p, s);
     };
     add_op(std::move(op));
@@ -375,16 +403,21 @@ class Builder {
 
   // Squeeze-excitation gate [N,1,1,C] (fp32) of x (src/cpu/model.rs:456-493,
   // :1069-1105).
-  View se(const View& x, const SeW& w, const std::string& name) {
+  // With sp->P > 0 the channel sums come from the depthwise that wrote x.
+  View se(const View& x, const SeW& w, const std::string& name, const SePartial* sp = nullptr) {
     int HW = x.h * x.w;
-    int P = std::max(1, std::min(HW / 64, std::max(1, 1024 / x.n)));
+    const bool given = sp && sp->P > 0;
+    int P = given ? sp->P : std::max(1, std::min(HW / 64, std::max(1, 1024 / x.n)));
     SeParams base{};
     base.N = x.n, base.HW = HW, base.C = x.c, base.in_ps = x.ps, base.P = P, base.Cr = w.cr, base.gate_act = w.act;
     base.dt = x.dt;
     // Small gates run in one kernel without the partial and hidden arrays.
-    const bool fused = se_fused(base);
+    const bool fused = !given && se_fused(base);
     View part, hid;
-    if (!fused) {
+    if (given) {
+      part = sp->part;
+      hid = alloc(x.n, 1, 1, (int)round_up(w.cr, 4), name + ".hidden", DT_F32);
+    } else if (!fused) {
       part = alloc(x.n, P, 1, x.c, name + ".partial", DT_F32);
       hid = alloc(x.n, 1, 1, (int)round_up(w.cr, 4), name + ".hidden", DT_F32);
     }
@@ -393,12 +426,16 @@ class Builder {
     SeW ww = w;
     Op op;
     op.name = name;
-    op.kernel = fused ? "se_fused" : "se_gate";
+    op.kernel = fused ? "se_fused" : given ? "se_gate+dw_sums" : "se_gate";
     op.flops = 2.0 * x.n * ((double)HW * x.c + 2.0 * x.c * w.cr);
-    op.bytes = (double)dtype_size(x.dt) * x.pixels() * x.c + 4.0 * (2.0 * x.c * w.cr + x.n * x.c);
-    op.reads = {x.buf};
+    op.bytes = (given ? 4.0 * x.n * P * x.c : (double)dtype_size(x.dt) * x.pixels() * x.c) +
+               4.0 * (2.0 * x.c * w.cr + x.n * x.c);
+    op.reads = {given ? part.buf : x.buf};
     op.writes = {gate.buf};
-    if (!fused) op.writes.insert(op.writes.end(), {part.buf, hid.buf});
+    if (given)
+      op.writes.push_back(hid.buf);
+    else if (!fused)
+      op.writes.insert(op.writes.end(), {part.buf, hid.buf});
     op.launch = [=](const Exec& ex, hipStream_t s) {
       SeParams p = base;
       p.in = ex.ptr(in);
@@ -409,7 +446,10 @@ class Builder {
       p.b2 = ex.w(ww.b2);
       p.hidden = fused ? nullptr : ex.fptr(hid);
       p.gate = ex.fptr(gate);
-      launch_se(p, s);
+      if (given)
+        launch_se_from_partials(p, s);
+      else
+        launch_se(p, s);
     };
     add_op(std::move(op));
     return gate;
@@ -613,13 +653,14 @@ View lcnet_block(Builder& B, const View& x, const std::string& p, BlockSpec s) {
   bool residual = s.ci == s.co && s.sh == 1 && s.sw == 1;
   DwW tw = residual ? B.dw_w(p + ".token_conv", s.ci, 3, 3, s.sh, s.sw, {1, 1, 1, 1}, true)
                     : B.dw_w(p + ".token_conv", s.ci, 3, 3, s.sh, s.sw, {1, 1, 1, 1}, false, "normalization");
-  View t = B.depthwise(x, tw, ACT_NONE, nullptr, p + ".token_conv");
-  View gate;
   bool has_se = s.se;
+  Builder::SePartial sums;
+  View t = B.depthwise(x, tw, ACT_NONE, nullptr, p + ".token_conv", has_se ? s.ci / 4 : 0, &sums);
+  View gate;
   if (has_se) {
     std::string q = p + ".token_squeeze_excitation.convolutions";
     SeW sw = B.se_w(q + ".0", q + ".2", s.ci, s.ci / 4, ACT_HSIG6);
-    gate = B.se(t, sw, p + ".se");
+    gate = B.se(t, sw, p + ".se", &sums);
   }
   ConvW c1 = B.conv_w(p + ".channel_conv1", s.ci, 2 * s.ci, 1, 1, 1, 1, {0, 0, 0, 0}, false, "normalization");
   ConvW c2 = B.conv_w(p + ".channel_conv2", 2 * s.ci, s.co, 1, 1, 1, 1, {0, 0, 0, 0}, false, "normalization");
