@@ -70,6 +70,7 @@ def check_recognizer(actual, expected):
     ("small", (8, 3, 416, 736), 11, "uniform"),
     ("medium", (1, 3, 416, 736), 7, "uniform"),
     ("medium", (2, 3, 128, 160), 9, "uniform"),
+    ("medium", (8, 3, 416, 736), 13, "uniform"),  # the throughput benchmark's batch (split-K choices differ)
 ])
 def test_detector_matches_oracle(gpu, size, shape, seed, pattern):
     x = seeded.seeded_batch(shape[0], shape[2], shape[3], seed, detector=True, pattern=pattern)
@@ -91,6 +92,7 @@ def test_detector_matches_oracle(gpu, size, shape, seed, pattern):
     ("small", 4, 320),
     ("medium", 4, 320),
     ("medium", 2, 648),
+    ("medium", 256, 320),  # the long-batch benchmark shape
 ])
 def test_recognizer_matches_oracle(gpu, size, batch, width):
     x = seeded.seeded_batch(batch, 48, width, 100 + batch, detector=False)
@@ -125,9 +127,11 @@ BF16_REC = {"mean": 1e-4, "confident_argmax": 0.99}
     ("det", "tiny", (1, 3, 416, 736)),
     ("det", "small", (2, 3, 416, 736)),
     ("det", "medium", (1, 3, 416, 736)),
+    ("det", "medium", (8, 3, 416, 736)),
     ("rec", "tiny", (16, 3, 48, 320)),
     ("rec", "small", (16, 3, 48, 320)),
     ("rec", "medium", (16, 3, 48, 320)),
+    ("rec", "medium", (256, 3, 48, 320)),
 ])
 def test_bf16_storage_within_stated_tolerance(gpu, kind, size, shape):
     x = seeded.seeded_batch(shape[0], shape[2], shape[3], 31, detector=(kind == "det"))
