@@ -88,7 +88,8 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
   constexpr int XG = 256 / (C4B * TY);    // lane groups along x
   constexpr int TX = XG * XR;
   constexpr int IH = TY + KH - 1, IW = TX + KW - 1;
-  __shared__ float4 tile[IH * IW * C4B];
+  constexpr int IWP = IW | 1;  // odd row pitch (pixels)
+  __shared__ float4 tile[IH * IWP * C4B];
   __shared__ float4 taps[KH * KW * C4B];
   const T* in = static_cast<const T*>(p.in);
 
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
     float4 v = f4_zero();
     if (c < p.C && gy >= 0 && gy < p.H && gx >= 0 && gx < p.W)
       v = ld4<T>(in + ((size_t)(n * p.H + gy) * p.W + gx) * p.in_ps + c);
-    tile[i] = v;
+    tile[(iy * IWP + ix) * C4B + c4] = v;
   }
   for (int i = tid; i < KH * KW * C4B; i += 256) {
     int c = ch0 + (i % C4B) * 4;
@@ -116,9 +117,13 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
   }
   __syncthreads();
 
+  // Channel groups fastest, then rows, then x groups: with C4B * TY = 64 a
+  // wave reads one x group, and the odd row pitch puts its lanes on
+  // consecutive 16-byte bank slots (4 cycles per ds_read_b128; x groups
+  // inside a wave measured 8).
   const int c4 = tid % C4B;
-  const int xg = (tid / C4B) % XG;
-  const int ty = tid / (C4B * XG);
+  const int ty = (tid / C4B) % TY;
+  const int xg = tid / (C4B * TY);
   float4 acc[XR];
 #pragma unroll
   for (int r = 0; r < XR; ++r) acc[r] = f4_zero();
@@ -127,7 +132,7 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
   for (int ky = 0; ky < KH; ++ky) {
     float4 win[XR + KW - 1];
 #pragma unroll
-    for (int j = 0; j < XR + KW - 1; ++j) win[j] = tile[((ty + ky) * IW + xg * XR + j) * C4B + c4];
+    for (int j = 0; j < XR + KW - 1; ++j) win[j] = tile[((ty + ky) * IWP + xg * XR + j) * C4B + c4];
 #pragma unroll
     for (int kx = 0; kx < KW; ++kx) {
       float4 w = taps[(ky * KW + kx) * C4B + c4];
