@@ -948,7 +948,9 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   constexpr int STAGE_BYTES = (BM + BN) * 64;
   constexpr int LDE = BN + 4;
   constexpr int RPA = (BM + S - 1) / S;  // epilogue rows staged per stage array
-  constexpr int PART = STAGE_BYTES > RPA * LDE * 4 ? STAGE_BYTES : RPA * LDE * 4;
+  // The LDS epilogue stages the tile across the stage arrays; the others
+  // need only the stages.
+  constexpr int PART = EPI != EPI_LDS || STAGE_BYTES > RPA * LDE * 4 ? STAGE_BYTES : RPA * LDE * 4;
   __shared__ __attribute__((aligned(16))) char st0[PART];
   __shared__ __attribute__((aligned(16))) char st1[PART];
   __shared__ __attribute__((aligned(16))) char st2[PART];
