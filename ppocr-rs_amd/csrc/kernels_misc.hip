@@ -99,16 +99,22 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
   const int oy0 = blockIdx.y * TY, ox0 = blockIdx.x * TX;
   const int tid = threadIdx.x;
 
-  for (int i = tid; i < IH * IW * C4B; i += 256) {
-    int c4 = i % C4B;
-    int px = i / C4B;
-    int ix = px % IW, iy = px / IW;
-    int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
-    int c = ch0 + c4 * 4;
-    float4 v = f4_zero();
-    if (c < p.C && gy >= 0 && gy < p.H && gx >= 0 && gx < p.W)
-      v = ld4<T>(in + ((size_t)(n * p.H + gy) * p.W + gx) * p.in_ps + c);
-    tile[(iy * IWP + ix) * C4B + c4] = v;
+  {
+    // A lane keeps one channel group (256 is a multiple of C4B) and steps
+    // through the tile's pixels; the image base and channel test are hoisted.
+    static_assert(256 % C4B == 0, "fixed channel group per lane");
+    const int c4 = tid % C4B;
+    const int c = ch0 + c4 * 4;
+    const bool cok = c < p.C;
+    const T* base = in + (size_t)n * p.H * p.W * p.in_ps + c;
+    for (int px = tid / C4B; px < IH * IW; px += 256 / C4B) {
+      const int iy = px / IW, ix = px - iy * IW;
+      const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
+      float4 v = f4_zero();
+      if (cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W)
+        v = ld4<T>(base + ((size_t)gy * p.W + gx) * p.in_ps);
+      tile[(iy * IWP + ix) * C4B + c4] = v;
+    }
   }
   for (int i = tid; i < KH * KW * C4B; i += 256) {
     int c = ch0 + (i % C4B) * 4;
@@ -207,16 +213,21 @@ __global__ __launch_bounds__(256) void depthwise_wave_kernel(DwParams p) {
   const int oy0 = blockIdx.y * TY, ox0 = blockIdx.x * TX;
   const int tid = threadIdx.x;
 
-  for (int i = tid; i < IH * IW * G; i += 256) {
-    const int g = i % G;
-    const int px = i / G;
-    const int ix = px % IW, iy = px / IW;
-    const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
+  {
+    // A lane keeps one channel group and steps through the tile's pixels 64
+    // at a time; the image base and channel test are hoisted.
+    const int g = tid & (G - 1);
     const int c = ch0 + g * 4;
-    float4 v = f4_zero();
-    if (c < p.C && gy >= 0 && gy < p.H && gx >= 0 && gx < p.W)
-      v = ld4<T>(in + ((size_t)(n * p.H + gy) * p.W + gx) * p.in_ps + c);
-    tile[(g * IH + iy) * IWP + ix] = v;
+    const bool cok = c < p.C;
+    const T* base = in + (size_t)n * p.H * p.W * p.in_ps + c;
+    for (int px = tid / G; px < IH * IW; px += 256 / G) {
+      const int iy = px / IW, ix = px - iy * IW;
+      const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
+      float4 v = f4_zero();
+      if (cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W)
+        v = ld4<T>(base + ((size_t)gy * p.W + gx) * p.in_ps);
+      tile[(g * IH + iy) * IWP + ix] = v;
+    }
   }
   __syncthreads();
 
