@@ -93,10 +93,18 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
   __shared__ float4 taps[KH * KW * C4B];
   const T* in = static_cast<const T*>(p.in);
 
+  // Tiles numbered channel block fastest, then x, y, image; XCD-contiguous
+  // ranges as in depthwise_wave_kernel.
   const int cblocks = (p.C + 4 * C4B - 1) / (4 * C4B);
-  const int n = blockIdx.z / cblocks;
-  const int ch0 = (blockIdx.z - n * cblocks) * 4 * C4B;
-  const int oy0 = blockIdx.y * TY, ox0 = blockIdx.x * TX;
+  const int tiles_x = (p.Wo + TX - 1) / TX, tiles_y = (p.Ho + TY - 1) / TY;
+  const int total = tiles_x * tiles_y * cblocks * p.N;
+  const int t = (blockIdx.x & 7) * ((total + 7) / 8) + (blockIdx.x >> 3);
+  if (t >= total) return;  // grid padding, before any barrier
+  const int txy = t / cblocks;
+  const int n = txy / (tiles_x * tiles_y);
+  const int blk = txy - n * tiles_x * tiles_y;  // tile within the image
+  const int ch0 = (t - txy * cblocks) * 4 * C4B;
+  const int oy0 = blk / tiles_x * TY, ox0 = blk % tiles_x * TX;
   const int tid = threadIdx.x;
 
   {
@@ -176,10 +184,9 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
     tile[tid] = sum;
     __syncthreads();
     if (tid < C4B && ch0 + tid * 4 < p.C) {
-      float4 t = tile[tid];
-      for (int k = 1; k < 256 / C4B; ++k) t = f4_sum(t, tile[k * C4B + tid]);
-      const int blk = blockIdx.y * gridDim.x + blockIdx.x;
-      *reinterpret_cast<float4*>(p.se_part + ((size_t)n * gridDim.x * gridDim.y + blk) * p.C + ch0 + tid * 4) = t;
+      float4 sums = tile[tid];
+      for (int k = 1; k < 256 / C4B; ++k) sums = f4_sum(sums, tile[k * C4B + tid]);
+      *reinterpret_cast<float4*>(p.se_part + ((size_t)n * tiles_x * tiles_y + blk) * p.C + ch0 + tid * 4) = sums;
     }
   }
 }
@@ -380,8 +387,9 @@ static void launch_dw_strip(const DwParams& p, hipStream_t s) {
 template <typename T, int KH, int KW, int TY, int XR = 4, int C4B = 8>
 static void launch_dw_tiled(const DwParams& p, hipStream_t s) {
   constexpr int TX = 256 / (C4B * TY) * XR;
-  dim3 grid((p.Wo + TX - 1) / TX, (p.Ho + TY - 1) / TY, p.N * ((p.C + 4 * C4B - 1) / (4 * C4B)));
-  hipLaunchKernelGGL((depthwise_tiled_kernel<T, KH, KW, TY, XR, C4B>), grid, dim3(256), 0, s, p);
+  const long tiles = (long)((p.Wo + TX - 1) / TX) * ((p.Ho + TY - 1) / TY) * p.N * ((p.C + 4 * C4B - 1) / (4 * C4B));
+  hipLaunchKernelGGL((depthwise_tiled_kernel<T, KH, KW, TY, XR, C4B>), dim3((unsigned)((tiles + 7) / 8 * 8)), dim3(256),
+                     0, s, p);
 }
 
 template <typename T, int KH, int KW>
