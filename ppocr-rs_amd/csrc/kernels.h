@@ -92,6 +92,9 @@ struct DwParams {
   // Per-block channel sums of the stored output for a squeeze-excitation
   // ([N][P][C] fp32, P = depthwise_se_blocks()), or null.
   float* se_part;
+  // bf16 matrix-core operand fragments of the taps (depthwise_mfma_table),
+  // or null; used when depthwise_uses_mfma() holds for the layer.
+  const void* wtab;
 };
 
 // Squeeze-excitation gate: g[n, c] = gate_act(W2 relu(W1 mean(x) + b1) + b2).
@@ -130,7 +133,18 @@ void launch_depthwise(const DwParams& p, hipStream_t s);
 // sums of its output for a squeeze-excitation (p.se_part), else 0.
 int depthwise_se_blocks(const DwParams& p);
 // Name of the kernel instance launch_depthwise picks.
-const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho);
+const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho, int dt = DT_F32, bool table = false);
+// bf16 layers with square stride-1 5x5, 7x7 or 9x9 kernels and at least 16
+// output rows run on the matrix cores when their taps come packed by
+// depthwise_mfma_table (pack for Ho = 16: the rows are known at launch).
+bool depthwise_uses_mfma(int kh, int kw, int sh, int sw, int dt, int Ho);
+// Elements (bf16) of the packed taps of a c-channel k x k layer.
+size_t depthwise_mfma_table_size(int c, int k);
+// Packs taps w [c][k * k] (fp32) as [c][ky][lane 0..63][8] bf16: lane l holds
+// w[ky][8 * (l / 16) + i - l % 16] for i = 0..7 (zero outside 0..k-1), the B
+// fragment of a 16x16x32 product whose A rows are input rows and whose K
+// runs over 32 input columns.
+void depthwise_mfma_table(const float* w, int c, int k, uint16_t* out);
 void launch_se(const SeParams& p, hipStream_t s);
 // Stages 2 and 3 of launch_se from partial sums already in p.partial
 // ([N][P][C], e.g. from the producing depthwise).

@@ -37,7 +37,7 @@ struct ConvW {
 };
 
 struct DwW {
-  size_t w = NOW, b = NOW;
+  size_t w = NOW, b = NOW, tab = NOW;  // tab: matrix-core tap fragments (bf16 plans)
   int c = 0, kh = 1, kw = 1, sh = 1, sw = 1, pt = 0, pl = 0, pb = 0, pr = 0;
 };
 
@@ -152,6 +152,14 @@ class Builder {
       for (int t = 0; t < kh * kw; ++t) packed[(size_t)t * c + ch] = W[(size_t)ch * kh * kw + t];
     d.w = put(packed);
     if (!b.empty()) d.b = put(b);
+    if (depthwise_uses_mfma(kh, kw, sh, sw, dt_, 16)) {
+      std::vector<uint16_t> tab(depthwise_mfma_table_size(c, kh));
+      depthwise_mfma_table(W.data(), c, kh, tab.data());
+      size_t off = round_up(plan_.weights.size(), 256);
+      plan_.weights.resize(off + tab.size() * 2, 0);
+      memcpy(plan_.weights.data() + off, tab.data(), tab.size() * 2);
+      d.tab = off;
+    }
     return d;
   }
 
@@ -376,10 +384,10 @@ class Builder {
     View r = res ? *res : View();
     bool has_res = res;
     base.res_ps = has_res ? r.ps : 0;
-    size_t wo = w.w, bo = w.b;
+    size_t wo = w.w, bo = w.b, to = w.tab;
     Op op;
     op.name = name;
-    op.kernel = depthwise_kernel_name(w.kh, w.kw, w.sh, w.sw, Ho);
+    op.kernel = depthwise_kernel_name(w.kh, w.kw, w.sh, w.sw, Ho, x.dt, w.tab != NOW);
     op.flops = 2.0 * out.pixels() * w.c * w.kh * w.kw;
     op.bytes = (double)dtype_size(x.dt) * ((double)x.pixels() * w.c + (double)out.pixels() * w.c * (has_res ? 2 : 1)) +
                4.0 * w.kh * w.kw * w.c;
@@ -395,6 +403,7 @@ class Builder {
       p.bias = ex.w(bo);
       p.res = has_res ? ex.ptr(r) : nullptr;
       p.se_part = has_part ? ex.fptr(part) : nullptr;
+      p.wtab = ex.w(to);
       launch_depthwise(p, s);
     };
     add_op(std::move(op));

@@ -125,4 +125,67 @@ const char* ppocr_probe_conv_kernel(int n, int h, int w, int c, int co, int kh, 
   return name.c_str();
 }
 
+// Depthwise: x [n][h][w][c] (c % 4 == 0), weight [c][k][k], bias [c] (or
+// null), residual [n][ho][wo][c] (or null): out = res + act(dw(x) + bias)
+// with stride 1 and pads (k / 2 each side), in storage type dt; table != 0
+// also packs the matrix-core tap fragments, as a bf16 plan does.  Returns 0,
+// or 1 on a HIP error.
+int ppocr_probe_depthwise(const float* x, int n, int h, int w, int c, const float* weight, const float* bias, int k,
+                          int act, const float* res, int dt, int table, float* out) {
+  const size_t px = (size_t)n * h * w;
+  std::vector<float> packed((size_t)k * k * c);
+  for (int ch = 0; ch < c; ++ch)
+    for (int t = 0; t < k * k; ++t) packed[(size_t)t * c + ch] = weight[(size_t)ch * k * k + t];
+  void* d_in = upload(x, px * c, dt);
+  void* d_wt = upload(packed.data(), packed.size(), ppocr::DT_F32);
+  void* d_bias = bias ? upload(bias, c, ppocr::DT_F32) : nullptr;
+  void* d_res = res ? upload(res, px * c, dt) : nullptr;
+  void *d_out = nullptr, *d_tab = nullptr;
+  int rc = 0;
+  const size_t es = dt == ppocr::DT_BF16 ? 2 : 4;
+  if (table) {
+    std::vector<uint16_t> tab(ppocr::depthwise_mfma_table_size(c, k));
+    ppocr::depthwise_mfma_table(weight, c, k, tab.data());
+    if (hipMalloc(&d_tab, tab.size() * 2) != hipSuccess ||
+        hipMemcpy(d_tab, tab.data(), tab.size() * 2, hipMemcpyHostToDevice) != hipSuccess)
+      rc = 1;
+  }
+  if (rc || !d_in || !d_wt || (bias && !d_bias) || (res && !d_res) || hipMalloc(&d_out, px * c * es) != hipSuccess) {
+    rc = 1;
+  } else {
+    ppocr::DwParams p{};
+    p.in = d_in;
+    p.N = n, p.H = h, p.W = w, p.C = c, p.in_ps = c;
+    p.out = d_out;
+    p.Ho = h, p.Wo = w, p.out_ps = c;
+    p.wt = static_cast<const float*>(d_wt);
+    p.bias = static_cast<const float*>(d_bias);
+    p.kh = p.kw = k, p.sh = p.sw = 1, p.pt = p.pl = k / 2;
+    p.act = act;
+    p.res = d_res;
+    p.res_ps = c;
+    p.dt = dt;
+    p.wtab = d_tab;
+    ppocr::launch_depthwise(p, nullptr);
+    if (hipDeviceSynchronize() != hipSuccess) rc = 1;
+    if (rc == 0) {
+      if (dt == ppocr::DT_BF16) {
+        std::vector<uint16_t> hb(px * c);
+        if (hipMemcpy(hb.data(), d_out, hb.size() * 2, hipMemcpyDeviceToHost) != hipSuccess) rc = 1;
+        for (size_t i = 0; i < hb.size(); ++i) out[i] = from_bf16(hb[i]);
+      } else if (hipMemcpy(out, d_out, px * c * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+        rc = 1;
+      }
+    }
+  }
+  for (void* ptr : {d_in, d_wt, d_bias, d_res, d_out, d_tab})
+    if (ptr) (void)hipFree(ptr);
+  return rc;
+}
+
+// The kernel instance ppocr_probe_depthwise runs.
+const char* ppocr_probe_depthwise_kernel(int h, int k, int dt, int table) {
+  return ppocr::depthwise_kernel_name(k, k, 1, 1, h, dt, table != 0);
+}
+
 }  // extern "C"

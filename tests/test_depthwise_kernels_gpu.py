@@ -1,0 +1,125 @@
+"""Kernel-level checks of the depthwise convolutions on the GPU.
+
+The bf16 matrix-core depthwise (5x5, 7x7, 9x9 as Toeplitz products of tap
+rows) and the VALU kernels run through the test harness
+libppocr_hip_probe.so on maps whose sides are not multiples of the tiles,
+and are compared with a float64 depthwise of the same operands (zero
+padding k / 2, bias, activation, then the residual: the reference depthwise
+semantics, src/cpu/ops.rs and the scalar references of
+src/cpu/kernels/mod.rs:2880-2997).  Each case first asserts which kernel
+instance it runs.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from test_conv_kernels_gpu import ACT_HSWISH, ACT_NONE, ACT_RELU, PROBE, _ptr, act, bf16_round
+
+
+def _lib():
+    if not PROBE.exists():
+        raise RuntimeError(f"{PROBE} is not built (make -C ppocr-rs_amd)")
+    lib = ctypes.CDLL(str(PROBE))
+    f = ctypes.POINTER(ctypes.c_float)
+    i = ctypes.c_int
+    lib.ppocr_probe_depthwise.argtypes = [f, i, i, i, i, f, f, i, i, f, i, i, f]
+    lib.ppocr_probe_depthwise.restype = i
+    lib.ppocr_probe_depthwise_kernel.argtypes = [i, i, i, i]
+    lib.ppocr_probe_depthwise_kernel.restype = ctypes.c_char_p
+    return lib
+
+
+def depthwise_ref(x, w, b, kind, res):
+    """float64 NHWC depthwise, stride 1, pads k // 2: x [n][h][w][c], w [c][k][k]."""
+    n, h, wd, c = x.shape
+    k = w.shape[-1]
+    p = k // 2
+    xp = np.zeros((n, h + 2 * p, wd + 2 * p, c))
+    xp[:, p:p + h, p:p + wd] = x
+    y = np.zeros((n, h, wd, c))
+    for ky in range(k):
+        for kx in range(k):
+            y += xp[:, ky:ky + h, kx:kx + wd, :] * w[:, ky, kx].astype(np.float64)
+    if b is not None:
+        y += b
+    y = act(y, kind)
+    if res is not None:
+        y += res
+    return y
+
+
+# (n, h, w, c, k, act, bias, residual): tails in both directions, one and
+# several channel groups, maps taller than one 32-row tile.
+MFMA_CASES = [
+    (1, 16, 16, 4, 9, ACT_NONE, False, False),
+    (2, 37, 45, 12, 9, ACT_NONE, False, False),
+    (1, 70, 33, 68, 9, ACT_RELU, True, False),
+    (1, 29, 71, 8, 7, ACT_HSWISH, True, True),
+    (2, 18, 40, 20, 5, ACT_NONE, True, True),
+    (1, 52, 92, 16, 5, ACT_RELU, False, False),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", MFMA_CASES, ids=lambda c: "x".join(map(str, c[:5])))
+def test_bf16_matrix_core_depthwise_matches_float64(case):
+    n, h, wd, c, k, kind, has_bias, has_res = case
+    lib = _lib()
+    kernel = lib.ppocr_probe_depthwise_kernel(h, k, 1, 1).decode()
+    assert kernel == f"depthwise_mfma<{k}x{k}>", kernel
+    rng = np.random.default_rng(1000 + 7 * h + wd + k)
+    x = rng.uniform(-1, 1, (n, h, wd, c)).astype(np.float32)
+    w = rng.uniform(-0.5, 0.5, (c, k, k)).astype(np.float32)
+    b = rng.uniform(-0.5, 0.5, c).astype(np.float32) if has_bias else None
+    res = rng.uniform(-1, 1, (n, h, wd, c)).astype(np.float32) if has_res else None
+    out = np.zeros((n, h, wd, c), np.float32)
+    assert lib.ppocr_probe_depthwise(_ptr(x), n, h, wd, c, _ptr(w), _ptr(b), k, kind, _ptr(res), 1, 1, _ptr(out)) == 0
+    # The kernel multiplies bf16 activations by bf16 taps exactly and sums in
+    # fp32, then stores bf16: against the float64 result of the same rounded
+    # operands the error is the output rounding (2^-9 relative) plus the fp32
+    # sum of k * k terms.
+    ref = depthwise_ref(bf16_round(x), bf16_round(w), b, kind, None if res is None else bf16_round(res))
+    err = np.abs(out - ref)
+    tol = 2.0 ** -8 * np.abs(ref) + 1e-4
+    assert np.all(err <= tol), (float(err.max()), np.unravel_index(np.argmax(err - tol), err.shape))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("k", [5, 7, 9])
+def test_matrix_core_and_valu_depthwise_agree(k):
+    """The same bf16 layer without the packed taps runs the VALU kernel (fp32
+    taps); the two differ only by the taps' bf16 rounding and summation order."""
+    lib = _lib()
+    n, h, wd, c = 2, 41, 57, 24
+    assert lib.ppocr_probe_depthwise_kernel(h, k, 1, 0).decode() != f"depthwise_mfma<{k}x{k}>"
+    rng = np.random.default_rng(k)
+    x = rng.uniform(-1, 1, (n, h, wd, c)).astype(np.float32)
+    w = rng.uniform(-0.5, 0.5, (c, k, k)).astype(np.float32)
+    outs = []
+    for table in (1, 0):
+        out = np.zeros((n, h, wd, c), np.float32)
+        assert lib.ppocr_probe_depthwise(_ptr(x), n, h, wd, c, _ptr(w), None, k, ACT_NONE, None, 1, table,
+                                         _ptr(out)) == 0
+        outs.append(out)
+    ref = depthwise_ref(bf16_round(x), w, None, ACT_NONE, None)
+    scale = np.sqrt(k * k) * 0.5 * 2.0 ** -8  # bf16 tap rounding, summed over k * k random-sign terms
+    for out in outs:
+        assert np.abs(out - ref).max() <= 2.0 ** -8 * np.abs(ref).max() + 4 * scale
+
+
+@pytest.mark.gpu
+def test_fp32_depthwise_probe_matches_float64():
+    """The probe's fp32 path (VALU kernels) against float64: pins the probe."""
+    lib = _lib()
+    for k in (5, 7, 9):
+        n, h, wd, c = 1, 23, 35, 8
+        rng = np.random.default_rng(50 + k)
+        x = rng.uniform(-1, 1, (n, h, wd, c)).astype(np.float32)
+        w = rng.uniform(-0.5, 0.5, (c, k, k)).astype(np.float32)
+        b = rng.uniform(-0.5, 0.5, c).astype(np.float32)
+        out = np.zeros((n, h, wd, c), np.float32)
+        assert lib.ppocr_probe_depthwise(_ptr(x), n, h, wd, c, _ptr(w), _ptr(b), k, ACT_RELU, None, 0, 0,
+                                         _ptr(out)) == 0
+        ref = depthwise_ref(x, w, b, ACT_RELU, None)
+        assert np.abs(out - ref).max() <= 1e-5
