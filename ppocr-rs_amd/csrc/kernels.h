@@ -133,11 +133,14 @@ void launch_depthwise(const DwParams& p, hipStream_t s);
 // sums of its output for a squeeze-excitation (p.se_part), else 0.
 int depthwise_se_blocks(const DwParams& p);
 // Name of the kernel instance launch_depthwise picks.
-const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho, int dt = DT_F32, bool table = false);
-// bf16 layers with square stride-1 5x5, 7x7 or 9x9 kernels and at least 16
-// output rows run on the matrix cores when their taps come packed by
-// depthwise_mfma_table (pack for Ho = 16: the rows are known at launch).
-bool depthwise_uses_mfma(int kh, int kw, int sh, int sw, int dt, int Ho);
+const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho, int dt = DT_F32, bool table = false,
+                                  int C = 0);
+// bf16 layers with square stride-1 5x5, 7x7 or 9x9 kernels, at least 16
+// output rows and a multiple of 8 channels run on the matrix cores when their
+// taps come packed by depthwise_mfma_table (pack for Ho = 16: the rows are
+// known at launch) and their pixel strides and addresses are in whole
+// 8-channel (16-byte) groups.
+bool depthwise_uses_mfma(int kh, int kw, int sh, int sw, int dt, int Ho, int C);
 // Elements (bf16) of the packed taps of a c-channel k x k layer.
 size_t depthwise_mfma_table_size(int c, int k);
 // Packs taps w [c][k * k] (fp32) as [c][ky][lane 0..63][8] bf16: lane l holds

@@ -312,88 +312,100 @@ __global__ __launch_bounds__(256) void depthwise_wave_kernel(DwParams p) {
 // (depthwise_mfma_table), and 16 + kw - 1 <= 32 input columns cover the tile.
 // Products of bf16 values are exact and accumulate in fp32, in K order per
 // tap row instead of the VALU kernels' (ky, kx) order.
-// A workgroup takes a 32 x 32 output tile of 4 channels (8 bytes a pixel):
-// wave w owns channel w as four 16 x 16 MFMA tiles.  The input tile sits in
-// LDS channel-major, [4][rows][28 dwords]: a 112-byte row pitch puts the 16
-// rows an A-fragment read touches on distinct banks, and the columns past
-// the tile's input (read as the zero-weight tail of the last K group) are
-// written as zeros.  Outputs are staged [row][col][4 channels] in the same
-// LDS so that each lane stores a pixel's 8 bytes.
-constexpr int kDwMfmaT = 32, kDwMfmaP = 28;  // output tile side, LDS row pitch (dwords)
+// A workgroup takes a 32 x 32 output tile of 8 channels (16 bytes a pixel,
+// one load or store per lane; 8-byte accesses measured 1.4 TB/s on the
+// neck's largest map): wave w owns channels 2w and 2w + 1, each as four
+// 16 x 16 MFMA tiles.  The input tile sits in LDS channel-major,
+// [8][rows][28 dwords]: a 112-byte row pitch puts the 16 rows an A-fragment
+// read touches on distinct banks, and the columns past the tile's input
+// (read as the zero-weight tail of the last K group) are written as zeros.
+// Outputs are staged [row][col][8 channels] in the same LDS.
+constexpr int kDwMfmaT = 32, kDwMfmaP = 28, kDwMfmaC = 8;  // tile side, LDS row pitch (dwords), channels
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 template <int K>
 __global__ __launch_bounds__(256) void depthwise_mfma_kernel(DwParams p) {
-  constexpr int T = kDwMfmaT, P = kDwMfmaP;
+  constexpr int T = kDwMfmaT, P = kDwMfmaP, CB = kDwMfmaC;
   constexpr int IH = T + K - 1, IW = T + K - 1;
   static_assert(16 + K - 1 <= 32 && IW <= 2 * (P - 4), "a tile's K window fits the padded row");
-  constexpr int SP = T * 4 + 4;  // staged output row pitch (floats)
-  constexpr int TILE = 4 * IH * P, STAGE = T * SP;
+  constexpr int SP = T * CB + 4;  // staged output row pitch (floats)
+  constexpr int TILE = CB * IH * P, STAGE = T * SP;
   __shared__ __align__(16) uint32_t lds[TILE > STAGE ? TILE : STAGE];
 
-  const int cgroups = p.C / 4;
+  const int cgroups = p.C / CB;
   const int tiles_x = (p.Wo + T - 1) / T, tiles_y = (p.Ho + T - 1) / T;
   const int total = tiles_x * tiles_y * cgroups * p.N;
   const int t = (blockIdx.x & 7) * ((total + 7) / 8) + (blockIdx.x >> 3);
   if (t >= total) return;  // grid padding, before any barrier
   const int txy = t / cgroups;
-  const int ch0 = (t - txy * cgroups) * 4;
+  const int ch0 = (t - txy * cgroups) * CB;
   const int n = txy / (tiles_x * tiles_y);
   const int oy0 = (txy / tiles_x) % tiles_y * T, ox0 = txy % tiles_x * T;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
 
-  // This wave's B fragments (one per tap row), issued before the tile loads.
-  bf16x8_t bw[K];
+  // This wave's B fragments (per channel, one per tap row), issued before
+  // the tile loads.
+  bf16x8_t bw[2][K];
   {
-    const uint4* tab = static_cast<const uint4*>(p.wtab) + (size_t)(ch0 + wave) * K * 64 + lane;
+    const uint4* tab = static_cast<const uint4*>(p.wtab) + (size_t)(ch0 + 2 * wave) * K * 64 + lane;
 #pragma unroll
-    for (int ky = 0; ky < K; ++ky) bw[ky] = __builtin_bit_cast(bf16x8_t, tab[ky * 64]);
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int ky = 0; ky < K; ++ky) bw[c][ky] = __builtin_bit_cast(bf16x8_t, tab[(c * K + ky) * 64]);
   }
 
-  // Input tile: pixel pairs along x, transposed to 4 channel planes.
+  // Input tile: pixel pairs along x, transposed to 8 channel planes.
   {
-    const uint2* in = static_cast<const uint2*>(p.in);  // 4 bf16 channels per pixel
+    const uint4* in = static_cast<const uint4*>(p.in);  // 8 bf16 channels per pixel
     for (int q = tid; q < IH * (P - 4); q += 256) {
       const int row = q / (P - 4), xp = q - row * (P - 4);
       const int gy = oy0 - p.pt + row, gx = ox0 - p.pl + 2 * xp;
-      uint2 u0 = make_uint2(0, 0), u1 = make_uint2(0, 0);
+      uint4 u0 = make_uint4(0, 0, 0, 0), u1 = make_uint4(0, 0, 0, 0);
       if ((unsigned)gy < (unsigned)p.H) {
         const size_t rowpix = (size_t)(n * p.H + gy) * p.W;
-        if (2 * xp < IW && (unsigned)gx < (unsigned)p.W) u0 = in[((rowpix + gx) * p.in_ps + ch0) / 4];
-        if (2 * xp + 1 < IW && (unsigned)(gx + 1) < (unsigned)p.W) u1 = in[((rowpix + gx + 1) * p.in_ps + ch0) / 4];
+        if (2 * xp < IW && (unsigned)gx < (unsigned)p.W) u0 = in[((rowpix + gx) * p.in_ps + ch0) / CB];
+        if (2 * xp + 1 < IW && (unsigned)(gx + 1) < (unsigned)p.W) u1 = in[((rowpix + gx + 1) * p.in_ps + ch0) / CB];
       }
       uint32_t* dst = lds + row * P + xp;
-      dst[0] = (u0.x & 0xFFFFu) | (u1.x << 16);
-      dst[IH * P] = (u0.x >> 16) | (u1.x & 0xFFFF0000u);
-      dst[2 * IH * P] = (u0.y & 0xFFFFu) | (u1.y << 16);
-      dst[3 * IH * P] = (u0.y >> 16) | (u1.y & 0xFFFF0000u);
+      const uint32_t a[4] = {u0.x, u0.y, u0.z, u0.w}, b[4] = {u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        dst[(2 * j) * IH * P] = (a[j] & 0xFFFFu) | (b[j] << 16);
+        dst[(2 * j + 1) * IH * P] = (a[j] >> 16) | (b[j] & 0xFFFF0000u);
+      }
     }
   }
   __syncthreads();
 
-  floatx4_t acc[2][2];
+  floatx4_t acc[2][2][2];  // [channel][ty][tx]
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int c = 0; c < 2; ++c)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-  // Lane (row lane % 16, K group lane / 16) reads 8 columns of an input row.
-  const uint32_t* base = lds + (wave * IH + (lane & 15)) * P + (lane >> 4) * 4;
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-  for (int ky = 0; ky < K; ++ky)
+      for (int j = 0; j < 2; ++j) acc[c][i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ty = 0; ty < 2; ++ty)
+  for (int c = 0; c < 2; ++c) {
+    // Lane (row lane % 16, K group lane / 16) reads 8 columns of an input row.
+    const uint32_t* base = lds + ((2 * wave + c) * IH + (lane & 15)) * P + (lane >> 4) * 4;
 #pragma unroll
-      for (int tx = 0; tx < 2; ++tx) {
-        const uint4 a = *reinterpret_cast<const uint4*>(base + (16 * ty + ky) * P + 8 * tx);
-        acc[ty][tx] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), bw[ky], acc[ty][tx],
-                                                               0, 0, 0);
-      }
+    for (int ky = 0; ky < K; ++ky)
+#pragma unroll
+      for (int ty = 0; ty < 2; ++ty)
+#pragma unroll
+        for (int tx = 0; tx < 2; ++tx) {
+          const uint4 a = *reinterpret_cast<const uint4*>(base + (16 * ty + ky) * P + 8 * tx);
+          acc[c][ty][tx] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), bw[c][ky],
+                                                                    acc[c][ty][tx], 0, 0, 0);
+        }
+  }
   __syncthreads();  // every wave is done with the input tile
 
-  // acc[ty][tx][r] is output (16 ty + 4 (lane / 16) + r, 16 tx + lane % 16).
+  // acc[c][ty][tx][r] is output (16 ty + 4 (lane / 16) + r, 16 tx + lane % 16)
+  // of channel 2 wave + c; the wave's two channels go out as one float2.
   float* stage = reinterpret_cast<float*>(lds);
 #pragma unroll
   for (int ty = 0; ty < 2; ++ty)
@@ -401,32 +413,50 @@ __global__ __launch_bounds__(256) void depthwise_mfma_kernel(DwParams p) {
     for (int tx = 0; tx < 2; ++tx)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        stage[(16 * ty + 4 * (lane >> 4) + r) * SP + (16 * tx + (lane & 15)) * 4 + wave] = acc[ty][tx][r];
+        *reinterpret_cast<float2*>(stage + (16 * ty + 4 * (lane >> 4) + r) * SP + (16 * tx + (lane & 15)) * CB +
+                                   2 * wave) = make_float2(acc[0][ty][tx][r], acc[1][ty][tx][r]);
   __syncthreads();
-  const float4 b = p.bias ? *reinterpret_cast<const float4*>(p.bias + ch0) : f4_zero();
+  float4 b0 = f4_zero(), b1 = f4_zero();
+  if (p.bias) {
+    b0 = *reinterpret_cast<const float4*>(p.bias + ch0);
+    b1 = *reinterpret_cast<const float4*>(p.bias + ch0 + 4);
+  }
 #pragma unroll
   for (int k = 0; k < T * T / 256; ++k) {
     const int px = tid + 256 * k;
     const int row = px / T, col = px % T;
     const int oy = oy0 + row, ox = ox0 + col;
     if (oy >= p.Ho || ox >= p.Wo) continue;
-    float4 v = *reinterpret_cast<const float4*>(stage + row * SP + col * 4);
-    if (p.bias) v = f4_sum(v, b);
-    v = f4_act(p.act, v);
+    float4 v0 = *reinterpret_cast<const float4*>(stage + row * SP + col * CB);
+    float4 v1 = *reinterpret_cast<const float4*>(stage + row * SP + col * CB + 4);
+    if (p.bias) v0 = f4_sum(v0, b0), v1 = f4_sum(v1, b1);
+    v0 = f4_act(p.act, v0);
+    v1 = f4_act(p.act, v1);
     const size_t pix = (size_t)(n * p.Ho + oy) * p.Wo + ox;
-    if (p.res) v = f4_sum(ld4<bf16>(static_cast<const bf16*>(p.res) + pix * p.res_ps + ch0), v);
-    st4<bf16>(static_cast<bf16*>(p.out) + pix * p.out_ps + ch0, v);
+    if (p.res) {
+      const bf16* rp = static_cast<const bf16*>(p.res) + pix * p.res_ps + ch0;
+      v0 = f4_sum(ld4<bf16>(rp), v0);
+      v1 = f4_sum(ld4<bf16>(rp + 4), v1);
+    }
+    uint4 o;
+    o.x = f32_to_bf16_bits(v0.x) | (f32_to_bf16_bits(v0.y) << 16);
+    o.y = f32_to_bf16_bits(v0.z) | (f32_to_bf16_bits(v0.w) << 16);
+    o.z = f32_to_bf16_bits(v1.x) | (f32_to_bf16_bits(v1.y) << 16);
+    o.w = f32_to_bf16_bits(v1.z) | (f32_to_bf16_bits(v1.w) << 16);
+    *reinterpret_cast<uint4*>(static_cast<bf16*>(p.out) + pix * p.out_ps + ch0) = o;
   }
 }
 
 template <int K>
 static void launch_dw_mfma(const DwParams& p, hipStream_t s) {
-  const long tiles = (long)((p.Wo + kDwMfmaT - 1) / kDwMfmaT) * ((p.Ho + kDwMfmaT - 1) / kDwMfmaT) * p.N * (p.C / 4);
+  const long tiles =
+      (long)((p.Wo + kDwMfmaT - 1) / kDwMfmaT) * ((p.Ho + kDwMfmaT - 1) / kDwMfmaT) * p.N * (p.C / kDwMfmaC);
   hipLaunchKernelGGL((depthwise_mfma_kernel<K>), dim3((unsigned)((tiles + 7) / 8 * 8)), dim3(256), 0, s, p);
 }
 
-bool depthwise_uses_mfma(int kh, int kw, int sh, int sw, int dt, int Ho) {
-  return dt == DT_BF16 && kh == kw && (kh == 5 || kh == 7 || kh == 9) && sh == 1 && sw == 1 && Ho >= 16;
+bool depthwise_uses_mfma(int kh, int kw, int sh, int sw, int dt, int Ho, int C) {
+  return dt == DT_BF16 && kh == kw && (kh == 5 || kh == 7 || kh == 9) && sh == 1 && sw == 1 && Ho >= 16 &&
+         C % kDwMfmaC == 0;
 }
 
 size_t depthwise_mfma_table_size(int c, int k) { return (size_t)c * k * 64 * 8; }
@@ -554,7 +584,11 @@ int depthwise_se_blocks(const DwParams& p) {
 template <typename T>
 static void launch_dw_typed(const DwParams& p, hipStream_t s) {
   if constexpr (sizeof(T) == 2) {
-    if (p.wtab && !p.se_part && p.C % 4 == 0 && depthwise_uses_mfma(p.kh, p.kw, p.sh, p.sw, DT_BF16, p.Ho)) {
+    // 16-byte pixel accesses: strides and base addresses in whole 8-channel groups.
+    const bool aligned = p.in_ps % kDwMfmaC == 0 && p.out_ps % kDwMfmaC == 0 &&
+                         (!p.res || p.res_ps % kDwMfmaC == 0) &&
+                         (((uintptr_t)p.in | (uintptr_t)p.out | (uintptr_t)p.res) & 15) == 0;
+    if (p.wtab && !p.se_part && aligned && depthwise_uses_mfma(p.kh, p.kw, p.sh, p.sw, DT_BF16, p.Ho, p.C)) {
       if (p.kh == 5) return launch_dw_mfma<5>(p, s);
       if (p.kh == 7) return launch_dw_mfma<7>(p, s);
       return launch_dw_mfma<9>(p, s);
@@ -582,8 +616,8 @@ static void launch_dw_typed(const DwParams& p, hipStream_t s) {
 
 void launch_depthwise(const DwParams& p, hipStream_t s) { DISPATCH_DT(p.dt, launch_dw_typed<T>(p, s)); }
 
-const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho, int dt, bool table) {
-  if (table && depthwise_uses_mfma(kh, kw, sh, sw, dt, Ho))
+const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho, int dt, bool table, int C) {
+  if (table && depthwise_uses_mfma(kh, kw, sh, sw, dt, Ho, C))
     return kh == 5 ? "depthwise_mfma<5x5>" : kh == 7 ? "depthwise_mfma<7x7>" : "depthwise_mfma<9x9>";
   if (kh == 3 && kw == 3 && sh == 2) return "depthwise_strip<3x3,s2>";
   if (kh == 3 && kw == 3 && sh == 1 && Ho <= 4) return "depthwise_strip<3x3>";

@@ -152,7 +152,7 @@ class Builder {
       for (int t = 0; t < kh * kw; ++t) packed[(size_t)t * c + ch] = W[(size_t)ch * kh * kw + t];
     d.w = put(packed);
     if (!b.empty()) d.b = put(b);
-    if (depthwise_uses_mfma(kh, kw, sh, sw, dt_, 16)) {
+    if (depthwise_uses_mfma(kh, kw, sh, sw, dt_, 16, c)) {
       std::vector<uint16_t> tab(depthwise_mfma_table_size(c, kh));
       depthwise_mfma_table(W.data(), c, kh, tab.data());
       size_t off = round_up(plan_.weights.size(), 256);
@@ -387,7 +387,7 @@ class Builder {
     size_t wo = w.w, bo = w.b, to = w.tab;
     Op op;
     op.name = name;
-    op.kernel = depthwise_kernel_name(w.kh, w.kw, w.sh, w.sw, Ho, x.dt, w.tab != NOW);
+    op.kernel = depthwise_kernel_name(w.kh, w.kw, w.sh, w.sw, Ho, x.dt, w.tab != NOW && x.ps % 8 == 0, w.c);
     op.flops = 2.0 * out.pixels() * w.c * w.kh * w.kw;
     op.bytes = (double)dtype_size(x.dt) * ((double)x.pixels() * w.c + (double)out.pixels() * w.c * (has_res ? 2 : 1)) +
                4.0 * w.kh * w.kw * w.c;

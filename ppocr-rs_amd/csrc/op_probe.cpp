@@ -184,8 +184,8 @@ int ppocr_probe_depthwise(const float* x, int n, int h, int w, int c, const floa
 }
 
 // The kernel instance ppocr_probe_depthwise runs.
-const char* ppocr_probe_depthwise_kernel(int h, int k, int dt, int table) {
-  return ppocr::depthwise_kernel_name(k, k, 1, 1, h, dt, table != 0);
+const char* ppocr_probe_depthwise_kernel(int h, int c, int k, int dt, int table) {
+  return ppocr::depthwise_kernel_name(k, k, 1, 1, h, dt, table != 0, c);
 }
 
 }  // extern "C"

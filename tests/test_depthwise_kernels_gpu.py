@@ -25,7 +25,7 @@ def _lib():
     i = ctypes.c_int
     lib.ppocr_probe_depthwise.argtypes = [f, i, i, i, i, f, f, i, i, f, i, i, f]
     lib.ppocr_probe_depthwise.restype = i
-    lib.ppocr_probe_depthwise_kernel.argtypes = [i, i, i, i]
+    lib.ppocr_probe_depthwise_kernel.argtypes = [i, i, i, i, i]
     lib.ppocr_probe_depthwise_kernel.restype = ctypes.c_char_p
     return lib
 
@@ -50,13 +50,13 @@ def depthwise_ref(x, w, b, kind, res):
 
 
 # (n, h, w, c, k, act, bias, residual): tails in both directions, one and
-# several channel groups, maps taller than one 32-row tile.
+# several 8-channel groups, maps taller than one 32-row tile.
 MFMA_CASES = [
-    (1, 16, 16, 4, 9, ACT_NONE, False, False),
-    (2, 37, 45, 12, 9, ACT_NONE, False, False),
-    (1, 70, 33, 68, 9, ACT_RELU, True, False),
+    (1, 16, 16, 8, 9, ACT_NONE, False, False),
+    (2, 37, 45, 24, 9, ACT_NONE, False, False),
+    (1, 70, 33, 72, 9, ACT_RELU, True, False),
     (1, 29, 71, 8, 7, ACT_HSWISH, True, True),
-    (2, 18, 40, 20, 5, ACT_NONE, True, True),
+    (2, 18, 40, 16, 5, ACT_NONE, True, True),
     (1, 52, 92, 16, 5, ACT_RELU, False, False),
 ]
 
@@ -66,7 +66,7 @@ MFMA_CASES = [
 def test_bf16_matrix_core_depthwise_matches_float64(case):
     n, h, wd, c, k, kind, has_bias, has_res = case
     lib = _lib()
-    kernel = lib.ppocr_probe_depthwise_kernel(h, k, 1, 1).decode()
+    kernel = lib.ppocr_probe_depthwise_kernel(h, c, k, 1, 1).decode()
     assert kernel == f"depthwise_mfma<{k}x{k}>", kernel
     rng = np.random.default_rng(1000 + 7 * h + wd + k)
     x = rng.uniform(-1, 1, (n, h, wd, c)).astype(np.float32)
@@ -92,7 +92,7 @@ def test_matrix_core_and_valu_depthwise_agree(k):
     taps); the two differ only by the taps' bf16 rounding and summation order."""
     lib = _lib()
     n, h, wd, c = 2, 41, 57, 24
-    assert lib.ppocr_probe_depthwise_kernel(h, k, 1, 0).decode() != f"depthwise_mfma<{k}x{k}>"
+    assert lib.ppocr_probe_depthwise_kernel(h, c, k, 1, 0).decode() != f"depthwise_mfma<{k}x{k}>"
     rng = np.random.default_rng(k)
     x = rng.uniform(-1, 1, (n, h, wd, c)).astype(np.float32)
     w = rng.uniform(-0.5, 0.5, (c, k, k)).astype(np.float32)
@@ -106,6 +106,23 @@ def test_matrix_core_and_valu_depthwise_agree(k):
     scale = np.sqrt(k * k) * 0.5 * 2.0 ** -8  # bf16 tap rounding, summed over k * k random-sign terms
     for out in outs:
         assert np.abs(out - ref).max() <= 2.0 ** -8 * np.abs(ref).max() + 4 * scale
+
+
+@pytest.mark.gpu
+def test_matrix_core_depthwise_needs_whole_channel_groups():
+    """12 channels (not a multiple of 8) and maps under 16 rows stay on the
+    VALU kernels; their outputs still match float64."""
+    lib = _lib()
+    assert lib.ppocr_probe_depthwise_kernel(30, 12, 9, 1, 1).decode() == "depthwise_wave<9x9>"
+    assert lib.ppocr_probe_depthwise_kernel(12, 16, 5, 1, 1).decode() == "depthwise_wave<5x5>"
+    for n, h, wd, c, k in ((1, 30, 41, 12, 9), (2, 12, 40, 16, 5)):
+        rng = np.random.default_rng(h + c)
+        x = rng.uniform(-1, 1, (n, h, wd, c)).astype(np.float32)
+        w = rng.uniform(-0.5, 0.5, (c, k, k)).astype(np.float32)
+        out = np.zeros((n, h, wd, c), np.float32)
+        assert lib.ppocr_probe_depthwise(_ptr(x), n, h, wd, c, _ptr(w), None, k, ACT_NONE, None, 1, 1, _ptr(out)) == 0
+        ref = depthwise_ref(bf16_round(x), w, None, ACT_NONE, None)
+        assert np.all(np.abs(out - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-4)
 
 
 @pytest.mark.gpu
