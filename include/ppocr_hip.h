@@ -153,7 +153,7 @@ typedef struct ppocr_kernel_stat {
   double avg_ms;
   double flops;
   double bytes;
-  int bound; /* 0: HBM-bound, 1: matrix-core bound */
+  int bound; /* 0: HBM-bound, 1: matrix-core bound, 2: fp32 vector-ALU bound */
 } ppocr_kernel_stat;
 
 /* Runs `runs` passes with a HIP event around every launch (on the stream the

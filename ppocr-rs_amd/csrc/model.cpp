@@ -391,6 +391,10 @@ class Builder {
     op.flops = 2.0 * out.pixels() * w.c * w.kh * w.kw;
     op.bytes = (double)dtype_size(x.dt) * ((double)x.pixels() * w.c + (double)out.pixels() * w.c * (has_res ? 2 : 1)) +
                4.0 * w.kh * w.kw * w.c;
+    // 5x5 and larger taps on the VALU kernels do more fp32 FMAs per byte than
+    // the vector ALU can retire at the HBM rate; the matrix-core form is
+    // HBM-bound again.
+    if (w.kh * w.kw >= 25 && op.kernel.rfind("depthwise_mfma", 0) != 0) op.bound = 2;
     op.reads = {x.buf};
     if (has_res) op.reads.push_back(r.buf);
     op.writes = {out.buf};

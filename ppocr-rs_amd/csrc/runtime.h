@@ -118,7 +118,7 @@ struct Op {
   std::string name;
   std::string kernel;
   double flops = 0.0, bytes = 0.0;
-  int bound = 0;  // 0 HBM, 1 matrix cores
+  int bound = 0;  // 0 HBM, 1 matrix cores, 2 fp32 vector ALU
   std::vector<int> reads, writes;
   std::function<void(const Exec&, hipStream_t)> launch;
 };

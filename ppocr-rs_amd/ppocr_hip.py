@@ -321,7 +321,7 @@ class _Model:
         stats = (KernelStat * count.value)()
         _check(lib().ppocr_hip_profile(self.handle, xp, x.size, runs, stats, count.value, ctypes.byref(count)))
         return [dict(name=s.name.decode(), kernel=s.kernel.decode(), avg_ms=s.avg_ms, flops=s.flops, bytes=s.bytes,
-                     bound=("mfma" if s.bound else "hbm")) for s in stats]
+                     bound={1: "mfma", 2: "valu"}.get(s.bound, "hbm")) for s in stats]
 
     def memory_report(self):
         a, u, w = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
