@@ -127,6 +127,24 @@ def test_engine_default_options_and_image_sizes(gpu):
         engine.close()
 
 
+def test_engine_page_without_detections(gpu):
+    # A minimum component area no component reaches: the detector runs, the
+    # postprocess keeps nothing, the recognizer gets an empty batch; the page
+    # has no lines and still reports its sizes (src/ocr.rs:497-600 with an
+    # empty detection list).  A blank page then runs through the same engine.
+    dictionary = synthetic_dictionary(6906)
+    engine = ppocr_hip.OcrEngine.load(gpu, model_path("det", "tiny"), model_path("rec", "tiny"), dictionary,
+                                      min_area=10 ** 9)
+    try:
+        r = engine.recognize(seeded.seeded_rgb(240, 320, 3, pattern="blocks"))
+        assert r.source_size == (320, 240)
+        assert r.lines == []
+        blank = engine.recognize(np.full((240, 320, 3), 255, np.uint8))
+        assert blank.source_size == (320, 240) and blank.lines == []
+    finally:
+        engine.close()
+
+
 def test_engine_rejects_mismatched_dictionary(gpu):
     with pytest.raises(ppocr_hip.GpuError) as e:
         ppocr_hip.OcrEngine.load(gpu, model_path("det", "tiny"), model_path("rec", "tiny"), ["a", "b"])

@@ -71,6 +71,40 @@ def test_reference_literal(gpu):
     assert abs(dets[0].polygon[0, 0] - 10.0) < 1e-4
 
 
+def test_empty_and_below_threshold_maps(gpu):
+    # No pixel at the binary threshold (0.2): no components, no detections,
+    # in a batch with a map that has one; a component whose mean score is
+    # under the box threshold (0.4) is dropped.
+    h, w = 64, 96
+    zero = np.zeros((h, w), np.float32)
+    under = np.full((h, w), 0.1999, np.float32)
+    one = np.zeros((h, w), np.float32)
+    one[10:20, 10:40] = 0.9
+    weak = np.zeros((h, w), np.float32)
+    weak[10:20, 10:40] = 0.39
+    maps = np.stack([zero, under, one, weak])
+    out = gpu.db_postprocess(maps, [(w, h, w, h)] * 4)
+    assert [len(d) for d in out] == [0, 0, 1, 0]
+    for i in range(4):
+        check(out[i], maps[i], (w, h, w, h))
+
+
+def test_component_touching_every_border(gpu):
+    # A frame one pixel inside the map edge and a block in a corner: contours
+    # and boxes at the map boundary, then clipped to the source size.
+    h, w = 80, 120
+    values = np.zeros((h, w), np.float32)
+    values[0:4, :] = 0.9
+    values[:, 0:4] = 0.9
+    values[h - 4:, w - 30:] = 0.8
+    transform = (2 * w, 2 * h, w, h)
+    (dets,) = gpu.db_postprocess(values, [transform], unclip_ratio=1.5)
+    assert len(dets) >= 1
+    for d in dets:
+        assert np.all(d.polygon >= 0) and np.all(d.polygon[:, 0] <= 2 * w) and np.all(d.polygon[:, 1] <= 2 * h)
+    check(dets, values, transform, 2.0, unclip_ratio=1.5)
+
+
 def test_random_blob_maps_batched(gpu):
     rng = np.random.default_rng(5)
     h, w = 96, 160
