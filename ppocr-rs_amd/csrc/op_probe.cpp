@@ -183,6 +183,12 @@ int ppocr_probe_depthwise(const float* x, int n, int h, int w, int c, const floa
   return rc;
 }
 
+// The matrix-core tap fragments a bf16 plan packs for a c-channel k x k
+// depthwise layer (host only): taps [c][k][k] -> out [c][k][64][8] bf16 bits.
+void ppocr_probe_depthwise_table(const float* weight, int c, int k, uint16_t* out) {
+  ppocr::depthwise_mfma_table(weight, c, k, out);
+}
+
 // The kernel instance ppocr_probe_depthwise runs.
 const char* ppocr_probe_depthwise_kernel(int h, int c, int k, int dt, int table) {
   return ppocr::depthwise_kernel_name(k, k, 1, 1, h, dt, table != 0, c);
