@@ -108,7 +108,7 @@ __device__ __forceinline__ PixelPos locate(const DbParams& p, long i) {
 }  // namespace
 
 __global__ void db_reset_kernel(int* counters) {
-  if (threadIdx.x < 2) counters[threadIdx.x] = 0;
+  if (threadIdx.x < 3) counters[threadIdx.x] = 0;
 }
 
 // One block per image row: label = index of the first pixel of the pixel's
@@ -125,8 +125,14 @@ __global__ __launch_bounds__(256) void db_runs_kernel(DbParams p) {
   const int x0 = min(p.W, (int)threadIdx.x * per), x1 = min(p.W, x0 + per);
   auto fg = [&](int x) { return x < cw && p.prob[base + x] >= p.threshold; };
   int last = -1;
-  for (int x = x0; x < x1; ++x)
+  bool finite = true;
+  for (int x = x0; x < x1; ++x) {
+    finite = finite && isfinite(p.prob[base + x]);
     if (fg(x) && (x == 0 || !fg(x - 1))) last = x;
+  }
+  // extract_detections rejects a map holding any non-finite value (also
+  // outside the content area); counters[2] tells the host.
+  if (!finite) atomicOr(&p.counters[2], 1);
   carry[threadIdx.x] = last;
   __syncthreads();
   for (int o = 1; o < 256; o <<= 1) {  // inclusive max-scan of the chunk maxima

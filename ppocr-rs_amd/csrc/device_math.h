@@ -61,9 +61,12 @@ typedef __bf16 bf16;
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
+// Round to nearest even; a NaN stays a (quiet) NaN instead of carrying into
+// the exponent, so non-finite values still reach the output checks.
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);
-  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  return f != f ? ((u >> 16) | 0x40u) : r;
 }
 
 // v rounded to the storage type T (what st4 stores and ld4 reads back).

@@ -470,7 +470,9 @@ void depthwise_mfma_table(const float* w, int c, int k, uint16_t* out) {
           const float v = j >= 0 && j < k ? w[((size_t)ch * k + ky) * k + j] : 0.f;
           uint32_t u;
           memcpy(&u, &v, 4);
-          out[(((size_t)ch * k + ky) * 64 + lane) * 8 + i] = (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+          out[(((size_t)ch * k + ky) * 64 + lane) * 8 + i] =
+              (u & 0x7FFFFFFFu) > 0x7F800000u ? (uint16_t)((u >> 16) | 0x40u)
+                                               : (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
         }
 }
 

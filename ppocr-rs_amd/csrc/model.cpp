@@ -27,6 +27,7 @@ size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 uint16_t to_bf16(float f) {
   uint32_t u;
   memcpy(&u, &f, 4);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);  // NaN stays NaN
   return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 

@@ -650,7 +650,8 @@ bool detection_before(const HostDetection& l, const HostDetection& r) {
 // returns the per-image sorted, truncated detections.  Caller holds ctx->mu.
 std::vector<std::vector<HostDetection>> run_db(ppocr_hip_ctx* ctx, const float* prob, int N, int H, int W,
                                                const ppocr_detector_transform* tr, const ppocr_db_options& o,
-                                               std::shared_ptr<DeviceBuffer>& work) {
+                                               std::shared_ptr<DeviceBuffer>& work,
+                                               ppocr_status non_finite_status) {
   if (!tr) raise(PPOCR_ERR_INVALID_INPUT, "transforms pointer is null");
   const long total = (long)N * H * W;
   if (total >= (long)INT32_MAX) raise(PPOCR_ERR_INVALID_INPUT, "probability maps too large for the postprocess");
@@ -676,7 +677,7 @@ std::vector<std::vector<HostDetection>> run_db(ppocr_hip_ctx* ctx, const float* 
   };
   size_t off = 0;
   const size_t o_label = carve(off, 4 * (size_t)total), o_slot = carve(off, 4 * (size_t)total);
-  const size_t o_counters = carve(off, 8), o_tables = carve(off, 4 * tables.size());
+  const size_t o_counters = carve(off, 12), o_tables = carve(off, 4 * tables.size());
   const size_t o_count = carve(off, 4 * (size_t)max_comp), o_root = carve(off, 4 * (size_t)max_comp);
   const size_t o_keep = carve(off, 4 * (size_t)max_comp), o_mom = carve(off, 48 * (size_t)max_comp);
   const size_t o_geom = carve(off, 32 * (size_t)max_comp), o_ext = carve(off, 16 * (size_t)max_comp);
@@ -708,9 +709,11 @@ std::vector<std::vector<HostDetection>> run_db(ppocr_hip_ctx* ctx, const float* 
   p.out = reinterpret_cast<float*>(base + o_out);
   launch_db_postprocess(p, ctx->stream);
   HIP_OK(hipGetLastError());
-  int counters[2] = {0, 0};
+  int counters[3] = {0, 0, 0};
   HIP_OK(hipMemcpyAsync(counters, p.counters, sizeof counters, hipMemcpyDeviceToHost, ctx->stream));
   HIP_OK(hipStreamSynchronize(ctx->stream));
+  // src/ocr.rs:731-733
+  if (counters[2]) raise(non_finite_status, "detector output contains non-finite values");
   const int n_det = std::max(0, std::min(counters[1], p.max_comp));
   std::vector<float> rec(12 * (size_t)n_det);
   if (n_det) {
@@ -784,14 +787,15 @@ ppocr_status ppocr_hip_db_postprocess(ppocr_hip_ctx* ctx, const float* prob, siz
       raise(PPOCR_ERR_INVALID_INPUT, "probability maps too large for the postprocess");
     const ppocr_db_options o = db_options(options);
     const size_t elems = n * height * width;
-    for (size_t i = 0; i < elems; ++i)
-      if (!std::isfinite(prob[i])) raise(PPOCR_ERR_INVALID_INPUT, "detector output contains non-finite values");
+    // Non-finite map values are found by the device pass (counters[2]) and
+    // reported as invalid input for caller-supplied maps.
     std::lock_guard<std::mutex> lock(ctx->mu);
     HIP_OK(hipSetDevice(ctx->device));
     auto maps = device_alloc(ctx->device, elems * sizeof(float));
     HIP_OK(hipMemcpyAsync(maps->ptr, prob, elems * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
     std::shared_ptr<DeviceBuffer> work;
-    auto per = run_db(ctx, static_cast<const float*>(maps->ptr), (int)n, (int)height, (int)width, transforms, o, work);
+    auto per = run_db(ctx, static_cast<const float*>(maps->ptr), (int)n, (int)height, (int)width, transforms, o, work,
+                      PPOCR_ERR_INVALID_INPUT);
     write_detections(per, out, cap, counts, total);
   });
 }
@@ -811,7 +815,8 @@ ppocr_status ppocr_hip_detect(ppocr_hip_model* model, const float* nchw, size_t 
     upload_input(model, nchw, len);
     run_graph(model);
     const auto& s = model->plan.output_shape;
-    auto per = run_db(model->ctx, output_ptr(model), (int)s[0], (int)s[2], (int)s[3], transforms, o, model->db_work);
+    auto per = run_db(model->ctx, output_ptr(model), (int)s[0], (int)s[2], (int)s[3], transforms, o, model->db_work,
+                      PPOCR_ERR_GPU);
     write_detections(per, out, cap, counts, total);
   });
 }
@@ -837,7 +842,8 @@ ppocr_status ppocr_hip_detect_image(ppocr_hip_model* model, const ppocr_hip_imag
                    true, staging_ptr(model));
     run_graph(model);
     const auto& s = model->plan.output_shape;
-    auto per = run_db(model->ctx, output_ptr(model), (int)s[0], (int)s[2], (int)s[3], transforms, o, model->db_work);
+    auto per = run_db(model->ctx, output_ptr(model), (int)s[0], (int)s[2], (int)s[3], transforms, o, model->db_work,
+                      PPOCR_ERR_GPU);
     write_detections(per, out, cap, counts, total);
   });
 }

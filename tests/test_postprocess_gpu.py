@@ -189,7 +189,13 @@ def test_invalid_arguments(gpu):
         assert e.value.kind == "InvalidInput"
     with pytest.raises(ppocr_hip.GpuError):
         gpu.db_postprocess(values, [(32, 0, 32, 32)])
-    bad = values.copy()
-    bad[3, 3] = np.nan
-    with pytest.raises(ppocr_hip.GpuError):
-        gpu.db_postprocess(bad, [(32, 32, 32, 32)])
+    # extract_detections rejects any non-finite map value, also outside the
+    # content area (src/ocr.rs:731-733); the device pass flags it.
+    for y, x, v in [(3, 3, np.nan), (31, 31, np.inf), (30, 2, -np.inf), (5, 28, np.nan)]:
+        bad = values.copy()
+        bad[y, x] = v
+        with pytest.raises(ppocr_hip.GpuError) as e:
+            gpu.db_postprocess(bad, [(32, 32, 24, 24)])
+        assert e.value.kind == "InvalidInput"
+    # the flag is cleared between calls: a finite map right after passes
+    assert gpu.db_postprocess(values, [(32, 32, 24, 24)]) == [[]]
