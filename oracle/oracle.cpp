@@ -61,6 +61,45 @@ struct Tensor {
   const float* data() const { return v.data(); }
 };
 
+// ---------------------------------------------------------------- test hooks
+// Two switches that only tests turn on, both off by default:
+//  * tracing records named intermediate tensors (block, neck, head and
+//    encoder outputs), so a test can check one module's output in closed
+//    form for weights it constructed;
+//  * a fault plants one wiring mistake in the model composition, so a test
+//    can show that its checks catch that mistake.
+bool g_tracing = false;
+std::map<std::string, Tensor> g_trace;
+int g_fault = 0;
+
+enum Fault {
+  FAULT_NONE = 0,
+  FAULT_LCNET_RESIDUAL_FROM_BLOCK_INPUT,  // residual adds the block input, not the post-token/SE tensor
+  FAULT_LCNET_SE_GATE_FIFTH,              // LCNet SE gate hard-sigmoid(x/5 + 0.5)
+  FAULT_NECK_SE_GATE_SIXTH,               // neck SE gate hard-sigmoid(x/6 + 0.5)
+  FAULT_NECK_CONCAT_SHALLOW_FIRST,        // FPN / medium-neck concat [f0, f1 up2, f2 up4, f3 up8]
+  FAULT_MISSING_GELU,                     // channel_conv1 without GELU
+  FAULT_HEAD_BN_INPUT_AXIS,               // conv_up BN folded over the input-channel axis
+  FAULT_SVTR_SKIP_BEFORE_NORM,            // LightSVTR: LN(seq + skip) instead of LN(seq) + skip
+  FAULT_RECBLOCK_RESIDUAL_NORMED,         // RecBlock residual adds LN1(x) instead of x
+  FAULT_QKV_HEAD_MAJOR,                   // qkv viewed as [heads, 3, hd] instead of [3, heads, hd]
+  FAULT_TINY_HEAD_NO_HSWISH1,             // tiny recognizer head: no hardswish after conv1
+  FAULT_NECK_SE_PLAIN_GATE,               // FPN residual SE as x * g instead of x + x * g
+  FAULT_STEM_CONCAT_SWAPPED,              // large stem concat [branch, pooled]
+  FAULT_INTRACLASS_ROW_COLUMN_SWAPPED,    // k x 1 kernel added into the centre row, 1 x k into the column
+  FAULT_PAN_FROM_PROJECTION,              // bottom-up adds pan(projection[i-1]) instead of pan(bottom_up[i-1])
+  FAULT_TOPDOWN_NOT_CASCADED,             // top-down adds the level above before its own update
+  FAULT_ATTENTION_SCALE_HIDDEN,           // scores scaled by hidden^-0.5 instead of head_dim^-0.5
+  FAULT_SMALL_STEM_NO_GELU,               // tiny recognizer stem without GELU
+  FAULT_COUNT
+};
+
+inline bool fault(int f) { return g_fault == f; }
+
+void trace(const std::string& name, const Tensor& t) {
+  if (g_tracing) g_trace[name] = t;
+}
+
 // ---------------------------------------------------------------- safetensors
 // Minimal reader: 8-byte little-endian header length, JSON header, raw data.
 // F32 only, as the reference CPU loader (src/cpu/weights.rs:14-47).
@@ -674,9 +713,9 @@ struct LcNetBlock {
   Tensor forward(const Tensor& x) const {
     Tensor t = token.forward(x);
     if (has_se) t = mul_gate(t, se.gate(t));
-    Tensor h = conv1.forward(t, ACT_GELU);
+    Tensor h = conv1.forward(t, fault(FAULT_MISSING_GELU) ? ACT_NONE : ACT_GELU);
     Tensor o = conv2.forward(h, ACT_NONE);
-    if (residual) return add(t, o);
+    if (residual) return add(fault(FAULT_LCNET_RESIDUAL_FROM_BLOCK_INPUT) ? x : t, o);
     return o;
   }
 };
@@ -700,7 +739,7 @@ LcNetBlock load_block(const Weights& wt, const std::string& p, BlockSpec s) {
     std::string q = p + ".token_squeeze_excitation.convolutions";
     b.se.reduce = load_conv(wt, q + ".0", s.ci, s.ci / 4, 1, 1, 1, 1, {0, 0, 0, 0}, true, 1);
     b.se.expand = load_conv(wt, q + ".2", s.ci / 4, s.ci, 1, 1, 1, 1, {0, 0, 0, 0}, true, 1);
-    b.se.gate_act = ACT_HSIG6;
+    b.se.gate_act = fault(FAULT_LCNET_SE_GATE_FIFTH) ? ACT_HSIG5 : ACT_HSIG6;
   }
   b.conv1 = load_conv_bn(wt, p + ".channel_conv1", s.ci, s.ci * 2, 1, 1, 1, 1, {0, 0, 0, 0}, false, 1,
                          "normalization", ACT_NONE);
@@ -718,18 +757,24 @@ struct Backbone {
   std::vector<std::vector<LcNetBlock>> stages;
 
   Tensor stem(const Tensor& x) const {
-    if (!large) return conv2.forward(conv1.forward(x, ACT_GELU), ACT_NONE);
+    if (!large)
+      return conv2.forward(conv1.forward(x, fault(FAULT_SMALL_STEM_NO_GELU) ? ACT_NONE : ACT_GELU), ACT_NONE);
     Tensor e = stem1.forward(x);
     Tensor br = stem2b.forward(stem2a.forward(e));
     Tensor pooled = max_pool_2x2_same(e);
-    Tensor merged = upsample_cat({pooled, br}, {1, 1});
+    Tensor merged = fault(FAULT_STEM_CONCAT_SWAPPED) ? upsample_cat({br, pooled}, {1, 1})
+                                                     : upsample_cat({pooled, br}, {1, 1});
     return stem4.forward(stem3.forward(merged));
   }
   std::vector<Tensor> forward(const Tensor& x) const {
     Tensor h = stem(x);
+    trace("stem", h);
     std::vector<Tensor> outs;
-    for (auto& st : stages) {
-      for (auto& b : st) h = b.forward(h);
+    for (size_t s = 0; s < stages.size(); ++s) {
+      for (size_t b = 0; b < stages[s].size(); ++b) {
+        h = stages[s][b].forward(h);
+        trace("block" + std::to_string(s) + "." + std::to_string(b), h);
+      }
       outs.push_back(h);
     }
     return outs;
@@ -890,8 +935,9 @@ void fuse_intraclass(Tensor& sym, std::vector<float>& sb, const Tensor& vert, co
     for (int i = 0; i < ci; ++i) {
       size_t bo = ((size_t)o * ci + i) * k;
       size_t so = bo * k;
-      for (int r = 0; r < k; ++r) sym.v[so + r * k + center] += vert.v[bo + r];
-      for (int c = 0; c < k; ++c) sym.v[so + center * k + c] += hor.v[bo + c];
+      const bool swap = fault(FAULT_INTRACLASS_ROW_COLUMN_SWAPPED);
+      for (int r = 0; r < k; ++r) sym.v[so + (swap ? center * k + r : r * k + center)] += vert.v[bo + r];
+      for (int c = 0; c < k; ++c) sym.v[so + (swap ? c * k + center : center * k + c)] += hor.v[bo + c];
     }
   for (int o = 0; o < co; ++o) {
     sb[o] += vb[o];
@@ -929,14 +975,21 @@ struct RepLkFpn {
     std::vector<Tensor> fused;
     for (int i = 0; i < 4; ++i) {
       Tensor h = in_conv[i].forward(st[i]);
-      fused.push_back(residual_mul_gate(h, in_se[i].gate(h)));
+      Tensor g = in_se[i].gate(h);
+      fused.push_back(fault(FAULT_NECK_SE_PLAIN_GATE) ? mul_gate(h, g) : residual_mul_gate(h, g));
+      trace("fpn.insert" + std::to_string(i), fused.back());
     }
-    for (int i = 2; i >= 0; --i) fused[i] = upsample_add(fused[i], fused[i + 1], 2);
+    const std::vector<Tensor> inserted = fused;
+    for (int i = 2; i >= 0; --i)
+      fused[i] = upsample_add(fused[i], fault(FAULT_TOPDOWN_NOT_CASCADED) ? inserted[i + 1] : fused[i + 1], 2);
     std::vector<Tensor> feats;
     for (int i = 0; i < 4; ++i) {
       Tensor h = pwc[i].forward(dwc[i].forward(fused[i]));
-      feats.push_back(residual_mul_gate(h, dw_se[i].gate(h)));
+      Tensor g = dw_se[i].gate(h);
+      feats.push_back(fault(FAULT_NECK_SE_PLAIN_GATE) ? mul_gate(h, g) : residual_mul_gate(h, g));
+      trace("fpn.feature" + std::to_string(i), feats.back());
     }
+    if (fault(FAULT_NECK_CONCAT_SHALLOW_FIRST)) return upsample_cat(feats, {1, 2, 4, 8});
     std::reverse(feats.begin(), feats.end());
     return upsample_cat(feats, {8, 4, 2, 1});
   }
@@ -951,7 +1004,7 @@ RepLkFpn load_fpn(const Weights& wt, const int chans[4], int nc, int k) {
                                   true, 1);
     f.in_se[i].expand = load_conv(wt, p + ".squeeze_excitation_block.conv2", nc / 4, nc, 1, 1, 1, 1, {0, 0, 0, 0},
                                   true, 1);
-    f.in_se[i].gate_act = ACT_HSIG5;
+    f.in_se[i].gate_act = fault(FAULT_NECK_SE_GATE_SIXTH) ? ACT_HSIG6 : ACT_HSIG5;
     std::string q = "model.neck.input_conv." + std::to_string(i);
     int pd = k / 2;
     f.dwc[i] = load_conv(wt, q + ".depthwise_convolution", nc, nc, k, k, 1, 1, {pd, pd, pd, pd}, true, nc);
@@ -960,7 +1013,7 @@ RepLkFpn load_fpn(const Weights& wt, const int chans[4], int nc, int k) {
                                   {0, 0, 0, 0}, true, 1);
     f.dw_se[i].expand = load_conv(wt, q + ".squeeze_excitation_module.conv2", nc / 16, nc / 4, 1, 1, 1, 1,
                                   {0, 0, 0, 0}, true, 1);
-    f.dw_se[i].gate_act = ACT_HSIG5;
+    f.dw_se[i].gate_act = fault(FAULT_NECK_SE_GATE_SIXTH) ? ACT_HSIG6 : ACT_HSIG5;
   }
   return f;
 }
@@ -999,15 +1052,24 @@ struct MediumNeck {
     for (int i = 0; i < 4; ++i) adj.push_back(adjust[i].forward(st[i]));
     std::vector<Tensor> td(4);
     td[3] = adj[3];
-    for (int i = 2; i >= 0; --i) td[i] = upsample_add(adj[i], td[i + 1], 2);
-    std::vector<Tensor> bu;
+    for (int i = 2; i >= 0; --i)
+      td[i] = upsample_add(adj[i], fault(FAULT_TOPDOWN_NOT_CASCADED) ? adj[i + 1] : td[i + 1], 2);
+    std::vector<Tensor> bu, projected;
     for (int i = 0; i < 4; ++i) {
       Tensor p = project[i].forward(td[i]);
-      if (i > 0) p = add(p, pan[i - 1].forward(bu[i - 1]));
+      projected.push_back(p);
+      if (i > 0) p = add(p, pan[i - 1].forward(fault(FAULT_PAN_FROM_PROJECTION) ? projected[i - 1] : bu[i - 1]));
       bu.push_back(p);
+      trace("neck.bottom_up" + std::to_string(i), p);
     }
     std::vector<Tensor> refined;
-    for (int i = 0; i < 4; ++i) refined.push_back(intra[i].forward(lateral[i].forward(bu[i])));
+    for (int i = 0; i < 4; ++i) {
+      Tensor l = lateral[i].forward(bu[i]);
+      trace("neck.lateral" + std::to_string(i), l);
+      refined.push_back(intra[i].forward(l));
+      trace("neck.refined" + std::to_string(i), refined.back());
+    }
+    if (fault(FAULT_NECK_CONCAT_SHALLOW_FIRST)) return upsample_cat(refined, {1, 2, 4, 8});
     std::reverse(refined.begin(), refined.end());
     return upsample_cat(refined, {8, 4, 2, 1});
   }
@@ -1044,8 +1106,10 @@ struct DetHead {
   std::vector<float> upb, finb;
   Tensor forward(const Tensor& x) const {
     Tensor d = down.forward(x);
+    trace("head.down", d);
     Tensor u = conv_transpose2x2(d, upW, upb.data());
     act_in_place(u, ACT_RELU);
+    trace("head.up", u);
     Tensor f = conv_transpose2x2(u, finW, finb.data());
     act_in_place(f, ACT_SIGMOID);
     return f;
@@ -1066,7 +1130,8 @@ DetHead load_head(const Weights& wt, int nc) {
   for (int o = 0; o < hid; ++o) {
     float s = g.v[o] / std::sqrt(var.v[o] + 1e-5f);
     for (int i = 0; i < hid; ++i)
-      for (int k = 0; k < 4; ++k) h.upW.v[((size_t)i * hid + o) * 4 + k] *= s;
+      for (int k = 0; k < 4; ++k)
+        h.upW.v[(fault(FAULT_HEAD_BN_INPUT_AXIS) ? (size_t)o * hid + i : (size_t)i * hid + o) * 4 + k] *= s;
     h.upb[o] = (h.upb[o] - mu.v[o]) * s + be.v[o];
   }
   h.finW = wt.get("head.conv_final.weight", {hid, 1, 2, 2});
@@ -1093,6 +1158,7 @@ struct Detector : Model {
   Tensor forward(const Tensor& x) const override {
     std::vector<Tensor> st = bb.forward(x);
     Tensor n = medium ? mneck.forward(st) : fpn.forward(st);
+    trace("neck", n);
     return head.forward(n);
   }
 };
@@ -1105,17 +1171,23 @@ struct RecBlock {
     int B = x.shape[0], T = x.shape[1], hd = hidden / heads;
     Tensor qkv = linear(x, qkvW, &qkvB, ACT_NONE, false);
     Tensor out({B, T, hidden});
-    float scale = std::pow((float)hd, -0.5f);
+    float scale = std::pow((float)(fault(FAULT_ATTENTION_SCALE_HIDDEN) ? hidden : hd), -0.5f);
+    // Column of part (q, k, v) for head h, dimension d within a qkv row: the
+    // row is viewed as [3, heads, hd] (src/cpu/model.rs:1706-1714).
+    const bool head_major = fault(FAULT_QKV_HEAD_MAJOR);
+    auto col = [&](int part, int h, int d) {
+      return head_major ? (h * 3 + part) * hd + d : part * hidden + h * hd + d;
+    };
 #pragma omp parallel for collapse(2) schedule(static)
     for (int b = 0; b < B; ++b)
       for (int h = 0; h < heads; ++h) {
         std::vector<float> s(T);
         for (int t = 0; t < T; ++t) {
-          const float* q = qkv.data() + ((size_t)b * T + t) * 3 * hidden + h * hd;
+          const float* q = qkv.data() + ((size_t)b * T + t) * 3 * hidden;
           for (int u = 0; u < T; ++u) {
-            const float* k = qkv.data() + ((size_t)b * T + u) * 3 * hidden + hidden + h * hd;
+            const float* k = qkv.data() + ((size_t)b * T + u) * 3 * hidden;
             float acc = 0.0f;
-            for (int d = 0; d < hd; ++d) acc = std::fma(q[d], k[d], acc);
+            for (int d = 0; d < hd; ++d) acc = std::fma(q[col(0, h, d)], k[col(1, h, d)], acc);
             s[u] = std::fma(acc, scale, 0.0f);
           }
           softmax_row(s.data(), T);
@@ -1123,7 +1195,7 @@ struct RecBlock {
           for (int d = 0; d < hd; ++d) {
             float acc = 0.0f;
             for (int u = 0; u < T; ++u)
-              acc = std::fma(s[u], qkv.v[((size_t)b * T + u) * 3 * hidden + 2 * hidden + h * hd + d], acc);
+              acc = std::fma(s[u], qkv.v[((size_t)b * T + u) * 3 * hidden + col(2, h, d)], acc);
             o[d] = acc;
           }
         }
@@ -1131,7 +1203,8 @@ struct RecBlock {
     return linear(out, projW, &projB, ACT_NONE, false);
   }
   Tensor forward(const Tensor& x) const {
-    Tensor o = add(x, attention(layer_norm(x, ln1w, ln1b, 1e-6f)));
+    Tensor n1 = layer_norm(x, ln1w, ln1b, 1e-6f);
+    Tensor o = add(fault(FAULT_RECBLOCK_RESIDUAL_NORMED) ? n1 : x, attention(n1));
     Tensor m = linear(linear(layer_norm(o, ln2w, ln2b, 1e-6f), fc1W, &fc1B, ACT_SILU, false), fc2W, &fc2B, ACT_NONE,
                       false);
     return add(o, m);
@@ -1153,11 +1226,14 @@ struct Recognizer : Model {
   Tensor forward(const Tensor& x) const override {
     std::vector<Tensor> st = bb.forward(x);
     Tensor pooled = avg_pool_3x2(st.back());  // [N, C, 1, T]
+    trace("pool", pooled);
     int N = pooled.n(), C = pooled.c(), T = pooled.w();
     ENSURE(pooled.h() == 1, "recognizer pooling must produce height 1");
     if (size == 2) {
-      Tensor h = tconv1.forward(pooled, ACT_HSWISH);
+      Tensor h = tconv1.forward(pooled, fault(FAULT_TINY_HEAD_NO_HSWISH1) ? ACT_NONE : ACT_HSWISH);
+      trace("tiny.conv1", h);
       h = tconv2.forward(h, ACT_HSWISH);
+      trace("tiny.conv2", h);
       Tensor seq({N, T, C});
       for (int n = 0; n < N; ++n)
         for (int c = 0; c < C; ++c)
@@ -1166,22 +1242,30 @@ struct Recognizer : Model {
     }
     // RecEncoder::forward (src/cpu/model.rs:1825-1842)
     Tensor res = skip.forward(pooled);
+    trace("svtr.skip", res);
     Tensor h = reduce.forward(pooled);
     Tensor loc = local.forward(h);
     h = add(h, loc);
+    trace("svtr.hidden", h);
     int Hc = h.c();
     Tensor seq({N, T, Hc});
     for (int n = 0; n < N; ++n)
       for (int c = 0; c < Hc; ++c)
         for (int t = 0; t < T; ++t) seq.v[((size_t)n * T + t) * Hc + c] = h.v[((size_t)n * Hc + c) * T + t];
-    for (auto& b : blocks) seq = b.forward(seq);
-    seq = layer_norm(seq, normW, normB, 1e-6f);
+    for (size_t i = 0; i < 2; ++i) {
+      seq = blocks[i].forward(seq);
+      trace("svtr.block" + std::to_string(i), seq);
+    }
+    const bool skip_first = fault(FAULT_SVTR_SKIP_BEFORE_NORM);
+    if (!skip_first) seq = layer_norm(seq, normW, normB, 1e-6f);
     for (int n = 0; n < N; ++n)
       for (int t = 0; t < T; ++t)
         for (int c = 0; c < Hc; ++c) {
           float& v = seq.v[((size_t)n * T + t) * Hc + c];
           v = v + res.v[((size_t)n * Hc + c) * T + t];
         }
+    if (skip_first) seq = layer_norm(seq, normW, normB, 1e-6f);
+    trace("svtr.encoder", seq);
     return linear(seq, clsW, &clsB, ACT_NONE, true);
   }
 };
@@ -1373,6 +1457,26 @@ void* oracle_recognizer_load(const char* path, int size) {
 }
 
 void oracle_model_free(void* m) { delete static_cast<Model*>(m); }
+
+// Test hooks (see "test hooks" above).  A fault applies to models loaded and
+// run while it is set; tracing keeps the tensors of the last forward.
+int oracle_fault_count(void) { return FAULT_COUNT; }
+void oracle_set_fault(int f) { g_fault = f; }
+void oracle_set_tracing(int on) {
+  g_tracing = on != 0;
+  g_trace.clear();
+}
+
+// Copies the traced tensor `name` into out (cap floats); returns its element
+// count (0 if absent) and writes its shape (unused dims 0).
+long oracle_trace_get(const char* name, float* out, size_t cap, int shape[4]) {
+  auto it = g_trace.find(name);
+  if (it == g_trace.end()) return 0;
+  const Tensor& t = it->second;
+  for (int i = 0; i < 4; ++i) shape[i] = i < (int)t.shape.size() ? t.shape[i] : 0;
+  if (out && cap >= t.count()) memcpy(out, t.data(), t.count() * 4);
+  return (long)t.count();
+}
 
 // Detector input: [N,3,H,W] with H,W % 32 == 0 -> [N,1,H,W].
 // Recognizer input: [N,3,48,W] -> [N,T,V] (src/cpu/model.rs:1627-1646).

@@ -326,3 +326,41 @@ def extract_detections(values, transform, binary_threshold=0.2, box_threshold=0.
     fn(*args, out.ctypes.data_as(_F), out.shape[0], ctypes.byref(count))
     out = out[:count.value]
     return out[:, :8].reshape(-1, 4, 2), out[:, 8].copy(), out[:, 9].copy()
+
+
+# ------------------------------------------------------------ test hooks
+def fault_count():
+    """Number of plantable wiring mistakes (fault ids 1 .. count-1; 0 = none)."""
+    L = lib()
+    L.oracle_fault_count.restype = ctypes.c_int
+    return int(L.oracle_fault_count())
+
+
+def set_fault(fault):
+    """Plants wiring mistake ``fault`` (0 = none) in models loaded and run
+    afterwards; see ``enum Fault`` in oracle.cpp.  Tests only."""
+    L = lib()
+    L.oracle_set_fault.argtypes = [ctypes.c_int]
+    L.oracle_set_fault(int(fault))
+
+
+def set_tracing(on):
+    """Records named intermediate tensors of the next forward passes."""
+    L = lib()
+    L.oracle_set_tracing.argtypes = [ctypes.c_int]
+    L.oracle_set_tracing(int(bool(on)))
+
+
+def traced(name):
+    """The traced tensor ``name`` of the last forward pass (KeyError if absent)."""
+    L = lib()
+    fn = L.oracle_trace_get
+    fn.restype = ctypes.c_long
+    fn.argtypes = [ctypes.c_char_p, _F, ctypes.c_size_t, _I]
+    shape = np.zeros(4, dtype=np.int32)
+    n = fn(name.encode(), None, 0, _i(shape))
+    if n == 0:
+        raise KeyError(name)
+    out = np.empty(n, dtype=np.float32)
+    fn(name.encode(), _f(out), n, _i(shape))
+    return out.reshape([int(d) for d in shape if d > 0])
