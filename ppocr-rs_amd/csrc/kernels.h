@@ -187,6 +187,8 @@ void launch_layer_norm(const void* in, int rows, int C, const float* w, const fl
                        void* out, int dt, hipStream_t s);
 
 // Multi-head attention core on qkv [B, T, 3*hidden] -> ctx [B, T, hidden].
+// Register tile of the attention kernel for head dimension hd (0: too wide).
+int attention_head_tile(int hd);
 void launch_attention(const void* qkv, int B, int T, int hidden, int heads, void* out, int dt, hipStream_t s);
 
 // In-place fp32 row softmax over `cols` columns.

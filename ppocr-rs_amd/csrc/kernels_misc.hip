@@ -1090,64 +1090,116 @@ void launch_layer_norm(const void* in, int rows, int C, const float* w, const fl
 // ----------------------------------------------------------------- attention
 // Replaces WGSL `attention_scores` + `attention_context`
 // (src/gpu/shaders/attention.wgsl:62, :151); RecAttention::forward
-// (src/cpu/model.rs:1703-1725): qkv laid out [B, T, 3, heads, hd];
-// scores = (q . k) * hd^-0.5, max-subtracted softmax, context = P v.
-// One block per (image, head, 16 query rows); the score rows stay in LDS.
-constexpr int ATT_Q = 16;
+// (src/cpu/model.rs:1703-1725): qkv rows laid out [3, heads, hd];
+// scores = (q . k) * hd^-0.5, softmax over the keys, context = P v.
+//
+// The softmax is computed online (running maximum and running sum, rescaled
+// when the maximum grows), so no score row is ever held whole and the
+// sequence length has no bound: a workgroup owns one (image, head) and 64
+// queries, four lanes per query; key and value rows stream through LDS 64 at
+// a time, each lane scoring every fourth key of a tile and folding them into
+// its own (max, sum, context) state; the four states of a query are merged
+// with lane shuffles at the end.  HD is the head dimension rounded up to the
+// register tile (16, 24 or 32); the padding lanes of q, k and v are zero.
+constexpr int FA_Q = 64;
+constexpr int FA_K = 64;
 
-template <typename T>
-__global__ __launch_bounds__(256) void attention_kernel(const T* qkv, int B, int T_, int hidden, int heads,
-                                                        float scale, T* out) {
-  extern __shared__ float sc[];  // [ATT_Q][T]
+template <typename T, int HD>
+__global__ __launch_bounds__(256) void flash_attention_kernel(const T* qkv, int T_, int hidden, int heads,
+                                                              float scale, T* out) {
+  __shared__ float ks[FA_K * HD];
+  __shared__ float vs[FA_K * HD];
   const int bh = blockIdx.x;
-  const int b = bh / heads, h = bh - (bh / heads) * heads;
-  const int t0 = blockIdx.y * ATT_Q;
+  const int b = bh / heads, h = bh - b * heads;
   const int hd = hidden / heads;
-  const int rows = min(ATT_Q, T_ - t0);
+  const int qi = threadIdx.x >> 2, sub = threadIdx.x & 3;
+  const int t = blockIdx.y * FA_Q + qi;
   const size_t stride = (size_t)3 * hidden;
   const T* base = qkv + (size_t)b * T_ * stride + h * hd;
-  for (int i = threadIdx.x; i < rows * T_; i += 256) {
-    int r = i / T_, u = i - (i / T_) * T_;
-    const T* q = base + (size_t)(t0 + r) * stride;
-    const T* k = base + (size_t)u * stride + hidden;
-    float acc = 0.0f;
-    for (int d = 0; d < hd; ++d) acc = fmaf(ld1<T>(q + d), ld1<T>(k + d), acc);
-    sc[r * T_ + u] = __fmul_rn(acc, scale);
+  const bool valid = t < T_;
+  float q[HD], acc[HD];
+#pragma unroll
+  for (int d = 0; d < HD; ++d) {
+    q[d] = valid && d < hd ? ld1<T>(base + (size_t)t * stride + d) : 0.0f;
+    acc[d] = 0.0f;
   }
-  __syncthreads();
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int r = wave; r < rows; r += 4) {
-    float* s = sc + r * T_;
-    float m = -INFINITY;
-    for (int u = lane; u < T_; u += 64) m = fmaxf(m, s[u]);
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    float sum = 0.0f;
-    for (int u = lane; u < T_; u += 64) {
-      float e = fast_exp(s[u] - m);
-      s[u] = e;
-      sum += e;
+  float m = -INFINITY, l = 0.0f;
+  for (int k0 = 0; k0 < T_; k0 += FA_K) {
+    const int nk = min(FA_K, T_ - k0);
+    __syncthreads();  // the previous tile is no longer read
+    for (int i = threadIdx.x; i < FA_K * HD; i += 256) {
+      const int j = i / HD, d = i - j * HD;
+      const bool in = j < nk && d < hd;
+      const T* row = base + (size_t)(k0 + j) * stride;
+      ks[i] = in ? ld1<T>(row + hidden + d) : 0.0f;
+      vs[i] = in ? ld1<T>(row + 2 * hidden + d) : 0.0f;
     }
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
-    float rcp = 1.0f / sum;
-    for (int u = lane; u < T_; u += 64) s[u] *= rcp;
+    __syncthreads();
+    float sc[FA_K / 4];
+    float cm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < FA_K / 4; ++i) {
+      const int j = sub + 4 * i;
+      const float* kr = ks + j * HD;
+      float a = 0.0f;
+#pragma unroll
+      for (int d = 0; d < HD; ++d) a = fmaf(q[d], kr[d], a);
+      sc[i] = j < nk ? a * scale : -INFINITY;
+      cm = fmaxf(cm, sc[i]);
+    }
+    const float mn = fmaxf(m, cm);
+    if (mn > -INFINITY) {
+      const float corr = fast_exp(m - mn);  // 0 while nothing was folded (m = -inf)
+      l *= corr;
+#pragma unroll
+      for (int d = 0; d < HD; ++d) acc[d] *= corr;
+#pragma unroll
+      for (int i = 0; i < FA_K / 4; ++i) {
+        const float pr = fast_exp(sc[i] - mn);  // 0 for keys past the sequence
+        l += pr;
+        const float* vr = vs + (sub + 4 * i) * HD;
+#pragma unroll
+        for (int d = 0; d < HD; ++d) acc[d] = fmaf(pr, vr[d], acc[d]);
+      }
+      m = mn;
+    }
   }
-  __syncthreads();
-  for (int i = threadIdx.x; i < rows * hd; i += 256) {
-    int r = i / hd, d = i - (i / hd) * hd;
-    const float* s = sc + r * T_;
-    const T* v = base + 2 * hidden + d;
-    float acc = 0.0f;
-    for (int u = 0; u < T_; ++u) acc = fmaf(s[u], ld1<T>(v + (size_t)u * stride), acc);
-    st1<T>(out + ((size_t)b * T_ + t0 + r) * hidden + h * hd + d, acc);
+  // Merge the four partial states of this query (lanes 4q .. 4q + 3).
+#pragma unroll
+  for (int o = 1; o < 4; o <<= 1) {
+    const float m2 = __shfl_xor(m, o), l2 = __shfl_xor(l, o);
+    const float mn = fmaxf(m, m2);
+    const float c1 = m == -INFINITY ? 0.0f : fast_exp(m - mn);
+    const float c2 = m2 == -INFINITY ? 0.0f : fast_exp(m2 - mn);
+    l = l * c1 + l2 * c2;
+#pragma unroll
+    for (int d = 0; d < HD; ++d) acc[d] = acc[d] * c1 + __shfl_xor(acc[d], o) * c2;
+    m = mn;
+  }
+  if (valid) {
+    const float r = 1.0f / l;
+    T* o = out + ((size_t)b * T_ + t) * hidden + h * hd;
+#pragma unroll
+    for (int d = 0; d < HD; ++d)
+      if ((d & 3) == sub && d < hd) st1<T>(o + d, acc[d] * r);
   }
 }
 
+int attention_head_tile(int hd) { return hd <= 16 ? 16 : hd <= 24 ? 24 : hd <= 32 ? 32 : 0; }
+
 void launch_attention(const void* qkv, int B, int T_, int hidden, int heads, void* out, int dt, hipStream_t s) {
-  float scale = powf((float)(hidden / heads), -0.5f);
-  dim3 grid(B * heads, (T_ + ATT_Q - 1) / ATT_Q);
-  size_t lds = (size_t)ATT_Q * T_ * sizeof(float);
-  DISPATCH_DT(dt, hipLaunchKernelGGL(attention_kernel<T>, grid, dim3(256), lds, s, static_cast<const T*>(qkv), B, T_,
-                                     hidden, heads, scale, static_cast<T*>(out)));
+  const int hd = hidden / heads;
+  const float scale = powf((float)hd, -0.5f);
+  dim3 grid(B * heads, (T_ + FA_Q - 1) / FA_Q);
+#define FA_LAUNCH(HDV)                                                                                     \
+  DISPATCH_DT(dt, hipLaunchKernelGGL((flash_attention_kernel<T, HDV>), grid, dim3(256), 0, s,             \
+                                     static_cast<const T*>(qkv), T_, hidden, heads, scale, static_cast<T*>(out)))
+  switch (attention_head_tile(hd)) {
+    case 16: FA_LAUNCH(16); break;
+    case 24: FA_LAUNCH(24); break;
+    default: FA_LAUNCH(32); break;
+  }
+#undef FA_LAUNCH
 }
 
 // ----------------------------------------------------------------- softmax

@@ -547,7 +547,8 @@ class Builder {
     View out = alloc(qkv.n, qkv.h, qkv.w, hidden, name);
     View in = qkv;
     int T = qkv.h * qkv.w;
-    if ((size_t)16 * T * 4 > 64 * 1024) raise(PPOCR_ERR_INVALID_INPUT, "recognizer sequence too long for attention");
+    if (hidden % heads || attention_head_tile(hidden / heads) == 0)
+      raise(PPOCR_ERR_INVALID_MODEL, name + ": head dimension must divide the hidden size and be at most 32");
     Op op;
     op.name = name;
     op.kernel = "attention";
@@ -1037,7 +1038,9 @@ void validate_detector_shape(const size_t s[4]) {
     raise(PPOCR_ERR_INVALID_INPUT,
           "detector expects [N, 3, H, W] with N > 0, H/W >= 32 and divisible by 32; got [" + std::to_string(s[0]) +
               ", " + std::to_string(s[1]) + ", " + std::to_string(s[2]) + ", " + std::to_string(s[3]) + "]");
-  if (s[0] > (1u << 16) || s[2] > (1u << 15) || s[3] > (1u << 15) || s[0] * s[2] * s[3] > (size_t)INT32_MAX / 64)
+  // Larger batches run in chunks sized to the per-buffer limit; one image's
+  // buffers must fit it on their own.
+  if (s[0] > (1u << 24) || s[2] > (1u << 15) || s[3] > (1u << 15))
     raise(PPOCR_ERR_INVALID_INPUT, "detector input shape is too large");
 }
 
@@ -1046,7 +1049,11 @@ void validate_recognizer_shape(const size_t s[4]) {
     raise(PPOCR_ERR_INVALID_INPUT,
           "recognizer expects [N, 3, 48, W] with N > 0, W >= 32 and divisible by 4; got [" + std::to_string(s[0]) +
               ", " + std::to_string(s[1]) + ", " + std::to_string(s[2]) + ", " + std::to_string(s[3]) + "]");
-  if (s[0] > (1u << 16) || s[3] > (1u << 15) || s[0] * s[3] > (size_t)INT32_MAX / 1024)
+  // The reference bounds a rectified crop to a 4096-px edge (src/ocr.rs:20,
+  // :1145-1156), i.e. canvases up to 48 * 4096 = 196608 px; one line's
+  // buffers fit the per-buffer limit up to about 229000 px, larger batches
+  // run in chunks.
+  if (s[0] > (1u << 24) || s[3] > (1u << 18))
     raise(PPOCR_ERR_INVALID_INPUT, "recognizer input shape is too large");
 }
 

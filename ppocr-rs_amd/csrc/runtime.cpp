@@ -64,6 +64,13 @@ struct ppocr_hip_model {
   ppocr_hip_ctx* ctx = nullptr;
   ppocr::Plan plan;
   size_t in_shape[4] = {0, 0, 0, 0};
+  // The plan (and its graph) covers `chunk` items; a batch of in_shape[0]
+  // items runs as ceil(in_shape[0] / chunk) graph replays.  chunk < batch
+  // only when one buffer of the whole-batch plan would pass the per-buffer
+  // limit (kernels index a buffer with 32-bit offsets).
+  size_t chunk = 0;
+  size_t item_in = 0, item_out = 0;  // fp32 input / output elements per item
+  std::vector<size_t> out_shape;     // whole-batch output shape
   std::shared_ptr<ppocr::DeviceBuffer> weights;
   size_t weight_blob_bytes = 0;
   std::string weights_path;
@@ -144,6 +151,13 @@ void ensure_graph(ppocr_hip_model* m) {
   m->graph_generation = ctx->generation;
 }
 
+size_t n_chunks(const ppocr_hip_model* m) { return (m->in_shape[0] + m->chunk - 1) / m->chunk; }
+// Items of chunk c (the last one may be partial; the graph still runs a
+// whole chunk, on the previous chunk's leftover inputs in the unused slots,
+// whose outputs are not read).
+size_t chunk_items(const ppocr_hip_model* m, size_t c) { return std::min(m->chunk, m->in_shape[0] - c * m->chunk); }
+size_t output_elems(const ppocr_hip_model* m) { return m->item_out * m->in_shape[0]; }
+
 void check_input(ppocr_hip_model* m, const float* nchw, size_t len) {
   size_t expected = m->in_shape[0] * m->in_shape[1] * m->in_shape[2] * m->in_shape[3];
   if (!nchw) raise(PPOCR_ERR_INVALID_INPUT, "input pointer is null");
@@ -162,20 +176,63 @@ float* output_ptr(ppocr_hip_model* m) {
   return reinterpret_cast<float*>(m->ctx->arena + m->plan.bufs[m->plan.output].arena_off);
 }
 
-void upload_input(ppocr_hip_model* m, const float* nchw, size_t len) {
-  HIP_OK(hipMemcpyAsync(staging_ptr(m), nchw, len * sizeof(float), hipMemcpyHostToDevice, m->ctx->stream));
+// Copies the NCHW input items of chunk c into the staging buffer.
+void upload_chunk(ppocr_hip_model* m, const float* nchw, size_t c) {
+  HIP_OK(hipMemcpyAsync(staging_ptr(m), nchw + c * m->chunk * m->item_in, chunk_items(m, c) * m->item_in * sizeof(float),
+                        hipMemcpyHostToDevice, m->ctx->stream));
 }
 
 void run_graph(ppocr_hip_model* m) { HIP_OK(hipGraphLaunch(m->graph, m->ctx->stream)); }
 
-void read_output(ppocr_hip_model* m, float* out, size_t cap) {
-  size_t n = m->plan.output_elems;
+void check_output_cap(ppocr_hip_model* m, const float* out, size_t cap) {
+  const size_t n = output_elems(m);
   if (!out || cap < n)
     raise(PPOCR_ERR_INVALID_INPUT, "output capacity " + std::to_string(cap) + " is below " + std::to_string(n));
-  HIP_OK(hipMemcpyAsync(out, output_ptr(m), n * sizeof(float), hipMemcpyDeviceToHost, m->ctx->stream));
+}
+
+// Queues the download of chunk c's outputs into their place in `out`.
+void download_chunk(ppocr_hip_model* m, float* out, size_t c) {
+  HIP_OK(hipMemcpyAsync(out + c * m->chunk * m->item_out, output_ptr(m), chunk_items(m, c) * m->item_out * sizeof(float),
+                        hipMemcpyDeviceToHost, m->ctx->stream));
+}
+
+// Waits for the queued downloads and rejects non-finite outputs
+// (src/gpu/runtime.rs:2217-2219).
+void finish_output(ppocr_hip_model* m, const float* out) {
   HIP_OK(hipStreamSynchronize(m->ctx->stream));
+  const size_t n = output_elems(m);
   for (size_t i = 0; i < n; ++i)
     if (!std::isfinite(out[i])) raise(PPOCR_ERR_GPU, "model output contains non-finite values");
+}
+
+// Runs the whole batch from host NCHW input to host output.  The output of
+// a chunk is downloaded before the next chunk's input overwrites staging (the
+// stream orders the copies after the graph that reads and writes them).
+void run_batch(ppocr_hip_model* m, const float* nchw, float* out) {
+  for (size_t c = 0; c < n_chunks(m); ++c) {
+    upload_chunk(m, nchw, c);
+    run_graph(m);
+    download_chunk(m, out, c);
+  }
+  finish_output(m, out);
+}
+
+// Largest buffer one plan may hold: every kernel addresses a buffer with
+// 32-bit signed byte offsets.  PPOCR_HIP_MAX_BUFFER_BYTES lowers it (tests
+// use it to exercise chunked batches at small shapes).
+size_t max_buffer_bytes() {
+  size_t limit = (size_t)INT32_MAX;
+  if (const char* e = std::getenv("PPOCR_HIP_MAX_BUFFER_BYTES")) {
+    const unsigned long long v = std::strtoull(e, nullptr, 10);
+    if (v > 0 && v < limit) limit = (size_t)v;
+  }
+  return limit;
+}
+
+size_t largest_buffer(const Plan& plan) {
+  size_t b = 0;
+  for (const Buffer& buf : plan.bufs) b = std::max(b, buf.bytes);
+  return b;
 }
 
 ppocr_hip_model* load_model(ppocr_hip_ctx* ctx, const char* path, ppocr_model_size size, const size_t nchw[4],
@@ -193,7 +250,27 @@ ppocr_hip_model* load_model(ppocr_hip_ctx* ctx, const char* path, ppocr_model_si
   m->size = size;
   m->weights_path = path;
   std::copy(nchw, nchw + 4, m->in_shape);
-  m->plan = detector ? build_detector(st, size, nchw, dt) : build_recognizer(st, size, nchw, dt, greedy);
+  auto build = [&](const size_t* shape) {
+    return detector ? build_detector(st, size, shape, dt) : build_recognizer(st, size, shape, dt, greedy);
+  };
+  m->plan = build(nchw);
+  m->chunk = nchw[0];
+  m->out_shape = m->plan.output_shape;
+  const size_t limit = max_buffer_bytes(), largest = largest_buffer(m->plan);
+  if (largest > limit) {
+    // Every buffer scales with the batch: plan the largest chunk that fits.
+    const size_t per_item = (largest + nchw[0] - 1) / nchw[0];
+    m->chunk = limit / per_item;
+    if (m->chunk == 0)
+      raise(PPOCR_ERR_INVALID_INPUT, "one input item needs a " + std::to_string(per_item) +
+                                         "-byte activation buffer; the limit is " + std::to_string(limit) + " bytes");
+    const size_t shape[4] = {m->chunk, nchw[1], nchw[2], nchw[3]};
+    m->plan = build(shape);
+    if (largest_buffer(m->plan) > limit)
+      raise(PPOCR_ERR_INVALID_INPUT, "input too large for the per-buffer limit of " + std::to_string(limit) + " bytes");
+  }
+  m->item_in = nchw[1] * nchw[2] * nchw[3];
+  m->item_out = m->plan.output_elems / m->chunk;
   m->weight_blob_bytes = m->plan.weights.size();
   std::lock_guard<std::mutex> lock(ctx->mu);
   HIP_OK(hipSetDevice(ctx->device));
@@ -281,8 +358,8 @@ void ppocr_hip_model_free(ppocr_hip_model* model) {
 ppocr_status ppocr_hip_output_shape(const ppocr_hip_model* model, size_t shape[4], size_t* rank) {
   return guarded([&] {
     if (!model || !shape || !rank) raise(PPOCR_ERR_INVALID_INPUT, "null argument");
-    *rank = model->plan.output_shape.size();
-    for (size_t i = 0; i < 4; ++i) shape[i] = i < *rank ? model->plan.output_shape[i] : 0;
+    *rank = model->out_shape.size();
+    for (size_t i = 0; i < 4; ++i) shape[i] = i < *rank ? model->out_shape[i] : 0;
   });
 }
 
@@ -290,13 +367,12 @@ ppocr_status ppocr_hip_forward(ppocr_hip_model* model, const float* nchw, size_t
   return guarded([&] {
     if (!model) raise(PPOCR_ERR_INVALID_INPUT, "model is null");
     check_input(model, nchw, len);
+    check_output_cap(model, out, out_cap);
     std::lock_guard<std::mutex> lock(model->ctx->mu);
     HIP_OK(hipSetDevice(model->ctx->device));
     ensure_arena(model->ctx, model->plan.arena_bytes);
     ensure_graph(model);
-    upload_input(model, nchw, len);
-    run_graph(model);
-    read_output(model, out, out_cap);
+    run_batch(model, nchw, out);
   });
 }
 
@@ -361,6 +437,16 @@ void pack_geometry(char* dst, const float* corners, const int* content_w, size_t
   memcpy(dst + n * 8 * sizeof(float), content_w, n * sizeof(int));
 }
 
+// Queues the upload of items [first, first + n) of a packed geometry table
+// of `total` items (corners, then widths) as an n-item table at `geo`.
+void upload_geometry_slice(ppocr_hip_ctx* ctx, const char* packet, size_t total, size_t first, size_t n) {
+  char* geo = static_cast<char*>(ctx->geo);
+  HIP_OK(hipMemcpyAsync(geo, packet + first * 8 * sizeof(float), n * 8 * sizeof(float), hipMemcpyHostToDevice,
+                        ctx->stream));
+  HIP_OK(hipMemcpyAsync(geo + n * 8 * sizeof(float), packet + total * 8 * sizeof(float) + first * sizeof(int),
+                        n * sizeof(int), hipMemcpyHostToDevice, ctx->stream));
+}
+
 // Sizes the context's device geometry buffer to at least `bytes`; a move
 // waits for the queued work that may still read the old one.  Caller holds
 // ctx->mu.
@@ -387,6 +473,15 @@ void run_preprocess(ppocr_hip_ctx* ctx, const ppocr_hip_image* image, const floa
   enqueue_preprocess(ctx, image, ctx->geo, n, cw, ch, detector, dst);
   // `host` is pageable and goes out of scope here.
   HIP_OK(hipStreamSynchronize(ctx->stream));
+}
+
+// Preprocesses chunk c of a model's image batch into its staging buffer and
+// waits for it.  Caller holds ctx->mu.
+void preprocess_chunk(ppocr_hip_model* m, const ppocr_hip_image* image, const float* corners, const int* content_w,
+                      size_t c) {
+  const size_t first = c * m->chunk;
+  run_preprocess(m->ctx, image, corners + first * 8, content_w + first, (int)chunk_items(m, c), (int)m->in_shape[3],
+                 (int)m->in_shape[2], m->plan.detector, staging_ptr(m));
 }
 
 std::vector<int> content_widths(const size_t* widths, size_t n, size_t canvas) {
@@ -417,9 +512,7 @@ void enqueue_forward_image(ppocr_hip_model* model, const ppocr_hip_image* image,
   if (image->ctx != model->ctx) raise(PPOCR_ERR_INVALID_INPUT, "image and model belong to different contexts");
   if (n != model->in_shape[0])
     raise(PPOCR_ERR_INVALID_INPUT, "geometry count " + std::to_string(n) + " differs from the planned batch");
-  if (out_cap < model->plan.output_elems)
-    raise(PPOCR_ERR_INVALID_INPUT,
-          "output capacity " + std::to_string(out_cap) + " is below " + std::to_string(model->plan.output_elems));
+  check_output_cap(model, out, out_cap);
   check_corners(corners, n);
   std::vector<int> cw = content_widths(content_w, n, model->in_shape[3]);
   pack_geometry(packet, corners, cw.data(), n);
@@ -428,15 +521,17 @@ void enqueue_forward_image(ppocr_hip_model* model, const ppocr_hip_image* image,
   HIP_OK(hipSetDevice(ctx->device));
   ensure_arena(ctx, model->plan.arena_bytes);
   ensure_graph(model);
-  // One geometry buffer serves every queued batch: each batch's upload is
-  // ordered after the previous batch's preprocess on the stream.
-  ensure_geometry(ctx, packet_bytes(n));
-  HIP_OK(hipMemcpyAsync(ctx->geo, packet, packet_bytes(n), hipMemcpyHostToDevice, ctx->stream));
-  enqueue_preprocess(ctx, image, ctx->geo, (int)n, (int)model->in_shape[3], (int)model->in_shape[2],
-                     model->plan.detector, staging_ptr(model));
-  run_graph(model);
-  HIP_OK(hipMemcpyAsync(out, output_ptr(model), model->plan.output_elems * sizeof(float), hipMemcpyDeviceToHost,
-                        ctx->stream));
+  // One geometry buffer serves every queued batch and chunk: each upload is
+  // ordered after the previous preprocess on the stream.
+  ensure_geometry(ctx, packet_bytes(model->chunk));
+  for (size_t c = 0; c < n_chunks(model); ++c) {
+    const size_t items = chunk_items(model, c);
+    upload_geometry_slice(ctx, packet, n, c * model->chunk, items);
+    enqueue_preprocess(ctx, image, ctx->geo, (int)items, (int)model->in_shape[3], (int)model->in_shape[2],
+                       model->plan.detector, staging_ptr(model));
+    run_graph(model);
+    download_chunk(model, out, c);
+  }
 }
 
 void sync_context(ppocr_hip_ctx* ctx) {
@@ -457,15 +552,18 @@ ppocr_status ppocr_hip_forward_image(ppocr_hip_model* model, const ppocr_hip_ima
       raise(PPOCR_ERR_INVALID_INPUT, "geometry count " + std::to_string(n) + " differs from the planned batch");
     check_corners(corners, n);
     std::vector<int> cw = content_widths(content_w, n, model->in_shape[3]);
+    check_output_cap(model, out, out_cap);
     std::lock_guard<std::mutex> lock(model->ctx->mu);
     HIP_OK(hipSetDevice(model->ctx->device));
     ensure_arena(model->ctx, model->plan.arena_bytes);
     ensure_graph(model);
     // Preprocess straight into the NCHW staging buffer the graph starts from.
-    run_preprocess(model->ctx, image, corners, cw.data(), (int)n, (int)model->in_shape[3], (int)model->in_shape[2],
-                   model->plan.detector, staging_ptr(model));
-    run_graph(model);
-    read_output(model, out, out_cap);
+    for (size_t c = 0; c < n_chunks(model); ++c) {
+      preprocess_chunk(model, image, corners, cw.data(), c);
+      run_graph(model);
+      download_chunk(model, out, c);
+    }
+    finish_output(model, out);
   });
 }
 
@@ -474,7 +572,7 @@ ppocr_status ppocr_hip_preprocess(ppocr_hip_ctx* ctx, const ppocr_hip_image* ima
                                   float* out_nchw) {
   return guarded([&] {
     if (!ctx || !image || !out_nchw) raise(PPOCR_ERR_INVALID_INPUT, "null argument");
-    if (canvas_w == 0 || canvas_h == 0 || canvas_w > (1u << 15) || canvas_h > (1u << 15))
+    if (canvas_w == 0 || canvas_h == 0 || canvas_w > (1u << 18) || canvas_h > (1u << 15))
       raise(PPOCR_ERR_INVALID_INPUT, "canvas dimensions out of range");
     check_corners(corners, 1);
     std::vector<int> cw = content_widths(&content_width, 1, canvas_w);
@@ -498,13 +596,17 @@ ppocr_status ppocr_hip_benchmark(ppocr_hip_model* model, const float* nchw, size
     HIP_OK(hipSetDevice(model->ctx->device));
     ensure_arena(model->ctx, model->plan.arena_bytes);
     ensure_graph(model);
-    upload_input(model, nchw, len);
+    // Device-only timing, like benchmark_nchw: the input is staged once
+    // (the first chunk's items) and each run replays the graph once per chunk.
+    upload_chunk(model, nchw, 0);
     HIP_OK(hipStreamSynchronize(model->ctx->stream));
-    for (size_t i = 0; i < warmup; ++i) run_graph(model);
+    const size_t chunks = n_chunks(model);
+    for (size_t i = 0; i < warmup; ++i)
+      for (size_t c = 0; c < chunks; ++c) run_graph(model);
     HIP_OK(hipStreamSynchronize(model->ctx->stream));
     for (size_t i = 0; i < runs; ++i) {
       auto t0 = std::chrono::steady_clock::now();
-      run_graph(model);
+      for (size_t c = 0; c < chunks; ++c) run_graph(model);
       HIP_OK(hipStreamSynchronize(model->ctx->stream));
       auto t1 = std::chrono::steady_clock::now();
       samples_ms[i] = std::chrono::duration<double, std::milli>(t1 - t0).count();
@@ -522,11 +624,12 @@ ppocr_status ppocr_hip_benchmark_stream(ppocr_hip_model* model, const float* nch
     HIP_OK(hipSetDevice(model->ctx->device));
     ensure_arena(model->ctx, model->plan.arena_bytes);
     ensure_graph(model);
-    upload_input(model, nchw, len);
-    for (size_t i = 0; i < warmup; ++i) run_graph(model);
+    upload_chunk(model, nchw, 0);
+    const size_t chunks = n_chunks(model);
+    for (size_t i = 0; i < warmup * chunks; ++i) run_graph(model);
     HIP_OK(hipStreamSynchronize(model->ctx->stream));
     auto t0 = std::chrono::steady_clock::now();
-    for (size_t i = 0; i < runs; ++i) run_graph(model);
+    for (size_t i = 0; i < runs * chunks; ++i) run_graph(model);
     HIP_OK(hipStreamSynchronize(model->ctx->stream));
     auto t1 = std::chrono::steady_clock::now();
     *total_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
@@ -543,7 +646,8 @@ ppocr_status ppocr_hip_profile(ppocr_hip_model* model, const float* nchw, size_t
     HIP_OK(hipSetDevice(model->ctx->device));
     ensure_arena(model->ctx, model->plan.arena_bytes);
     hipStream_t s = model->ctx->stream;
-    upload_input(model, nchw, len);
+    upload_chunk(model, nchw, 0);
+    const size_t chunks = n_chunks(model);
     const auto& ops = model->plan.ops;
     std::vector<hipEvent_t> ev(ops.size() + 1);
     for (auto& e : ev) HIP_OK(hipEventCreate(&e));
@@ -553,7 +657,8 @@ ppocr_status ppocr_hip_profile(ppocr_hip_model* model, const float* nchw, size_t
     for (const Op& op : ops) op.launch(ex, s);
     HIP_OK(hipStreamSynchronize(s));
     hipError_t err = hipSuccess;
-    for (size_t r = 0; r < runs && err == hipSuccess; ++r) {
+    // A run covers the whole batch: every op once per chunk.
+    for (size_t r = 0; r < runs * chunks && err == hipSuccess; ++r) {
       for (size_t i = 0; i < ops.size(); ++i) {
         (void)hipEventRecord(ev[i], s);
         ops[i].launch(ex, s);
@@ -808,15 +913,20 @@ ppocr_status ppocr_hip_detect(ppocr_hip_model* model, const float* nchw, size_t 
     if (!model->plan.detector) raise(PPOCR_ERR_INVALID_INPUT, "detection needs a detector model");
     const ppocr_db_options o = db_options(options);
     check_input(model, nchw, len);
+    if (!transforms) raise(PPOCR_ERR_INVALID_INPUT, "transforms pointer is null");
     std::lock_guard<std::mutex> lock(model->ctx->mu);
     HIP_OK(hipSetDevice(model->ctx->device));
     ensure_arena(model->ctx, model->plan.arena_bytes);
     ensure_graph(model);
-    upload_input(model, nchw, len);
-    run_graph(model);
     const auto& s = model->plan.output_shape;
-    auto per = run_db(model->ctx, output_ptr(model), (int)s[0], (int)s[2], (int)s[3], transforms, o, model->db_work,
-                      PPOCR_ERR_GPU);
+    std::vector<std::vector<HostDetection>> per;
+    for (size_t c = 0; c < n_chunks(model); ++c) {
+      upload_chunk(model, nchw, c);
+      run_graph(model);
+      auto part = run_db(model->ctx, output_ptr(model), (int)chunk_items(model, c), (int)s[2], (int)s[3],
+                         transforms + c * model->chunk, o, model->db_work, PPOCR_ERR_GPU);
+      for (auto& v : part) per.push_back(std::move(v));
+    }
     write_detections(per, out, cap, counts, total);
   });
 }
@@ -834,16 +944,20 @@ ppocr_status ppocr_hip_detect_image(ppocr_hip_model* model, const ppocr_hip_imag
     check_corners(corners, n);
     const ppocr_db_options o = db_options(options);
     std::vector<int> cw = content_widths(nullptr, n, model->in_shape[3]);
+    if (!transforms) raise(PPOCR_ERR_INVALID_INPUT, "transforms pointer is null");
     std::lock_guard<std::mutex> lock(model->ctx->mu);
     HIP_OK(hipSetDevice(model->ctx->device));
     ensure_arena(model->ctx, model->plan.arena_bytes);
     ensure_graph(model);
-    run_preprocess(model->ctx, image, corners, cw.data(), (int)n, (int)model->in_shape[3], (int)model->in_shape[2],
-                   true, staging_ptr(model));
-    run_graph(model);
     const auto& s = model->plan.output_shape;
-    auto per = run_db(model->ctx, output_ptr(model), (int)s[0], (int)s[2], (int)s[3], transforms, o, model->db_work,
-                      PPOCR_ERR_GPU);
+    std::vector<std::vector<HostDetection>> per;
+    for (size_t c = 0; c < n_chunks(model); ++c) {
+      preprocess_chunk(model, image, corners, cw.data(), c);
+      run_graph(model);
+      auto part = run_db(model->ctx, output_ptr(model), (int)chunk_items(model, c), (int)s[2], (int)s[3],
+                         transforms + c * model->chunk, o, model->db_work, PPOCR_ERR_GPU);
+      for (auto& v : part) per.push_back(std::move(v));
+    }
     write_detections(per, out, cap, counts, total);
   });
 }
