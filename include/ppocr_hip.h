@@ -209,6 +209,20 @@ ppocr_status ppocr_hip_db_postprocess(ppocr_hip_ctx* ctx, const float* prob, siz
                                       const ppocr_detector_transform* transforms, const ppocr_db_options* options,
                                       ppocr_detection* out, size_t cap, size_t* counts, size_t* total);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): ppocr_hip_db_postprocess with the same arguments and
+ * results, whose staged maps and work arrays live in a static device scratch
+ * of 64 MiB per GPU, held until the process ends; it calls no hipMalloc or
+ * hipFree.  Maps needing more scratch (about 51 bytes per pixel, e.g. four
+ * 416 x 736 maps) are rejected with PPOCR_ERR_INVALID_INPUT.  All calls on
+ * one GPU share its scratch: calls that overlap on one GPU (from different
+ * contexts; one context serialises its own calls) race. */
+ppocr_status ppocr_hip_db_postprocess_static(ppocr_hip_ctx* ctx, const float* prob, size_t n, size_t height,
+                                             size_t width, const ppocr_detector_transform* transforms,
+                                             const ppocr_db_options* options, ppocr_detection* out, size_t cap,
+                                             size_t* counts, size_t* total);
+
 /* Detector forward followed by the device postprocess on its output, which
  * never leaves the device: `GpuOcrRuntime::run_detector` +
  * `extract_detections` (src/ocr.rs:608-646, :723-790).  One transform per

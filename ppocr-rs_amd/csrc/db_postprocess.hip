@@ -19,9 +19,42 @@
 //
 // Pixel p of image n is index n*H*W + y*W + x; only pixels inside the
 // image's content rectangle take part.
+#include <mutex>
+
 #include "device_math.h"
 
 namespace ppocr {
+
+// Device scratch of ppocr_hip_db_postprocess_static, for callers that cannot
+// allocate: the staged maps and the work arrays of one call live here.
+// Every GPU holds its own copy at its own address; the name is only a host
+// stand-in, so host code uses the address db_scratch returns.
+constexpr size_t kDbScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kDbScratchBytes];
+
+size_t db_scratch_bytes() { return kDbScratchBytes; }
+
+hipError_t db_scratch(int device, void** ptr) {
+  static std::mutex mu;
+  static void* cached[64] = {};
+  if (device < 0 || device >= 64) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!cached[device]) {
+    int current = 0;
+    hipError_t e = hipGetDevice(&current);
+    if (e != hipSuccess) return e;
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return e;
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t back = hipSetDevice(current);
+    if (e != hipSuccess) return e;
+    if (back != hipSuccess) return back;
+    cached[device] = p;
+  }
+  *ptr = cached[device];
+  return hipSuccess;
+}
 
 namespace {
 

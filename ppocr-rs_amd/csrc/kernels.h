@@ -223,6 +223,13 @@ struct DbParams {
 };
 void launch_db_postprocess(const DbParams& p, hipStream_t s);
 
+// Static device scratch of the no-allocation postprocess entry point
+// (db_scratch_bytes() bytes per device, held until the process ends).
+// db_scratch looks its address up once per device (with that device made
+// current for the lookup) and returns the cached address afterwards.
+size_t db_scratch_bytes();
+hipError_t db_scratch(int device, void** ptr);
+
 // Quad-bilinear RGB8 sampling -> rounded -> normalised NCHW fp32 planes.  One
 // geometry per image: corners [N][8], content widths [N].
 struct PreParams {

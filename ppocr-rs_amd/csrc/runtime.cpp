@@ -51,6 +51,7 @@ struct ppocr_hip_ctx {
   uint64_t generation = 0;  // bumped whenever the arena moves
   void* geo = nullptr;      // crop geometry of the synchronous image calls, grown on demand
   size_t geo_bytes = 0;
+  void* db_scratch_ptr = nullptr;  // this device's static postprocess scratch (not owned)
   ~ppocr_hip_ctx() {
     (void)hipSetDevice(device);
     if (stream) (void)hipStreamSynchronize(stream);
@@ -309,6 +310,7 @@ ppocr_status ppocr_hip_create(int device, ppocr_hip_ctx** out) {
     ctx->device = device;
     HIP_OK(hipSetDevice(device));
     HIP_OK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+    HIP_OK(db_scratch(device, &ctx->db_scratch_ptr));
     *out = ctx.release();
   });
 }
@@ -751,15 +753,57 @@ bool detection_before(const HostDetection& l, const HostDetection& r) {
   return l.root < r.root;
 }
 
+// Byte offsets of the postprocess work arrays of N maps of H x W in one
+// work buffer (256-byte aligned), and its size.
+struct DbLayout {
+  size_t label, slot, counters, tables, count, root, keep, mom, geom, ext, out, bytes;
+  long max_comp;
+};
+
+DbLayout db_layout(int N, int H, int W) {
+  DbLayout l;
+  const size_t total = (size_t)N * H * W;
+  // At most one component per 2x2 pixel block: two pixels of one block are
+  // 8-neighbours, so they cannot start different components.
+  l.max_comp = (long)N * ((H + 1) / 2) * ((W + 1) / 2);
+  const size_t mc = (size_t)l.max_comp;
+  size_t off = 0;
+  auto carve = [&](size_t bytes) {
+    size_t at = off;
+    off += (bytes + 255) / 256 * 256;
+    return at;
+  };
+  l.label = carve(4 * total);
+  l.slot = carve(4 * total);
+  l.counters = carve(12);
+  l.tables = carve(4 * 6 * (size_t)N);
+  l.count = carve(4 * mc);
+  l.root = carve(4 * mc);
+  l.keep = carve(4 * mc);
+  l.mom = carve(48 * mc);
+  l.geom = carve(32 * mc);
+  l.ext = carve(16 * mc);
+  l.out = carve(48 * mc);
+  l.bytes = off;
+  return l;
+}
+
+// Grows a model's or call's postprocess work buffer to `bytes`.
+char* db_work(ppocr_hip_ctx* ctx, std::shared_ptr<DeviceBuffer>& work, size_t bytes) {
+  if (!work || work->bytes < bytes) work = device_alloc(ctx->device, bytes);
+  return static_cast<char*>(work->ptr);
+}
+
 // Runs the device postprocess over N maps already in device memory and
-// returns the per-image sorted, truncated detections.  Caller holds ctx->mu.
+// returns the per-image sorted, truncated detections.  `base` holds at least
+// db_layout(N, H, W).bytes of work space.  Caller holds ctx->mu.
 std::vector<std::vector<HostDetection>> run_db(ppocr_hip_ctx* ctx, const float* prob, int N, int H, int W,
                                                const ppocr_detector_transform* tr, const ppocr_db_options& o,
-                                               std::shared_ptr<DeviceBuffer>& work,
-                                               ppocr_status non_finite_status) {
+                                               char* base, ppocr_status non_finite_status) {
   if (!tr) raise(PPOCR_ERR_INVALID_INPUT, "transforms pointer is null");
   const long total = (long)N * H * W;
   if (total >= (long)INT32_MAX) raise(PPOCR_ERR_INVALID_INPUT, "probability maps too large for the postprocess");
+  const DbLayout L = db_layout(N, H, W);
   std::vector<int> tables(6 * (size_t)N);
   for (int n = 0; n < N; ++n) {
     const ppocr_detector_transform& t = tr[n];
@@ -772,46 +816,29 @@ std::vector<std::vector<HostDetection>> run_db(ppocr_hip_ctx* ctx, const float* 
     tables[4 * N + 2 * n] = (int)std::min<uint32_t>(t.content_width, INT32_MAX);
     tables[4 * N + 2 * n + 1] = (int)std::min<uint32_t>(t.content_height, INT32_MAX);
   }
-  // At most one component per 2x2 pixel block: two pixels of one block are
-  // 8-neighbours, so they cannot start different components.
-  const long max_comp = (long)N * ((H + 1) / 2) * ((W + 1) / 2);
-  auto carve = [](size_t& off, size_t bytes) {
-    size_t at = off;
-    off += (bytes + 255) / 256 * 256;
-    return at;
-  };
-  size_t off = 0;
-  const size_t o_label = carve(off, 4 * (size_t)total), o_slot = carve(off, 4 * (size_t)total);
-  const size_t o_counters = carve(off, 12), o_tables = carve(off, 4 * tables.size());
-  const size_t o_count = carve(off, 4 * (size_t)max_comp), o_root = carve(off, 4 * (size_t)max_comp);
-  const size_t o_keep = carve(off, 4 * (size_t)max_comp), o_mom = carve(off, 48 * (size_t)max_comp);
-  const size_t o_geom = carve(off, 32 * (size_t)max_comp), o_ext = carve(off, 16 * (size_t)max_comp);
-  const size_t o_out = carve(off, 48 * (size_t)max_comp);
-  if (!work || work->bytes < off) work = device_alloc(ctx->device, off);
-  char* base = static_cast<char*>(work->ptr);
-  HIP_OK(hipMemcpyAsync(base + o_tables, tables.data(), 4 * tables.size(), hipMemcpyHostToDevice, ctx->stream));
+  HIP_OK(hipMemcpyAsync(base + L.tables, tables.data(), 4 * tables.size(), hipMemcpyHostToDevice, ctx->stream));
   DbParams p{};
   p.prob = prob;
   p.N = N, p.H = H, p.W = W;
   p.total = total;
-  p.content = reinterpret_cast<const int*>(base + o_tables);
+  p.content = reinterpret_cast<const int*>(base + L.tables);
   p.source = p.content + 2 * N;
   p.content_scale = p.content + 4 * N;
   p.threshold = o.binary_threshold;
   p.box_threshold = o.box_threshold;
   p.unclip = o.unclip_ratio;
   p.min_area = (int)std::min<size_t>(o.min_area, (size_t)INT32_MAX);
-  p.max_comp = (int)max_comp;
-  p.label = reinterpret_cast<int*>(base + o_label);
-  p.slot = reinterpret_cast<int*>(base + o_slot);
-  p.counters = reinterpret_cast<int*>(base + o_counters);
-  p.count = reinterpret_cast<int*>(base + o_count);
-  p.root = reinterpret_cast<int*>(base + o_root);
-  p.keep = reinterpret_cast<int*>(base + o_keep);
-  p.moments = reinterpret_cast<double*>(base + o_mom);
-  p.geom = reinterpret_cast<float*>(base + o_geom);
-  p.extent = reinterpret_cast<int*>(base + o_ext);
-  p.out = reinterpret_cast<float*>(base + o_out);
+  p.max_comp = (int)L.max_comp;
+  p.label = reinterpret_cast<int*>(base + L.label);
+  p.slot = reinterpret_cast<int*>(base + L.slot);
+  p.counters = reinterpret_cast<int*>(base + L.counters);
+  p.count = reinterpret_cast<int*>(base + L.count);
+  p.root = reinterpret_cast<int*>(base + L.root);
+  p.keep = reinterpret_cast<int*>(base + L.keep);
+  p.moments = reinterpret_cast<double*>(base + L.mom);
+  p.geom = reinterpret_cast<float*>(base + L.geom);
+  p.extent = reinterpret_cast<int*>(base + L.ext);
+  p.out = reinterpret_cast<float*>(base + L.out);
   launch_db_postprocess(p, ctx->stream);
   HIP_OK(hipGetLastError());
   int counters[3] = {0, 0, 0};
@@ -899,8 +926,39 @@ ppocr_status ppocr_hip_db_postprocess(ppocr_hip_ctx* ctx, const float* prob, siz
     auto maps = device_alloc(ctx->device, elems * sizeof(float));
     HIP_OK(hipMemcpyAsync(maps->ptr, prob, elems * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
     std::shared_ptr<DeviceBuffer> work;
-    auto per = run_db(ctx, static_cast<const float*>(maps->ptr), (int)n, (int)height, (int)width, transforms, o, work,
+    char* base = db_work(ctx, work, db_layout((int)n, (int)height, (int)width).bytes);
+    auto per = run_db(ctx, static_cast<const float*>(maps->ptr), (int)n, (int)height, (int)width, transforms, o, base,
                       PPOCR_ERR_INVALID_INPUT);
+    write_detections(per, out, cap, counts, total);
+  });
+}
+
+// The no-allocation variant: the maps are staged, and the work arrays laid
+// out, in the library's static device scratch (db_scratch), whose address
+// was looked up for the context's device by ppocr_hip_create.
+ppocr_status ppocr_hip_db_postprocess_static(ppocr_hip_ctx* ctx, const float* prob, size_t n, size_t height,
+                                             size_t width, const ppocr_detector_transform* transforms,
+                                             const ppocr_db_options* options, ppocr_detection* out, size_t cap,
+                                             size_t* counts, size_t* total) {
+  return guarded([&] {
+    if (!ctx || !prob) raise(PPOCR_ERR_INVALID_INPUT, "null argument");
+    if (n == 0 || height == 0 || width == 0) raise(PPOCR_ERR_INVALID_INPUT, "probability maps must be non-empty");
+    if (n * height * width >= (size_t)INT32_MAX)
+      raise(PPOCR_ERR_INVALID_INPUT, "probability maps too large for the postprocess");
+    const ppocr_db_options o = db_options(options);
+    const size_t elems = n * height * width;
+    const size_t map_bytes = (elems * sizeof(float) + 255) / 256 * 256;
+    const size_t need = map_bytes + db_layout((int)n, (int)height, (int)width).bytes;
+    if (need > db_scratch_bytes())
+      raise(PPOCR_ERR_INVALID_INPUT, "maps need " + std::to_string(need) + " bytes of postprocess scratch; the static "
+                                     "scratch holds " + std::to_string(db_scratch_bytes()) + " bytes");
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    HIP_OK(hipSetDevice(ctx->device));
+    char* base = static_cast<char*>(ctx->db_scratch_ptr);
+    if (!base) raise(PPOCR_ERR_GPU, "postprocess scratch address unknown for this device");
+    HIP_OK(hipMemcpyAsync(base, prob, elems * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    auto per = run_db(ctx, reinterpret_cast<const float*>(base), (int)n, (int)height, (int)width, transforms, o,
+                      base + map_bytes, PPOCR_ERR_INVALID_INPUT);
     write_detections(per, out, cap, counts, total);
   });
 }
@@ -923,8 +981,10 @@ ppocr_status ppocr_hip_detect(ppocr_hip_model* model, const float* nchw, size_t 
     for (size_t c = 0; c < n_chunks(model); ++c) {
       upload_chunk(model, nchw, c);
       run_graph(model);
-      auto part = run_db(model->ctx, output_ptr(model), (int)chunk_items(model, c), (int)s[2], (int)s[3],
-                         transforms + c * model->chunk, o, model->db_work, PPOCR_ERR_GPU);
+      const int items = (int)chunk_items(model, c);
+      char* base = db_work(model->ctx, model->db_work, db_layout(items, (int)s[2], (int)s[3]).bytes);
+      auto part = run_db(model->ctx, output_ptr(model), items, (int)s[2], (int)s[3], transforms + c * model->chunk, o,
+                         base, PPOCR_ERR_GPU);
       for (auto& v : part) per.push_back(std::move(v));
     }
     write_detections(per, out, cap, counts, total);
@@ -954,8 +1014,10 @@ ppocr_status ppocr_hip_detect_image(ppocr_hip_model* model, const ppocr_hip_imag
     for (size_t c = 0; c < n_chunks(model); ++c) {
       preprocess_chunk(model, image, corners, cw.data(), c);
       run_graph(model);
-      auto part = run_db(model->ctx, output_ptr(model), (int)chunk_items(model, c), (int)s[2], (int)s[3],
-                         transforms + c * model->chunk, o, model->db_work, PPOCR_ERR_GPU);
+      const int items = (int)chunk_items(model, c);
+      char* base = db_work(model->ctx, model->db_work, db_layout(items, (int)s[2], (int)s[3]).bytes);
+      auto part = run_db(model->ctx, output_ptr(model), items, (int)s[2], (int)s[3], transforms + c * model->chunk, o,
+                         base, PPOCR_ERR_GPU);
       for (auto& v : part) per.push_back(std::move(v));
     }
     write_detections(per, out, cap, counts, total);

@@ -39,7 +39,7 @@ EXPORTS = (
     "ppocr_hip_benchmark", "ppocr_hip_benchmark_stream", "ppocr_hip_profile", "ppocr_hip_memory_report",
     "ppocr_hip_recognizer_load_greedy", "ppocr_detector_input_plan", "ppocr_recognizer_batch_width",
     "ppocr_recognition_input_plan", "ppocr_ctc_greedy_decode", "ppocr_db_default_options",
-    "ppocr_hip_db_postprocess", "ppocr_hip_detect", "ppocr_hip_detect_image", "ppocr_engine_default_options",
+    "ppocr_hip_db_postprocess", "ppocr_hip_db_postprocess_static", "ppocr_hip_detect", "ppocr_hip_detect_image", "ppocr_engine_default_options",
     "ppocr_hip_engine_load", "ppocr_hip_engine_free", "ppocr_hip_engine_recognize", "ppocr_ocr_result_lines",
     "ppocr_ocr_result_tokens", "ppocr_ocr_result_sizes", "ppocr_ocr_result_free",
 )
@@ -165,6 +165,7 @@ def lib():
         L.ppocr_db_default_options.restype = None
         L.ppocr_hip_db_postprocess.argtypes = [_VP, _F, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _T, _O,
                                                _D8, ctypes.c_size_t, _SZ, _SZ]
+        L.ppocr_hip_db_postprocess_static.argtypes = L.ppocr_hip_db_postprocess.argtypes
         L.ppocr_hip_detect.argtypes = [_VP, _F, ctypes.c_size_t, _T, _O, _D8, ctypes.c_size_t, _SZ, _SZ]
         L.ppocr_hip_detect_image.argtypes = [_VP, _VP, _F, ctypes.c_size_t, _T, _O, _D8, ctypes.c_size_t, _SZ,
                                              _SZ]
@@ -238,6 +239,20 @@ class Gpu:
             raise ValueError("one transform per map")
         o = db_options(**options)
         return _collect(lambda buf, cap, counts, total: lib().ppocr_hip_db_postprocess(
+            self.handle, p.ctypes.data_as(_F), n, h, w, tr, ctypes.byref(o), buf, cap, counts, total), n, o.max_boxes)
+
+    def db_postprocess_static(self, prob, transforms, **options):
+        """As ``db_postprocess``, through the entry point that allocates no
+        device memory (maps and work arrays in the library's static scratch)."""
+        p = np.ascontiguousarray(prob, dtype=np.float32)
+        if p.ndim == 2:
+            p = p[None]
+        n, h, w = p.shape
+        tr, nt = _transforms(transforms)
+        if nt != n:
+            raise ValueError("one transform per map")
+        o = db_options(**options)
+        return _collect(lambda buf, cap, counts, total: lib().ppocr_hip_db_postprocess_static(
             self.handle, p.ctypes.data_as(_F), n, h, w, tr, ctypes.byref(o), buf, cap, counts, total), n, o.max_boxes)
 
     def close(self):
