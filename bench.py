@@ -11,13 +11,21 @@ Alongside ``value`` the line carries:
 * ``roofline``: the dominant kernel (most device time per step), its
   algorithmic FLOPs (2 x MACs) or bytes per step over its HIP-event-timed
   duration (events recorded on the stream the kernels run on), against the
-  MI355X peak (fp32 matrix 157.3 TFLOP/s, HBM 8 TB/s);
+  MI355X peak for its bound and storage type (fp32 matrix 157.3 TFLOP/s,
+  bf16 matrix 2.5 PFLOP/s, fp32 vector 78.6 TFLOP/s without packed fp32,
+  HBM 8 TB/s); ``traffic`` is its measured HBM bytes per launch from the
+  committed counter summary, when one covers this kernel and workload;
 * ``kernels``: the same measure for the twelve kernel instances with the
   most device time (the depthwise and elementwise ones against HBM);
+* ``pass``: the whole pass's algorithmic FLOPs and bytes per step over the
+  step time;
 * ``cpu_baseline``: the C++ restatement of the reference CPU path (the
-  parity oracle) timed on this host on a bounded sample of the same workload;
+  parity oracle) timed on this host on a bounded sample of the same
+  workload, at the reference's default thread count (min(cores, 4),
+  src/cpu/model.rs:19-27); ``others`` holds the same at every CPU this
+  process may use and for the tiny and medium recognizers;
 * ``also``: the other benchmark configurations, measured after the timed
-  region.
+  region, each with its own dominant-kernel roofline and pass rates.
 """
 
 import argparse
@@ -38,6 +46,7 @@ import seeded  # noqa: E402
 
 METRIC = "detector images/s @416×736 + rec lines/s @48×320; % HBM/MFMA roofline"
 PEAK_F32_TFLOPS = 157.3
+PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 # fp32 FMAs on the vector ALU without packed-fp32 instructions (this build
 # disables them): 256 CUs x 4 SIMDs x 16 lanes x 2 FLOP x 2.4 GHz.
@@ -81,23 +90,23 @@ def kernel_groups(stats):
     return groups
 
 
-def rate(g):
+def rate(g, precision="f32"):
     """(achieved, peak, unit) of a kernel group against its bound's peak."""
     secs = g["ms"] * 1e-3
     if g["bound"] == "mfma":
-        return g["flops"] / secs / 1e12, PEAK_F32_TFLOPS, "TFLOP/s"
+        return g["flops"] / secs / 1e12, PEAK_BF16_TFLOPS if precision == "bf16" else PEAK_F32_TFLOPS, "TFLOP/s"
     if g["bound"] == "valu":
         return g["flops"] / secs / 1e12, PEAK_VALU_F32_TFLOPS, "TFLOP/s"
     return g["bytes"] / secs / 1e9, PEAK_HBM_GBS, "GB/s"
 
 
-def kernel_table(stats, top=12):
+def kernel_table(stats, top=12, precision="f32"):
     """The `top` kernel instances by device time, each against its roofline."""
     groups = kernel_groups(stats)
     total_ms = sum(v["ms"] for v in groups.values())
     rows = []
     for name, g in sorted(groups.items(), key=lambda kv: -kv[1]["ms"])[:top]:
-        achieved, peak, unit = rate(g)
+        achieved, peak, unit = rate(g, precision)
         rows.append({"kernel": name, "bound": g["bound"],
                      "launches_per_step": g["launches"], "ms_per_step": round(g["ms"], 4),
                      "share_of_device_time": round(g["ms"] / total_ms, 3) if total_ms else None,
@@ -105,11 +114,11 @@ def kernel_table(stats, top=12):
     return rows
 
 
-def roofline(stats):
+def roofline(stats, key, precision="f32"):
     """Dominant kernel instance: the one with the most device time per step."""
     groups = kernel_groups(stats)
     name, g = max(groups.items(), key=lambda kv: kv[1]["ms"])
-    achieved, peak, unit = rate(g)
+    achieved, peak, unit = rate(g, precision)
     total_ms = sum(v["ms"] for v in groups.values())
     return {
         "bound": g["bound"],
@@ -117,7 +126,7 @@ def roofline(stats):
         "peak": peak,
         "unit": unit,
         "frac": round(achieved / peak, 4),
-        "traffic": traffic_for(name),
+        "traffic": traffic_for(key, name),
         "kernel": name,
         "launches_per_step": g["launches"],
         "avg_launch_ms": round(g["ms"] / g["launches"], 5),
@@ -127,21 +136,20 @@ def roofline(stats):
     }
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "dominant_kernel_traffic.txt"
+def traffic_for(key, kernel):
+    """HBM bytes per launch of `kernel` in workload `key` from the committed
+    counter summary ``profiles/traffic_<key>.txt``.
 
-
-def traffic_for(kernel):
-    """HBM bytes per launch of `kernel` from the committed counter summary.
-
-    The summary is written from two rocprofv3 --pmc runs of this benchmark
+    A summary is written from two rocprofv3 --pmc runs of this benchmark
     (FETCH_SIZE, WRITE_SIZE, KiB per dispatch), each scaled by the same
     counter's reading for a copy kernel of known size (``--copy-calibration``).
-    Returns None when the summary covers a different kernel.
+    Returns None when no summary covers this kernel.
     """
-    if not TRAFFIC_FILE.exists():
+    path = ROOT / "profiles" / f"traffic_{key}.txt"
+    if not path.exists():
         return None
     fields = {}
-    for line in TRAFFIC_FILE.read_text().splitlines():
+    for line in path.read_text().splitlines():
         if ":" in line and not line.startswith("#"):
             k, v = line.split(":", 1)
             fields[k.strip()] = v.strip()
@@ -167,14 +175,26 @@ def copy_calibration(mib=256, reps=5):
     print(json.dumps({"copy_calibration": {"bytes_read": n * 4, "bytes_written": n * 4, "launches": reps}}))
 
 
-def cpu_baseline(kind, size, shape, budget_s=12.0):
+def usable_cpus():
+    """CPUs this process may run on (its affinity mask, capped by
+    OMP_NUM_THREADS when that is set), and a description of how it was found."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    n = min(affinity, int(omp)) if omp.isdigit() and int(omp) > 0 else affinity
+    return n, f"os.cpu_count()={os.cpu_count()}, affinity={affinity}, OMP_NUM_THREADS={omp or 'unset'}"
+
+
+def cpu_time(kind, size, threads, budget_s):
+    """Single-item passes of the oracle for `budget_s` seconds (one warm-up)."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
 
-    threads = min(os.cpu_count() or 1, 16)
     oracle.set_threads(threads)
     model = oracle.Model(kind, weights(kind, size), size)
-    one = (1,) + tuple(shape[1:])
+    one = (1, 3, 416, 736) if kind == "det" else (1, 3, 48, 320)
     x = inputs(kind, one)
     model.forward(x)  # warm-up
     runs, t0 = 0, time.perf_counter()
@@ -182,12 +202,62 @@ def cpu_baseline(kind, size, shape, budget_s=12.0):
         model.forward(x)
         runs += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or runs >= 30:
+        if el >= budget_s or runs >= 200:
             break
     unit = "images/s" if kind == "det" else "lines/s"
-    return {"value": round(runs * one[0] / el, 3), "unit": unit, "cores": threads, "kind": "port",
-            "sample": f"{runs} single-image passes of the {size} {'detector' if kind == 'det' else 'recognizer'} "
-                      f"at {one}, C++ restatement of the reference CPU path (fp32, OpenMP)"}
+    what = "detector" if kind == "det" else "recognizer"
+    return {"value": round(runs / el, 3), "unit": unit, "cores": threads, "kind": "port",
+            "sample": f"{runs} single-{'image' if kind == 'det' else 'line'} passes ({el:.1f} s) of the {size} "
+                      f"{what} at {one}, C++ restatement of the reference CPU path (fp32, OpenMP, "
+                      f"{threads} threads)"}
+
+
+def cpu_baseline(kind, size):
+    """The oracle at the reference's default thread count, min(cores, 4)
+    (src/cpu/model.rs:19-27), with the same at every usable CPU and for the
+    tiny and medium recognizers under ``others``."""
+    cpus, how = usable_cpus()
+    base = cpu_time(kind, size, min(cpus, 4), 10.0)
+    base["cpus"] = how
+    base["others"] = [cpu_time(kind, size, cpus, 8.0), cpu_time("rec", "tiny", min(cpus, 4), 3.0),
+                      cpu_time("rec", "tiny", cpus, 3.0), cpu_time("rec", "medium", min(cpus, 4), 4.0)]
+    return base
+
+
+def config_key(kind, size, shape, precision, greedy=False):
+    return f"{size}_{kind}_{shape[0]}x{shape[2]}x{shape[3]}_{precision}" + ("_greedy" if greedy else "")
+
+
+HEADLINE = ("det", "medium", (8, 3, 416, 736), "f32")
+HEADLINE_KEY = config_key(*HEADLINE)
+
+
+def pass_rates(stats, ms_per_step, precision):
+    """Whole-pass algorithmic FLOP and byte rates per step."""
+    flops = sum(s["flops"] for s in stats)
+    nbytes = sum(s["bytes"] for s in stats)
+    secs = ms_per_step * 1e-3
+    peak = PEAK_BF16_TFLOPS if precision == "bf16" else PEAK_F32_TFLOPS
+    return {"gflop_per_step": round(flops / 1e9, 3), "mb_per_step": round(nbytes / 1e6, 2),
+            "tflops": round(flops / secs / 1e12, 3), "frac_of_matrix_peak": round(flops / secs / 1e12 / peak, 4),
+            "gbs": round(nbytes / secs / 1e9, 1), "frac_of_hbm": round(nbytes / secs / 1e9 / PEAK_HBM_GBS, 4),
+            "kernels_per_step": len(stats)}
+
+
+def measure(gpu, kind, size, shape, precision, greedy, warmup, steps, top=5):
+    """Throughput, dominant-kernel roofline and pass rates of one configuration."""
+    key = config_key(kind, size, shape, precision, greedy)
+    m = load(gpu, kind, size, shape, precision, greedy)
+    try:
+        x = inputs(kind, shape)
+        ms = throughput(m, x, warmup, steps)
+        stats = m.profile(x, runs=3)
+    finally:
+        m.close()
+    unit = "images/s" if kind == "det" else "lines/s"
+    return {"value": round(shape[0] * steps / (ms / 1e3), 2), "unit": unit, "ms_per_step": round(ms / steps, 4),
+            "roofline": roofline(stats, key, precision), "pass": pass_rates(stats, ms / steps, precision),
+            "kernels": kernel_table(stats, top, precision)}
 
 
 def also(gpu, warmup, steps):
@@ -215,18 +285,34 @@ def also(gpu, warmup, steps):
     ]
     for kind, size, shape, precision, *mode in configs:
         greedy = mode == ["greedy"]
-        key = f"{size}_{kind}_{shape[0]}x{shape[2]}x{shape[3]}_{precision}" + ("_greedy" if greedy else "")
+        key = config_key(kind, size, shape, precision, greedy)
         try:
-            m = load(gpu, kind, size, shape, precision, greedy)
-            x = inputs(kind, shape)
-            ms = throughput(m, x, warmup, steps)
-            m.close()
-            unit = "images/s" if kind == "det" else "lines/s"
-            out[key] = {"value": round(shape[0] * steps / (ms / 1e3), 2), "unit": unit,
-                        "ms_per_step": round(ms / steps, 4)}
+            out[key] = measure(gpu, kind, size, shape, precision, greedy, warmup, steps)
         except Exception as e:  # report, keep going
             out[key] = {"error": str(e)}
     return out
+
+
+def only(key, warmup, steps):
+    """Runs one configuration's timed loop alone (for rocprofv3 runs)."""
+    gpu = ppocr_hip.Gpu(0)
+    for kind in ("det", "rec"):
+        for size in ("tiny", "small", "medium"):
+            for precision in ("f32", "bf16"):
+                for greedy in (False, True):
+                    for n, h, w in ((1, 416, 736), (8, 416, 736), (1, 832, 1472), (1, 48, 320), (64, 48, 320),
+                                    (256, 48, 320)):
+                        shape = (n, 3, h, w)
+                        if config_key(kind, size, shape, precision, greedy) != key:
+                            continue
+                        m = load(gpu, kind, size, shape, precision, greedy)
+                        ms = throughput(m, inputs(kind, shape), warmup, steps)
+                        m.close()
+                        gpu.close()
+                        print(json.dumps({"config": key, "ms_per_step": round(ms / steps, 4)}), flush=True)
+                        return
+    gpu.close()
+    raise SystemExit(f"unknown configuration {key}")
 
 
 def pipeline(gpu, reps=20):
@@ -274,9 +360,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a known-size copy kernel (for rocprofv3 counter scaling)")
+    ap.add_argument("--only", metavar="KEY", help="run only this configuration's timed loop (rocprofv3 runs)")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.only:
+        only(args.only, args.warmup, args.steps)
         return
     if args.gpus != 1:
         print("bench.py measures one GPU: the detector/recognizer path has no multi-GPU form in this build "
@@ -284,7 +374,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    kind, size, shape = "det", "medium", (8, 3, 416, 736)
+    kind, size, shape, precision = HEADLINE
     gpu = ppocr_hip.Gpu(0)
     model = load(gpu, kind, size, shape)
     x = inputs(kind, shape)
@@ -292,7 +382,7 @@ def main():
     ms_per_step = total_ms / args.steps
     value = shape[0] * args.steps / (total_ms / 1e3)
     stats = model.profile(x, runs=max(3, min(args.steps, 10)))
-    roof = roofline(stats)
+    roof = roofline(stats, HEADLINE_KEY, precision)
     model.close()
 
     line = {
@@ -313,9 +403,10 @@ def main():
                    "model_size": "medium", "batch": shape[0], "height": shape[2], "width": shape[3]},
         "roofline": roof,
         "kernels": kernel_table(stats),
+        "pass": pass_rates(stats, ms_per_step, precision),
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(kind, size, shape)
+        line["cpu_baseline"] = cpu_baseline(kind, size)
     if not args.no_extra:
         line["also"] = also(gpu, args.warmup, max(5, args.steps // 2))
         line["pipeline"] = pipeline(gpu)
