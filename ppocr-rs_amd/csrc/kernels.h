@@ -115,6 +115,30 @@ struct SeParams {
 };
 
 void launch_conv(const ConvParams& p, hipStream_t s);
+
+// Fused pointwise pair of an LCNet block (pair_gemm.hip), fp32, rows are
+// pixels: x' = x * gate[image] (gate null: x' = x), h = GELU(x' W1^T + b1)
+// kept on chip, out = h W2^T + b2 (+ x' when residual; Co == C).  C, H2
+// and Co multiples of 16; weights packed [rows][ldw] as the conv GEMM's.
+struct PairParams {
+  const float* in;
+  int in_ps;
+  const float* gate;  // [N][C] or null
+  int HW;             // pixels per image (the gate's image of a row)
+  int M, C, H2, Co;
+  const float* w1;
+  int ldw1;
+  const float* b1;
+  const float* w2;
+  int ldw2;
+  const float* b2;
+  int residual;
+  float* out;
+  int out_ps;
+};
+bool pointwise_pair_supported(int C, int H2, int Co, int dt);
+size_t pointwise_pair_lds(int C, int H2);
+void launch_pointwise_pair(const PairParams& p, hipStream_t s);
 // Name of the kernel instance launch_conv runs for p (tile, and the variant:
 // 1x1 or k x k, gated, register-staged); the pointers of p are only tested
 // for null and 16-byte alignment.

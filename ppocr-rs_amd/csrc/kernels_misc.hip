@@ -752,11 +752,13 @@ __global__ __launch_bounds__(256) void se_expand_kernel(SeParams p) {
   if (lane < 4 && c0 + lane < p.C) p.gate[(size_t)n * p.C + c0 + lane] = act_apply(p.gate_act, a[lane] + p.b2[c0 + lane]);
 }
 
-// The whole gate of one image in one workgroup, for small maps and weights
-// (where three dependent launches cost more than the work): channel means
-// (lanes split channels x pixel phases, fixed-order LDS reduction), then the
-// reducing and expanding 1x1 convs as in stages 2 and 3, 16 waves at a time.
-template <typename T>
+// The whole gate of one image in one workgroup (where dependent launches
+// cost more than the work): channel means (lanes split channels x pixel
+// phases, fixed-order LDS reduction) from the map itself, for small maps, or
+// (PARTIALS) from the per-chunk sums left by se_partial or by the depthwise
+// that wrote the map; then the reducing and expanding 1x1 convs as in stages
+// 2 and 3, 16 waves at a time.
+template <typename T, bool PARTIALS>
 __global__ __launch_bounds__(1024) void se_fused_kernel(SeParams p) {
   extern __shared__ float sm[];
   const int cr4 = (p.Cr + 3) & ~3;
@@ -770,7 +772,12 @@ __global__ __launch_bounds__(1024) void se_fused_kernel(SeParams p) {
   const int lanes_p = 1024 / C4;
   const int cq = tid % C4, pl = tid / C4;
   float4 s = f4_zero();
-  if (pl < lanes_p) s = strided_sum4<T>(s, in + (size_t)n * p.HW * p.in_ps + cq * 4, p.in_ps, pl, p.HW, lanes_p);
+  if (pl < lanes_p) {
+    if constexpr (PARTIALS)
+      s = strided_sum4<float>(s, p.partial + (size_t)n * p.P * p.C + cq * 4, p.C, pl, p.P, lanes_p);
+    else
+      s = strided_sum4<T>(s, in + (size_t)n * p.HW * p.in_ps + cq * 4, p.in_ps, pl, p.HW, lanes_p);
+  }
   red[tid] = s;
   __syncthreads();
   if (tid < C4) {
@@ -804,7 +811,20 @@ bool se_fused(const SeParams& p) {
          (size_t)p.C * p.Cr * 2 * sizeof(float) <= (128u << 10);
 }
 
+// From the partial sums: one workgroup per image does the means and both
+// 1x1 convs while their weights are small (one CU pulls them from L2 at a
+// few hundred bytes per cycle); otherwise the two stages spread the weight
+// rows over many workgroups.
+static bool se_gate_one_block(const SeParams& p) {
+  return p.C <= 4096 && (size_t)p.C * p.Cr * 2 * sizeof(float) <= (128u << 10);
+}
+
 void launch_se_from_partials(const SeParams& p, hipStream_t s) {
+  if (se_gate_one_block(p)) {
+    const size_t lds = ((size_t)p.C + ((p.Cr + 3) & ~3)) * sizeof(float) + 1024 * sizeof(float4);
+    hipLaunchKernelGGL((se_fused_kernel<float, true>), dim3(p.N), dim3(1024), lds, s, p);
+    return;
+  }
   size_t lds = (size_t)p.C * sizeof(float) + 256 * sizeof(float4);
   hipLaunchKernelGGL(se_reduce_kernel, dim3(p.N, (p.Cr + 15) / 16), dim3(256), lds, s, p);
   hipLaunchKernelGGL(se_expand_kernel, dim3(p.N, (p.C + 15) / 16), dim3(256), (size_t)p.Cr * sizeof(float), s, p);
@@ -813,14 +833,12 @@ void launch_se_from_partials(const SeParams& p, hipStream_t s) {
 void launch_se(const SeParams& p, hipStream_t s) {
   if (se_fused(p)) {
     const size_t lds = ((size_t)p.C + ((p.Cr + 3) & ~3)) * sizeof(float) + 1024 * sizeof(float4);
-    DISPATCH_DT(p.dt, hipLaunchKernelGGL(se_fused_kernel<T>, dim3(p.N), dim3(1024), lds, s, p));
+    DISPATCH_DT(p.dt, hipLaunchKernelGGL((se_fused_kernel<T, false>), dim3(p.N), dim3(1024), lds, s, p));
     return;
   }
   int chunk = (p.HW + p.P - 1) / p.P;
   DISPATCH_DT(p.dt, hipLaunchKernelGGL(se_partial_kernel<T>, dim3(p.P, p.N), dim3(256), 0, s, p, chunk));
-  size_t lds = (size_t)p.C * sizeof(float) + 256 * sizeof(float4);
-  hipLaunchKernelGGL(se_reduce_kernel, dim3(p.N, (p.Cr + 15) / 16), dim3(256), lds, s, p);
-  hipLaunchKernelGGL(se_expand_kernel, dim3(p.N, (p.C + 15) / 16), dim3(256), (size_t)p.Cr * sizeof(float), s, p);
+  launch_se_from_partials(p, s);
 }
 
 // ----------------------------------------------------------------- layout

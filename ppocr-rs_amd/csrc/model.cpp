@@ -415,6 +415,52 @@ class Builder {
     return out;
   }
 
+  // The LCNet pointwise pair as one fused op (pair_gemm.hip): channel_conv1
+  // (GELU) and channel_conv2 with the hidden tile on chip; `gate` is the SE
+  // gate of x (or null) and `residual` adds the gated x.
+  View pointwise_pair(const View& x, const ConvW& w1, const ConvW& w2, const View* gate, bool residual,
+                      const std::string& name) {
+    if (x.c != w1.ci_pad || w2.ci_pad != w1.co || w1.kh * w1.kw * w2.kh * w2.kw != 1)
+      raise(PPOCR_ERR_INVALID_MODEL, name + ": pointwise pair shapes do not chain");
+    if (residual && w2.co != x.c) raise(PPOCR_ERR_INVALID_MODEL, name + ": residual needs equal channel counts");
+    View out = alloc(x.n, x.h, x.w, w2.co, name);
+    View in = x;
+    View g = gate ? *gate : View();
+    const bool has_gate = gate;
+    PairParams base{};
+    base.in_ps = x.ps;
+    base.HW = x.h * x.w;
+    base.M = (int)x.pixels();
+    base.C = x.c, base.H2 = w1.co, base.Co = w2.co;
+    base.ldw1 = w1.ldw, base.ldw2 = w2.ldw;
+    base.residual = residual;
+    base.out_ps = out.ps;
+    const size_t w1o = w1.w, b1o = w1.b, w2o = w2.w, b2o = w2.b;
+    Op op;
+    op.name = name;
+    op.kernel = std::string("pointwise_pair") + (has_gate ? "<gate>" : "");
+    op.bound = 1;
+    const double M = (double)x.pixels();
+    op.flops = 2.0 * M * ((double)x.c * w1.co + (double)w1.co * w2.co);
+    op.bytes = 4.0 * (M * x.c + (double)x.c * w1.co + (double)w1.co * w2.co + M * w2.co);
+    op.reads = {x.buf};
+    if (has_gate) op.reads.push_back(g.buf);
+    op.writes = {out.buf};
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      PairParams p = base;
+      p.in = ex.fptr(in);
+      p.gate = has_gate ? ex.fptr(g) : nullptr;
+      p.w1 = ex.w(w1o);
+      p.b1 = ex.w(b1o);
+      p.w2 = ex.w(w2o);
+      p.b2 = ex.w(b2o);
+      p.out = ex.fptr(out);
+      launch_pointwise_pair(p, s);
+    };
+    add_op(std::move(op));
+    return out;
+  }
+
   // Squeeze-excitation gate [N,1,1,C] (fp32) of x (src/cpu/model.rs:456-493,
   // :1069-1105).
   // With sp->P > 0 the channel sums come from the depthwise that wrote x.
@@ -664,6 +710,16 @@ class Builder {
 // ------------------------------------------------------------------ backbone
 
 // LcNetBlock (src/cpu/model.rs:509-603).
+// Whether an LCNet block's pointwise pair runs fused (pair_gemm.hip): fp32,
+// channel counts in multiples of 16, and at most 64 input channels.  Wider
+// pairs measured slower fused than as two GEMMs (small detector at batch 1
+// 0.82x with pairs up to 192 channels fused): every workgroup streams both
+// weight matrices from L2 for its 32 pixels.
+bool pair_fusion_pays(const View& t, int ci, int co, int dt) {
+  (void)t;
+  return ci <= 64 && pointwise_pair_supported(ci, 2 * ci, co, dt);
+}
+
 View lcnet_block(Builder& B, const View& x, const std::string& p, BlockSpec s) {
   bool residual = s.ci == s.co && s.sh == 1 && s.sw == 1;
   DwW tw = residual ? B.dw_w(p + ".token_conv", s.ci, 3, 3, s.sh, s.sw, {1, 1, 1, 1}, true)
@@ -679,6 +735,8 @@ View lcnet_block(Builder& B, const View& x, const std::string& p, BlockSpec s) {
   }
   ConvW c1 = B.conv_w(p + ".channel_conv1", s.ci, 2 * s.ci, 1, 1, 1, 1, {0, 0, 0, 0}, false, "normalization");
   ConvW c2 = B.conv_w(p + ".channel_conv2", 2 * s.ci, s.co, 1, 1, 1, 1, {0, 0, 0, 0}, false, "normalization");
+  if (pair_fusion_pays(t, s.ci, s.co, B.dt()))
+    return B.pointwise_pair(t, c1, c2, has_se ? &gate : nullptr, residual, p + ".channel_conv");
   Epi e1;
   e1.act = ACT_GELU;
   if (has_se) e1.in_gate = &gate;

@@ -190,6 +190,47 @@ void ppocr_probe_depthwise_table(const float* weight, int c, int k, uint16_t* ou
   ppocr::depthwise_mfma_table(weight, c, k, out);
 }
 
+// Fused pointwise pair (pair_gemm.hip) on host arrays: x [m][c] rows
+// (pixels of n images of hw pixels each), gate [n][c] or null, w1 [h2][c],
+// b1 [h2], w2 [co][h2], b2 [co]; out [m][co] = w2 GELU(w1 x' + b1) + b2
+// (+ x' when residual), x' = x * gate.  Returns 0, or 1 on a HIP error.
+int ppocr_probe_pointwise_pair(const float* x, int m, int hw, int c, const float* gate, const float* w1,
+                               const float* b1, int h2, const float* w2, const float* b2, int co, int residual,
+                               float* out) {
+  const int n = (m + hw - 1) / hw;
+  void* d_in = upload(x, (size_t)m * c, ppocr::DT_F32);
+  void* d_gate = gate ? upload(gate, (size_t)n * c, ppocr::DT_F32) : nullptr;
+  void* d_w1 = upload(w1, (size_t)h2 * c, ppocr::DT_F32);
+  void* d_b1 = upload(b1, h2, ppocr::DT_F32);
+  void* d_w2 = upload(w2, (size_t)co * h2, ppocr::DT_F32);
+  void* d_b2 = upload(b2, co, ppocr::DT_F32);
+  void* d_out = nullptr;
+  int rc = 0;
+  if (!d_in || (gate && !d_gate) || !d_w1 || !d_b1 || !d_w2 || !d_b2 ||
+      hipMalloc(&d_out, (size_t)m * co * 4) != hipSuccess || !ppocr::pointwise_pair_supported(c, h2, co, 0)) {
+    rc = 1;
+  } else {
+    ppocr::PairParams p{};
+    p.in = static_cast<const float*>(d_in);
+    p.in_ps = c;
+    p.gate = static_cast<const float*>(d_gate);
+    p.HW = hw;
+    p.M = m, p.C = c, p.H2 = h2, p.Co = co;
+    p.w1 = static_cast<const float*>(d_w1), p.ldw1 = c, p.b1 = static_cast<const float*>(d_b1);
+    p.w2 = static_cast<const float*>(d_w2), p.ldw2 = h2, p.b2 = static_cast<const float*>(d_b2);
+    p.residual = residual;
+    p.out = static_cast<float*>(d_out);
+    p.out_ps = co;
+    ppocr::launch_pointwise_pair(p, nullptr);
+    if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(out, d_out, (size_t)m * co * 4, hipMemcpyDeviceToHost) != hipSuccess)
+      rc = 1;
+  }
+  for (void* d : {d_in, d_gate, d_w1, d_b1, d_w2, d_b2, d_out})
+    if (d) (void)hipFree(d);
+  return rc;
+}
+
 // The kernel instance ppocr_probe_depthwise runs.
 const char* ppocr_probe_depthwise_kernel(int h, int c, int k, int dt, int table) {
   return ppocr::depthwise_kernel_name(k, k, 1, 1, h, dt, table != 0, c);

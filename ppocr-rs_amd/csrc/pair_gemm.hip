@@ -1,0 +1,139 @@
+// Fused pointwise pair of an LCNet block: y = W2 GELU(W1 x + b1) + b2, plus
+// the block's residual.  Replaces two conv GEMM launches (and the HBM round
+// trip of the 2C-channel hidden tensor) with one, as the reference CPU path
+// fuses the pair per pixel tile (Conv2d::forward_pointwise_pair_gelu,
+// src/cpu/backend.rs:443-695).
+//
+// A workgroup owns PB_M consecutive pixels.  Their input rows (C channels,
+// multiplied by the SE gate when the block has one, rounded to fp32 as the
+// unfused gather does) are staged in LDS; the four waves compute the hidden
+// tile GELU(x W1^T + b1) on the matrix cores (v_mfma_f32_16x16x4f32), 16
+// hidden channels at a time, into a second LDS tile; then the output tile
+// h W2^T + b2 (+ x for a residual block) from that, 16 output channels at a
+// time.  Weights stream from L2.  The sums run in the order of the unfused
+// kernel (K slices of 16 ascending, four MFMAs per slice), so results match
+// it up to its split-K choices.
+#include "device_math.h"
+#include "kernels.h"
+
+namespace ppocr {
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int PB_M = 32;  // pixels per workgroup (two 16-row MFMA tiles)
+
+__device__ __forceinline__ void mfma4(f32x4& acc, float4 a, float4 b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
+}
+
+// Two 16-row tiles of src (row stride lds floats, K columns) times 16 rows of
+// w (row stride ldw, K columns): lane (lrow, g) reads k = k0 + 4g .. +3.
+__device__ __forceinline__ void tile_product(const float* src, int lds, const float* wrow, int K, int lrow, int g,
+                                             f32x4& acc0, f32x4& acc1) {
+  acc0 = f32x4{0.f, 0.f, 0.f, 0.f};
+  acc1 = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float* a0p = src + lrow * lds + 4 * g;
+  const float* a1p = src + (16 + lrow) * lds + 4 * g;
+  const float* bp = wrow + 4 * g;
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    const float4 b = *reinterpret_cast<const float4*>(bp + k0);
+    const float4 a0 = *reinterpret_cast<const float4*>(a0p + k0);
+    const float4 a1 = *reinterpret_cast<const float4*>(a1p + k0);
+    mfma4(acc0, a0, b);
+    mfma4(acc1, a1, b);
+  }
+}
+
+template <bool GATE, bool RES>
+__global__ __launch_bounds__(256) void pointwise_pair_kernel(PairParams p) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  const int ldx = p.C + 4, ldh = p.H2 + 4;  // +4 floats: conflict-free 16-byte row reads
+  float* xs = sm;                           // [PB_M][ldx]
+  float* hs = sm + PB_M * ldx;              // [PB_M][ldh]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int lrow = lane & 15, g = lane >> 4;
+  const int m0 = blockIdx.x * PB_M;
+
+  // Input tile, gated; rows past M are zero.
+  const int c4 = p.C >> 2;
+  for (int i = tid; i < PB_M * c4; i += 256) {
+    const int r = i / c4, c = (i - r * c4) * 4;
+    const int m = m0 + r;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (m < p.M) {
+      v = *reinterpret_cast<const float4*>(p.in + (size_t)m * p.in_ps + c);
+      if constexpr (GATE) {
+        const float4 gt = *reinterpret_cast<const float4*>(p.gate + (size_t)(m / p.HW) * p.C + c);
+        v = make_float4(__fmul_rn(v.x, gt.x), __fmul_rn(v.y, gt.y), __fmul_rn(v.z, gt.z), __fmul_rn(v.w, gt.w));
+      }
+    }
+    *reinterpret_cast<float4*>(xs + r * ldx + c) = v;
+  }
+  __syncthreads();
+
+  // Hidden tile: lane (lrow, g) of column tile ct holds rows 4g + v (and
+  // 16 + 4g + v) of hidden channel ct * 16 + lrow.
+  for (int ct = wave; ct < p.H2 / 16; ct += 4) {
+    f32x4 acc0, acc1;
+    const int col = ct * 16 + lrow;
+    tile_product(xs, ldx, p.w1 + (size_t)col * p.ldw1, p.C, lrow, g, acc0, acc1);
+    const float b = p.b1 ? p.b1[col] : 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      hs[(4 * g + v) * ldh + col] = act_apply(ACT_GELU, acc0[v] + b);
+      hs[(16 + 4 * g + v) * ldh + col] = act_apply(ACT_GELU, acc1[v] + b);
+    }
+  }
+  __syncthreads();
+
+  // Output tile.
+  for (int ct = wave; ct < p.Co / 16; ct += 4) {
+    f32x4 acc0, acc1;
+    const int col = ct * 16 + lrow;
+    tile_product(hs, ldh, p.w2 + (size_t)col * p.ldw2, p.H2, lrow, g, acc0, acc1);
+    const float b = p.b2 ? p.b2[col] : 0.0f;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const f32x4& acc = half ? acc1 : acc0;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = half * 16 + 4 * g + v;
+        const int m = m0 + row;
+        if (m >= p.M) continue;
+        float o = acc[v] + b;
+        if constexpr (RES) o = o + xs[row * ldx + col];  // the gated input, as the unfused residual
+        p.out[(size_t)m * p.out_ps + col] = o;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+bool pointwise_pair_supported(int C, int H2, int Co, int dt) {
+  return dt == DT_F32 && C % 16 == 0 && H2 % 16 == 0 && Co % 16 == 0 && pointwise_pair_lds(C, H2) <= (160u << 10);
+}
+
+size_t pointwise_pair_lds(int C, int H2) { return (size_t)PB_M * ((C + 4) + (H2 + 4)) * sizeof(float); }
+
+void launch_pointwise_pair(const PairParams& p, hipStream_t s) {
+  const dim3 grid((unsigned)((p.M + PB_M - 1) / PB_M));
+  const size_t lds = pointwise_pair_lds(p.C, p.H2);
+  const bool gate = p.gate != nullptr, res = p.residual != 0;
+  if (gate && res)
+    hipLaunchKernelGGL((pointwise_pair_kernel<true, true>), grid, dim3(256), lds, s, p);
+  else if (gate)
+    hipLaunchKernelGGL((pointwise_pair_kernel<true, false>), grid, dim3(256), lds, s, p);
+  else if (res)
+    hipLaunchKernelGGL((pointwise_pair_kernel<false, true>), grid, dim3(256), lds, s, p);
+  else
+    hipLaunchKernelGGL((pointwise_pair_kernel<false, false>), grid, dim3(256), lds, s, p);
+}
+
+}  // namespace ppocr

@@ -155,3 +155,53 @@ def test_split_k_agrees_with_unsplit():
         outs.append(out)
     for o in outs[1:]:
         assert np.max(np.abs(o - outs[0])) <= 1e-4
+
+
+# Fused pointwise pair (pair_gemm.hip): out = w2 GELU(w1 x' + b1) + b2
+# (+ x'), x' = x * gate[image], against float64 with the exact-erf GELU (the
+# kernel's A-S erf differs by < 1.5e-7).  Rows not a multiple of the 32-pixel
+# tile, tiles straddling images, 16-channel multiples from 16 to 192.
+PAIR_CASES = [
+    # name, rows, pixels per image, C, Co, gate, residual
+    ("tiny stage 1 residual gated", 1000, 400, 32, 32, True, True),
+    ("plain, one tile", 17, 17, 16, 16, False, False),
+    ("widen, no residual", 333, 111, 48, 96, False, False),
+    ("residual", 259, 259, 64, 64, False, True),
+    ("gated, narrow", 70, 23, 96, 48, True, False),
+    ("widest", 95, 45, 192, 192, True, True),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,m,hw,c,co,gated,residual", PAIR_CASES, ids=[c[0] for c in PAIR_CASES])
+def test_pointwise_pair_matches_float64(name, m, hw, c, co, gated, residual):
+    from scipy.special import erf
+
+    lib = _lib()
+    f = ctypes.POINTER(ctypes.c_float)
+    i = ctypes.c_int
+    lib.ppocr_probe_pointwise_pair.argtypes = [f, i, i, i, f, f, f, i, f, f, i, i, f]
+    lib.ppocr_probe_pointwise_pair.restype = i
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    h2 = 2 * c
+    x = rng.standard_normal((m, c)).astype(np.float32)
+    n = (m + hw - 1) // hw
+    gate = rng.uniform(0, 1, (n, c)).astype(np.float32) if gated else None
+    w1 = (rng.standard_normal((h2, c)) / np.sqrt(c)).astype(np.float32)
+    b1 = rng.standard_normal(h2).astype(np.float32) * 0.1
+    w2 = (rng.standard_normal((co, h2)) / np.sqrt(h2)).astype(np.float32)
+    b2 = rng.standard_normal(co).astype(np.float32) * 0.1
+    out = np.empty((m, co), np.float32)
+    rc = lib.ppocr_probe_pointwise_pair(_ptr(x), m, hw, c, _ptr(gate), _ptr(w1), _ptr(b1), h2, _ptr(w2), _ptr(b2), co,
+                                        int(residual), _ptr(out))
+    assert rc == 0
+    xg = x.astype(np.float64)
+    if gated:
+        xg = (x * gate[np.arange(m) // hw]).astype(np.float64)  # x * g rounded to fp32, as the kernel forms it
+    h = xg @ w1.T.astype(np.float64) + b1
+    h = 0.5 * h * (1.0 + erf(h / np.sqrt(2.0)))
+    want = h @ w2.T.astype(np.float64) + b2
+    if residual:
+        want = want + xg
+    err = np.abs(out - want)
+    assert np.all(err <= 1e-4 + 1e-5 * np.abs(want)), f"max err {err.max()}"
