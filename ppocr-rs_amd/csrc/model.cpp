@@ -712,9 +712,11 @@ class Builder {
 // LcNetBlock (src/cpu/model.rs:509-603).
 // Whether an LCNet block's pointwise pair runs fused (pair_gemm.hip): fp32,
 // channel counts in multiples of 16, and at most 64 input channels.  Wider
-// pairs measured slower fused than as two GEMMs (small detector at batch 1
-// 0.82x with pairs up to 192 channels fused): every workgroup streams both
-// weight matrices from L2 for its 32 pixels.
+// pairs measured slower fused than as two GEMMs (pairs up to 192 channels
+// fused: small detector at batch 1 0.87x, small recognizer at batch 1 0.74x):
+// a workgroup owns 32 pixels, so the deep stages' few hundred pixels give a
+// few workgroups where the two GEMMs split K over the whole GPU, and every
+// workgroup streams both weight matrices from L2.
 bool pair_fusion_pays(const View& t, int ci, int co, int dt) {
   (void)t;
   return ci <= 64 && pointwise_pair_supported(ci, 2 * ci, co, dt);

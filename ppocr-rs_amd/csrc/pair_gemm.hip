@@ -33,6 +33,11 @@ __device__ __forceinline__ void mfma4(f32x4& acc, float4 a, float4 b) {
 
 // Two 16-row tiles of src (row stride lds floats, K columns) times 16 rows of
 // w (row stride ldw, K columns): lane (lrow, g) reads k = k0 + 4g .. +3.
+// The weight vectors come from L2 in chunks of KC slices, the next chunk's
+// loads issued before the current chunk's products, so one load latency is
+// exposed per column tile rather than one per K slice.
+constexpr int KC = 4;
+
 __device__ __forceinline__ void tile_product(const float* src, int lds, const float* wrow, int K, int lrow, int g,
                                              f32x4& acc0, f32x4& acc1) {
   acc0 = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -40,12 +45,28 @@ __device__ __forceinline__ void tile_product(const float* src, int lds, const fl
   const float* a0p = src + lrow * lds + 4 * g;
   const float* a1p = src + (16 + lrow) * lds + 4 * g;
   const float* bp = wrow + 4 * g;
-  for (int k0 = 0; k0 < K; k0 += 16) {
-    const float4 b = *reinterpret_cast<const float4*>(bp + k0);
-    const float4 a0 = *reinterpret_cast<const float4*>(a0p + k0);
-    const float4 a1 = *reinterpret_cast<const float4*>(a1p + k0);
-    mfma4(acc0, a0, b);
-    mfma4(acc1, a1, b);
+  const int nk = K / 16;
+  float4 cur[KC];
+#pragma unroll
+  for (int i = 0; i < KC; ++i)
+    if (i < nk) cur[i] = *reinterpret_cast<const float4*>(bp + i * 16);
+  for (int c0 = 0; c0 < nk; c0 += KC) {
+    float4 nxt[KC];
+#pragma unroll
+    for (int i = 0; i < KC; ++i)
+      if (c0 + KC + i < nk) nxt[i] = *reinterpret_cast<const float4*>(bp + (c0 + KC + i) * 16);
+#pragma unroll
+    for (int i = 0; i < KC; ++i) {
+      if (c0 + i < nk) {
+        const int k0 = (c0 + i) * 16;
+        const float4 a0 = *reinterpret_cast<const float4*>(a0p + k0);
+        const float4 a1 = *reinterpret_cast<const float4*>(a1p + k0);
+        mfma4(acc0, a0, cur[i]);
+        mfma4(acc1, a1, cur[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < KC; ++i) cur[i] = nxt[i];
   }
 }
 
