@@ -137,6 +137,27 @@ struct PairParams {
   int out_ps;
 };
 bool pointwise_pair_supported(int C, int H2, int Co, int dt);
+
+// LayerNorm fused into the linear layer that reads it (pair_gemm.hip), fp32:
+// out[m][n] = act(sum_k LN(x[m])[k] w[n][k] + b[n]), LN with eps over K
+// features (K a multiple of 4); weights packed [N][ldw].
+struct LnLinearParams {
+  const float* in;
+  int in_ps;
+  int M, K, N;
+  const float* ln_w;
+  const float* ln_b;
+  float eps;
+  const float* w;
+  int ldw;
+  const float* b;
+  int act;
+  float* out;
+  int out_ps;
+};
+size_t ln_linear_lds(int K);
+bool ln_linear_supported(int K, int N, int dt);
+void launch_ln_linear(const LnLinearParams& p, hipStream_t s);
 size_t pointwise_pair_lds(int C, int H2);
 void launch_pointwise_pair(const PairParams& p, hipStream_t s);
 // Name of the kernel instance launch_conv runs for p (tile, and the variant:

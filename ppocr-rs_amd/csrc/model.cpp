@@ -589,6 +589,46 @@ class Builder {
     return out;
   }
 
+  // LayerNorm `p` (eps 1e-6) of x fused into the linear layer w that reads
+  // it (pair_gemm.hip), with activation act.
+  View ln_linear(const View& x, const std::string& p, const ConvW& w, int act, const std::string& name) {
+    const int C = x.c;
+    if (w.ci_pad != C || w.kh * w.kw != 1) raise(PPOCR_ERR_INVALID_MODEL, name + ": linear input mismatch");
+    const size_t lwo = put(get(p + ".weight", {C}).v), lbo = put(get(p + ".bias", {C}).v);
+    View out = alloc(x.n, x.h, x.w, w.co, name);
+    View in = x;
+    LnLinearParams base{};
+    base.in_ps = x.ps;
+    base.M = (int)x.pixels();
+    base.K = C, base.N = w.co;
+    base.eps = 1e-6f;
+    base.ldw = w.ldw;
+    base.act = act;
+    base.out_ps = out.ps;
+    const size_t wo = w.w, bo = w.b;
+    Op op;
+    op.name = name;
+    op.kernel = "ln_linear";
+    op.bound = 1;
+    const double M = (double)x.pixels();
+    op.flops = 2.0 * M * C * w.co;
+    op.bytes = 4.0 * (M * C + (double)C * w.co + M * w.co) + 8.0 * C;
+    op.reads = {x.buf};
+    op.writes = {out.buf};
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      LnLinearParams q = base;
+      q.in = ex.fptr(in);
+      q.ln_w = ex.w(lwo);
+      q.ln_b = ex.w(lbo);
+      q.w = ex.w(wo);
+      q.b = ex.w(bo);
+      q.out = ex.fptr(out);
+      launch_ln_linear(q, s);
+    };
+    add_op(std::move(op));
+    return out;
+  }
+
   View attention(const View& qkv, int hidden, int heads, const std::string& name) {
     View out = alloc(qkv.n, qkv.h, qkv.w, hidden, name);
     View in = qkv;
@@ -1207,14 +1247,20 @@ Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4], int
     h = B.depthwise(h, lw, ACT_SILU, &h, e + ".conv_block.2");
     for (int i = 0; i < 2; ++i) {
       std::string p = e + ".svtr_block." + std::to_string(i);
-      View a = B.layer_norm(h, p + ".layer_norm1", nullptr, p + ".layer_norm1");
-      View qkv = B.conv(a, B.linear_w(p + ".self_attn.qkv", hid, 3 * hid), Epi{}, p + ".self_attn.qkv");
+      // fp32 plans fuse each block LayerNorm into the linear layer after it.
+      const bool fuse_ln = ln_linear_supported(hid, 3 * hid, B.dt()) && ln_linear_supported(hid, mlp, B.dt());
+      ConvW qkv_w = B.linear_w(p + ".self_attn.qkv", hid, 3 * hid);
+      View qkv = fuse_ln ? B.ln_linear(h, p + ".layer_norm1", qkv_w, ACT_NONE, p + ".layer_norm1+qkv")
+                         : B.conv(B.layer_norm(h, p + ".layer_norm1", nullptr, p + ".layer_norm1"), qkv_w, Epi{},
+                                  p + ".self_attn.qkv");
       View ctx = B.attention(qkv, hid, 8, p + ".self_attn");
       Epi r1;
       r1.res = &h;
       View h1 = B.conv(ctx, B.linear_w(p + ".self_attn.projection", hid, hid), r1, p + ".self_attn.projection");
-      View a2 = B.layer_norm(h1, p + ".layer_norm2", nullptr, p + ".layer_norm2");
-      View m = B.conv(a2, B.linear_w(p + ".mlp.fc1", hid, mlp), silu, p + ".mlp.fc1");
+      ConvW fc1_w = B.linear_w(p + ".mlp.fc1", hid, mlp);
+      View m = fuse_ln ? B.ln_linear(h1, p + ".layer_norm2", fc1_w, ACT_SILU, p + ".layer_norm2+fc1")
+                       : B.conv(B.layer_norm(h1, p + ".layer_norm2", nullptr, p + ".layer_norm2"), fc1_w, silu,
+                                p + ".mlp.fc1");
       Epi r2;
       r2.res = &h1;
       h = B.conv(m, B.linear_w(p + ".mlp.fc2", mlp, hid), r2, p + ".mlp.fc2");

@@ -38,8 +38,13 @@ __device__ __forceinline__ void mfma4(f32x4& acc, float4 a, float4 b) {
 // exposed per column tile rather than one per K slice.
 constexpr int KC = 4;
 
+// Weight vectors at k >= kmax (k a multiple of 4) read as zero.
+__device__ __forceinline__ float4 wvec(const float* p, int k, int kmax) {
+  return k < kmax ? *reinterpret_cast<const float4*>(p) : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
 __device__ __forceinline__ void tile_product(const float* src, int lds, const float* wrow, int K, int lrow, int g,
-                                             f32x4& acc0, f32x4& acc1) {
+                                             f32x4& acc0, f32x4& acc1, int kmax) {
   acc0 = f32x4{0.f, 0.f, 0.f, 0.f};
   acc1 = f32x4{0.f, 0.f, 0.f, 0.f};
   const float* a0p = src + lrow * lds + 4 * g;
@@ -49,12 +54,12 @@ __device__ __forceinline__ void tile_product(const float* src, int lds, const fl
   float4 cur[KC];
 #pragma unroll
   for (int i = 0; i < KC; ++i)
-    if (i < nk) cur[i] = *reinterpret_cast<const float4*>(bp + i * 16);
+    if (i < nk) cur[i] = wvec(bp + i * 16, i * 16 + 4 * g, kmax);
   for (int c0 = 0; c0 < nk; c0 += KC) {
     float4 nxt[KC];
 #pragma unroll
     for (int i = 0; i < KC; ++i)
-      if (c0 + KC + i < nk) nxt[i] = *reinterpret_cast<const float4*>(bp + (c0 + KC + i) * 16);
+      if (c0 + KC + i < nk) nxt[i] = wvec(bp + (c0 + KC + i) * 16, (c0 + KC + i) * 16 + 4 * g, kmax);
 #pragma unroll
     for (int i = 0; i < KC; ++i) {
       if (c0 + i < nk) {
@@ -103,7 +108,7 @@ __global__ __launch_bounds__(256) void pointwise_pair_kernel(PairParams p) {
   for (int ct = wave; ct < p.H2 / 16; ct += 4) {
     f32x4 acc0, acc1;
     const int col = ct * 16 + lrow;
-    tile_product(xs, ldx, p.w1 + (size_t)col * p.ldw1, p.C, lrow, g, acc0, acc1);
+    tile_product(xs, ldx, p.w1 + (size_t)col * p.ldw1, p.C, lrow, g, acc0, acc1, p.C);
     const float b = p.b1 ? p.b1[col] : 0.0f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -117,7 +122,7 @@ __global__ __launch_bounds__(256) void pointwise_pair_kernel(PairParams p) {
   for (int ct = wave; ct < p.Co / 16; ct += 4) {
     f32x4 acc0, acc1;
     const int col = ct * 16 + lrow;
-    tile_product(hs, ldh, p.w2 + (size_t)col * p.ldw2, p.H2, lrow, g, acc0, acc1);
+    tile_product(hs, ldh, p.w2 + (size_t)col * p.ldw2, p.H2, lrow, g, acc0, acc1, p.H2);
     const float b = p.b2 ? p.b2[col] : 0.0f;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
@@ -135,7 +140,105 @@ __global__ __launch_bounds__(256) void pointwise_pair_kernel(PairParams p) {
   }
 }
 
+// LayerNorm fused into the linear layer that reads it (RecBlock's
+// layer_norm1 -> qkv and layer_norm2 -> fc1, src/cpu/model.rs:1768-1772):
+// out = act(LN(x) W^T + b).  A workgroup owns 32 rows and 64 output
+// columns (grid y), one 16-column tile per wave.  Eight lanes normalise one
+// row: each holds up to LN_V float4 of it in registers, the row's sum and
+// squared deviations are reduced over the eight lanes, and the normalised
+// values fma(x - mean, inv * w, b) (layer_norm_in_place's formula) go to LDS,
+// zero-padded to a multiple of 16 features; each column group redoes this
+// for its rows (32 x K reads against 64 x K weights).  The product then runs
+// as in the pair kernel (columns past N computed on row N - 1 of W and not
+// stored).
+constexpr int LN_V = 8;  // float4 per lane: K <= 8 lanes * 8 * 4 = 256
+
+__global__ __launch_bounds__(256) void ln_linear_kernel(LnLinearParams p) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  const int K16 = (p.K + 15) & ~15;
+  const int ldx = K16 + 4;
+  float* xs = sm;  // [PB_M][ldx]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int lrow = lane & 15, g = lane >> 4;
+  const int m0 = blockIdx.x * PB_M;
+  {
+    const int r = tid >> 3, sub = tid & 7;  // row r of the tile, lane sub of its eight
+    const int m = m0 + r;
+    const int k4 = p.K >> 2;
+    float4 v[LN_V];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < LN_V; ++i) {
+      const int j = sub + 8 * i;
+      v[i] = m < p.M && j < k4 ? *reinterpret_cast<const float4*>(p.in + (size_t)m * p.in_ps + 4 * j)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+      s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    }
+    for (int o = 1; o < 8; o <<= 1) s += __shfl_xor(s, o);
+    const float mean = s / (float)p.K;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < LN_V; ++i) {
+      if (sub + 8 * i < k4) {
+        const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
+        q = fmaf(a, a, q);
+        q = fmaf(b, b, q);
+        q = fmaf(c, c, q);
+        q = fmaf(d, d, q);
+      }
+    }
+    for (int o = 1; o < 8; o <<= 1) q += __shfl_xor(q, o);
+    const float inv = 1.0f / sqrtf(q / (float)p.K + p.eps);
+    float* y = xs + r * ldx;
+#pragma unroll
+    for (int i = 0; i < LN_V; ++i) {
+      const int j = sub + 8 * i;
+      if (4 * j >= K16) continue;
+      float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (m < p.M && j < k4) {
+        const float4 w = *reinterpret_cast<const float4*>(p.ln_w + 4 * j);
+        const float4 b = *reinterpret_cast<const float4*>(p.ln_b + 4 * j);
+        o = make_float4(fmaf(v[i].x - mean, inv * w.x, b.x), fmaf(v[i].y - mean, inv * w.y, b.y),
+                        fmaf(v[i].z - mean, inv * w.z, b.z), fmaf(v[i].w - mean, inv * w.w, b.w));
+      }
+      *reinterpret_cast<float4*>(y + 4 * j) = o;
+    }
+  }
+  __syncthreads();
+  {
+    const int ct = blockIdx.y * 4 + wave;
+    if (ct * 16 >= p.N) return;  // after the only barrier
+    f32x4 acc0, acc1;
+    const int col = ct * 16 + lrow;
+    const int wr = col < p.N ? col : p.N - 1;
+    tile_product(xs, ldx, p.w + (size_t)wr * p.ldw, K16, lrow, g, acc0, acc1, p.K);
+    if (col >= p.N) return;
+    const float b = p.b ? p.b[col] : 0.0f;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const f32x4& acc = half ? acc1 : acc0;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = m0 + half * 16 + 4 * g + v;
+        if (m < p.M) p.out[(size_t)m * p.out_ps + col] = act_apply(p.act, acc[v] + b);
+      }
+    }
+  }
+}
+
 }  // namespace
+
+size_t ln_linear_lds(int K) { return (size_t)PB_M * (((K + 15) & ~15) + 4) * sizeof(float); }
+
+bool ln_linear_supported(int K, int N, int dt) {
+  return dt == DT_F32 && K % 4 == 0 && K <= 32 * LN_V && N >= 1;
+}
+
+void launch_ln_linear(const LnLinearParams& p, hipStream_t s) {
+  const dim3 grid((unsigned)((p.M + PB_M - 1) / PB_M), (unsigned)((p.N + 63) / 64));
+  hipLaunchKernelGGL(ln_linear_kernel, grid, dim3(256), ln_linear_lds(p.K), s, p);
+}
 
 bool pointwise_pair_supported(int C, int H2, int Co, int dt) {
   return dt == DT_F32 && C % 16 == 0 && H2 % 16 == 0 && Co % 16 == 0 && pointwise_pair_lds(C, H2) <= (160u << 10);
