@@ -96,6 +96,37 @@ enum Fault {
 
 inline bool fault(int f) { return g_fault == f; }
 
+// bf16 storage emulation (tests of the bf16 path): when on, the tensors a
+// bf16 plan stores are rounded to bf16 (nearest even) as they are produced,
+// and so are the weights it feeds to the matrix cores (after BN folding);
+// sums, SE gates, LayerNorm parameters, biases and the outputs stay fp32.
+// The error of this emulation against the fp32 oracle is the yardstick of
+// the bf16 path's tolerances.
+bool g_bf16 = false;
+
+inline float round_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return f;
+  u = ((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16) << 16;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+// Rounds t in place when the emulation is on; returns it.
+Tensor& bf(Tensor& t) {
+  if (g_bf16)
+    for (float& v : t.v) v = round_bf16(v);
+  return t;
+}
+
+// w itself, or with the emulation on a bf16-rounded copy of it held in tmp.
+const Tensor& bf_weights(const Tensor& w, Tensor& tmp) {
+  if (!g_bf16) return w;
+  tmp = w;
+  return bf(tmp);
+}
+
 void trace(const std::string& name, const Tensor& t) {
   if (g_tracing) g_trace[name] = t;
 }
@@ -514,7 +545,7 @@ Tensor avg_pool_3x2(const Tensor& x) {
         d[(long)oy * Wo + ox] = v / 6.0f;
       }
   }
-  return y;
+  return bf(y);
 }
 
 // global_average_pool: mean over the plane (src/cpu/ops.rs:1480-1495).
@@ -538,7 +569,7 @@ Tensor add(const Tensor& a, const Tensor& b) {
   long n = (long)a.count();
 #pragma omp parallel for schedule(static)
   for (long i = 0; i < n; ++i) y.v[i] = a.v[i] + b.v[i];
-  return y;
+  return bf(y);
 }
 
 // x * gate[n, c] (plain SE, src/cpu/model.rs:487-492).
@@ -549,7 +580,7 @@ Tensor mul_gate(const Tensor& x, const Tensor& g) {
 #pragma omp parallel for schedule(static)
   for (long p = 0; p < planes; ++p)
     for (long i = 0; i < plane; ++i) y.v[p * plane + i] = x.v[p * plane + i] * g.v[p];
-  return y;
+  return bf(y);
 }
 
 // into_residual_mul (src/cpu/backend.rs:180-199).
@@ -560,7 +591,7 @@ Tensor residual_mul_gate(const Tensor& x, const Tensor& g) {
 #pragma omp parallel for schedule(static)
   for (long p = 0; p < planes; ++p)
     for (long i = 0; i < plane; ++i) y.v[p * plane + i] = residual_mul(x.v[p * plane + i], g.v[p]);
-  return y;
+  return bf(y);
 }
 
 // upsample_add_nchw: feature[y][x] += upper[y/s][x/s] (src/cpu/model.rs:1265-1320).
@@ -575,7 +606,7 @@ Tensor upsample_add(Tensor feature, const Tensor& upper, int s) {
     for (int y = 0; y < H; ++y)
       for (int x = 0; x < W; ++x)
         feature.v[(p * H + y) * W + x] += upper.v[(p * uh + y / s) * uw + x / s];
-  return feature;
+  return bf(feature);
 }
 
 // upsample_and_cat_nchw: nearest integer upsample then channel concat
@@ -608,7 +639,9 @@ Tensor upsample_cat(const std::vector<Tensor>& fs, const std::vector<int>& scale
 
 // Linear::run: y = x W^T + b, optional activation / row softmax
 // (src/cpu/backend.rs:1292-1370).
-Tensor linear(const Tensor& x, const Tensor& W, const Tensor* b, int act, bool softmax) {
+Tensor linear(const Tensor& x, const Tensor& W_, const Tensor* b, int act, bool softmax) {
+  Tensor tmp;
+  const Tensor& W = bf_weights(W_, tmp);
   int K = W.shape[1], M = W.shape[0];
   ENSURE(x.shape.back() == K, "Linear input feature count");
   long rows = (long)x.count() / K;
@@ -627,7 +660,7 @@ Tensor linear(const Tensor& x, const Tensor& W, const Tensor* b, int act, bool s
     }
     if (softmax) softmax_row(yo, M);
   }
-  return y;
+  return softmax ? y : bf(y);
 }
 
 Tensor layer_norm(const Tensor& x, const Tensor& w, const Tensor& b, float eps) {
@@ -636,7 +669,7 @@ Tensor layer_norm(const Tensor& x, const Tensor& w, const Tensor& b, float eps) 
   long rows = (long)x.count() / F;
 #pragma omp parallel for schedule(static)
   for (long r = 0; r < rows; ++r) layer_norm_row(y.data() + r * F, w.data(), b.data(), F, eps);
-  return y;
+  return bf(y);
 }
 
 // ---------------------------------------------------------------- layers
@@ -662,8 +695,15 @@ struct Conv {
   std::vector<float> b;
   int sh = 1, sw = 1, pads[4] = {0, 0, 0, 0}, groups = 1;
   int act = ACT_NONE;
+  bool fp32_only = false;  // SE 1x1 convs: fp32 weights and outputs in every plan
   Tensor forward(const Tensor& x, int a = -1) const {
-    return conv2d(x, W, b.empty() ? nullptr : b.data(), sh, sw, pads, groups, a < 0 ? act : a);
+    // Matrix-core layers (dense convs, depthwise 5x5 and wider) take bf16
+    // weights in a bf16 plan.
+    const bool mfma = groups == 1 || (W.shape[2] >= 5 && W.shape[3] >= 5);
+    Tensor tmp;
+    const Tensor& w = !fp32_only && mfma ? bf_weights(W, tmp) : W;
+    Tensor y = conv2d(x, w, b.empty() ? nullptr : b.data(), sh, sw, pads, groups, a < 0 ? act : a);
+    return fp32_only ? y : bf(y);
   }
 };
 
@@ -695,6 +735,8 @@ struct SE {
   Conv reduce, expand;
   int gate_act = ACT_HSIG6;
   Tensor gate(const Tensor& x) const {
+    const_cast<Conv&>(reduce).fp32_only = true;
+    const_cast<Conv&>(expand).fp32_only = true;
     Tensor pooled = global_mean(x);
     Tensor r = reduce.forward(pooled, ACT_RELU);
     Tensor e = expand.forward(r, ACT_NONE);
@@ -1107,7 +1149,8 @@ struct DetHead {
   Tensor forward(const Tensor& x) const {
     Tensor d = down.forward(x);
     trace("head.down", d);
-    Tensor u = conv_transpose2x2(d, upW, upb.data());
+    Tensor tmp;
+    Tensor u = conv_transpose2x2(d, bf_weights(upW, tmp), upb.data());
     act_in_place(u, ACT_RELU);
     trace("head.up", u);
     Tensor f = conv_transpose2x2(u, finW, finb.data());
@@ -1200,7 +1243,7 @@ struct RecBlock {
           }
         }
       }
-    return linear(out, projW, &projB, ACT_NONE, false);
+    return linear(bf(out), projW, &projB, ACT_NONE, false);
   }
   Tensor forward(const Tensor& x) const {
     Tensor n1 = layer_norm(x, ln1w, ln1b, 1e-6f);
@@ -1265,6 +1308,7 @@ struct Recognizer : Model {
           v = v + res.v[((size_t)n * Hc + c) * T + t];
         }
     if (skip_first) seq = layer_norm(seq, normW, normB, 1e-6f);
+    bf(seq);  // stored in bf16 by a bf16 plan
     trace("svtr.encoder", seq);
     return linear(seq, clsW, &clsB, ACT_NONE, true);
   }
@@ -1462,6 +1506,7 @@ void oracle_model_free(void* m) { delete static_cast<Model*>(m); }
 // run while it is set; tracing keeps the tensors of the last forward.
 int oracle_fault_count(void) { return FAULT_COUNT; }
 void oracle_set_fault(int f) { g_fault = f; }
+void oracle_set_bf16(int on) { g_bf16 = on != 0; }
 void oracle_set_tracing(int on) {
   g_tracing = on != 0;
   g_trace.clear();
@@ -1494,6 +1539,7 @@ int oracle_forward(void* handle, const float* in, const int shape[4], float* out
     }
     Tensor x({shape[0], shape[1], shape[2], shape[3]});
     memcpy(x.data(), in, x.count() * 4);
+    bf(x);  // a bf16 plan stores its input in bf16
     Tensor y = m->forward(x);
     ENSURE(y.count() <= cap, "output buffer too small");
     memcpy(out, y.data(), y.count() * 4);

@@ -364,3 +364,11 @@ def traced(name):
     out = np.empty(n, dtype=np.float32)
     fn(name.encode(), _f(out), n, _i(shape))
     return out.reshape([int(d) for d in shape if d > 0])
+
+
+def set_bf16(on):
+    """bf16 storage emulation for models run afterwards: the tensors a bf16
+    plan stores, and its matrix-core weights, rounded to bf16 (tests only)."""
+    L = lib()
+    L.oracle_set_bf16.argtypes = [ctypes.c_int]
+    L.oracle_set_bf16(int(bool(on)))

@@ -375,3 +375,23 @@ def test_identity_geometry_preprocess_equals_pixel_normalisation():
     rgb = seeded.seeded_rgb(32, 64, 9)
     got = oracle.preprocess(rgb, [[0, 0], [64, 0], [64, 32], [0, 32]], 64, 32, 64, True)
     assert np.array_equal(got, seeded.normalize_identity(rgb, True))
+
+
+def test_bf16_emulation_rounds_and_resets():
+    # The bf16 storage emulation moves the output by the size of bf16
+    # rounding (not zero, far below the signal) and is off again afterwards.
+    import seeded
+    from helpers import model_path
+
+    x = seeded.seeded_batch(1, 64, 96, 3)
+    path = model_path("det", "tiny")
+    ref = oracle.Model("det", path, "tiny").forward(x)
+    oracle.set_bf16(True)
+    try:
+        emu = oracle.Model("det", path, "tiny").forward(x)
+    finally:
+        oracle.set_bf16(False)
+    again = oracle.Model("det", path, "tiny").forward(x)
+    d = np.abs(emu - ref)
+    assert 1e-4 < d.max() < 0.2 and d.mean() < 2e-2
+    assert np.array_equal(again, ref)
