@@ -117,13 +117,23 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
     const int c = ch0 + c4 * 4;
     const bool cok = c < p.C;
     const T* base = in + (size_t)n * p.H * p.W * p.in_ps + c;
-    for (int px = tid / C4B; px < IH * IW; px += 256 / C4B) {
+    // All of this lane's loads are issued before the first LDS store.
+    constexpr int STEP = 256 / C4B, NL = (IH * IW + STEP - 1) / STEP;
+    float4 v[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int px = tid / C4B + i * STEP;
       const int iy = px / IW, ix = px - iy * IW;
       const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
-      float4 v = f4_zero();
-      if (cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W)
-        v = ld4<T>(base + ((size_t)gy * p.W + gx) * p.in_ps);
-      tile[(iy * IWP + ix) * C4B + c4] = v;
+      v[i] = f4_zero();
+      if (px < IH * IW && cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W)
+        v[i] = ld4<T>(base + ((size_t)gy * p.W + gx) * p.in_ps);
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int px = tid / C4B + i * STEP;
+      const int iy = px / IW, ix = px - iy * IW;
+      if (px < IH * IW) tile[(iy * IWP + ix) * C4B + c4] = v[i];
     }
   }
   for (int i = tid; i < KH * KW * C4B; i += 256) {
@@ -862,35 +872,56 @@ void launch_nchw_to_nhwc4(const float* in, void* out, int N, int H, int W, int d
 // Max pool 2x2 / stride 1 / pads (0,0,1,1) of the large stem
 // (src/cpu/model.rs:689, src/cpu/ops.rs:1520-1535); fmaxf ignores NaN like
 // f32::max.
+// 2x2 stride-1 max pool whose windows past the bottom / right edge are
+// clipped (pads 0,0,1,1; NaN-ignoring max as f32::max).  A lane computes
+// MP_R output rows of one pixel column and four channels: it loads the
+// MP_R + 1 input rows it needs (two pixels each) once, all before its first
+// store, and reuses each row's pair maximum for the two outputs that share it
+// (every input row is read by one strip, plus the strip above at its edge,
+// instead of by four windows).
+constexpr int MP_R = 4;
+
 template <typename T>
-__global__ void maxpool_same_kernel(const T* in, int N, int H, int W, int C, int in_ps, T* out, int out_ps) {
+__global__ void maxpool_same_kernel(const T* __restrict__ in, int N, int H, int W, int C, int in_ps,
+                                    T* __restrict__ out, int out_ps) {
   const int C4 = C >> 2;
-  long idx = (long)blockIdx.x * 256 + threadIdx.x;
-  long total = (long)N * H * W * C4;
+  const int strips = (H + MP_R - 1) / MP_R;
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  const long total = (long)N * strips * W * C4;
   if (idx >= total) return;
-  int c = (int)(idx % C4) * 4;
-  long pix = idx / C4;
-  int x = (int)(pix % W);
-  long t = pix / W;
-  int y = (int)(t % H);
-  int n = (int)(t / H);
-  float4 m = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-  for (int dy = 0; dy < 2; ++dy)
-    for (int dx = 0; dx < 2; ++dx) {
-      int iy = y + dy, ix = x + dx;
-      if (iy >= H || ix >= W) continue;
-      float4 v = ld4<T>(in + ((size_t)(n * H + iy) * W + ix) * in_ps + c);
-      m.x = fmaxf(m.x, v.x);
-      m.y = fmaxf(m.y, v.y);
-      m.z = fmaxf(m.z, v.z);
-      m.w = fmaxf(m.w, v.w);
+  const int c = (int)(idx % C4) * 4;
+  long t = idx / C4;
+  const int x = (int)(t % W);
+  t /= W;
+  const int s = (int)(t % strips);
+  const int n = (int)(t / strips);
+  const int y0 = s * MP_R;
+  const bool right = x + 1 < W;
+  float4 rm[MP_R + 1];  // pair maximum of rows y0 .. y0 + MP_R (rows past H unused)
+#pragma unroll
+  for (int r = 0; r <= MP_R; ++r) {
+    const int y = y0 + r;
+    rm[r] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    if (y < H) {
+      const T* px = in + ((size_t)(n * H + y) * W + x) * in_ps + c;
+      const float4 a = ld4<T>(px);
+      const float4 b = right ? ld4<T>(px + in_ps) : a;
+      rm[r] = make_float4(fmaxf(a.x, b.x), fmaxf(a.y, b.y), fmaxf(a.z, b.z), fmaxf(a.w, b.w));
     }
-  st4<T>(out + (size_t)pix * out_ps + c, m);
+  }
+#pragma unroll
+  for (int r = 0; r < MP_R; ++r) {
+    const int y = y0 + r;
+    if (y >= H) break;
+    const float4 a = rm[r], b = rm[r + 1];  // rm[r + 1] is -inf past the last row
+    st4<T>(out + ((size_t)(n * H + y) * W + x) * out_ps + c,
+           make_float4(fmaxf(a.x, b.x), fmaxf(a.y, b.y), fmaxf(a.z, b.z), fmaxf(a.w, b.w)));
+  }
 }
 
 void launch_maxpool_same(const void* in, int N, int H, int W, int C, int in_ps, void* out, int out_ps, int dt,
                          hipStream_t s) {
-  long total = (long)N * H * W * (C / 4);
+  const long total = (long)N * ((H + MP_R - 1) / MP_R) * W * (C / 4);
   DISPATCH_DT(dt, hipLaunchKernelGGL(maxpool_same_kernel<T>, dim3(blocks_for(total)), dim3(256), 0, s,
                                      static_cast<const T*>(in), N, H, W, C, in_ps, static_cast<T*>(out), out_ps));
 }
