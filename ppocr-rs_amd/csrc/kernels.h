@@ -284,7 +284,9 @@ struct PreParams {
   const int* content_w;
   int N, cw, ch;
   float scale[3], bias[3];
-  float* out;
+  float* out;     // fp32 NCHW planes [N][3][ch][cw], or
+  void* nhwc4;    // (when set) the model input [N][ch][cw][4] in type `dt`, channel 3 zero
+  int dt;
 };
 void launch_preprocess(const PreParams& p, hipStream_t s);
 

@@ -7,6 +7,7 @@
 // segments: every global access of these kernels is coalesced.  Arithmetic
 // is fp32 for both storage types.
 #include <cstring>
+#include <type_traits>
 
 #include "device_math.h"
 
@@ -1328,6 +1329,10 @@ void launch_ctc_merge(const float* part, int M, int n_tiles, float* out, hipStre
 // clamped; v * (1/(255 std)) - mean/std as BGR planes; zero past
 // content_width.  Contraction is off so every product and sum rounds as in
 // the reference.
+// NHWC4 (T non-void): the pixel's four channels (B, G, R, 0) go straight to
+// the model input in its storage type, the values the fp32 planes would
+// hold after nchw_to_nhwc4_kernel.
+template <typename T>
 __global__ void preprocess_kernel(PreParams p) {
 #pragma clang fp contract(off)
   long idx = (long)blockIdx.x * 256 + threadIdx.x;
@@ -1368,15 +1373,22 @@ __global__ void preprocess_kernel(PreParams p) {
     g = rgb[1] * p.scale[1] + p.bias[1];
     rr = rgb[0] * p.scale[2] + p.bias[2];
   }
-  float* o = p.out + (size_t)n * 3 * plane + r;
-  o[0] = b;
-  o[plane] = g;
-  o[2 * plane] = rr;
+  if constexpr (std::is_void_v<T>) {
+    float* o = p.out + (size_t)n * 3 * plane + r;
+    o[0] = b;
+    o[plane] = g;
+    o[2 * plane] = rr;
+  } else {
+    st4<T>(static_cast<T*>(p.nhwc4) + (size_t)idx * 4, make_float4(b, g, rr, 0.0f));
+  }
 }
 
 void launch_preprocess(const PreParams& p, hipStream_t s) {
   long total = (long)p.N * p.ch * p.cw;
-  hipLaunchKernelGGL(preprocess_kernel, dim3(blocks_for(total)), dim3(256), 0, s, p);
+  if (!p.nhwc4)
+    hipLaunchKernelGGL(preprocess_kernel<void>, dim3(blocks_for(total)), dim3(256), 0, s, p);
+  else
+    DISPATCH_DT(p.dt, hipLaunchKernelGGL(preprocess_kernel<T>, dim3(blocks_for(total)), dim3(256), 0, s, p));
 }
 
 }  // namespace ppocr

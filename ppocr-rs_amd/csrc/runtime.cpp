@@ -77,10 +77,14 @@ struct ppocr_hip_model {
   std::string weights_path;
   int size = 0;
   hipGraphExec_t graph = nullptr;
+  // The plan without its first op (the NCHW -> NHWC4 input conversion), for
+  // inputs that device preprocessing writes as NHWC4 directly.
+  hipGraphExec_t image_graph = nullptr;
   uint64_t graph_generation = UINT64_MAX;
   std::shared_ptr<ppocr::DeviceBuffer> db_work;  // postprocess work arrays, grown on demand
   ~ppocr_hip_model() {
     if (graph) (void)hipGraphExecDestroy(graph);
+    if (image_graph) (void)hipGraphExecDestroy(image_graph);
   }
 };
 
@@ -121,34 +125,49 @@ Exec exec_of(ppocr_hip_model* m) {
   return ex;
 }
 
-void launch_all(ppocr_hip_model* m, hipStream_t s) {
+void launch_all(ppocr_hip_model* m, hipStream_t s, size_t first = 0) {
   Exec ex = exec_of(m);
-  for (const Op& op : m->plan.ops) op.launch(ex, s);
+  for (size_t i = first; i < m->plan.ops.size(); ++i) m->plan.ops[i].launch(ex, s);
 }
 
-// Captures the launch list into a graph if the arena moved since the last
-// capture (caller holds ctx->mu and has sized the arena).
-void ensure_graph(ppocr_hip_model* m) {
+// Whether the plan starts with the NCHW -> NHWC4 input conversion, which
+// device preprocessing can do itself.
+bool direct_input(const ppocr_hip_model* m) { return !m->plan.ops.empty() && m->plan.ops[0].name == "input"; }
+
+// Captures the launch list from op `first` on into an instantiated graph.
+hipGraphExec_t capture(ppocr_hip_model* m, size_t first) {
   ppocr_hip_ctx* ctx = m->ctx;
-  if (m->graph && m->graph_generation == ctx->generation) return;
-  if (m->graph) {
-    HIP_OK(hipGraphExecDestroy(m->graph));
-    m->graph = nullptr;
-  }
   hipGraph_t graph = nullptr;
-  // Queued work of other models may still be pending on the stream (the
-  // engine's batch queue): let it drain so the capture starts from an idle stream.
-  HIP_OK(hipStreamSynchronize(ctx->stream));
   HIP_OK(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-  launch_all(m, ctx->stream);
+  launch_all(m, ctx->stream, first);
   hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
   if (e != hipSuccess) {
     (void)hipGetLastError();
     raise(PPOCR_ERR_GPU, std::string("graph capture failed: ") + hipGetErrorString(e));
   }
-  hipError_t ie = hipGraphInstantiate(&m->graph, graph, nullptr, nullptr, 0);
+  hipGraphExec_t exec = nullptr;
+  hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
   (void)hipGraphDestroy(graph);
   if (ie != hipSuccess) raise(PPOCR_ERR_GPU, std::string("graph instantiate failed: ") + hipGetErrorString(ie));
+  return exec;
+}
+
+// Captures the launch list into a graph (and the list without its input
+// conversion into the image graph) if the arena moved since the last
+// capture (caller holds ctx->mu and has sized the arena).
+void ensure_graph(ppocr_hip_model* m) {
+  ppocr_hip_ctx* ctx = m->ctx;
+  if (m->graph && m->graph_generation == ctx->generation) return;
+  for (hipGraphExec_t* g : {&m->graph, &m->image_graph})
+    if (*g) {
+      HIP_OK(hipGraphExecDestroy(*g));
+      *g = nullptr;
+    }
+  // Queued work of other models may still be pending on the stream (the
+  // engine's batch queue): let it drain so the capture starts from an idle stream.
+  HIP_OK(hipStreamSynchronize(ctx->stream));
+  m->graph = capture(m, 0);
+  if (direct_input(m)) m->image_graph = capture(m, 1);
   m->graph_generation = ctx->generation;
 }
 
@@ -176,6 +195,8 @@ float* staging_ptr(ppocr_hip_model* m) {
 float* output_ptr(ppocr_hip_model* m) {
   return reinterpret_cast<float*>(m->ctx->arena + m->plan.bufs[m->plan.output].arena_off);
 }
+// Device pointer of the plan's NHWC4 model input.
+void* input_ptr(ppocr_hip_model* m) { return exec_of(m).ptr(m->plan.input); }
 
 // Copies the NCHW input items of chunk c into the staging buffer.
 void upload_chunk(ppocr_hip_model* m, const float* nchw, size_t c) {
@@ -184,6 +205,12 @@ void upload_chunk(ppocr_hip_model* m, const float* nchw, size_t c) {
 }
 
 void run_graph(ppocr_hip_model* m) { HIP_OK(hipGraphLaunch(m->graph, m->ctx->stream)); }
+// Runs the plan on an input that preprocess_chunk / enqueue_forward_image
+// wrote: NHWC4 when the plan allows it (the image graph), else the staging
+// planes (the whole graph).
+void run_image_graph(ppocr_hip_model* m) {
+  HIP_OK(hipGraphLaunch(m->image_graph ? m->image_graph : m->graph, m->ctx->stream));
+}
 
 void check_output_cap(ppocr_hip_model* m, const float* out, size_t cap) {
   const size_t n = output_elems(m);
@@ -411,7 +438,7 @@ namespace {
 // memory: corners [n][8] floats, then content widths [n] ints.  Caller holds
 // ctx->mu.
 void enqueue_preprocess(ppocr_hip_ctx* ctx, const ppocr_hip_image* image, const void* geo, int n, int cw, int ch,
-                        bool detector, float* dst) {
+                        bool detector, float* dst, void* nhwc4 = nullptr, int dt = DT_F32) {
   static const float det_mean[3] = {0.485f, 0.456f, 0.406f}, det_std[3] = {0.229f, 0.224f, 0.225f};
   static const float rec_mean[3] = {0.5f, 0.5f, 0.5f}, rec_std[3] = {0.5f, 0.5f, 0.5f};
   const float* mean = detector ? det_mean : rec_mean;
@@ -430,6 +457,8 @@ void enqueue_preprocess(ppocr_hip_ctx* ctx, const ppocr_hip_image* image, const 
     p.bias[c] = -mean[c] / stdv[c];
   }
   p.out = dst;
+  p.nhwc4 = nhwc4;
+  p.dt = dt;
   launch_preprocess(p, ctx->stream);
   HIP_OK(hipGetLastError());
 }
@@ -466,24 +495,28 @@ void ensure_geometry(ppocr_hip_ctx* ctx, size_t bytes) {
 // it: the geometry goes through the context's geometry buffer, which the
 // next call may overwrite.  Caller holds ctx->mu.
 void run_preprocess(ppocr_hip_ctx* ctx, const ppocr_hip_image* image, const float* corners, const int* content_w,
-                    int n, int cw, int ch, bool detector, float* dst) {
+                    int n, int cw, int ch, bool detector, float* dst, void* nhwc4 = nullptr, int dt = DT_F32) {
   const size_t bytes = packet_bytes((size_t)n);
   ensure_geometry(ctx, bytes);
   std::vector<char> host(bytes);
   pack_geometry(host.data(), corners, content_w, (size_t)n);
   HIP_OK(hipMemcpyAsync(ctx->geo, host.data(), bytes, hipMemcpyHostToDevice, ctx->stream));
-  enqueue_preprocess(ctx, image, ctx->geo, n, cw, ch, detector, dst);
+  enqueue_preprocess(ctx, image, ctx->geo, n, cw, ch, detector, dst, nhwc4, dt);
   // `host` is pageable and goes out of scope here.
   HIP_OK(hipStreamSynchronize(ctx->stream));
 }
 
-// Preprocesses chunk c of a model's image batch into its staging buffer and
-// waits for it.  Caller holds ctx->mu.
+// Preprocesses chunk c of a model's image batch and waits for it: into the
+// NHWC4 model input when the plan starts with the input conversion (run
+// the image graph next), else into the staging planes.  Caller holds
+// ctx->mu and has run ensure_graph.
 void preprocess_chunk(ppocr_hip_model* m, const ppocr_hip_image* image, const float* corners, const int* content_w,
                       size_t c) {
   const size_t first = c * m->chunk;
+  const bool direct = m->image_graph != nullptr;
   run_preprocess(m->ctx, image, corners + first * 8, content_w + first, (int)chunk_items(m, c), (int)m->in_shape[3],
-                 (int)m->in_shape[2], m->plan.detector, staging_ptr(m));
+                 (int)m->in_shape[2], m->plan.detector, direct ? nullptr : staging_ptr(m),
+                 direct ? input_ptr(m) : nullptr, m->plan.input.dt);
 }
 
 std::vector<int> content_widths(const size_t* widths, size_t n, size_t canvas) {
@@ -529,9 +562,11 @@ void enqueue_forward_image(ppocr_hip_model* model, const ppocr_hip_image* image,
   for (size_t c = 0; c < n_chunks(model); ++c) {
     const size_t items = chunk_items(model, c);
     upload_geometry_slice(ctx, packet, n, c * model->chunk, items);
+    const bool direct = model->image_graph != nullptr;
     enqueue_preprocess(ctx, image, ctx->geo, (int)items, (int)model->in_shape[3], (int)model->in_shape[2],
-                       model->plan.detector, staging_ptr(model));
-    run_graph(model);
+                       model->plan.detector, direct ? nullptr : staging_ptr(model),
+                       direct ? input_ptr(model) : nullptr, model->plan.input.dt);
+    run_image_graph(model);
     download_chunk(model, out, c);
   }
 }
@@ -559,10 +594,10 @@ ppocr_status ppocr_hip_forward_image(ppocr_hip_model* model, const ppocr_hip_ima
     HIP_OK(hipSetDevice(model->ctx->device));
     ensure_arena(model->ctx, model->plan.arena_bytes);
     ensure_graph(model);
-    // Preprocess straight into the NCHW staging buffer the graph starts from.
+    // Preprocess straight into the model input the image graph starts from.
     for (size_t c = 0; c < n_chunks(model); ++c) {
       preprocess_chunk(model, image, corners, cw.data(), c);
-      run_graph(model);
+      run_image_graph(model);
       download_chunk(model, out, c);
     }
     finish_output(model, out);
@@ -1013,7 +1048,7 @@ ppocr_status ppocr_hip_detect_image(ppocr_hip_model* model, const ppocr_hip_imag
     std::vector<std::vector<HostDetection>> per;
     for (size_t c = 0; c < n_chunks(model); ++c) {
       preprocess_chunk(model, image, corners, cw.data(), c);
-      run_graph(model);
+      run_image_graph(model);
       const int items = (int)chunk_items(model, c);
       char* base = db_work(model->ctx, model->db_work, db_layout(items, (int)s[2], (int)s[3]).bytes);
       auto part = run_db(model->ctx, output_ptr(model), items, (int)s[2], (int)s[3], transforms + c * model->chunk, o,

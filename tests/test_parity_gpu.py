@@ -226,6 +226,32 @@ def test_detector_forward_image_matches_host_preprocess(gpu):
         det.close()
 
 
+@pytest.mark.parametrize("precision", ["f32", "bf16"])
+@pytest.mark.parametrize("kind", ["det", "rec"])
+def test_forward_image_equals_forward_of_device_preprocess(gpu, kind, precision):
+    """Device preprocessing writes the model input (NHWC4, activation type)
+    itself and the plan skips its input conversion: the result must be the
+    forward pass of the preprocessed planes, bit for bit."""
+    img = seeded.seeded_rgb(300, 500, 41, pattern="blocks")
+    quads = np.stack([quad_corners(0, 0, 500, 300), np.array([[40, 30], [420, 50], [410, 260], [30, 240]], np.float32)])
+    if kind == "det":
+        h, w, widths = 64, 96, None
+        model = ppocr_hip.Detector.load(gpu, model_path("det", "tiny"), "tiny", (2, 3, h, w), precision=precision)
+    else:
+        h, w, widths = 48, 128, [128, 72]
+        model = ppocr_hip.Recognizer.load(gpu, model_path("rec", "tiny"), "tiny", (2, 3, h, w), precision=precision)
+    image = gpu.upload_rgb(img)
+    try:
+        got = model.forward_image(image, quads, widths).array()
+        x = np.stack([gpu.preprocess(image, q, w, h, None if widths is None else widths[i], kind == "det")
+                      for i, q in enumerate(quads)])
+        want = model.forward(x).array()
+        assert np.array_equal(got, want)
+    finally:
+        image.close()
+        model.close()
+
+
 def test_recognizer_forward_image_batched_crops(gpu):
     img = seeded.seeded_rgb(300, 500, 33, pattern="blocks")
     quads = np.stack([quad_corners(10, 20, 210, 60), quad_corners(100, 100, 180, 120),
