@@ -135,6 +135,15 @@ struct PairParams {
   int residual;
   float* out;
   int out_ps;
+  // Depthwise prologue (dw_in set, no gate): the pair's input x is the 3x3
+  // depthwise conv of dw_in [N][dw_h][dw_w] (pixel stride dw_ps), weights
+  // [9][C], bias [C], stride (dw_sh, dw_sw), pads (dw_pt, dw_pl), no
+  // activation, computed per tile and never stored; the pair's pixel grid
+  // is HW pixels per image, dw_wo of them per row.
+  const float* dw_in;
+  int dw_ps, dw_h, dw_w, dw_wo, dw_sh, dw_sw, dw_pt, dw_pl;
+  const float* dw_wt;
+  const float* dw_b;
 };
 bool pointwise_pair_supported(int C, int H2, int Co, int dt);
 

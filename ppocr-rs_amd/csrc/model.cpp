@@ -417,38 +417,54 @@ class Builder {
 
   // The LCNet pointwise pair as one fused op (pair_gemm.hip): channel_conv1
   // (GELU) and channel_conv2 with the hidden tile on chip; `gate` is the SE
-  // gate of x (or null) and `residual` adds the gated x.
+  // gate of x (or null) and `residual` adds the gated x.  With `dw` (no
+  // gate), x is the input of the block's 3x3 depthwise token conv `dw`,
+  // which the op computes per tile instead of reading its stored output.
   View pointwise_pair(const View& x, const ConvW& w1, const ConvW& w2, const View* gate, bool residual,
-                      const std::string& name) {
+                      const std::string& name, const DwW* dw = nullptr) {
+    if (dw && (gate || dw->kh != 3 || dw->kw != 3 || dw->c != x.c))
+      raise(PPOCR_ERR_INVALID_MODEL, name + ": depthwise prologue needs an ungated 3x3 depthwise");
+    const int h = dw ? (x.h + dw->pt + dw->pb - 3) / dw->sh + 1 : x.h;
+    const int w = dw ? (x.w + dw->pl + dw->pr - 3) / dw->sw + 1 : x.w;
     if (x.c != w1.ci_pad || w2.ci_pad != w1.co || w1.kh * w1.kw * w2.kh * w2.kw != 1)
       raise(PPOCR_ERR_INVALID_MODEL, name + ": pointwise pair shapes do not chain");
     if (residual && w2.co != x.c) raise(PPOCR_ERR_INVALID_MODEL, name + ": residual needs equal channel counts");
-    View out = alloc(x.n, x.h, x.w, w2.co, name);
+    View out = alloc(x.n, h, w, w2.co, name);
     View in = x;
     View g = gate ? *gate : View();
     const bool has_gate = gate;
     PairParams base{};
     base.in_ps = x.ps;
-    base.HW = x.h * x.w;
-    base.M = (int)x.pixels();
+    base.HW = h * w;
+    base.M = x.n * h * w;
     base.C = x.c, base.H2 = w1.co, base.Co = w2.co;
     base.ldw1 = w1.ldw, base.ldw2 = w2.ldw;
     base.residual = residual;
     base.out_ps = out.ps;
+    if (dw) {
+      base.dw_ps = x.ps, base.dw_h = x.h, base.dw_w = x.w, base.dw_wo = w;
+      base.dw_sh = dw->sh, base.dw_sw = dw->sw, base.dw_pt = dw->pt, base.dw_pl = dw->pl;
+    }
     const size_t w1o = w1.w, b1o = w1.b, w2o = w2.w, b2o = w2.b;
+    const size_t dwo = dw ? dw->w : NOW, dbo = dw ? dw->b : NOW;
+    const bool has_dw = dw;
     Op op;
     op.name = name;
-    op.kernel = std::string("pointwise_pair") + (has_gate ? "<gate>" : "");
+    op.kernel = std::string("pointwise_pair") + (has_gate ? "<gate>" : has_dw ? "<dw3x3>" : "");
     op.bound = 1;
-    const double M = (double)x.pixels();
-    op.flops = 2.0 * M * ((double)x.c * w1.co + (double)w1.co * w2.co);
-    op.bytes = 4.0 * (M * x.c + (double)x.c * w1.co + (double)w1.co * w2.co + M * w2.co);
+    const double M = (double)base.M;
+    op.flops = 2.0 * M * ((double)x.c * w1.co + (double)w1.co * w2.co + (has_dw ? 9.0 * x.c : 0.0));
+    op.bytes = 4.0 * ((double)x.pixels() * x.c + (double)x.c * w1.co + (double)w1.co * w2.co + M * w2.co +
+                      (has_dw ? 10.0 * x.c : 0.0));
     op.reads = {x.buf};
     if (has_gate) op.reads.push_back(g.buf);
     op.writes = {out.buf};
     op.launch = [=](const Exec& ex, hipStream_t s) {
       PairParams p = base;
-      p.in = ex.fptr(in);
+      p.in = has_dw ? nullptr : ex.fptr(in);
+      p.dw_in = has_dw ? ex.fptr(in) : nullptr;
+      p.dw_wt = ex.w(dwo);
+      p.dw_b = ex.w(dbo);
       p.gate = has_gate ? ex.fptr(g) : nullptr;
       p.w1 = ex.w(w1o);
       p.b1 = ex.w(b1o);
@@ -767,6 +783,12 @@ View lcnet_block(Builder& B, const View& x, const std::string& p, BlockSpec s) {
   DwW tw = residual ? B.dw_w(p + ".token_conv", s.ci, 3, 3, s.sh, s.sw, {1, 1, 1, 1}, true)
                     : B.dw_w(p + ".token_conv", s.ci, 3, 3, s.sh, s.sw, {1, 1, 1, 1}, false, "normalization");
   bool has_se = s.se;
+  ConvW c1 = B.conv_w(p + ".channel_conv1", s.ci, 2 * s.ci, 1, 1, 1, 1, {0, 0, 0, 0}, false, "normalization");
+  ConvW c2 = B.conv_w(p + ".channel_conv2", 2 * s.ci, s.co, 1, 1, 1, 1, {0, 0, 0, 0}, false, "normalization");
+  // Without SE the token conv's output feeds only the pair: the pair
+  // computes it per tile (src/cpu/backend.rs:697-816).
+  if (!has_se && pair_fusion_pays(x, s.ci, s.co, B.dt()))
+    return B.pointwise_pair(x, c1, c2, nullptr, residual, p + ".channel_conv", &tw);
   Builder::SePartial sums;
   View t = B.depthwise(x, tw, ACT_NONE, nullptr, p + ".token_conv", has_se ? s.ci / 4 : 0, &sums);
   View gate;
@@ -775,8 +797,6 @@ View lcnet_block(Builder& B, const View& x, const std::string& p, BlockSpec s) {
     SeW sw = B.se_w(q + ".0", q + ".2", s.ci, s.ci / 4, ACT_HSIG6);
     gate = B.se(t, sw, p + ".se", &sums);
   }
-  ConvW c1 = B.conv_w(p + ".channel_conv1", s.ci, 2 * s.ci, 1, 1, 1, 1, {0, 0, 0, 0}, false, "normalization");
-  ConvW c2 = B.conv_w(p + ".channel_conv2", 2 * s.ci, s.co, 1, 1, 1, 1, {0, 0, 0, 0}, false, "normalization");
   if (pair_fusion_pays(t, s.ci, s.co, B.dt()))
     return B.pointwise_pair(t, c1, c2, has_se ? &gate : nullptr, residual, p + ".channel_conv");
   Epi e1;

@@ -231,6 +231,51 @@ int ppocr_probe_pointwise_pair(const float* x, int m, int hw, int c, const float
   return rc;
 }
 
+// Fused 3x3 depthwise -> pointwise pair (the pair kernel's depthwise
+// prologue) on host arrays: x [n][h][w][c], dw [9][c] taps, dwb [c], stride
+// (sh, sw), pads 1; then as ppocr_probe_pointwise_pair on the depthwise
+// output (never stored) without a gate; out [n][ho][wo][co].  Returns 0, or
+// 1 on a HIP error.
+int ppocr_probe_pointwise_pair_dw(const float* x, int n, int h, int w, int c, const float* dw, const float* dwb,
+                                  int sh, int sw, const float* w1, const float* b1, int h2, const float* w2,
+                                  const float* b2, int co, int residual, float* out) {
+  const int ho = (h + 2 - 3) / sh + 1, wo = (w + 2 - 3) / sw + 1;
+  const size_t m = (size_t)n * ho * wo;
+  void* d_in = upload(x, (size_t)n * h * w * c, ppocr::DT_F32);
+  void* d_dw = upload(dw, (size_t)9 * c, ppocr::DT_F32);
+  void* d_dwb = upload(dwb, c, ppocr::DT_F32);
+  void* d_w1 = upload(w1, (size_t)h2 * c, ppocr::DT_F32);
+  void* d_b1 = upload(b1, h2, ppocr::DT_F32);
+  void* d_w2 = upload(w2, (size_t)co * h2, ppocr::DT_F32);
+  void* d_b2 = upload(b2, co, ppocr::DT_F32);
+  void* d_out = nullptr;
+  int rc = 0;
+  if (!d_in || !d_dw || !d_dwb || !d_w1 || !d_b1 || !d_w2 || !d_b2 || hipMalloc(&d_out, m * co * 4) != hipSuccess ||
+      !ppocr::pointwise_pair_supported(c, h2, co, 0)) {
+    rc = 1;
+  } else {
+    ppocr::PairParams p{};
+    p.HW = ho * wo;
+    p.M = (int)m, p.C = c, p.H2 = h2, p.Co = co;
+    p.w1 = static_cast<const float*>(d_w1), p.ldw1 = c, p.b1 = static_cast<const float*>(d_b1);
+    p.w2 = static_cast<const float*>(d_w2), p.ldw2 = h2, p.b2 = static_cast<const float*>(d_b2);
+    p.residual = residual;
+    p.out = static_cast<float*>(d_out);
+    p.out_ps = co;
+    p.dw_in = static_cast<const float*>(d_in);
+    p.dw_ps = c, p.dw_h = h, p.dw_w = w, p.dw_wo = wo, p.dw_sh = sh, p.dw_sw = sw, p.dw_pt = 1, p.dw_pl = 1;
+    p.dw_wt = static_cast<const float*>(d_dw);
+    p.dw_b = static_cast<const float*>(d_dwb);
+    ppocr::launch_pointwise_pair(p, nullptr);
+    if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(out, d_out, m * co * 4, hipMemcpyDeviceToHost) != hipSuccess)
+      rc = 1;
+  }
+  for (void* d : {d_in, d_dw, d_dwb, d_w1, d_b1, d_w2, d_b2, d_out})
+    if (d) (void)hipFree(d);
+  return rc;
+}
+
 // The kernel instance ppocr_probe_depthwise runs.
 const char* ppocr_probe_depthwise_kernel(int h, int c, int k, int dt, int table) {
   return ppocr::depthwise_kernel_name(k, k, 1, 1, h, dt, table != 0, c);

@@ -6,7 +6,9 @@
 //
 // A workgroup owns PB_M consecutive pixels.  Their input rows (C channels,
 // multiplied by the SE gate when the block has one, rounded to fp32 as the
-// unfused gather does) are staged in LDS; the four waves compute the hidden
+// unfused gather does; or, for blocks without SE, computed from the block
+// input by its 3x3 depthwise token conv, the reference's depthwise ->
+// pointwise strip fusion, src/cpu/backend.rs:697-816) are staged in LDS; the four waves compute the hidden
 // tile GELU(x W1^T + b1) on the matrix cores (v_mfma_f32_16x16x4f32), 16
 // hidden channels at a time, into a second LDS tile; then the output tile
 // h W2^T + b2 (+ x for a residual block) from that, 16 output channels at a
@@ -75,7 +77,10 @@ __device__ __forceinline__ void tile_product(const float* src, int lds, const fl
   }
 }
 
-template <bool GATE, bool RES>
+// DW: the input tile is the 3x3 depthwise conv of p.dw_in at the tile's
+// pixels, summed as the depthwise kernels do (taps row-major, one fmaf per
+// tap and channel, zeros for taps in the padding, then the bias).
+template <bool GATE, bool RES, bool DW>
 __global__ __launch_bounds__(256) void pointwise_pair_kernel(PairParams p) {
   extern __shared__ __attribute__((aligned(16))) float sm[];
   const int ldx = p.C + 4, ldh = p.H2 + 4;  // +4 floats: conflict-free 16-byte row reads
@@ -92,7 +97,31 @@ __global__ __launch_bounds__(256) void pointwise_pair_kernel(PairParams p) {
     const int r = i / c4, c = (i - r * c4) * 4;
     const int m = m0 + r;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (m < p.M) {
+    if (DW && m < p.M) {
+      const int n = m / p.HW, rem = m - n * p.HW;
+      const int oy = rem / p.dw_wo, ox = rem - oy * p.dw_wo;
+      const float* img = p.dw_in + (size_t)n * p.dw_h * p.dw_w * p.dw_ps + c;
+#pragma unroll
+      for (int ky = 0; ky < 3; ++ky) {
+        const int iy = oy * p.dw_sh - p.dw_pt + ky;
+#pragma unroll
+        for (int kx = 0; kx < 3; ++kx) {
+          const int ix = ox * p.dw_sw - p.dw_pl + kx;
+          const float4 x = (unsigned)iy < (unsigned)p.dw_h && (unsigned)ix < (unsigned)p.dw_w
+                               ? *reinterpret_cast<const float4*>(img + ((size_t)iy * p.dw_w + ix) * p.dw_ps)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+          const float4 w = *reinterpret_cast<const float4*>(p.dw_wt + (size_t)(ky * 3 + kx) * p.C + c);
+          v.x = fmaf(x.x, w.x, v.x);
+          v.y = fmaf(x.y, w.y, v.y);
+          v.z = fmaf(x.z, w.z, v.z);
+          v.w = fmaf(x.w, w.w, v.w);
+        }
+      }
+      if (p.dw_b) {
+        const float4 b = *reinterpret_cast<const float4*>(p.dw_b + c);
+        v = make_float4(v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w);
+      }
+    } else if (m < p.M) {
       v = *reinterpret_cast<const float4*>(p.in + (size_t)m * p.in_ps + c);
       if constexpr (GATE) {
         const float4 gt = *reinterpret_cast<const float4*>(p.gate + (size_t)(m / p.HW) * p.C + c);
@@ -250,14 +279,19 @@ void launch_pointwise_pair(const PairParams& p, hipStream_t s) {
   const dim3 grid((unsigned)((p.M + PB_M - 1) / PB_M));
   const size_t lds = pointwise_pair_lds(p.C, p.H2);
   const bool gate = p.gate != nullptr, res = p.residual != 0;
-  if (gate && res)
-    hipLaunchKernelGGL((pointwise_pair_kernel<true, true>), grid, dim3(256), lds, s, p);
+  if (p.dw_in) {
+    if (res)
+      hipLaunchKernelGGL((pointwise_pair_kernel<false, true, true>), grid, dim3(256), lds, s, p);
+    else
+      hipLaunchKernelGGL((pointwise_pair_kernel<false, false, true>), grid, dim3(256), lds, s, p);
+  } else if (gate && res)
+    hipLaunchKernelGGL((pointwise_pair_kernel<true, true, false>), grid, dim3(256), lds, s, p);
   else if (gate)
-    hipLaunchKernelGGL((pointwise_pair_kernel<true, false>), grid, dim3(256), lds, s, p);
+    hipLaunchKernelGGL((pointwise_pair_kernel<true, false, false>), grid, dim3(256), lds, s, p);
   else if (res)
-    hipLaunchKernelGGL((pointwise_pair_kernel<false, true>), grid, dim3(256), lds, s, p);
+    hipLaunchKernelGGL((pointwise_pair_kernel<false, true, false>), grid, dim3(256), lds, s, p);
   else
-    hipLaunchKernelGGL((pointwise_pair_kernel<false, false>), grid, dim3(256), lds, s, p);
+    hipLaunchKernelGGL((pointwise_pair_kernel<false, false, false>), grid, dim3(256), lds, s, p);
 }
 
 }  // namespace ppocr

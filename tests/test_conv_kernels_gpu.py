@@ -205,3 +205,53 @@ def test_pointwise_pair_matches_float64(name, m, hw, c, co, gated, residual):
         want = want + xg
     err = np.abs(out - want)
     assert np.all(err <= 1e-4 + 1e-5 * np.abs(want)), f"max err {err.max()}"
+
+
+# (name, n, h, w, c, stride, co, residual): maps whose pixel count is not a
+# multiple of the 32-pixel tile, strides 1 and 2, a tile spanning two images.
+PAIR_DW_CASES = [
+    ("s1 residual", 2, 13, 11, 32, 1, 32, True),
+    ("s1 plain", 1, 9, 20, 16, 1, 48, False),
+    ("s2", 2, 15, 18, 64, 2, 64, False),
+    ("s2 odd", 1, 7, 9, 16, 2, 32, False),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,n,h,w,c,stride,co,residual", PAIR_DW_CASES, ids=[c[0] for c in PAIR_DW_CASES])
+def test_pointwise_pair_depthwise_prologue_matches_float64(name, n, h, w, c, stride, co, residual):
+    from scipy.special import erf
+
+    lib = _lib()
+    f = ctypes.POINTER(ctypes.c_float)
+    i = ctypes.c_int
+    lib.ppocr_probe_pointwise_pair_dw.argtypes = [f, i, i, i, i, f, f, i, i, f, f, i, f, f, i, i, f]
+    lib.ppocr_probe_pointwise_pair_dw.restype = i
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    h2 = 2 * c
+    x = rng.standard_normal((n, h, w, c)).astype(np.float32)
+    dw = (rng.standard_normal((9, c)) / 3).astype(np.float32)
+    dwb = rng.standard_normal(c).astype(np.float32) * 0.1
+    w1 = (rng.standard_normal((h2, c)) / np.sqrt(c)).astype(np.float32)
+    b1 = rng.standard_normal(h2).astype(np.float32) * 0.1
+    w2 = (rng.standard_normal((co, h2)) / np.sqrt(h2)).astype(np.float32)
+    b2 = rng.standard_normal(co).astype(np.float32) * 0.1
+    ho, wo = (h - 1) // stride + 1, (w - 1) // stride + 1
+    out = np.empty((n, ho, wo, co), np.float32)
+    rc = lib.ppocr_probe_pointwise_pair_dw(_ptr(x), n, h, w, c, _ptr(dw), _ptr(dwb), stride, stride, _ptr(w1),
+                                           _ptr(b1), h2, _ptr(w2), _ptr(b2), co, int(residual), _ptr(out))
+    assert rc == 0
+    # float64 3x3 depthwise, pads 1, then the pair.
+    xp = np.pad(x.astype(np.float64), ((0, 0), (1, 1), (1, 1), (0, 0)))
+    t = np.zeros((n, ho, wo, c))
+    for ky in range(3):
+        for kx in range(3):
+            t += xp[:, ky:ky + stride * (ho - 1) + 1:stride, kx:kx + stride * (wo - 1) + 1:stride, :] * dw[ky * 3 + kx]
+    t += dwb
+    hid = t @ w1.T.astype(np.float64) + b1
+    hid = 0.5 * hid * (1.0 + erf(hid / np.sqrt(2.0)))
+    want = hid @ w2.T.astype(np.float64) + b2
+    if residual:
+        want = want + t
+    err = np.abs(out - want)
+    assert np.all(err <= 1e-4 + 1e-5 * np.abs(want)), f"max err {err.max()}"
