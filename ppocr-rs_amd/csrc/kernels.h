@@ -95,6 +95,17 @@ struct DwParams {
   // bf16 matrix-core operand fragments of the taps (depthwise_mfma_table),
   // or null; used when depthwise_uses_mfma() holds for the layer.
   const void* wtab;
+  // Gate-residual prologue (gr_gate set; 5x5, 7x7 and 9x9 stride-1
+  // layers): the conv's input is x = in + in * gr_gate[n] (two roundings,
+  // as gate_residual_kernel) plus, with gr_up, the nearest 2x upsample of
+  // gr_up [N][H/2][W/2] (pixel stride gr_up_ps), rounded to the storage
+  // type; it is formed per tile from `in` and, with gr_out, also stored at
+  // the layer's output pixels (pixel stride gr_out_ps).
+  const float* gr_gate;
+  const void* gr_up;
+  int gr_up_ps;
+  void* gr_out;
+  int gr_out_ps;
 };
 
 // Squeeze-excitation gate: g[n, c] = gate_act(W2 relu(W1 mean(x) + b1) + b2).
@@ -115,6 +126,10 @@ struct SeParams {
 };
 
 void launch_conv(const ConvParams& p, hipStream_t s);
+// Layers whose depthwise launch can take the gate-residual prologue
+// (DwParams::gr_gate): 5x5 / 7x7 / 9x9, stride 1 (with gr_up the map sides must
+// be twice gr_up's).
+bool depthwise_gate_residual_supported(int kh, int kw, int sh, int sw);
 
 // Fused pointwise pair of an LCNet block (pair_gemm.hip), fp32, rows are
 // pixels: x' = x * gate[image] (gate null: x' = x), h = GELU(x' W1^T + b1)

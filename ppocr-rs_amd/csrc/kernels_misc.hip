@@ -118,8 +118,45 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
     const int c = ch0 + c4 * 4;
     const bool cok = c < p.C;
     const T* base = in + (size_t)n * p.H * p.W * p.in_ps + c;
-    // All of this lane's loads are issued before the first LDS store.
     constexpr int STEP = 256 / C4B, NL = (IH * IW + STEP - 1) / STEP;
+    // Gate-residual prologue, as in depthwise_wave_kernel (7x7 layers only:
+    // the 3x3 instances keep their registers for occupancy).
+    if (KH == 7 && p.gr_gate) {
+      const float4 gt = cok ? *reinterpret_cast<const float4*>(p.gr_gate + (size_t)n * p.C + c) : f4_zero();
+      const int uh = p.H / 2, uw = p.W / 2;
+      const T* up = p.gr_up ? static_cast<const T*>(p.gr_up) + (size_t)n * uh * uw * p.gr_up_ps + c : nullptr;
+      // All of this lane's loads (the conv output, then the upper level's)
+      // are issued before the first store.
+      float4 hv[NL], uv[NL];
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        const int px = tid / C4B + i * STEP;
+        const int iy = px / IW, ix = px - iy * IW;
+        const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
+        const bool ok = px < IH * IW && cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W;
+        hv[i] = ok ? ld4<T>(base + ((size_t)gy * p.W + gx) * p.in_ps) : f4_zero();
+        uv[i] = ok && up ? ld4<T>(up + ((size_t)(gy / 2) * uw + gx / 2) * p.gr_up_ps) : f4_zero();
+      }
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        const int px = tid / C4B + i * STEP;
+        if (px >= IH * IW) break;
+        const int iy = px / IW, ix = px - iy * IW;
+        const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
+        float4 x = f4_zero();
+        if (cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W) {
+          const float4 h = hv[i];
+          x = make_float4(residual_mul(h.x, gt.x), residual_mul(h.y, gt.y), residual_mul(h.z, gt.z),
+                          residual_mul(h.w, gt.w));
+          if (up) x = f4_sum(x, uv[i]);
+          x = round4<T>(x);
+          if (p.gr_out && (unsigned)(iy - p.pt) < (unsigned)TY && (unsigned)(ix - p.pl) < (unsigned)TX)
+            st4<T>(static_cast<T*>(p.gr_out) + ((size_t)(n * p.H + gy) * p.W + gx) * p.gr_out_ps + c, x);
+        }
+        tile[(iy * IWP + ix) * C4B + c4] = x;
+      }
+    } else {
+    // All of this lane's loads are issued before the first LDS store.
     float4 v[NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
@@ -135,6 +172,7 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
       const int px = tid / C4B + i * STEP;
       const int iy = px / IW, ix = px - iy * IW;
       if (px < IH * IW) tile[(iy * IWP + ix) * C4B + c4] = v[i];
+    }
     }
   }
   for (int i = tid; i < KH * KW * C4B; i += 256) {
@@ -253,13 +291,36 @@ __global__ __launch_bounds__(256) void depthwise_wave_kernel(DwParams p) {
     const int c = ch0 + g * 4;
     const bool cok = c < p.C;
     const T* base = in + (size_t)n * p.H * p.W * p.in_ps + c;
-    for (int px = tid / G; px < IH * IW; px += 256 / G) {
-      const int iy = px / IW, ix = px - iy * IW;
-      const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
-      float4 v = f4_zero();
-      if (cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W)
-        v = ld4<T>(base + ((size_t)gy * p.W + gx) * p.in_ps);
-      tile[(g * IH + iy) * IWP + ix] = v;
+    if (p.gr_gate) {
+      // x = in + in * gate (+ up2(upper)), rounded as gate_residual_kernel
+      // stores it; pixels of the tile's output block also go to gr_out.
+      const float4 gt = cok ? *reinterpret_cast<const float4*>(p.gr_gate + (size_t)n * p.C + c) : f4_zero();
+      const int uh = p.H / 2, uw = p.W / 2;
+      const T* up = p.gr_up ? static_cast<const T*>(p.gr_up) + (size_t)n * uh * uw * p.gr_up_ps + c : nullptr;
+      for (int px = tid / G; px < IH * IW; px += 256 / G) {
+        const int iy = px / IW, ix = px - iy * IW;
+        const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
+        float4 v = f4_zero();
+        if (cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W) {
+          const float4 h = ld4<T>(base + ((size_t)gy * p.W + gx) * p.in_ps);
+          v = make_float4(residual_mul(h.x, gt.x), residual_mul(h.y, gt.y), residual_mul(h.z, gt.z),
+                          residual_mul(h.w, gt.w));
+          if (up) v = f4_sum(v, ld4<T>(up + ((size_t)(gy / 2) * uw + gx / 2) * p.gr_up_ps));
+          v = round4<T>(v);
+          if (p.gr_out && (unsigned)(iy - p.pt) < (unsigned)TY && (unsigned)(ix - p.pl) < (unsigned)TX)
+            st4<T>(static_cast<T*>(p.gr_out) + ((size_t)(n * p.H + gy) * p.W + gx) * p.gr_out_ps + c, v);
+        }
+        tile[(g * IH + iy) * IWP + ix] = v;
+      }
+    } else {
+      for (int px = tid / G; px < IH * IW; px += 256 / G) {
+        const int iy = px / IW, ix = px - iy * IW;
+        const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
+        float4 v = f4_zero();
+        if (cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W)
+          v = ld4<T>(base + ((size_t)gy * p.W + gx) * p.in_ps);
+        tile[(g * IH + iy) * IWP + ix] = v;
+      }
     }
   }
   __syncthreads();
@@ -596,6 +657,12 @@ int depthwise_se_blocks(const DwParams& p) {
 
 template <typename T>
 static void launch_dw_typed(const DwParams& p, hipStream_t s) {
+  if (p.gr_gate) {  // the gate-residual prologue: wave (5x5, 9x9) and tiled (7x7) kernels
+    if (p.kh == 5 && p.kw == 5 && p.sh == 1 && p.sw == 1) return launch_dw_wave<T, 5, 5>(p, s);
+    if (p.kh == 7 && p.kw == 7 && p.sh == 1 && p.sw == 1) return launch_dw_tiled<T, 7, 7, 16, 4, 4>(p, s);
+    if (p.kh == 9 && p.kw == 9 && p.sh == 1 && p.sw == 1) return launch_dw_wave<T, 9, 9>(p, s);
+    return;  // depthwise_gate_residual_supported() rules this out at plan time
+  }
   if constexpr (sizeof(T) == 2) {
     // 16-byte pixel accesses: strides and base addresses in whole 8-channel groups.
     const bool aligned = p.in_ps % kDwMfmaC == 0 && p.out_ps % kDwMfmaC == 0 &&
@@ -628,6 +695,10 @@ static void launch_dw_typed(const DwParams& p, hipStream_t s) {
 }
 
 void launch_depthwise(const DwParams& p, hipStream_t s) { DISPATCH_DT(p.dt, launch_dw_typed<T>(p, s)); }
+
+bool depthwise_gate_residual_supported(int kh, int kw, int sh, int sw) {
+  return kh == kw && (kh == 5 || kh == 7 || kh == 9) && sh == 1 && sw == 1;
+}
 
 const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho, int dt, bool table, int C) {
   if (table && depthwise_uses_mfma(kh, kw, sh, sw, dt, Ho, C))

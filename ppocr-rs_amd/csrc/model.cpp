@@ -355,9 +355,21 @@ class Builder {
   // se_cr reads the output next; when the kernel can, and the gate is not
   // small enough for its one-kernel form, it also leaves the gate's channel
   // sums in *sp (sp->P = 0 otherwise).
+  // The FPN gate-residual x = h + h * g (+ up2(upper)) applied as the
+  // depthwise conv's input prologue: `x` passed to depthwise() is h, and
+  // `out` (when set) receives x itself for the layers that read it next.
+  struct GateResidual {
+    View gate;
+    const View* upper = nullptr;
+    const View* out = nullptr;
+  };
+
   View depthwise(const View& x, const DwW& w, int act, const View* res, const std::string& name, int se_cr = 0,
-                 SePartial* sp = nullptr) {
+                 SePartial* sp = nullptr, const GateResidual* gr = nullptr) {
     if (x.c != w.c) raise(PPOCR_ERR_INVALID_MODEL, name + ": channel mismatch");
+    if (gr && (res || se_cr || !depthwise_gate_residual_supported(w.kh, w.kw, w.sh, w.sw) || w.pt != w.kh / 2 ||
+               w.pl != w.kw / 2 || (gr->upper && (x.h != 2 * gr->upper->h || x.w != 2 * gr->upper->w))))
+      raise(PPOCR_ERR_INVALID_MODEL, name + ": gate-residual prologue needs a plain same-size 5x5, 7x7 or 9x9 layer");
     int Ho = (x.h + w.pt + w.pb - w.kh) / w.sh + 1;
     int Wo = (x.w + w.pl + w.pr - w.kw) / w.sw + 1;
     View out = alloc(x.n, Ho, Wo, w.c, name);
@@ -400,6 +412,18 @@ class Builder {
     if (has_res) op.reads.push_back(r.buf);
     op.writes = {out.buf};
     if (has_part) op.writes.push_back(part.buf);
+    const bool has_gr = gr, has_up = gr && gr->upper, has_grout = gr && gr->out;
+    const View grg = gr ? gr->gate : View(), gru = has_up ? *gr->upper : View(), gro = has_grout ? *gr->out : View();
+    if (has_gr) {
+      op.kernel += "+gate_residual";
+      op.reads.push_back(grg.buf);
+      if (has_up) op.reads.push_back(gru.buf);
+      if (has_grout) op.writes.push_back(gro.buf);
+      const double px = (double)x.pixels() * w.c * dtype_size(x.dt);
+      op.bytes += (has_up ? px / 4 : 0.0) + (has_grout ? px : 0.0);
+      base.gr_up_ps = has_up ? gru.ps : 0;
+      base.gr_out_ps = has_grout ? gro.ps : 0;
+    }
     op.launch = [=](const Exec& ex, hipStream_t s) {
       DwParams p = base;
       p.in = ex.ptr(in);
@@ -409,6 +433,11 @@ class Builder {
       p.res = has_res ? ex.ptr(r) : nullptr;
       p.se_part = has_part ? ex.fptr(part) : nullptr;
       p.wtab = ex.w(to);
+      if (has_gr) {
+        p.gr_gate = ex.fptr(grg);
+        p.gr_up = has_up ? ex.ptr(gru) : nullptr;
+        p.gr_out = has_grout ? ex.ptr(gro) : nullptr;
+      }
       launch_depthwise(p, s);
     };
     add_op(std::move(op));
@@ -908,19 +937,43 @@ View rep_lk_fpn(Builder& B, const std::vector<View>& st, const int chans[4], int
                     ACT_HSIG5);
     g[i] = B.se(h[i], sw, p + ".se");
   }
-  for (int i = 3; i >= 0; --i) {
-    fused[i] = B.alloc(h[i].n, h[i].h, h[i].w, nc, "model.neck.fused." + std::to_string(i));
-    B.gate_residual(h[i], g[i], i < 3 ? &fused[i + 1] : nullptr, fused[i], 1, "model.neck.fused." + std::to_string(i));
-  }
-  const View& f0 = fused[0];
-  View cat = B.alloc(f0.n, f0.h, f0.w, nc, "model.neck.concat");
+  // fused[i] = h + h * g (+ up2(fused[i + 1])) feeds input_conv i's
+  // depthwise and level i - 1.  Where the depthwise can form it from h in its
+  // tile loads, levels run deepest first and the depthwise also stores it for
+  // the next level (level 0's is read by nothing else and is not stored);
+  // otherwise gate_residual writes every level first.
+  int pd = k / 2;
+  bool gr_fused = true;
+  for (int i = 0; i < 4; ++i)
+    gr_fused = gr_fused && depthwise_gate_residual_supported(k, k, 1, 1) &&
+               (i == 3 || (h[i].h == 2 * h[i + 1].h && h[i].w == 2 * h[i + 1].w));
+  if (!gr_fused)
+    for (int i = 3; i >= 0; --i) {
+      fused[i] = B.alloc(h[i].n, h[i].h, h[i].w, nc, "model.neck.fused." + std::to_string(i));
+      B.gate_residual(h[i], g[i], i < 3 ? &fused[i + 1] : nullptr, fused[i], 1,
+                      "model.neck.fused." + std::to_string(i));
+    }
+  View cat = B.alloc(h[0].n, h[0].h, h[0].w, nc, "model.neck.concat");
+  std::vector<DwW> dws(4);
+  for (int i = 0; i < 4; ++i)
+    dws[i] = B.dw_w("model.neck.input_conv." + std::to_string(i) + ".depthwise_convolution", nc, k, k, 1, 1,
+                    {pd, pd, pd, pd}, true);
+  std::vector<View> d(4);
+  if (gr_fused)
+    for (int i = 3; i >= 0; --i) {
+      if (i > 0) fused[i] = B.alloc(h[i].n, h[i].h, h[i].w, nc, "model.neck.fused." + std::to_string(i));
+      Builder::GateResidual gr;
+      gr.gate = g[i];
+      gr.upper = i < 3 ? &fused[i + 1] : nullptr;
+      gr.out = i > 0 ? &fused[i] : nullptr;
+      d[i] = B.depthwise(h[i], dws[i], ACT_NONE, nullptr, "model.neck.input_conv." + std::to_string(i) +
+                         ".depthwise_convolution", 0, nullptr, &gr);
+    }
   for (int i = 0; i < 4; ++i) {
     std::string p = "model.neck.input_conv." + std::to_string(i);
-    int pd = k / 2;
-    DwW dw = B.dw_w(p + ".depthwise_convolution", nc, k, k, 1, 1, {pd, pd, pd, pd}, true);
-    View d = B.depthwise(fused[i], dw, ACT_NONE, nullptr, p + ".depthwise_convolution");
+    if (!gr_fused) d[i] = B.depthwise(fused[i], dws[i], ACT_NONE, nullptr, p + ".depthwise_convolution");
     ConvW pw = B.conv_w(p + ".pointwise_convolution", nc, q, 1, 1, 1, 1, {0, 0, 0, 0}, false);
-    View pt = B.conv(d, pw, Epi{}, p + ".pointwise_convolution");
+    View pt = B.conv(d[i], pw, Epi{}, p + ".pointwise_convolution");
     SeW sw = B.se_w(p + ".squeeze_excitation_module.conv1", p + ".squeeze_excitation_module.conv2", q, q / 4,
                     ACT_HSIG5);
     View gi = B.se(pt, sw, p + ".se");
