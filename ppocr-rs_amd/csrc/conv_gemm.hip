@@ -345,8 +345,7 @@ __device__ __forceinline__ EpiTerms epilogue_load(const ConvParams& p, int m, in
     t.r = ld4<T>(static_cast<const T*>(p.res) + (size_t)m * p.res_ps + col);
     if (p.res_gate) {
       const float4 gt = *reinterpret_cast<const float4*>(p.res_gate + (size_t)img * p.Co + col);
-      t.r = make_float4(__fmul_rn(t.r.x, gt.x), __fmul_rn(t.r.y, gt.y), __fmul_rn(t.r.z, gt.z),
-                        __fmul_rn(t.r.w, gt.w));
+      t.r = make_float4(mul_rn(t.r.x, gt.x), mul_rn(t.r.y, gt.y), mul_rn(t.r.z, gt.z), mul_rn(t.r.w, gt.w));
     }
   }
   if (p.up) {

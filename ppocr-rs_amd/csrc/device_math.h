@@ -51,8 +51,19 @@ __device__ __forceinline__ float act_apply(int act, float v) {
   }
 }
 
+// x * y rounded to fp32 on its own.  Device code is compiled with FMA
+// contraction allowed; the pragma keeps this product out of any fused
+// multiply-add with a later sum (the reference rounds it first).
+__device__ __forceinline__ float mul_rn(float x, float y) {
+#pragma clang fp contract(off)
+  return x * y;
+}
+
 // x + x*g with the reference's two roundings (src/cpu/kernels/mod.rs:790-795).
-__device__ __forceinline__ float residual_mul(float x, float g) { return __fadd_rn(__fmul_rn(x, g), x); }
+__device__ __forceinline__ float residual_mul(float x, float g) {
+#pragma clang fp contract(off)
+  return x * g + x;
+}
 
 __device__ __forceinline__ float4 f4_zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
 

@@ -184,6 +184,56 @@ int ppocr_probe_depthwise(const float* x, int n, int h, int w, int c, const floa
   return rc;
 }
 
+// Depthwise with the gate-residual prologue (fp32): x = h + h * gate[n]
+// (+ the nearest 2x upsample of up [n][h/2][w/2][c], or null) is the input
+// of a k x k stride-1 depthwise (pads k / 2, bias, no activation); out [n][h][w][c]
+// is the conv, xout [n][h][w][c] (or null) receives x.  Returns 0, or 1 on a
+// HIP error.
+int ppocr_probe_depthwise_gate_residual(const float* h, int n, int ht, int wd, int c, const float* gate,
+                                        const float* up, const float* weight, const float* bias, int k, float* out,
+                                        float* xout) {
+  const size_t px = (size_t)n * ht * wd;
+  std::vector<float> packed((size_t)k * k * c);
+  for (int ch = 0; ch < c; ++ch)
+    for (int t = 0; t < k * k; ++t) packed[(size_t)t * c + ch] = weight[(size_t)ch * k * k + t];
+  void* d_in = upload(h, px * c, ppocr::DT_F32);
+  void* d_gate = upload(gate, (size_t)n * c, ppocr::DT_F32);
+  void* d_up = up ? upload(up, (size_t)n * (ht / 2) * (wd / 2) * c, ppocr::DT_F32) : nullptr;
+  void* d_wt = upload(packed.data(), packed.size(), ppocr::DT_F32);
+  void* d_bias = upload(bias, c, ppocr::DT_F32);
+  void *d_out = nullptr, *d_x = nullptr;
+  int rc = 0;
+  if (!d_in || !d_gate || (up && !d_up) || !d_wt || !d_bias || hipMalloc(&d_out, px * c * 4) != hipSuccess ||
+      (xout && hipMalloc(&d_x, px * c * 4) != hipSuccess) || !ppocr::depthwise_gate_residual_supported(k, k, 1, 1) ||
+      (up && (ht % 2 || wd % 2))) {
+    rc = 1;
+  } else {
+    ppocr::DwParams p{};
+    p.in = d_in;
+    p.N = n, p.H = ht, p.W = wd, p.C = c, p.in_ps = c;
+    p.out = d_out;
+    p.Ho = ht, p.Wo = wd, p.out_ps = c;
+    p.wt = static_cast<const float*>(d_wt);
+    p.bias = static_cast<const float*>(d_bias);
+    p.kh = p.kw = k, p.sh = p.sw = 1, p.pt = p.pl = k / 2;
+    p.act = 0;
+    p.dt = ppocr::DT_F32;
+    p.gr_gate = static_cast<const float*>(d_gate);
+    p.gr_up = d_up;
+    p.gr_up_ps = c;
+    p.gr_out = d_x;
+    p.gr_out_ps = c;
+    ppocr::launch_depthwise(p, nullptr);
+    if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(out, d_out, px * c * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        (xout && hipMemcpy(xout, d_x, px * c * 4, hipMemcpyDeviceToHost) != hipSuccess))
+      rc = 1;
+  }
+  for (void* ptr : {d_in, d_gate, d_up, d_wt, d_bias, d_out, d_x})
+    if (ptr) (void)hipFree(ptr);
+  return rc;
+}
+
 // The matrix-core tap fragments a bf16 plan packs for a c-channel k x k
 // depthwise layer (host only): taps [c][k][k] -> out [c][k][64][8] bf16 bits.
 void ppocr_probe_depthwise_table(const float* weight, int c, int k, uint16_t* out) {

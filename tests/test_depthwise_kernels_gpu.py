@@ -140,3 +140,46 @@ def test_fp32_depthwise_probe_matches_float64():
                                          _ptr(out)) == 0
         ref = depthwise_ref(x, w, b, ACT_RELU, None)
         assert np.abs(out - ref).max() <= 1e-5
+
+
+# (k, n, h, w, c, with upper level): the RepLK FPN's input-conv layers with
+# the gate-residual formed in the tile loads (5x5 wave, 7x7 tiled, 9x9 wave).
+GR_CASES = [(5, 1, 26, 46, 64, True), (5, 2, 13, 23, 32, False), (7, 1, 20, 34, 96, True), (9, 1, 18, 22, 16, True)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", GR_CASES, ids=[f"k{c[0]}-{c[2]}x{c[3]}x{c[4]}{'-up' if c[5] else ''}" for c in GR_CASES])
+def test_gate_residual_prologue_matches_float64(case):
+    k, n, h, wd, c, with_up = case
+    lib = _lib()
+    f = ctypes.POINTER(ctypes.c_float)
+    i = ctypes.c_int
+    lib.ppocr_probe_depthwise_gate_residual.argtypes = [f, i, i, i, i, f, f, f, f, i, f, f]
+    lib.ppocr_probe_depthwise_gate_residual.restype = i
+    rng = np.random.default_rng(1000 * k + h)
+    hx = rng.standard_normal((n, h, wd, c)).astype(np.float32)
+    gate = rng.uniform(0, 1, (n, c)).astype(np.float32)
+    up = rng.standard_normal((n, h // 2, wd // 2, c)).astype(np.float32) if with_up else None
+    w = (rng.standard_normal((c, k, k)) / k).astype(np.float32)
+    b = rng.standard_normal(c).astype(np.float32) * 0.1
+    out = np.empty((n, h, wd, c), np.float32)
+    xout = np.empty((n, h, wd, c), np.float32)
+    assert lib.ppocr_probe_depthwise_gate_residual(_ptr(hx), n, h, wd, c, _ptr(gate), _ptr(up), _ptr(w), _ptr(b), k,
+                                                   _ptr(out), _ptr(xout)) == 0
+    # x = h + h*g with both roundings in fp32 (the reference's two-step
+    # residual multiply), then + up2(upper) in fp32: bit-exact.
+    x = (hx * gate[:, None, None, :]).astype(np.float32) + hx
+    if with_up:
+        x = x + np.repeat(np.repeat(up, 2, axis=1), 2, axis=2)
+    bad = np.argwhere(xout != x)
+    assert bad.size == 0, f"{len(bad)} of {x.size} differ, first {bad[:3].tolist()}: {xout[tuple(bad[0])]} vs {x[tuple(bad[0])]}"
+    # float64 depthwise of x.
+    pd = k // 2
+    xp = np.pad(x.astype(np.float64), ((0, 0), (pd, pd), (pd, pd), (0, 0)))
+    want = np.zeros((n, h, wd, c))
+    for ky in range(k):
+        for kx in range(k):
+            want += xp[:, ky:ky + h, kx:kx + wd, :] * w[:, ky, kx]
+    want += b
+    err = np.abs(out - want)
+    assert np.all(err <= 1e-5 + 1e-5 * np.abs(want)), f"max err {err.max()}"
