@@ -375,6 +375,9 @@ __device__ __forceinline__ void epilogue_store(const ConvParams& p, float4 v, fl
     *reinterpret_cast<float4*>(static_cast<float*>(p.out) + (size_t)m * p.out_ps + col) = v;
   } else if (p.rep == 1) {
     st4<T>(static_cast<T*>(p.out) + (size_t)m * p.out_ps + col, v);
+  } else if (p.rep_split) {
+    T* row = static_cast<T*>(p.out) + ((size_t)(img * p.out_h + oy * p.rep + (int)blockIdx.z) * p.out_w + ox * p.rep) * p.out_ps + col;
+    for (int dx = 0; dx < p.rep; ++dx) st4<T>(row + (size_t)dx * p.out_ps, v);
   } else {
     for (int dy = 0; dy < p.rep; ++dy)
       for (int dx = 0; dx < p.rep; ++dx)
@@ -1375,9 +1378,21 @@ template <typename T, int BM, int BN, int WM, int WN>
 static void launch_tile(const ConvParams& p, int M, hipStream_t s) {
   // Grid rows of workgroups rounded up to a multiple of the 8 XCDs; surplus
   // workgroups exit before touching memory (see the tile order above).  With
-  // split K, grid row y takes split y.
+  // split K, grid row y takes split y.  Upsample-on-write layers of short K
+  // (the medium neck's intraclass conv_final, K = 32, writing each pixel as
+  // a 2x2 to 8x8 block) recompute the tile once per replica row, grid layer
+  // z writing output row z of every block: the few tiles of the deep levels
+  // would otherwise store rep^2 copies each from a handful of CUs (the 8x8
+  // level at batch 1: 5 workgroups storing 4.9 MB).
   const long tiles = (long)((M + BM - 1) / BM) * ((p.Co + BN - 1) / BN);
   const int splits = p.splits > 1 ? p.splits : 1;
+  const int K = p.kh * p.kw * p.C;
+  if (p.rep > 1 && splits == 1 && K <= 64 && !p.ctc_part && !p.db_ch) {
+    ConvParams q = p;
+    q.rep_split = 1;
+    launch_tile_kernel<T, BM, BN, WM, WN>(q, dim3((unsigned)((tiles + 7) / 8 * 8), 1, (unsigned)p.rep), s);
+    return;
+  }
   launch_tile_kernel<T, BM, BN, WM, WN>(p, dim3((unsigned)((tiles + 7) / 8 * 8), (unsigned)splits), s);
   if (splits > 1) {
     const long fin = (long)((M + kFinishBM - 1) / kFinishBM) * ((p.Co + kFinishBN - 1) / kFinishBN);

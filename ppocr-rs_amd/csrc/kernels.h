@@ -51,6 +51,7 @@ struct ConvParams {
   const void* up;         // nearest-upsample-add source [N, Ho/up_s, Wo/up_s, Co]
   int up_s, up_ps;
   int rep;           // write each output pixel as a rep x rep block (upsample on write)
+  int rep_split;     // set by the launcher: workgroup z writes output row z of each rep x rep block only
   int out_h, out_w;  // dims of the tensor `out` points into (Ho*rep, Wo*rep)
   int dt;            // activation type of in / res / up / out
   // Greedy-CTC epilogue (classifier only; `out` unused, no other epilogue

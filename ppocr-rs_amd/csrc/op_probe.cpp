@@ -107,6 +107,49 @@ int ppocr_probe_conv(const float* x, int n, int h, int w, int c, const float* we
   return rc;
 }
 
+// 1x1 conv with upsample-on-write (the medium neck's intraclass conv_final):
+// x [n][h][w][c], weight [co][c], bias [co], residual res [n][h][w][co] (or
+// null): y = res + act(x W^T + b), each pixel written as a rep x rep block
+// of out [n][h*rep][w*rep][co]; fp32.  Returns 0, or 1 on a HIP error.
+int ppocr_probe_conv_rep(const float* x, int n, int h, int w, int c, const float* weight, const float* bias, int co,
+                         int act, const float* res, int rep, float* out) {
+  const size_t M = (size_t)n * h * w, O = M * rep * rep * co;
+  void* d_in = upload(x, M * c, ppocr::DT_F32);
+  void* d_wt = upload(weight, (size_t)co * c, ppocr::DT_F32);
+  void* d_bias = upload(bias, co, ppocr::DT_F32);
+  void* d_res = res ? upload(res, M * co, ppocr::DT_F32) : nullptr;
+  void* d_out = nullptr;
+  int rc = 0;
+  if (!d_in || !d_wt || !d_bias || (res && !d_res) || hipMalloc(&d_out, O * 4) != hipSuccess) {
+    rc = 1;
+  } else {
+    ppocr::ConvParams p{};
+    p.in = d_in;
+    p.N = n, p.H = h, p.W = w, p.C = c, p.in_ps = c;
+    p.out = d_out;
+    p.Ho = h, p.Wo = w, p.Co = co, p.out_ps = co;
+    p.wt = d_wt;
+    p.ldw = c;
+    p.bias = static_cast<const float*>(d_bias);
+    p.kh = p.kw = 1, p.sh = p.sw = 1;
+    p.act = act;
+    p.res = d_res;
+    p.res_ps = co;
+    p.up_s = 2;
+    p.rep = rep;
+    p.out_h = h * rep, p.out_w = w * rep;
+    p.dt = ppocr::DT_F32;
+    p.splits = 1;
+    ppocr::launch_conv(p, nullptr);
+    if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(out, d_out, O * 4, hipMemcpyDeviceToHost) != hipSuccess)
+      rc = 1;
+  }
+  for (void* ptr : {d_in, d_wt, d_bias, d_res, d_out})
+    if (ptr) (void)hipFree(ptr);
+  return rc;
+}
+
 // The kernel instance ppocr_probe_conv runs for these arguments (pointers
 // stand in by their alignment: the probe's buffers are hipMalloc'd), and the
 // split count the planner would choose for the layer.

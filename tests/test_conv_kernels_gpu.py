@@ -255,3 +255,36 @@ def test_pointwise_pair_depthwise_prologue_matches_float64(name, n, h, w, c, str
         want = want + t
     err = np.abs(out - want)
     assert np.all(err <= 1e-4 + 1e-5 * np.abs(want)), f"max err {err.max()}"
+
+
+# (name, n, h, w, c, co, rep): upsample-on-write convs; K <= 64 writes one
+# replica per workgroup layer, wider K all replicas per workgroup.
+REP_CASES = [
+    ("rep8 K32", 2, 5, 7, 32, 64, 8),
+    ("rep4 K32", 1, 13, 23, 32, 64, 4),
+    ("rep2 K32 tails", 1, 9, 11, 32, 48, 2),
+    ("rep4 K96", 1, 6, 9, 96, 64, 4),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,n,h,w,c,co,rep", REP_CASES, ids=[c[0] for c in REP_CASES])
+def test_upsample_on_write_matches_float64(name, n, h, w, c, co, rep):
+    lib = _lib()
+    f = ctypes.POINTER(ctypes.c_float)
+    i = ctypes.c_int
+    lib.ppocr_probe_conv_rep.argtypes = [f, i, i, i, i, f, f, i, i, f, i, f]
+    lib.ppocr_probe_conv_rep.restype = i
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    x = rng.standard_normal((n, h, w, c)).astype(np.float32)
+    wt = (rng.standard_normal((co, c)) / np.sqrt(c)).astype(np.float32)
+    b = rng.standard_normal(co).astype(np.float32) * 0.1
+    res = rng.standard_normal((n, h, w, co)).astype(np.float32)
+    out = np.full((n, h * rep, w * rep, co), np.nan, np.float32)
+    assert lib.ppocr_probe_conv_rep(_ptr(x), n, h, w, c, _ptr(wt), _ptr(b), co, ACT_RELU, _ptr(res), rep,
+                                    _ptr(out)) == 0
+    y = res + np.maximum(x.astype(np.float64) @ wt.T.astype(np.float64) + b, 0.0)
+    want = np.repeat(np.repeat(y, rep, axis=1), rep, axis=2)
+    assert np.all(np.isfinite(out)), "an output block was not written"
+    err = np.abs(out - want)
+    assert np.all(err <= 1e-4 + 1e-5 * np.abs(want)), f"{name}: max abs diff {err.max():.3e}"
