@@ -1234,6 +1234,202 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
       m0, n0, M, n_tiles, &bias_pre[0]);
 }
 
+// ---------------------------------------------------------------------------
+// Wide-tile bf16 1x1 layers (no SE input gate): 256x256 tiles, eight waves
+// (2 x 4) of 128x64 each as 4 x 2 blocks of v_mfma_f32_32x32x16_bf16, so a
+// tile multiplies 4.2 MFLOP per 32 KB K slice it stages: twice the operand
+// reuse of the 128x64 tile, for the deep-K, wide-N layers whose MFMAs the
+// smaller tiles' load latency starves.  One workgroup per CU (128 KB of LDS:
+// four stages of 32-deep slices with 64-byte rows, filled by direct-to-LDS
+// loads as in the kernel above; two waves per SIMD take turns on the matrix
+// core).  The operand read of a 32x32x16 MFMA (lane l: 16 bytes of row
+// l % 32, vector 2 kk + l / 32 of the row) is conflict-free with the row
+// key (r / 4) % 4 (measured at the linear-read rate; without the key it
+// runs at a third of it).  Epilogue from registers after the quad
+// transpose.
+constexpr int kWideBM = 256, kWideBN = 256;
+
+__device__ __forceinline__ int wide_key(int r) { return (r >> 2) & 3; }
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// Waits until at most N LDS reads of this wave are in flight; the six
+// operands are the values whose reads must have completed (issued first).
+template <int N>
+__device__ __forceinline__ void lds_wait6(floatx4& a, floatx4& b, floatx4& c, floatx4& d, floatx4& e, floatx4& f) {
+  asm volatile("s_waitcnt lgkmcnt(%6)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f) : "n"(N));
+}
+
+// RES: 0 no residual, 1 plain, 2 gated (res * res_gate of the row's image).
+template <int RES, int ACT>
+__global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
+  constexpr int BM = kWideBM, BN = kWideBN, BK = 32, S = 4;
+  constexpr int WN = 4;
+  constexpr int TM = 4, TN = 2;  // 32x32 blocks per wave
+  constexpr int STAGE = (BM + BN) * 64;
+  constexpr int ES = 2;
+  constexpr int L = 4;  // loads per wave per slice: two A passes, two B passes
+  __shared__ __attribute__((aligned(16))) char lds[S * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int M = p.N * p.Ho * p.Wo;
+  const int K = p.C;
+
+  const int n_tiles = (p.Co + BN - 1) / BN;
+  const int m_tiles = (M + BM - 1) / BM;
+  const int per_xcd = gridDim.x / 8;
+  const int t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (t >= m_tiles * n_tiles) return;
+  const int m0 = (t / n_tiles) * BM;
+  const int n0 = (t % n_tiles) * BN;
+
+  const int32x4_t a_rsrc = buffer_resource(p.in, (unsigned)((size_t)p.N * p.H * p.W * p.in_ps * ES));
+  const int32x4_t b_rsrc = buffer_resource(p.wt, (unsigned)((size_t)p.Co * p.ldw * ES));
+
+  // Load lanes: a pass of 512 lanes fills 128 rows, four lanes per row; lane
+  // fills row pass * 128 + prow, position lane % 4, with k vector kvec.
+  const int prow = wave * 16 + (lane >> 2);
+  const int kvec = (lane & 3) ^ wide_key(prow);
+  unsigned a_off[2], b_off[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int m = m0 + i * 128 + prow;
+    a_off[i] = m < M ? (unsigned)(((size_t)m * p.in_ps + kvec * 8) * ES) : kOutOfRange;
+    const int n = n0 + i * 128 + prow;
+    b_off[i] = n < p.Co ? (unsigned)(((size_t)n * p.ldw + kvec * 8) * ES) : kOutOfRange;
+  }
+  const int nk = (K + BK - 1) / BK;
+  auto stage = [&](int j) { return lds + j * STAGE; };
+  auto issue = [&](int j, int k0) {
+    const unsigned ks = (unsigned)k0 * ES;
+    const bool kin = k0 + kvec * 8 < K;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) lds_load16(a_rsrc, kin ? a_off[i] : kOutOfRange, ks, stage(j) + (i * 128 + wave * 16) * 64);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      lds_load16(b_rsrc, kin ? b_off[i] : kOutOfRange, ks, stage(j) + (BM + i * 128 + wave * 16) * 64);
+  };
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Operand reads: row lane % 32 of each block, vector 2 kk + lane / 32.
+  const int lr = lane & 31;
+  const unsigned a_row = (unsigned)(wm * 128 + lr) * 64, b_row = (unsigned)(BM + wn * 64 + lr) * 64;
+  const unsigned sw0 = (unsigned)((0 + (lane >> 5)) ^ wide_key(lr)) << 4;
+  const unsigned sw1 = (unsigned)((2 + (lane >> 5)) ^ wide_key(lr)) << 4;
+  auto compute = [&](int j) {
+    const unsigned base = lds_addr(stage(j));
+    floatx4 a0[TM], b0[TN], a1[TM], b1[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a0[i] = lds_read16(base + a_row + i * 32 * 64 + sw0);
+#pragma unroll
+    for (int q = 0; q < TN; ++q) b0[q] = lds_read16(base + b_row + q * 32 * 64 + sw0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a1[i] = lds_read16(base + a_row + i * 32 * 64 + sw1);
+#pragma unroll
+    for (int q = 0; q < TN; ++q) b1[q] = lds_read16(base + b_row + q * 32 * 64 + sw1);
+    lds_wait6<6>(a0[0], a0[1], a0[2], a0[3], b0[0], b0[1]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int q = 0; q < TN; ++q)
+        acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a0[i]),
+                                                             __builtin_bit_cast(bf16x8, b0[q]), acc[i][q], 0, 0, 0);
+    lds_wait6<0>(a1[0], a1[1], a1[2], a1[3], b1[0], b1[1]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int q = 0; q < TN; ++q)
+        acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a1[i]),
+                                                             __builtin_bit_cast(bf16x8, b1[q]), acc[i][q], 0, 0, 0);
+  };
+  auto step = [&](int cur, int refill, int s) {
+    const int after = nk - 1 - s;
+    if (after >= S - 2)
+      wait_vmcnt<(S - 2) * L>();
+    else if (after == 1)
+      wait_vmcnt<L>();
+    else
+      wait_vmcnt<0>();
+    stage_barrier();
+    if (s + S - 1 < nk) issue(refill, (s + S - 1) * BK);
+    compute(cur);
+  };
+
+  // Bias of this lane's two column groups (see the epilogue), loaded ahead.
+  const int ccol = 4 * (lr >> 2);
+  float4 bias_pre[TN];
+#pragma unroll
+  for (int q = 0; q < TN; ++q) bias_pre[q] = bias4(p, n0 + wn * 64 + q * 32 + ccol);
+
+  issue(0, 0);
+  if (nk > 1) issue(1, BK);
+  if (nk > 2) issue(2, 2 * BK);
+  for (int s = 0; s < nk; s += S) {
+    step(0, 3, s);
+    if (s + 1 < nk) step(1, 0, s + 1);
+    if (s + 2 < nk) step(2, 1, s + 2);
+    if (s + 3 < nk) step(3, 2, s + 3);
+  }
+  wait_vmcnt<0>();
+
+  // Epilogue: bias, activation, (gated) residual; the launcher sends the
+  // other epilogue terms to the other kernels.  Block element e of lane l is row
+  // 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32; after the quad transpose
+  // of elements 4 g .. 4 g + 3, lane l holds row 8 g + 4 (l / 32) + l % 4,
+  // columns 4 ((l % 32) / 4) .. + 3: a store writes 64 contiguous bytes of
+  // eight rows.
+  const int rsub = 4 * (lane >> 5) + (lane & 3);
+  const bool has_bias = p.bias != nullptr;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      floatx4 v[TN];
+#pragma unroll
+      for (int q = 0; q < TN; ++q)
+        v[q] = quad_transpose(floatx4{acc[i][q][4 * g], acc[i][q][4 * g + 1], acc[i][q][4 * g + 2], acc[i][q][4 * g + 3]},
+                              lane);
+      const int m = m0 + wm * 128 + i * 32 + 8 * g + rsub;
+      float4 r[TN];
+      if constexpr (RES != 0) {
+        const int img = RES == 2 ? min(m, M - 1) / (p.Ho * p.Wo) : 0;
+#pragma unroll
+        for (int q = 0; q < TN; ++q) {
+          const int col = n0 + wn * 64 + q * 32 + ccol;
+          const bool ok = m < M && col < p.Co;
+          r[q] = ok ? ld4<bf16>(static_cast<const bf16*>(p.res) + (size_t)m * p.res_ps + col) : float4{0.f, 0.f, 0.f, 0.f};
+          if constexpr (RES == 2) {
+            const float4 gt = ok ? *reinterpret_cast<const float4*>(p.res_gate + (size_t)img * p.Co + col)
+                                 : float4{0.f, 0.f, 0.f, 0.f};
+            r[q] = make_float4(mul_rn(r[q].x, gt.x), mul_rn(r[q].y, gt.y), mul_rn(r[q].z, gt.z), mul_rn(r[q].w, gt.w));
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < TN; ++q) {
+        const int col = n0 + wn * 64 + q * 32 + ccol;
+        float4 x = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+        if (has_bias) x = f4_add(x, bias_pre[q]);
+        x.x = act_apply(ACT, x.x);
+        x.y = act_apply(ACT, x.y);
+        x.z = act_apply(ACT, x.z);
+        x.w = act_apply(ACT, x.w);
+        if constexpr (RES != 0) x = f4_add(r[q], x);
+        if (m < M && col < p.Co) st4<bf16>(static_cast<bf16*>(p.out) + (size_t)m * p.out_ps + col, x);
+      }
+    }
+}
+
 // Split-K finish: one workgroup per 16x64 output tile, one float4 of it per
 // lane.  A lane issues the loads of all its split partials at once (the
 // reduction is short and latency-bound), adds them in split order, stages
@@ -1400,6 +1596,30 @@ static void launch_tile(const ConvParams& p, int M, hipStream_t s) {
   }
 }
 
+// Layers conv1x1_wide_kernel runs: bf16 1x1 layers without an SE input
+// gate, at least 256 output channels and K >= 512, whose 256x256 tiles
+// number at least 128 (shape test, shared with the planner's split choice),
+// with at most the bias, one of the activations the kernel is built for and
+// a (gated) residual in the epilogue.  Measured against the 128x64 / 64x64
+// kernel inside the recognizer and detector plans: 1.07-1.37x at K = 512 to
+// 1536, about even at K = 256 and 0.91-0.93x at K = 128 (a CU holds one
+// wide tile, so nothing overlaps its short K loop's ramp and its epilogue);
+// on isolated layers 0.57-0.85x on 70-76 tiles and 0.72-0.74x with 128
+// output channels, where half of each tile is empty.
+constexpr int kWideMinTiles = 128, kWideMinK = 512, kWideMinCo = 256;
+
+static bool wide_shape(int M, int Co, int K, int dt) {
+  const long tiles = (long)((M + kWideBM - 1) / kWideBM) * ((Co + kWideBN - 1) / kWideBN);
+  return dt == DT_BF16 && Co % 4 == 0 && Co >= kWideMinCo && K >= kWideMinK && tiles >= kWideMinTiles;
+}
+
+static bool wide_layer(const ConvParams& p) {
+  const bool act = p.act == ACT_NONE || p.act == ACT_RELU || p.act == ACT_HSWISH || p.act == ACT_GELU;
+  return act && wide_shape(p.N * p.Ho * p.Wo, p.Co, p.C, p.dt) && conv_variant(p, 128) == CV_DIRECT_1X1 &&
+         (!p.res_gate || p.res) && !p.up && p.rep == 1 && !p.out_f32 && !p.ctc_part && !p.db_ch && p.splits <= 1 &&
+         p.out_ps % 4 == 0 && (!p.res || p.res_ps % 4 == 0);
+}
+
 // Tile choice: narrow output channel counts get tall tiles so no MFMA
 // column is wasted.  Wide layers: fp32 takes 64x64 (its MFMA is slow enough
 // that the smaller tile's occupancy wins); bf16 takes 128x64 when that
@@ -1413,6 +1633,7 @@ static int pick_tile(int M, int cols, int dt) {
 }
 
 std::string conv_kernel_name(const ConvParams& p) {
+  if (wide_layer(p)) return "conv_gemm_bf16<256x256,1x1>";
   static const char* tiles[] = {"256x16", "128x32", "128x64", "64x64"};
   static const int bm[] = {256, 128, 128, 64};
   static const char* variants[] = {",1x1", "", ",1x1,gate", ",1x1,reg", ",reg", ",1x1,reg4", ",reg4"};
@@ -1441,7 +1662,7 @@ int conv_split_k(int M, int Co, int K, int dt) {
   const long tiles = (long)((M + bm[t] - 1) / bm[t]) * ((Co + bn[t] - 1) / bn[t]);
   const int bk = dt == DT_BF16 ? GemmTraits<bf16>::BK : GemmTraits<float>::BK;
   const int nk = (K + bk - 1) / bk;
-  if (Co % 4 != 0) return 1;
+  if (Co % 4 != 0 || wide_shape(M, Co, K, dt)) return 1;
   long s;
   if (tiles < 192)
     s = (512 + tiles - 1) / tiles;
@@ -1457,6 +1678,30 @@ int conv_split_k(int M, int Co, int K, int dt) {
 template <typename T>
 static void launch_typed(const ConvParams& p, hipStream_t s) {
   int M = p.N * p.Ho * p.Wo;
+  if constexpr (sizeof(T) == 2) {
+    if (wide_layer(p)) {
+      const long tiles = (long)((M + kWideBM - 1) / kWideBM) * ((p.Co + kWideBN - 1) / kWideBN);
+      const dim3 grid((unsigned)((tiles + 7) / 8 * 8));
+      auto go = [&](auto res, auto act) {
+        hipLaunchKernelGGL((conv1x1_wide_kernel<decltype(res)::value, decltype(act)::value>), grid, dim3(512), 0, s, p);
+      };
+      auto with_act = [&](auto res) {
+        switch (p.act) {
+          case ACT_RELU: go(res, std::integral_constant<int, ACT_RELU>{}); break;
+          case ACT_HSWISH: go(res, std::integral_constant<int, ACT_HSWISH>{}); break;
+          case ACT_GELU: go(res, std::integral_constant<int, ACT_GELU>{}); break;
+          default: go(res, std::integral_constant<int, ACT_NONE>{}); break;
+        }
+      };
+      if (p.res_gate)
+        with_act(std::integral_constant<int, 2>{});
+      else if (p.res)
+        with_act(std::integral_constant<int, 1>{});
+      else
+        with_act(std::integral_constant<int, 0>{});
+      return;
+    }
+  }
   switch (pick_tile(M, p.Co, p.dt)) {
     case 0: launch_tile<T, 256, 16, 4, 1>(p, M, s); break;
     case 1: launch_tile<T, 128, 32, 4, 1>(p, M, s); break;

@@ -240,12 +240,20 @@ class Builder {
   // Name of the kernel instance launch_conv will run for `base` reading view
   // x with weights at blob offset wo.  The pointers are stood in for by
   // their offsets, which decide their alignment: arena buffers and weight
-  // offsets are 256-byte aligned.
-  static std::string conv_kernel(const ConvParams& base, const View& x, size_t wo, bool gated) {
+  // offsets are 256-byte aligned.  `terms`: the epilogue inputs the launch
+  // will pass (kTermRes, kTermResGate, kTermUp, kTermCtc), stood in for by
+  // non-null aligned values.
+  static constexpr unsigned kTermRes = 1, kTermResGate = 2, kTermUp = 4, kTermCtc = 8;
+  static std::string conv_kernel(const ConvParams& base, const View& x, size_t wo, bool gated, unsigned terms = 0) {
     ConvParams probe = base;
     probe.in = reinterpret_cast<const void*>((uintptr_t)(x.off * dtype_size(x.dt)));
     probe.wt = reinterpret_cast<const void*>((uintptr_t)wo);
     probe.in_gate = gated ? reinterpret_cast<const float*>((uintptr_t)16) : nullptr;
+    const uintptr_t stand_in = 256;
+    if (terms & kTermRes) probe.res = reinterpret_cast<const void*>(stand_in);
+    if (terms & kTermResGate) probe.res_gate = reinterpret_cast<const float*>(stand_in);
+    if (terms & kTermUp) probe.up = reinterpret_cast<const void*>(stand_in);
+    if (terms & kTermCtc) probe.ctc_part = reinterpret_cast<float*>(stand_in);
     return conv_kernel_name(probe);
   }
 
@@ -301,7 +309,8 @@ class Builder {
     base.splits = splits;
     Op op;
     op.name = name;
-    op.kernel = conv_kernel(base, a_src, wo, has_ig && !prescale);
+    op.kernel = conv_kernel(base, a_src, wo, has_ig && !prescale,
+                            (has_res ? kTermRes : 0u) | (has_rg ? kTermResGate : 0u) | (has_up ? kTermUp : 0u));
     if (prescale) op.kernel += "+gate_pass";
     if (splits > 1) op.kernel += "+split_k" + std::to_string(splits);
     op.bound = 1;
@@ -737,7 +746,7 @@ class Builder {
     const double es = (double)dtype_size(x.dt), part_bytes = 12.0 * tiles * M;
     Op op;
     op.name = name;
-    op.kernel = conv_kernel(base, x, wo, false);
+    op.kernel = conv_kernel(base, x, wo, false, kTermCtc);
     op.bound = 1;
     op.flops = 2.0 * M * w.co * w.ci;
     op.bytes = es * ((double)M * w.ci + (double)w.ci * w.co) + 4.0 * w.co + part_bytes;

@@ -150,6 +150,65 @@ int ppocr_probe_conv_rep(const float* x, int n, int h, int w, int c, const float
   return rc;
 }
 
+// 1x1 conv with a residual in storage type dt: x [n][h][w][c], weight
+// [co][c], bias [co], res [n][h][w][co] (or null), res_gate [n][co] (or
+// null: plain residual): y = res * res_gate + act(x W^T + b).  `kernel`
+// (if not null) receives the kernel instance's name.  Returns 0, or 1 on a
+// HIP error.
+int ppocr_probe_conv1x1_res(const float* x, int n, int h, int w, int c, const float* weight, const float* bias, int co,
+                            int act, const float* res, const float* res_gate, int dt, float* out,
+                            const char** kernel) {
+  static thread_local std::string name;
+  const size_t M = (size_t)n * h * w;
+  void* d_in = upload(x, M * c, dt);
+  void* d_wt = upload(weight, (size_t)co * c, dt);
+  void* d_bias = upload(bias, co, ppocr::DT_F32);
+  void* d_res = res ? upload(res, M * co, dt) : nullptr;
+  void* d_rg = res_gate ? upload(res_gate, (size_t)n * co, ppocr::DT_F32) : nullptr;
+  void* d_out = nullptr;
+  const size_t es = dt == ppocr::DT_BF16 ? 2 : 4;
+  int rc = 0;
+  if (!d_in || !d_wt || !d_bias || (res && !d_res) || (res_gate && !d_rg) ||
+      hipMalloc(&d_out, M * co * es) != hipSuccess) {
+    rc = 1;
+  } else {
+    ppocr::ConvParams p{};
+    p.in = d_in;
+    p.N = n, p.H = h, p.W = w, p.C = c, p.in_ps = c;
+    p.out = d_out;
+    p.Ho = h, p.Wo = w, p.Co = co, p.out_ps = co;
+    p.wt = d_wt;
+    p.ldw = c;
+    p.bias = static_cast<const float*>(d_bias);
+    p.kh = p.kw = 1, p.sh = p.sw = 1;
+    p.act = act;
+    p.res = d_res;
+    p.res_ps = co;
+    p.res_gate = static_cast<const float*>(d_rg);
+    p.up_s = 2;
+    p.rep = 1;
+    p.out_h = h, p.out_w = w;
+    p.dt = dt;
+    p.splits = 1;
+    name = ppocr::conv_kernel_name(p);
+    if (kernel) *kernel = name.c_str();
+    ppocr::launch_conv(p, nullptr);
+    if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess) rc = 1;
+    if (rc == 0) {
+      if (dt == ppocr::DT_BF16) {
+        std::vector<uint16_t> hb(M * co);
+        if (hipMemcpy(hb.data(), d_out, hb.size() * 2, hipMemcpyDeviceToHost) != hipSuccess) rc = 1;
+        for (size_t i = 0; i < hb.size(); ++i) out[i] = from_bf16(hb[i]);
+      } else if (hipMemcpy(out, d_out, M * co * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+        rc = 1;
+      }
+    }
+  }
+  for (void* ptr : {d_in, d_wt, d_bias, d_res, d_rg, d_out})
+    if (ptr) (void)hipFree(ptr);
+  return rc;
+}
+
 // The kernel instance ppocr_probe_conv runs for these arguments (pointers
 // stand in by their alignment: the probe's buffers are hipMalloc'd), and the
 // split count the planner would choose for the layer.
