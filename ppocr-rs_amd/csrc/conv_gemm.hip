@@ -1237,19 +1237,20 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
 // ---------------------------------------------------------------------------
 // Wide-tile bf16 1x1 layers (no SE input gate): 256x256 tiles, eight waves
 // (2 x 4) of 128x64 each as 4 x 2 blocks of v_mfma_f32_32x32x16_bf16, so a
-// tile multiplies 4.2 MFLOP per 32 KB K slice it stages: twice the operand
+// tile multiplies 8.4 MFLOP per 64 KB K slice it stages: twice the operand
 // reuse of the 128x64 tile, for the deep-K, wide-N layers whose MFMAs the
-// smaller tiles' load latency starves.  One workgroup per CU (128 KB of LDS:
-// four stages of 32-deep slices with 64-byte rows, filled by direct-to-LDS
-// loads as in the kernel above; two waves per SIMD take turns on the matrix
-// core).  The operand read of a 32x32x16 MFMA (lane l: 16 bytes of row
-// l % 32, vector 2 kk + l / 32 of the row) is conflict-free with the row
-// key (r / 4) % 4 (measured at the linear-read rate; without the key it
-// runs at a third of it).  Epilogue from registers after the quad
-// transpose.
+// smaller tiles' load latency starves.  One workgroup per CU: two LDS stages
+// of 64-deep K slices, 128-byte rows (one cache line of each operand row per
+// slice; 64-byte half-line rows measured 10-17 % slower: twice the L1
+// requests per byte), filled by direct-to-LDS loads as in the kernel above
+// while the other stage is multiplied; two waves per SIMD take turns on the
+// matrix core.  The operand read of a 32x32x16 MFMA (lane l: 16 bytes of
+// row l % 32, vector 2 kk + l / 32 of the row) is conflict-free with the
+// row key (r / 2) % 8 (measured at the linear-read rate; without a key it
+// runs at a sixth of it).  Epilogue from registers after the quad transpose.
 constexpr int kWideBM = 256, kWideBN = 256;
 
-__device__ __forceinline__ int wide_key(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ int wide_key(int r) { return (r >> 1) & 7; }
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
@@ -1263,13 +1264,14 @@ __device__ __forceinline__ void lds_wait6(floatx4& a, floatx4& b, floatx4& c, fl
 // RES: 0 no residual, 1 plain, 2 gated (res * res_gate of the row's image).
 template <int RES, int ACT>
 __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
-  constexpr int BM = kWideBM, BN = kWideBN, BK = 32, S = 4;
-  constexpr int WN = 4;
+  constexpr int BM = kWideBM, BN = kWideBN, BK = 64;
+  constexpr int WN = 4;          // 2 x 4 waves of 128x64
   constexpr int TM = 4, TN = 2;  // 32x32 blocks per wave
-  constexpr int STAGE = (BM + BN) * 64;
+  constexpr int STAGE = (BM + BN) * 128;
   constexpr int ES = 2;
-  constexpr int L = 4;  // loads per wave per slice: two A passes, two B passes
-  __shared__ __attribute__((aligned(16))) char lds[S * STAGE];
+  constexpr int PASS = 64;  // rows one load pass of the 512 lanes fills (eight lanes per row)
+  constexpr int AP = BM / PASS, BP = BN / PASS;
+  __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1289,16 +1291,19 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
   const int32x4_t a_rsrc = buffer_resource(p.in, (unsigned)((size_t)p.N * p.H * p.W * p.in_ps * ES));
   const int32x4_t b_rsrc = buffer_resource(p.wt, (unsigned)((size_t)p.Co * p.ldw * ES));
 
-  // Load lanes: a pass of 512 lanes fills 128 rows, four lanes per row; lane
-  // fills row pass * 128 + prow, position lane % 4, with k vector kvec.
-  const int prow = wave * 16 + (lane >> 2);
-  const int kvec = (lane & 3) ^ wide_key(prow);
-  unsigned a_off[2], b_off[2];
+  // Load lanes: lane fills row pass * PASS + prow, position lane % 8, with
+  // k vector kvec of its source row.
+  const int prow = wave * 8 + (lane >> 3);
+  const int kvec = (lane & 7) ^ wide_key(prow);
+  unsigned a_off[AP], b_off[BP];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int m = m0 + i * 128 + prow;
+  for (int i = 0; i < AP; ++i) {
+    const int m = m0 + i * PASS + prow;
     a_off[i] = m < M ? (unsigned)(((size_t)m * p.in_ps + kvec * 8) * ES) : kOutOfRange;
-    const int n = n0 + i * 128 + prow;
+  }
+#pragma unroll
+  for (int i = 0; i < BP; ++i) {
+    const int n = n0 + i * PASS + prow;
     b_off[i] = n < p.Co ? (unsigned)(((size_t)n * p.ldw + kvec * 8) * ES) : kOutOfRange;
   }
   const int nk = (K + BK - 1) / BK;
@@ -1307,10 +1312,11 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
     const unsigned ks = (unsigned)k0 * ES;
     const bool kin = k0 + kvec * 8 < K;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) lds_load16(a_rsrc, kin ? a_off[i] : kOutOfRange, ks, stage(j) + (i * 128 + wave * 16) * 64);
+    for (int i = 0; i < AP; ++i)
+      lds_load16(a_rsrc, kin ? a_off[i] : kOutOfRange, ks, stage(j) + (i * PASS + wave * 8) * 128);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      lds_load16(b_rsrc, kin ? b_off[i] : kOutOfRange, ks, stage(j) + (BM + i * 128 + wave * 16) * 64);
+    for (int i = 0; i < BP; ++i)
+      lds_load16(b_rsrc, kin ? b_off[i] : kOutOfRange, ks, stage(j) + (BM + i * PASS + wave * 8) * 128);
   };
 
   floatx16 acc[TM][TN];
@@ -1321,47 +1327,56 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  // Operand reads: row lane % 32 of each block, vector 2 kk + lane / 32.
+  // Operand reads: row lane % 32 of each block, vector 2 kk + lane / 32 for
+  // k step kk of the slice.  Two fragment sets alternate: the reads of k
+  // step kk + 2 are issued once the MFMAs of step kk are, so they overlap
+  // the MFMAs of step kk + 1 (the scheduling barriers keep each wait after
+  // the MFMAs it follows).
   const int lr = lane & 31;
-  const unsigned a_row = (unsigned)(wm * 128 + lr) * 64, b_row = (unsigned)(BM + wn * 64 + lr) * 64;
-  const unsigned sw0 = (unsigned)((0 + (lane >> 5)) ^ wide_key(lr)) << 4;
-  const unsigned sw1 = (unsigned)((2 + (lane >> 5)) ^ wide_key(lr)) << 4;
+  const unsigned a_row = (unsigned)(wm * 128 + lr) * 128, b_row = (unsigned)(BM + wn * 64 + lr) * 128;
+  unsigned swz[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) swz[kk] = (unsigned)((2 * kk + (lane >> 5)) ^ wide_key(lr)) << 4;
   auto compute = [&](int j) {
     const unsigned base = lds_addr(stage(j));
     floatx4 a0[TM], b0[TN], a1[TM], b1[TN];
+    auto rd = [&](floatx4(&a)[TM], floatx4(&b)[TN], int kk) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) a0[i] = lds_read16(base + a_row + i * 32 * 64 + sw0);
+      for (int i = 0; i < TM; ++i) a[i] = lds_read16(base + a_row + i * 32 * 128 + swz[kk]);
 #pragma unroll
-    for (int q = 0; q < TN; ++q) b0[q] = lds_read16(base + b_row + q * 32 * 64 + sw0);
+      for (int q = 0; q < TN; ++q) b[q] = lds_read16(base + b_row + q * 32 * 128 + swz[kk]);
+    };
+    auto mm = [&](floatx4(&a)[TM], floatx4(&b)[TN]) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) a1[i] = lds_read16(base + a_row + i * 32 * 64 + sw1);
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int q = 0; q < TN; ++q) b1[q] = lds_read16(base + b_row + q * 32 * 64 + sw1);
+        for (int q = 0; q < TN; ++q)
+          acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[i]),
+                                                               __builtin_bit_cast(bf16x8, b[q]), acc[i][q], 0, 0, 0);
+    };
+    rd(a0, b0, 0);
+    rd(a1, b1, 1);
     lds_wait6<6>(a0[0], a0[1], a0[2], a0[3], b0[0], b0[1]);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int q = 0; q < TN; ++q)
-        acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a0[i]),
-                                                             __builtin_bit_cast(bf16x8, b0[q]), acc[i][q], 0, 0, 0);
+    mm(a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    rd(a0, b0, 2);
+    lds_wait6<6>(a1[0], a1[1], a1[2], a1[3], b1[0], b1[1]);
+    mm(a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    rd(a1, b1, 3);
+    lds_wait6<6>(a0[0], a0[1], a0[2], a0[3], b0[0], b0[1]);
+    mm(a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
     lds_wait6<0>(a1[0], a1[1], a1[2], a1[3], b1[0], b1[1]);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int q = 0; q < TN; ++q)
-        acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a1[i]),
-                                                             __builtin_bit_cast(bf16x8, b1[q]), acc[i][q], 0, 0, 0);
+    mm(a1, b1);
   };
-  auto step = [&](int cur, int refill, int s) {
-    const int after = nk - 1 - s;
-    if (after >= S - 2)
-      wait_vmcnt<(S - 2) * L>();
-    else if (after == 1)
-      wait_vmcnt<L>();
-    else
-      wait_vmcnt<0>();
+  // Slice s: wait for its loads (the only ones in flight), barrier (every
+  // wave's loads of slice s are in LDS and every wave is done reading slice
+  // s - 1), load slice s + 1 into the stage slice s - 1 used, multiply.
+  auto step = [&](int cur, int s) {
+    wait_vmcnt<0>();
     stage_barrier();
-    if (s + S - 1 < nk) issue(refill, (s + S - 1) * BK);
+    if (s + 1 < nk) issue(cur ^ 1, (s + 1) * BK);
     compute(cur);
   };
 
@@ -1372,13 +1387,9 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
   for (int q = 0; q < TN; ++q) bias_pre[q] = bias4(p, n0 + wn * 64 + q * 32 + ccol);
 
   issue(0, 0);
-  if (nk > 1) issue(1, BK);
-  if (nk > 2) issue(2, 2 * BK);
-  for (int s = 0; s < nk; s += S) {
-    step(0, 3, s);
-    if (s + 1 < nk) step(1, 0, s + 1);
-    if (s + 2 < nk) step(2, 1, s + 2);
-    if (s + 3 < nk) step(3, 2, s + 3);
+  for (int s = 0; s < nk; s += 2) {
+    step(0, s);
+    if (s + 1 < nk) step(1, s + 1);
   }
   wait_vmcnt<0>();
 

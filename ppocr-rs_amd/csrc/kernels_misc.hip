@@ -1354,8 +1354,54 @@ __global__ __launch_bounds__(1024) void softmax_rows_kernel(float* x, int cols) 
   for (int i = threadIdx.x; i < cols; i += blockDim.x) row[i] = fast_exp(row[i] - m) * rcp;
 }
 
+// Even row lengths up to 2048 * PER (the recognizers' 6.9k-18.7k classes):
+// the row is read once into registers (PER float2 per thread; rows are
+// 8-byte aligned), so it crosses HBM once each way instead of being read
+// for the maximum, again for the sum and again for the store.
+template <int PER>
+__global__ __launch_bounds__(1024) void softmax_rows_reg_kernel(float* x, int cols) {
+  __shared__ float red[16];
+  float2* row = reinterpret_cast<float2*>(x + (size_t)blockIdx.x * cols);
+  const int n2 = cols >> 1;
+  float2 v[PER];
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = threadIdx.x + j * 1024;
+    v[j] = i < n2 ? row[i] : make_float2(-INFINITY, -INFINITY);
+    m = fmaxf(m, fmaxf(v[j].x, v[j].y));
+  }
+  m = block_reduce(m, red, true);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    if (threadIdx.x + j * 1024 < n2) {
+      v[j].x = fast_exp(v[j].x - m);
+      v[j].y = fast_exp(v[j].y - m);
+      s += v[j].x + v[j].y;
+    }
+  }
+  s = block_reduce(s, red, false);
+  const float rcp = 1.0f / s;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = threadIdx.x + j * 1024;
+    if (i < n2) row[i] = make_float2(v[j].x * rcp, v[j].y * rcp);
+  }
+}
+
 void launch_softmax_rows(float* x, long rows, int cols, hipStream_t s) {
-  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(1024), 0, s, x, cols);
+  const int per = (cols / 2 + 1023) / 1024;
+  const bool even = cols % 2 == 0 && reinterpret_cast<uintptr_t>(x) % 8 == 0;
+  const dim3 grid((unsigned)rows), block(1024);
+  if (even && per <= 4)
+    hipLaunchKernelGGL(softmax_rows_reg_kernel<4>, grid, block, 0, s, x, cols);
+  else if (even && per <= 10)
+    hipLaunchKernelGGL(softmax_rows_reg_kernel<10>, grid, block, 0, s, x, cols);
+  else if (even && per <= 16)
+    hipLaunchKernelGGL(softmax_rows_reg_kernel<16>, grid, block, 0, s, x, cols);
+  else
+    hipLaunchKernelGGL(softmax_rows_kernel, grid, block, 0, s, x, cols);
 }
 
 // ------------------------------------------------------------ greedy CTC merge
