@@ -936,18 +936,30 @@ enum DirectEpi : int {
   EPI_DB = 2,    // finish_db_regs (DB head tail)
 };
 
-template <typename T, int BM, int BN, int WM, int WN, bool PW, int S, bool GATE, int EPI>
+// RB: bytes of one operand row per K slice, 64 (half a cache line, key
+// swizzle_key) or 128 (a whole line, key direct_key<128>).
+template <int RB>
+__device__ __forceinline__ int direct_key(int r) {
+  return RB == 64 ? swizzle_key(r) : (r >> 1) & 7;
+}
+
+template <typename T, int BM, int BN, int WM, int WN, bool PW, int S, bool GATE, int EPI, int RB = 64>
 __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
-  constexpr int BK = GemmTraits<T>::BK;  // one 64-byte row per K slice
+  constexpr int BK = RB / sizeof(T);  // k values of one row per K slice
   constexpr int VE = 16 / sizeof(T);
   constexpr int TM = BM / (WM * 16);
   constexpr int TN = BN / (WN * 16);
+  constexpr int LPR = RB / 16;     // load lanes per row
+  constexpr int RPW = 64 / LPR;    // rows a wave fills per pass
+  constexpr int RPP = 4 * RPW;     // rows a pass fills
+  constexpr int H = RB / 64;       // 64-byte sub-slices (MFMA k steps of 16 fp32 / 32 bf16)
   static_assert(WM * WN == 4, "four waves per block");
-  static_assert(BM % 64 == 0, "A rows load in passes of 64");
+  static_assert(BM % RPP == 0, "A rows load in whole passes");
   static_assert(S == 3 || S == 4, "three or four stages");
-  constexpr int A_PASS = BM / 64;
-  constexpr int B_PASS = (BN + 63) / 64;
-  constexpr int STAGE_BYTES = (BM + BN) * 64;
+  static_assert(RB == 64 || RB == 128, "64- or 128-byte rows");
+  constexpr int A_PASS = BM / RPP;
+  constexpr int B_PASS = (BN + RPP - 1) / RPP;
+  constexpr int STAGE_BYTES = (BM + BN) * RB;
   constexpr int LDE = BN + 4;
   constexpr int RPA = (BM + S - 1) / S;  // epilogue rows staged per stage array
   // The LDS epilogue stages the tile across the stage arrays; the others
@@ -1002,11 +1014,11 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   const int32x4_t a_rsrc = buffer_resource(p.in, (unsigned)((size_t)p.N * p.H * p.W * p.in_ps * ES));
   const int32x4_t b_rsrc = buffer_resource(p.wt, (unsigned)((size_t)p.Co * p.ldw * ES));
 
-  // This lane fills LDS row pass*64 + prow, position lane % 4, with k vector
-  // kvec of its source row: position ^ swizzle_key(row), where prow % 16 is
-  // (lane >> 2) & 15.
-  const int prow = wave * 16 + (lane >> 2);
-  const int kvec = (lane & 3) ^ swizzle_key((lane >> 2) & 15);
+  // This lane fills LDS row pass * RPP + prow, position lane % LPR, with k
+  // vector kvec of its source row: position ^ direct_key(row) (the key
+  // depends on the row's low four bits only, and RPP is a multiple of 16).
+  const int prow = wave * RPW + lane / LPR;
+  const int kvec = (lane % LPR) ^ direct_key<RB>(prow);
 
   // Byte offsets of this lane's rows in the buffers (kOutOfRange for rows
   // past M or Co).  1x1: the row's k vector kvec, the slice's k0 goes in the
@@ -1015,7 +1027,7 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   int a_iy0[A_PASS], a_ix0[A_PASS];
 #pragma unroll
   for (int i = 0; i < A_PASS; ++i) {
-    const int m = m0 + i * 64 + prow;
+    const int m = m0 + i * RPP + prow;
     const bool ok = m < M;
     const int mm = ok ? m : 0;
     const int img = mm / HoWo;
@@ -1034,7 +1046,7 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   unsigned b_off[B_PASS];
 #pragma unroll
   for (int i = 0; i < B_PASS; ++i) {
-    const int r = i * 64 + prow;
+    const int r = i * RPP + prow;
     const int n = n0 + r;
     b_off[i] = r < BN && n < p.Co ? (unsigned)(((size_t)n * p.ldw + kvec * VE) * ES) : kOutOfRange;
   }
@@ -1063,7 +1075,7 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
     const bool kin = !TAIL || k0 + kvec * VE < K;
 #pragma unroll
     for (int i = 0; i < A_PASS; ++i) {
-      char* dst = stage + (i * 64 + wave * 16) * 64;
+      char* dst = stage + (i * RPP + wave * RPW) * RB;
       if constexpr (PW) {
         lds_load16(a_rsrc, kin ? a_off[i] : kOutOfRange, ks, dst);
       } else {
@@ -1076,7 +1088,8 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
     }
 #pragma unroll
     for (int i = 0; i < B_PASS; ++i)
-      if (i * 64 + wave * 16 < BN) lds_load16(b_rsrc, kin ? b_off[i] : kOutOfRange, ks, stage + (BM + i * 64 + wave * 16) * 64);
+      if (i * RPP + wave * RPW < BN)
+        lds_load16(b_rsrc, kin ? b_off[i] : kOutOfRange, ks, stage + (BM + i * RPP + wave * RPW) * RB);
   };
   auto issue = [&](int j, int k0) {
     if (k0 + BK > K)
@@ -1101,68 +1114,91 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  const int swz = (g ^ swizzle_key(lrow)) << 4;  // byte offset of this lane's vector in its row
+  // Byte offset of this lane's vector in its row for sub-slice h: vector
+  // g + 4 h (lane l reads vector l / 16 of row l % 16 in each 64-byte half).
+  int swz[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) swz[h] = ((g + 4 * h) ^ direct_key<RB>(lrow)) << 4;
 
   // Operand reads go through lds_read16 (outside the compiler's view): the
   // compiler cannot tell the stage being read from the stages being filled
   // by the loads in flight and would otherwise wait for all of them before
-  // every LDS read, draining the pipeline.
+  // every LDS read, draining the pipeline.  All sub-slices' reads are issued
+  // before the first wait.
   auto compute = [&](int j, int k0) {
     const unsigned stage = lds_addr(pick(j));
-    floatx4 ra[TM], rb[TN], gv[TM];
+    floatx4 ra[H][TM], rb[H][TN], gv[H][TM];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) ra[i] = lds_read16(stage + (wm * TM * 16 + i * 16 + lrow) * 64 + swz);
+    for (int h = 0; h < H; ++h) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) rb[j] = lds_read16(stage + (BM + wn * TN * 16 + j * 16 + lrow) * 64 + swz);
+      for (int i = 0; i < TM; ++i) ra[h][i] = lds_read16(stage + (wm * TM * 16 + i * 16 + lrow) * RB + swz[h]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) rb[h][j] = lds_read16(stage + (BM + wn * TN * 16 + j * 16 + lrow) * RB + swz[h]);
+    }
     if constexpr (GATE) {
-      // This lane's A values are k0 + 4g .. k0 + 4g + 3 of its row.
+      // This lane's A values of sub-slice h are k0 + 16 h + 4g .. + 3 of its row.
 #pragma unroll
-      for (int i = 0; i < TM; ++i) gv[i] = lds_read16(lds_addr(gate_lds) + (g_sel[i] + k0 + 4 * g) * 4);
+      for (int h = 0; h < H; ++h)
 #pragma unroll
-      for (int i = 0; i < TM; ++i) lds_wait(gv[i]);
+        for (int i = 0; i < TM; ++i) gv[h][i] = lds_read16(lds_addr(gate_lds) + (g_sel[i] + k0 + 16 * h + 4 * g) * 4);
+#pragma unroll
+      for (int h = 0; h < H; ++h)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) lds_wait(gv[h][i]);
     }
 #pragma unroll
-    for (int i = 0; i < TM; ++i) lds_wait(ra[i]);
+    for (int h = 0; h < H; ++h) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) lds_wait(rb[j]);
-    if constexpr (sizeof(T) == 4) {
-      float4 a[TM], b[TN];
+      for (int i = 0; i < TM; ++i) lds_wait(ra[h][i]);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) a[i] = make_float4(ra[i][0], ra[i][1], ra[i][2], ra[i][3]);
-      if constexpr (GATE) {
+      for (int j = 0; j < TN; ++j) lds_wait(rb[h][j]);
+    }
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      if constexpr (sizeof(T) == 4) {
+        float4 a[TM], b[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) a[i] = make_float4(ra[h][i][0], ra[h][i][1], ra[h][i][2], ra[h][i][3]);
+        if constexpr (GATE) {
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+            a[i] = make_float4(__fmul_rn(a[i].x, gv[h][i][0]), __fmul_rn(a[i].y, gv[h][i][1]),
+                               __fmul_rn(a[i].z, gv[h][i][2]), __fmul_rn(a[i].w, gv[h][i][3]));
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) b[j] = make_float4(rb[h][j][0], rb[h][j][1], rb[h][j][2], rb[h][j][3]);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
-          a[i] = make_float4(__fmul_rn(a[i].x, gv[i][0]), __fmul_rn(a[i].y, gv[i][1]), __fmul_rn(a[i].z, gv[i][2]),
-                             __fmul_rn(a[i].w, gv[i][3]));
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
+      } else {
+        bf16x8 a[TM], b[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) a[i] = __builtin_bit_cast(bf16x8, ra[h][i]);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) b[j] = __builtin_bit_cast(bf16x8, rb[h][j]);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
       }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) b[j] = make_float4(rb[j][0], rb[j][1], rb[j][2], rb[j][3]);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
-    } else {
-      bf16x8 a[TM], b[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) a[i] = __builtin_bit_cast(bf16x8, ra[i]);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) b[j] = __builtin_bit_cast(bf16x8, rb[j]);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
   };
 
@@ -1171,10 +1207,10 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   // is done with slice s-1), refill the stage slice s-1 used with slice
   // s+S-1, multiply slice s.
   // Loads per wave per slice counted by the waits: the A passes, plus the B
-  // passes when every wave takes part in them (BN >= 64).  With BN < 64 only
-  // some waves load B; counting A alone makes those waves wait a little
+  // passes when every wave takes part in them (BN >= RPP).  With BN < RPP
+  // only some waves load B; counting A alone makes those waves wait a little
   // longer than needed, never less.
-  constexpr int L = A_PASS + (BN >= 64 ? B_PASS : 0);
+  constexpr int L = A_PASS + (BN >= RPP ? B_PASS : 0);
   auto step = [&](int cur, int refill, int s) {
     const int after = nk - 1 - s;  // slices issued after s (capped at S - 2)
     if (after >= S - 2)
@@ -1262,7 +1298,9 @@ __device__ __forceinline__ void lds_wait6(floatx4& a, floatx4& b, floatx4& c, fl
 }
 
 // RES: 0 no residual, 1 plain, 2 gated (res * res_gate of the row's image).
-template <int RES, int ACT>
+// F32OUT: fp32 output stored as float2 pairs (Co and out_ps even: the
+// recognizer's classifier logits, 18710 columns, rows 8-byte aligned).
+template <int RES, int ACT, bool F32OUT = false>
 __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
   constexpr int BM = kWideBM, BN = kWideBN, BK = 64;
   constexpr int WN = 4;          // 2 x 4 waves of 128x64
@@ -1380,11 +1418,17 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
     compute(cur);
   };
 
-  // Bias of this lane's two column groups (see the epilogue), loaded ahead.
+  // Bias of this lane's two column groups (see the epilogue), loaded ahead
+  // (a group with only two columns left in an even Co takes those two).
   const int ccol = 4 * (lr >> 2);
   float4 bias_pre[TN];
 #pragma unroll
-  for (int q = 0; q < TN; ++q) bias_pre[q] = bias4(p, n0 + wn * 64 + q * 32 + ccol);
+  for (int q = 0; q < TN; ++q) {
+    const int col = n0 + wn * 64 + q * 32 + ccol;
+    bias_pre[q] = bias4(p, col);
+    if (F32OUT && p.bias && col + 1 < p.Co && col + 3 >= p.Co)
+      bias_pre[q] = make_float4(p.bias[col], p.bias[col + 1], 0.f, 0.f);
+  }
 
   issue(0, 0);
   for (int s = 0; s < nk; s += 2) {
@@ -1436,7 +1480,13 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
         x.z = act_apply(ACT, x.z);
         x.w = act_apply(ACT, x.w);
         if constexpr (RES != 0) x = f4_add(r[q], x);
-        if (m < M && col < p.Co) st4<bf16>(static_cast<bf16*>(p.out) + (size_t)m * p.out_ps + col, x);
+        if constexpr (F32OUT) {
+          float* o = static_cast<float*>(p.out) + (size_t)m * p.out_ps + col;
+          if (m < M && col < p.Co) *reinterpret_cast<float2*>(o) = make_float2(x.x, x.y);
+          if (m < M && col + 2 < p.Co) *reinterpret_cast<float2*>(o + 2) = make_float2(x.z, x.w);
+        } else if (m < M && col < p.Co) {
+          st4<bf16>(static_cast<bf16*>(p.out) + (size_t)m * p.out_ps + col, x);
+        }
       }
     }
 }
@@ -1527,6 +1577,16 @@ static bool regs_epilogue(const ConvParams& p) {
   return p.Co % 4 == 0 && p.out_ps % 4 == 0 && p.rep == 1 && (p.dt == DT_F32 || K <= 512);
 }
 
+// bf16 64x64 1x1 layers of deep K and at least 512 output channels (the
+// detector's 13x23 and 26x46 levels) stage whole 128-byte rows (three
+// stages): 1.06-1.1x per layer in the detector plan; shallower K, the
+// other tiles and fp32 measured slower with the larger LDS footprint (fewer
+// workgroups per CU), and so did the recognizer's 192-channel K = 768
+// layers.
+static bool rows128_layer(const ConvParams& p) {
+  return p.dt == DT_BF16 && p.C >= 768 && p.Co >= 512 && p.splits <= 1 && !p.db_ch && !p.ctc_part;
+}
+
 template <typename T, int BM, int BN, int WM, int WN>
 static void launch_tile_kernel(const ConvParams& p, dim3 grid, hipStream_t s) {
   // Stages: fp32 slices take long enough on the MFMAs that three cover the
@@ -1537,6 +1597,13 @@ static void launch_tile_kernel(const ConvParams& p, dim3 grid, hipStream_t s) {
   const bool regs = regs_epilogue(p);
   switch (conv_variant(p, BM)) {
     case CV_DIRECT_1X1:
+      if constexpr (sizeof(T) == 2 && BM == 64 && BN == 64) {
+        if (rows128_layer(p)) {  // K >= 768: the LDS epilogue (regs_epilogue)
+          hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, 3, false, EPI_LDS, 128>), grid,
+                             dim3(256), 0, s, p);
+          break;
+        }
+      }
       if (regs && p.db_ch)
         hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, false, EPI_DB>), grid, dim3(256), 0,
                            s, p);
@@ -1619,16 +1686,25 @@ static void launch_tile(const ConvParams& p, int M, hipStream_t s) {
 // output channels, where half of each tile is empty.
 constexpr int kWideMinTiles = 128, kWideMinK = 512, kWideMinCo = 256;
 
-static bool wide_shape(int M, int Co, int K, int dt) {
+// Layers with an fp32 output (the recognizer's classifier logits: even Co,
+// K >= 128, no residual) take the kernel from K = 128 on: their store
+// stream bounds them, and the float2 register epilogue writes it 1.9x faster
+// than the LDS epilogue the other kernels need for a Co that is not a
+// multiple of 4 (18710 x 192 classifier: 486 -> 252 us in isolation).
+constexpr int kWideMinKF32 = 128;
+
+static bool wide_shape(int M, int Co, int K, int dt, bool f32out = false) {
   const long tiles = (long)((M + kWideBM - 1) / kWideBM) * ((Co + kWideBN - 1) / kWideBN);
-  return dt == DT_BF16 && Co % 4 == 0 && Co >= kWideMinCo && K >= kWideMinK && tiles >= kWideMinTiles;
+  return dt == DT_BF16 && Co % (f32out ? 2 : 4) == 0 && Co >= kWideMinCo && K >= (f32out ? kWideMinKF32 : kWideMinK) &&
+         tiles >= kWideMinTiles;
 }
 
 static bool wide_layer(const ConvParams& p) {
   const bool act = p.act == ACT_NONE || p.act == ACT_RELU || p.act == ACT_HSWISH || p.act == ACT_GELU;
-  return act && wide_shape(p.N * p.Ho * p.Wo, p.Co, p.C, p.dt) && conv_variant(p, 128) == CV_DIRECT_1X1 &&
-         (!p.res_gate || p.res) && !p.up && p.rep == 1 && !p.out_f32 && !p.ctc_part && !p.db_ch && p.splits <= 1 &&
-         p.out_ps % 4 == 0 && (!p.res || p.res_ps % 4 == 0);
+  const bool f32 = p.out_f32 != 0;
+  return act && wide_shape(p.N * p.Ho * p.Wo, p.Co, p.C, p.dt, f32) && conv_variant(p, 128) == CV_DIRECT_1X1 &&
+         (!p.res_gate || p.res) && !p.up && p.rep == 1 && !(f32 && p.res) && !p.ctc_part && !p.db_ch &&
+         p.splits <= 1 && p.out_ps % (f32 ? 2 : 4) == 0 && (!p.res || p.res_ps % 4 == 0);
 }
 
 // Tile choice: narrow output channel counts get tall tiles so no MFMA
@@ -1649,8 +1725,10 @@ std::string conv_kernel_name(const ConvParams& p) {
   static const int bm[] = {256, 128, 128, 64};
   static const char* variants[] = {",1x1", "", ",1x1,gate", ",1x1,reg", ",reg", ",1x1,reg4", ",reg4"};
   const int t = pick_tile(p.N * p.Ho * p.Wo, p.Co, p.dt);
-  return std::string(p.dt == DT_BF16 ? "conv_gemm_bf16<" : "conv_gemm<") + tiles[t] +
-         variants[conv_variant(p, bm[t])] + ">";
+  const int v = conv_variant(p, bm[t]);
+  const bool r128 = t == 3 && v == CV_DIRECT_1X1 && rows128_layer(p);
+  return std::string(p.dt == DT_BF16 ? "conv_gemm_bf16<" : "conv_gemm<") + tiles[t] + variants[v] +
+         (r128 ? ",r128" : "") + ">";
 }
 
 int conv_tile_cols(int M, int cols, int dt) {
@@ -1694,7 +1772,13 @@ static void launch_typed(const ConvParams& p, hipStream_t s) {
       const long tiles = (long)((M + kWideBM - 1) / kWideBM) * ((p.Co + kWideBN - 1) / kWideBN);
       const dim3 grid((unsigned)((tiles + 7) / 8 * 8));
       auto go = [&](auto res, auto act) {
-        hipLaunchKernelGGL((conv1x1_wide_kernel<decltype(res)::value, decltype(act)::value>), grid, dim3(512), 0, s, p);
+        if (p.out_f32) {
+          if constexpr (decltype(res)::value == 0)
+            hipLaunchKernelGGL((conv1x1_wide_kernel<0, decltype(act)::value, true>), grid, dim3(512), 0, s, p);
+        } else {
+          hipLaunchKernelGGL((conv1x1_wide_kernel<decltype(res)::value, decltype(act)::value>), grid, dim3(512), 0, s,
+                             p);
+        }
       };
       auto with_act = [&](auto res) {
         switch (p.act) {

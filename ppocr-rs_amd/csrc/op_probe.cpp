@@ -152,11 +152,11 @@ int ppocr_probe_conv_rep(const float* x, int n, int h, int w, int c, const float
 
 // 1x1 conv with a residual in storage type dt: x [n][h][w][c], weight
 // [co][c], bias [co], res [n][h][w][co] (or null), res_gate [n][co] (or
-// null: plain residual): y = res * res_gate + act(x W^T + b).  `kernel`
-// (if not null) receives the kernel instance's name.  Returns 0, or 1 on a
-// HIP error.
+// null: plain residual): y = res * res_gate + act(x W^T + b), stored in dt,
+// or in fp32 with out_f32.  `kernel` (if not null) receives the kernel
+// instance's name.  Returns 0, or 1 on a HIP error.
 int ppocr_probe_conv1x1_res(const float* x, int n, int h, int w, int c, const float* weight, const float* bias, int co,
-                            int act, const float* res, const float* res_gate, int dt, float* out,
+                            int act, const float* res, const float* res_gate, int dt, int out_f32, float* out,
                             const char** kernel) {
   static thread_local std::string name;
   const size_t M = (size_t)n * h * w;
@@ -166,7 +166,7 @@ int ppocr_probe_conv1x1_res(const float* x, int n, int h, int w, int c, const fl
   void* d_res = res ? upload(res, M * co, dt) : nullptr;
   void* d_rg = res_gate ? upload(res_gate, (size_t)n * co, ppocr::DT_F32) : nullptr;
   void* d_out = nullptr;
-  const size_t es = dt == ppocr::DT_BF16 ? 2 : 4;
+  const size_t es = dt == ppocr::DT_BF16 && !out_f32 ? 2 : 4;
   int rc = 0;
   if (!d_in || !d_wt || !d_bias || (res && !d_res) || (res_gate && !d_rg) ||
       hipMalloc(&d_out, M * co * es) != hipSuccess) {
@@ -189,13 +189,14 @@ int ppocr_probe_conv1x1_res(const float* x, int n, int h, int w, int c, const fl
     p.rep = 1;
     p.out_h = h, p.out_w = w;
     p.dt = dt;
+    p.out_f32 = out_f32 && dt != ppocr::DT_F32;
     p.splits = 1;
     name = ppocr::conv_kernel_name(p);
     if (kernel) *kernel = name.c_str();
     ppocr::launch_conv(p, nullptr);
     if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess) rc = 1;
     if (rc == 0) {
-      if (dt == ppocr::DT_BF16) {
+      if (es == 2) {
         std::vector<uint16_t> hb(M * co);
         if (hipMemcpy(hb.data(), d_out, hb.size() * 2, hipMemcpyDeviceToHost) != hipSuccess) rc = 1;
         for (size_t i = 0; i < hb.size(); ++i) out[i] = from_bf16(hb[i]);

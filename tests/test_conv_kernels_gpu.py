@@ -99,6 +99,8 @@ CASES = [
      "conv_gemm_bf16<64x64,1x1,reg>"),
     ("bf16 split K", 1, 7, 5, 256, 64, (1, 1), (1, 1), (0, 0, 0, 0), False, 2, 1, ACT_RELU,
      "conv_gemm_bf16<64x64,1x1>"),
+    ("bf16 128-byte rows", 1, 37, 41, 776, 520, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 1, ACT_HSWISH,
+     "conv_gemm_bf16<64x64,1x1,r128>"),
 ]
 
 
@@ -292,25 +294,28 @@ def test_upsample_on_write_matches_float64(name, n, h, w, c, co, rep):
 
 # Wide-tile bf16 1x1 kernel (256x256 tiles of 32x32x16 MFMAs): M, N and K
 # tails, plain and gated residual, and a layer just below its K threshold.
-# (name, n, h, w, c, co, act, residual: 0 none / 1 plain / 2 gated, kernel)
+# (name, n, h, w, c, co, act, residual: 0 none / 1 plain / 2 gated, fp32 output, kernel)
 ACT_GELU = 2
 WIDE_CASES = [
-    ("wide M/N/K tails", 2, 65, 127, 520, 516, ACT_HSWISH, 0, "conv_gemm_bf16<256x256,1x1>"),
-    ("wide residual", 1, 130, 127, 512, 512, ACT_NONE, 1, "conv_gemm_bf16<256x256,1x1>"),
-    ("wide gated residual", 4, 33, 128, 768, 260, ACT_GELU, 2, "conv_gemm_bf16<256x256,1x1>"),
-    ("K below threshold", 2, 65, 127, 256, 516, ACT_RELU, 1, "conv_gemm_bf16<64x64,1x1>"),
+    ("wide M/N/K tails", 2, 65, 127, 520, 516, ACT_HSWISH, 0, False, "conv_gemm_bf16<256x256,1x1>"),
+    ("wide residual", 1, 130, 127, 512, 512, ACT_NONE, 1, False, "conv_gemm_bf16<256x256,1x1>"),
+    ("wide gated residual", 4, 33, 128, 768, 260, ACT_GELU, 2, False, "conv_gemm_bf16<256x256,1x1>"),
+    ("K below threshold", 2, 65, 127, 256, 516, ACT_RELU, 1, False, "conv_gemm_bf16<64x64,1x1>"),
+    # The classifier form: fp32 logits, Co % 4 == 2 (float2 stores), short K.
+    ("wide fp32 out, Co % 4 = 2", 1, 61, 110, 200, 1030, ACT_NONE, 0, True, "conv_gemm_bf16<256x256,1x1>"),
 ]
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name,n,h,w,c,co,kind,residual,want_kernel", WIDE_CASES, ids=[c[0] for c in WIDE_CASES])
-def test_wide_bf16_1x1_matches_float64(name, n, h, w, c, co, kind, residual, want_kernel):
+@pytest.mark.parametrize("name,n,h,w,c,co,kind,residual,f32out,want_kernel", WIDE_CASES,
+                         ids=[c[0] for c in WIDE_CASES])
+def test_wide_bf16_1x1_matches_float64(name, n, h, w, c, co, kind, residual, f32out, want_kernel):
     from scipy.special import erf
 
     lib = _lib()
     f = ctypes.POINTER(ctypes.c_float)
     i = ctypes.c_int
-    lib.ppocr_probe_conv1x1_res.argtypes = [f, i, i, i, i, f, f, i, i, f, f, i, f, ctypes.POINTER(ctypes.c_char_p)]
+    lib.ppocr_probe_conv1x1_res.argtypes = [f, i, i, i, i, f, f, i, i, f, f, i, i, f, ctypes.POINTER(ctypes.c_char_p)]
     lib.ppocr_probe_conv1x1_res.restype = i
     rng = np.random.default_rng(zlib.crc32(name.encode()))
     x = rng.standard_normal((n, h, w, c)).astype(np.float32)
@@ -321,7 +326,7 @@ def test_wide_bf16_1x1_matches_float64(name, n, h, w, c, co, kind, residual, wan
     out = np.empty((n, h, w, co), dtype=np.float32)
     kernel = ctypes.c_char_p()
     assert lib.ppocr_probe_conv1x1_res(_ptr(x), n, h, w, c, _ptr(wt), _ptr(b), co, kind, _ptr(res), _ptr(rg), 1,
-                                       _ptr(out), ctypes.byref(kernel)) == 0
+                                       int(f32out), _ptr(out), ctypes.byref(kernel)) == 0
     assert kernel.value.decode() == want_kernel, f"{name}: runs {kernel.value.decode()}"
 
     y = bf16_round(x).astype(np.float64).reshape(-1, c) @ bf16_round(wt).astype(np.float64).T + b
@@ -335,6 +340,8 @@ def test_wide_bf16_1x1_matches_float64(name, n, h, w, c, co, kind, residual, wan
         if residual == 2:
             r = r * rg[:, None, None, :]
         y = y + r
-    tol = 1e-3 + 8e-3 * np.abs(y)
+    # bf16 storage rounds the output (2^-9 relative); fp32 logits keep only
+    # the fp32 accumulation error.
+    tol = 1e-3 + (1e-5 if f32out else 8e-3) * np.abs(y)
     err = np.abs(out - y)
     assert np.all(err <= tol), f"{name} ({want_kernel}): max abs diff {err.max():.3e}"
