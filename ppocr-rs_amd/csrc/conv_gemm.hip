@@ -1441,8 +1441,9 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
   // other epilogue terms to the other kernels.  Block element e of lane l is row
   // 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32; after the quad transpose
   // of elements 4 g .. 4 g + 3, lane l holds row 8 g + 4 (l / 32) + l % 4,
-  // columns 4 ((l % 32) / 4) .. + 3: a store writes 64 contiguous bytes of
-  // eight rows.
+  // columns 4 ((l % 32) / 4) .. + 3 of each 32-column block.  (Trading
+  // halves between lanes l and l ^ 4 so that each lane stores 16 bytes and
+  // each row segment is a whole cache line measured no faster.)
   const int rsub = 4 * (lane >> 5) + (lane & 3);
   const bool has_bias = p.bias != nullptr;
 #pragma unroll
@@ -1470,9 +1471,9 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
           }
         }
       }
+      float4 xs[TN];
 #pragma unroll
       for (int q = 0; q < TN; ++q) {
-        const int col = n0 + wn * 64 + q * 32 + ccol;
         float4 x = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
         if (has_bias) x = f4_add(x, bias_pre[q]);
         x.x = act_apply(ACT, x.x);
@@ -1480,12 +1481,21 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
         x.z = act_apply(ACT, x.z);
         x.w = act_apply(ACT, x.w);
         if constexpr (RES != 0) x = f4_add(r[q], x);
-        if constexpr (F32OUT) {
+        xs[q] = x;
+      }
+      if constexpr (F32OUT) {
+#pragma unroll
+        for (int q = 0; q < TN; ++q) {
+          const int col = n0 + wn * 64 + q * 32 + ccol;
           float* o = static_cast<float*>(p.out) + (size_t)m * p.out_ps + col;
-          if (m < M && col < p.Co) *reinterpret_cast<float2*>(o) = make_float2(x.x, x.y);
-          if (m < M && col + 2 < p.Co) *reinterpret_cast<float2*>(o + 2) = make_float2(x.z, x.w);
-        } else if (m < M && col < p.Co) {
-          st4<bf16>(static_cast<bf16*>(p.out) + (size_t)m * p.out_ps + col, x);
+          if (m < M && col < p.Co) *reinterpret_cast<float2*>(o) = make_float2(xs[q].x, xs[q].y);
+          if (m < M && col + 2 < p.Co) *reinterpret_cast<float2*>(o + 2) = make_float2(xs[q].z, xs[q].w);
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < TN; ++q) {
+          const int col = n0 + wn * 64 + q * 32 + ccol;
+          if (m < M && col < p.Co) st4<bf16>(static_cast<bf16*>(p.out) + (size_t)m * p.out_ps + col, xs[q]);
         }
       }
     }
@@ -1678,13 +1688,16 @@ static void launch_tile(const ConvParams& p, int M, hipStream_t s) {
 // gate, at least 256 output channels and K >= 512, whose 256x256 tiles
 // number at least 128 (shape test, shared with the planner's split choice),
 // with at most the bias, one of the activations the kernel is built for and
-// a (gated) residual in the epilogue.  Measured against the 128x64 / 64x64
-// kernel inside the recognizer and detector plans: 1.07-1.37x at K = 512 to
-// 1536, about even at K = 256 and 0.91-0.93x at K = 128 (a CU holds one
-// wide tile, so nothing overlaps its short K loop's ramp and its epilogue);
-// on isolated layers 0.57-0.85x on 70-76 tiles and 0.72-0.74x with 128
-// output channels, where half of each tile is empty.
+// a (gated) residual in the epilogue; K = 256 only with at least 480
+// tiles.  Measured against the 128x64 / 64x64 kernel inside the recognizer
+// and detector plans: 1.07-1.37x at K = 512 to 1536; at K = 256 1.1x on the
+// recognizer's 960-tile layers but 0.92x on the detector's 300-tile ones, and
+// 0.91-0.93x at K = 128 (a CU holds one wide tile, so nothing overlaps its
+// short K loop's ramp and its epilogue); on isolated layers 0.57-0.85x on
+// 70-76 tiles and 0.72-0.74x with 128 output channels, where half of each
+// tile is empty.
 constexpr int kWideMinTiles = 128, kWideMinK = 512, kWideMinCo = 256;
+constexpr int kWideMinKShort = 256, kWideMinTilesShort = 480;
 
 // Layers with an fp32 output (the recognizer's classifier logits: even Co,
 // K >= 128, no residual) take the kernel from K = 128 on: their store
@@ -1695,8 +1708,8 @@ constexpr int kWideMinKF32 = 128;
 
 static bool wide_shape(int M, int Co, int K, int dt, bool f32out = false) {
   const long tiles = (long)((M + kWideBM - 1) / kWideBM) * ((Co + kWideBN - 1) / kWideBN);
-  return dt == DT_BF16 && Co % (f32out ? 2 : 4) == 0 && Co >= kWideMinCo && K >= (f32out ? kWideMinKF32 : kWideMinK) &&
-         tiles >= kWideMinTiles;
+  const bool deep = f32out ? K >= kWideMinKF32 : K >= kWideMinK || (K >= kWideMinKShort && tiles >= kWideMinTilesShort);
+  return dt == DT_BF16 && Co % (f32out ? 2 : 4) == 0 && Co >= kWideMinCo && deep && tiles >= kWideMinTiles;
 }
 
 static bool wide_layer(const ConvParams& p) {
