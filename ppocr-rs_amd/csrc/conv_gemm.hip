@@ -1446,8 +1446,31 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
   // each row segment is a whole cache line measured no faster.)
   const int rsub = 4 * (lane >> 5) + (lane & 3);
   const bool has_bias = p.bias != nullptr;
+  // Row block by row block: the residual (and gate) loads of a block's four
+  // row groups are all issued before its first store (a load cannot move
+  // above a store that may alias it, so issued group by group each would
+  // wait a full memory latency).
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < TM; ++i) {
+    uint2 rraw[4][TN];
+    float4 rgate[4][TN];
+    if constexpr (RES != 0) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int m = m0 + wm * 128 + i * 32 + 8 * g + rsub;
+        const int img = RES == 2 ? min(m, M - 1) / (p.Ho * p.Wo) : 0;
+#pragma unroll
+        for (int q = 0; q < TN; ++q) {
+          const int col = n0 + wn * 64 + q * 32 + ccol;
+          const bool ok = m < M && col < p.Co;
+          rraw[g][q] = ok ? *reinterpret_cast<const uint2*>(static_cast<const bf16*>(p.res) + (size_t)m * p.res_ps + col)
+                          : make_uint2(0u, 0u);
+          if constexpr (RES == 2)
+            rgate[g][q] = ok ? *reinterpret_cast<const float4*>(p.res_gate + (size_t)img * p.Co + col)
+                             : float4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       floatx4 v[TN];
@@ -1458,15 +1481,13 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
       const int m = m0 + wm * 128 + i * 32 + 8 * g + rsub;
       float4 r[TN];
       if constexpr (RES != 0) {
-        const int img = RES == 2 ? min(m, M - 1) / (p.Ho * p.Wo) : 0;
 #pragma unroll
         for (int q = 0; q < TN; ++q) {
-          const int col = n0 + wn * 64 + q * 32 + ccol;
-          const bool ok = m < M && col < p.Co;
-          r[q] = ok ? ld4<bf16>(static_cast<const bf16*>(p.res) + (size_t)m * p.res_ps + col) : float4{0.f, 0.f, 0.f, 0.f};
+          const uint2 u = rraw[g][q];
+          r[q] = make_float4(bf16_bits_to_f32(u.x & 0xFFFFu), bf16_bits_to_f32(u.x >> 16), bf16_bits_to_f32(u.y & 0xFFFFu),
+                             bf16_bits_to_f32(u.y >> 16));
           if constexpr (RES == 2) {
-            const float4 gt = ok ? *reinterpret_cast<const float4*>(p.res_gate + (size_t)img * p.Co + col)
-                                 : float4{0.f, 0.f, 0.f, 0.f};
+            const float4 gt = rgate[g][q];
             r[q] = make_float4(mul_rn(r[q].x, gt.x), mul_rn(r[q].y, gt.y), mul_rn(r[q].z, gt.z), mul_rn(r[q].w, gt.w));
           }
         }
@@ -1499,6 +1520,7 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
         }
       }
     }
+  }
 }
 
 // Split-K finish: one workgroup per 16x64 output tile, one float4 of it per
