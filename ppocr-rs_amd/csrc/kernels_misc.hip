@@ -647,12 +647,19 @@ static void launch_dw_wave(const DwParams& p, hipStream_t s) {
 }
 
 // The launch shape of the tiled 3x3 kernel, the one that can leave SE
-// partial sums (stride 1 and more than 4 output rows).
-constexpr int kDw3TY = 8, kDw3C4B = 8, kDw3TX = 256 / (kDw3C4B * kDw3TY) * 4;
+// partial sums (stride 1 and more than 4 output rows): 8-row tiles of 32
+// channels, 2 outputs per lane along x for fp32 (8-pixel-wide tiles: 1.03-
+// 1.22x over 4 outputs on the detector's maps, more blocks for the same
+// work and less tail) and 4 for bf16 (16-pixel-wide; 2 measured 0.94-0.96x
+// on the recognizer's 6- and 12-row maps).
+constexpr int kDw3TY = 8, kDw3C4B = 8;
+constexpr int dw3_xr(int dt) { return dt == DT_BF16 ? 4 : 2; }
+static int dw3_tx(int dt) { return 256 / (kDw3C4B * kDw3TY) * dw3_xr(dt); }
 
 int depthwise_se_blocks(const DwParams& p) {
   if (!(p.kh == 3 && p.kw == 3 && p.sh == 1 && p.sw == 1 && p.Ho > 4)) return 0;
-  return ((p.Wo + kDw3TX - 1) / kDw3TX) * ((p.Ho + kDw3TY - 1) / kDw3TY);
+  const int tx = dw3_tx(p.dt);
+  return ((p.Wo + tx - 1) / tx) * ((p.Ho + kDw3TY - 1) / kDw3TY);
 }
 
 template <typename T>
@@ -681,7 +688,7 @@ static void launch_dw_typed(const DwParams& p, hipStream_t s) {
   if (p.kh == 3 && p.kw == 3 && p.sh == 1 && p.Ho <= 4)
     return p.Ho == 3 ? launch_dw_strip<T, 3, 3, 3, 1>(p, s) : launch_dw_strip<T, 3, 3, 4, 1>(p, s);
   if (p.sh == 1 && p.sw == 1) {
-    if (p.kh == 3 && p.kw == 3) return launch_dw_tiled<T, 3, 3, kDw3TY, 4, kDw3C4B>(p, s);
+    if (p.kh == 3 && p.kw == 3) return launch_dw_tiled<T, 3, 3, kDw3TY, dw3_xr(sizeof(T) == 2 ? DT_BF16 : DT_F32), kDw3C4B>(p, s);
     // 5x5 and 9x9: taps in scalar registers (1.1-1.2x the LDS-tap kernel);
     // 7x7 (32 channels here) measured even: 16-row tiles of 16 channels.
     if (p.kh == 5 && p.kw == 5) return launch_dw_wave<T, 5, 5>(p, s);
