@@ -606,8 +606,29 @@ __device__ __forceinline__ void finish_staged(const ConvParams& p, RowPtr row_pt
     return;
   }
   // Channel counts that are not a multiple of 4 (the recognizer classifiers,
-  // 6906 and 18710) go element by element; they carry no residual, gate or
-  // upsample terms.
+  // 6906 and 18710) carry no residual, gate or upsample terms.  An even Co
+  // with fp32 output stores column pairs (8-byte aligned rows; half the
+  // store instructions of element stores), anything else element by
+  // element.
+  if ((sizeof(T) == 4 || p.out_f32) && (p.out_ps & 1) == 0 && (p.Co & 1) == 0) {
+    for (int row = row0; row < BM; row += 256 / NQ) {
+      const int m = m0 + row;
+      if (m >= M || col >= p.Co) continue;
+      const float* v = row_ptr(row) + (col - n0);
+      float* o = static_cast<float*>(p.out) + (size_t)m * p.out_ps + col;
+#pragma unroll
+      for (int e = 0; e < 4; e += 2) {
+        if (col + e >= p.Co) break;
+        float t0 = v[e], t1 = v[e + 1];
+        if (p.bias) {
+          t0 = t0 + p.bias[col + e];
+          t1 = t1 + p.bias[col + e + 1];
+        }
+        *reinterpret_cast<float2*>(o + e) = make_float2(act_apply(p.act, t0), act_apply(p.act, t1));
+      }
+    }
+    return;
+  }
   for (int row = row0; row < BM; row += 256 / NQ) {
     const int m = m0 + row;
     if (m >= M || col >= p.Co) continue;
@@ -736,6 +757,15 @@ __device__ __forceinline__ void finish_regs(const ConvParams& p, floatx4 (&acc)[
       const int col = regs_col<BN, WN>(n0, j);
       if (col >= p.Co) continue;
       const float4 v = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      if ((p.Co & 3) != 0) {
+        // Even Co, fp32 output, no epilogue terms (regs_epilogue): pairs.
+        float4 x = p.bias ? f4_add(v, bias[j]) : v;
+        x = make_float4(act_apply(p.act, x.x), act_apply(p.act, x.y), act_apply(p.act, x.z), act_apply(p.act, x.w));
+        float* o = static_cast<float*>(p.out) + (size_t)m * p.out_ps + col;
+        *reinterpret_cast<float2*>(o) = make_float2(x.x, x.y);
+        if (col + 2 < p.Co) *reinterpret_cast<float2*>(o + 2) = make_float2(x.z, x.w);
+        continue;
+      }
       epilogue_store<T>(p, v, bias[j], t[j], m, col, img, oy, ox);
     }
   }
@@ -1229,9 +1259,13 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   constexpr int NB = REGS ? TN : 1;
   float4 bias_pre[NB];
 #pragma unroll
-  for (int j = 0; j < NB; ++j)
-    bias_pre[j] = p.splits > 1 ? float4{0.f, 0.f, 0.f, 0.f}
-                               : bias4(p, REGS ? regs_col<BN, WN>(n0, j) : staged_col<BN>(n0));
+  for (int j = 0; j < NB; ++j) {
+    const int bcol = REGS ? regs_col<BN, WN>(n0, j) : staged_col<BN>(n0);
+    bias_pre[j] = p.splits > 1 ? float4{0.f, 0.f, 0.f, 0.f} : bias4(p, bcol);
+    // The last group of an even Co that is not a multiple of 4 has two columns.
+    if (REGS && p.splits <= 1 && p.bias && bcol + 1 < p.Co && bcol + 3 >= p.Co)
+      bias_pre[j] = make_float4(p.bias[bcol], p.bias[bcol + 1], 0.f, 0.f);
+  }
 
   issue(0, kbase);
   if (nk > 1) issue(1, kbase + BK);
@@ -1606,7 +1640,13 @@ static bool regs_epilogue(const ConvParams& p) {
   const int K = p.kh * p.kw * p.C;
   if (p.ctc_part) return false;
   if (p.db_ch) return p.db_ch % 16 == 0;
-  return p.Co % 4 == 0 && p.out_ps % 4 == 0 && p.rep == 1 && (p.dt == DT_F32 || K <= 512);
+  if (p.dt != DT_F32 && K > 512) return false;
+  // Even channel counts with an fp32 output and no epilogue terms (the
+  // recognizer classifiers' logits, 6906 and 18710 columns) store column
+  // pairs from registers.
+  const bool pairs = p.Co % 2 == 0 && p.out_ps % 2 == 0 && (p.dt == DT_F32 || p.out_f32) && !p.res && !p.up &&
+                     p.rep == 1;
+  return (p.Co % 4 == 0 && p.out_ps % 4 == 0 && p.rep == 1) || pairs;
 }
 
 // bf16 64x64 1x1 layers of deep K and at least 512 output channels (the
