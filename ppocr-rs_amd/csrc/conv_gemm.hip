@@ -1659,6 +1659,14 @@ static bool rows128_layer(const ConvParams& p) {
   return p.dt == DT_BF16 && p.C >= 768 && p.Co >= 512 && p.splits <= 1 && !p.db_ch && !p.ctc_part;
 }
 
+// bf16 64x64 k x k layers of K >= 1024 whose channel count is a multiple
+// of 64 (a 128-byte row then stays within one tap): 128-byte rows too (the
+// detector head's 3x3 K = 2304 conv 1.18x, the stem's K = 1152 conv 1.04x
+// at batch 8).
+static bool rows128_kxk(const ConvParams& p) {
+  return p.dt == DT_BF16 && p.kh * p.kw * p.C >= 1024 && p.C % 64 == 0 && p.splits <= 1 && !p.db_ch && !p.ctc_part;
+}
+
 template <typename T, int BM, int BN, int WM, int WN>
 static void launch_tile_kernel(const ConvParams& p, dim3 grid, hipStream_t s) {
   // Stages: fp32 slices take long enough on the MFMAs that three cover the
@@ -1687,6 +1695,13 @@ static void launch_tile_kernel(const ConvParams& p, dim3 grid, hipStream_t s) {
                            s, p);
       break;
     case CV_DIRECT:
+      if constexpr (sizeof(T) == 2 && BM == 64 && BN == 64) {
+        if (rows128_kxk(p)) {
+          hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, false, 3, false, EPI_LDS, 128>), grid,
+                             dim3(256), 0, s, p);
+          break;
+        }
+      }
       if (regs && !p.db_ch)
         hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, false, S, false, EPI_REGS>), grid, dim3(256),
                            0, s, p);
@@ -1801,7 +1816,7 @@ std::string conv_kernel_name(const ConvParams& p) {
   static const char* variants[] = {",1x1", "", ",1x1,gate", ",1x1,reg", ",reg", ",1x1,reg4", ",reg4"};
   const int t = pick_tile(p.N * p.Ho * p.Wo, p.Co, p.dt);
   const int v = conv_variant(p, bm[t]);
-  const bool r128 = t == 3 && v == CV_DIRECT_1X1 && rows128_layer(p);
+  const bool r128 = t == 3 && ((v == CV_DIRECT_1X1 && rows128_layer(p)) || (v == CV_DIRECT && rows128_kxk(p)));
   return std::string(p.dt == DT_BF16 ? "conv_gemm_bf16<" : "conv_gemm<") + tiles[t] + variants[v] +
          (r128 ? ",r128" : "") + ">";
 }

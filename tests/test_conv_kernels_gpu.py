@@ -101,6 +101,10 @@ CASES = [
      "conv_gemm_bf16<64x64,1x1>"),
     ("bf16 128-byte rows", 1, 37, 41, 776, 520, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 1, ACT_HSWISH,
      "conv_gemm_bf16<64x64,1x1,r128>"),
+    ("bf16 3x3 128-byte rows", 1, 19, 23, 320, 72, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 1, ACT_RELU,
+     "conv_gemm_bf16<64x64,r128>"),
+    ("bf16 3x3 s2 128-byte rows", 2, 21, 17, 128, 68, (3, 3), (2, 2), (1, 1, 0, 0), False, 1, 1, ACT_NONE,
+     "conv_gemm_bf16<64x64,r128>"),
 ]
 
 
