@@ -391,18 +391,21 @@ __global__ __launch_bounds__(256) void depthwise_wave_kernel(DwParams p) {
 // [8][rows][28 dwords]: a 112-byte row pitch puts the 16 rows an A-fragment
 // read touches on distinct banks, and the columns past the tile's input
 // (read as the zero-weight tail of the last K group) are written as zeros.
-// Outputs are staged [row][col][8 channels] in the same LDS.
+// Outputs are staged in the same LDS as four planes of channel pairs.
 constexpr int kDwMfmaT = 32, kDwMfmaP = 28, kDwMfmaC = 8;  // tile side, LDS row pitch (dwords), channels
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 template <int K>
-__global__ __launch_bounds__(256) void depthwise_mfma_kernel(DwParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void depthwise_mfma_kernel(DwParams p) {
   constexpr int T = kDwMfmaT, P = kDwMfmaP, CB = kDwMfmaC;
   constexpr int IH = T + K - 1, IW = T + K - 1;
   static_assert(16 + K - 1 <= 32 && IW <= 2 * (P - 4), "a tile's K window fits the padded row");
-  constexpr int SP = T * CB + 4;  // staged output row pitch (floats)
-  constexpr int TILE = CB * IH * P, STAGE = T * SP;
+  // Staged outputs: one plane of channel pairs per wave, [row][col] float2
+  // with a row pitch of 72 floats, so the 32 lanes of a float2 write phase
+  // (16 columns of rows r and r + 4) cover the 64 banks once.
+  constexpr int SP = 2 * T + 8, PLANE = T * SP;
+  constexpr int TILE = CB * IH * P, STAGE = 4 * PLANE;
   __shared__ __align__(16) uint32_t lds[TILE > STAGE ? TILE : STAGE];
 
   const int cgroups = p.C / CB;
@@ -429,20 +432,32 @@ __global__ __launch_bounds__(256) void depthwise_mfma_kernel(DwParams p) {
       for (int ky = 0; ky < K; ++ky) bw[c][ky] = __builtin_bit_cast(bf16x8_t, tab[(c * K + ky) * 64]);
   }
 
-  // Input tile: pixel pairs along x, transposed to 8 channel planes.
+  // Input tile: pixel pairs along x, transposed to 8 channel planes.  A
+  // lane issues the loads of all its pixel pairs before its first LDS write.
   {
     const uint4* in = static_cast<const uint4*>(p.in);  // 8 bf16 channels per pixel
-    for (int q = tid; q < IH * (P - 4); q += 256) {
+    constexpr int NQ = IH * (P - 4), IT = (NQ + 255) / 256;
+    uint4 u0[IT], u1[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int q = tid + 256 * it;
       const int row = q / (P - 4), xp = q - row * (P - 4);
       const int gy = oy0 - p.pt + row, gx = ox0 - p.pl + 2 * xp;
-      uint4 u0 = make_uint4(0, 0, 0, 0), u1 = make_uint4(0, 0, 0, 0);
-      if ((unsigned)gy < (unsigned)p.H) {
+      u0[it] = u1[it] = make_uint4(0, 0, 0, 0);
+      if (q < NQ && (unsigned)gy < (unsigned)p.H) {
         const size_t rowpix = (size_t)(n * p.H + gy) * p.W;
-        if (2 * xp < IW && (unsigned)gx < (unsigned)p.W) u0 = in[((rowpix + gx) * p.in_ps + ch0) / CB];
-        if (2 * xp + 1 < IW && (unsigned)(gx + 1) < (unsigned)p.W) u1 = in[((rowpix + gx + 1) * p.in_ps + ch0) / CB];
+        if (2 * xp < IW && (unsigned)gx < (unsigned)p.W) u0[it] = in[((rowpix + gx) * p.in_ps + ch0) / CB];
+        if (2 * xp + 1 < IW && (unsigned)(gx + 1) < (unsigned)p.W)
+          u1[it] = in[((rowpix + gx + 1) * p.in_ps + ch0) / CB];
       }
+    }
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int q = tid + 256 * it;
+      if (q >= NQ) break;
+      const int row = q / (P - 4), xp = q - row * (P - 4);
       uint32_t* dst = lds + row * P + xp;
-      const uint32_t a[4] = {u0.x, u0.y, u0.z, u0.w}, b[4] = {u1.x, u1.y, u1.z, u1.w};
+      const uint32_t a[4] = {u0[it].x, u0[it].y, u0[it].z, u0[it].w}, b[4] = {u1[it].x, u1[it].y, u1[it].z, u1[it].w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         dst[(2 * j) * IH * P] = (a[j] & 0xFFFFu) | (b[j] << 16);
@@ -479,14 +494,17 @@ __global__ __launch_bounds__(256) void depthwise_mfma_kernel(DwParams p) {
   // acc[c][ty][tx][r] is output (16 ty + 4 (lane / 16) + r, 16 tx + lane % 16)
   // of channel 2 wave + c; the wave's two channels go out as one float2.
   float* stage = reinterpret_cast<float*>(lds);
+  {
+    float* plane = stage + wave * PLANE;
 #pragma unroll
-  for (int ty = 0; ty < 2; ++ty)
+    for (int ty = 0; ty < 2; ++ty)
 #pragma unroll
-    for (int tx = 0; tx < 2; ++tx)
+      for (int tx = 0; tx < 2; ++tx)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        *reinterpret_cast<float2*>(stage + (16 * ty + 4 * (lane >> 4) + r) * SP + (16 * tx + (lane & 15)) * CB +
-                                   2 * wave) = make_float2(acc[0][ty][tx][r], acc[1][ty][tx][r]);
+        for (int r = 0; r < 4; ++r)
+          *reinterpret_cast<float2*>(plane + (16 * ty + 4 * (lane >> 4) + r) * SP + 2 * (16 * tx + (lane & 15))) =
+              make_float2(acc[0][ty][tx][r], acc[1][ty][tx][r]);
+  }
   __syncthreads();
   float4 b0 = f4_zero(), b1 = f4_zero();
   if (p.bias) {
@@ -499,8 +517,12 @@ __global__ __launch_bounds__(256) void depthwise_mfma_kernel(DwParams p) {
     const int row = px / T, col = px % T;
     const int oy = oy0 + row, ox = ox0 + col;
     if (oy >= p.Ho || ox >= p.Wo) continue;
-    float4 v0 = *reinterpret_cast<const float4*>(stage + row * SP + col * CB);
-    float4 v1 = *reinterpret_cast<const float4*>(stage + row * SP + col * CB + 4);
+    const float* sp = stage + row * SP + 2 * col;
+    const float2 c01 = *reinterpret_cast<const float2*>(sp), c23 = *reinterpret_cast<const float2*>(sp + PLANE);
+    const float2 c45 = *reinterpret_cast<const float2*>(sp + 2 * PLANE);
+    const float2 c67 = *reinterpret_cast<const float2*>(sp + 3 * PLANE);
+    float4 v0 = make_float4(c01.x, c01.y, c23.x, c23.y);
+    float4 v1 = make_float4(c45.x, c45.y, c67.x, c67.y);
     if (p.bias) v0 = f4_sum(v0, b0), v1 = f4_sum(v1, b1);
     v0 = f4_act(p.act, v0);
     v1 = f4_act(p.act, v1);
