@@ -361,9 +361,10 @@ __device__ __forceinline__ float4 bias4(const ConvParams& p, int col) {
   return p.bias && col + 3 < p.Co ? *reinterpret_cast<const float4*>(p.bias + col) : float4{0.f, 0.f, 0.f, 0.f};
 }
 
+// Returns the value stored (rounded to the storage type).
 template <typename T>
-__device__ __forceinline__ void epilogue_store(const ConvParams& p, float4 v, float4 b, const EpiTerms& t, int m,
-                                               int col, int img, int oy, int ox) {
+__device__ __forceinline__ float4 epilogue_store(const ConvParams& p, float4 v, float4 b, const EpiTerms& t, int m,
+                                                 int col, int img, int oy, int ox) {
   if (p.bias) v = f4_add(v, b);
   v.x = act_apply(p.act, v.x);
   v.y = act_apply(p.act, v.y);
@@ -373,6 +374,7 @@ __device__ __forceinline__ void epilogue_store(const ConvParams& p, float4 v, fl
   if (p.up) v = f4_add(v, t.u);
   if (p.out_f32) {
     *reinterpret_cast<float4*>(static_cast<float*>(p.out) + (size_t)m * p.out_ps + col) = v;
+    return v;
   } else if (p.rep == 1) {
     st4<T>(static_cast<T*>(p.out) + (size_t)m * p.out_ps + col, v);
   } else if (p.rep_split) {
@@ -385,6 +387,7 @@ __device__ __forceinline__ void epilogue_store(const ConvParams& p, float4 v, fl
                    ((size_t)(img * p.out_h + oy * p.rep + dy) * p.out_w + ox * p.rep + dx) * p.out_ps + col,
                v);
   }
+  return round4<T>(v);
 }
 
 template <typename T, int BM, int BN, typename RowPtr>
@@ -731,6 +734,11 @@ __device__ __forceinline__ void finish_regs(const ConvParams& p, floatx4 (&acc)[
   const int HoWo = p.Ho * p.Wo;
   const bool need_coords = p.up != nullptr || p.rep != 1;
   const bool need_img = need_coords || p.res_gate != nullptr;
+  // SE channel sums (single image): this lane's rows of each column group,
+  // then the wave's 16 row lanes of the group.
+  float4 se_sum[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) se_sum[j] = float4{0.f, 0.f, 0.f, 0.f};
   // Row block by row block (the memory terms of a whole tile would cost the
   // main loop its occupancy): loads of the block's columns, then the stores.
 #pragma unroll
@@ -766,7 +774,25 @@ __device__ __forceinline__ void finish_regs(const ConvParams& p, floatx4 (&acc)[
         if (col + 2 < p.Co) *reinterpret_cast<float2*>(o + 2) = make_float2(x.z, x.w);
         continue;
       }
-      epilogue_store<T>(p, v, bias[j], t[j], m, col, img, oy, ox);
+      const float4 stored = epilogue_store<T>(p, v, bias[j], t[j], m, col, img, oy, ox);
+      if (p.se_part) se_sum[j] = f4_add(se_sum[j], stored);
+    }
+  }
+  if (p.se_part) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      float4 a = se_sum[j];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int o = k < 2 ? 1 << k : 1 << (k + 2);  // lane bits 0, 1, 4, 5: the rows of a column group
+        a.x += __shfl_xor(a.x, o);
+        a.y += __shfl_xor(a.y, o);
+        a.z += __shfl_xor(a.z, o);
+        a.w += __shfl_xor(a.w, o);
+      }
+      const int col = regs_col<BN, WN>(n0, j);
+      if ((lane & 0x33) == 0 && col < p.Co)
+        *reinterpret_cast<float4*>(p.se_part + ((size_t)(m0 / BM) * WM + wm) * p.Co + col) = a;
     }
   }
 }
@@ -1819,6 +1845,20 @@ std::string conv_kernel_name(const ConvParams& p) {
   const bool r128 = t == 3 && ((v == CV_DIRECT_1X1 && rows128_layer(p)) || (v == CV_DIRECT && rows128_kxk(p)));
   return std::string(p.dt == DT_BF16 ? "conv_gemm_bf16<" : "conv_gemm<") + tiles[t] + variants[v] +
          (r128 ? ",r128" : "") + ">";
+}
+
+int conv_se_blocks(const ConvParams& p) {
+  if (p.N != 1 || p.splits > 1 || p.Co % 4 || p.out_ps % 4 || p.rep != 1 || p.db_ch || p.ctc_part || wide_layer(p) ||
+      !regs_epilogue(p))
+    return 0;
+  static const int bm[] = {256, 128, 128, 64};
+  static const int wm[] = {4, 4, 2, 2};
+  const int M = p.Ho * p.Wo;
+  const int t = pick_tile(M, p.Co, p.dt);
+  const int v = conv_variant(p, bm[t]);
+  if (v != CV_DIRECT_1X1 && v != CV_DIRECT && v != CV_DIRECT_GATE) return 0;
+  if (t == 3 && ((v == CV_DIRECT_1X1 && rows128_layer(p)) || (v == CV_DIRECT && rows128_kxk(p)))) return 0;
+  return (M + bm[t] - 1) / bm[t] * wm[t];
 }
 
 int conv_tile_cols(int M, int cols, int dt) {

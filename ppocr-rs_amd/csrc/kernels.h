@@ -75,6 +75,10 @@ struct ConvParams {
   int db_ch;
   const float* db_wf;
   float db_bf;
+  // Channel sums of the stored output for a squeeze-excitation that reads
+  // it next ([P][Co] fp32, P = conv_se_blocks(): one row per tile row block
+  // of a wave), or null.
+  float* se_part;
 };
 
 // Depthwise k x k convolution (groups == C), 4 channels per lane.
@@ -191,6 +195,9 @@ void launch_pointwise_pair(const PairParams& p, hipStream_t s);
 std::string conv_kernel_name(const ConvParams& p);
 // Column width of that instance's tiles.
 int conv_tile_cols(int M, int cols, int dt);
+// Rows of the SE channel-sum array the conv leaves in se_part (single-image
+// layers finished from registers), or 0 where it cannot.
+int conv_se_blocks(const ConvParams& p);
 // K splits for a convolution of M rows, Co columns and reduction depth K:
 // more than 1 when its tiles alone would leave most of the 256 CUs idle and
 // K is deep enough to divide (the workspace is splits * M * Co floats).

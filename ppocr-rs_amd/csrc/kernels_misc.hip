@@ -869,7 +869,13 @@ __global__ __launch_bounds__(256) void se_expand_kernel(SeParams p) {
 // (PARTIALS) from the per-chunk sums left by se_partial or by the depthwise
 // that wrote the map; then the reducing and expanding 1x1 convs as in stages
 // 2 and 3, 16 waves at a time.
-template <typename T, bool PARTIALS>
+// SMALL (C <= 256, Cr <= 64, the detectors' gates): every weight and bias a
+// lane multiplies is loaded before the channel sums, so the two convs wait
+// on LDS only (the loop form waits on a load round trip per 64 inputs and per
+// bias); the products and their order are those of wave_dot4.
+constexpr int kSeSmallC = 256, kSeSmallCr = 64;
+
+template <typename T, bool PARTIALS, bool SMALL>
 __global__ __launch_bounds__(1024) void se_fused_kernel(SeParams p) {
   extern __shared__ float sm[];
   const int cr4 = (p.Cr + 3) & ~3;
@@ -882,6 +888,28 @@ __global__ __launch_bounds__(1024) void se_fused_kernel(SeParams p) {
   const int C4 = p.C >> 2;
   const int lanes_p = 1024 / C4;
   const int cq = tid % C4, pl = tid / C4;
+  const int wave = tid >> 6, lane = tid & 63;
+  constexpr int NI = SMALL ? kSeSmallC / 64 : 1;  // 64-input groups of the reducing conv, passes of the expanding one
+  float w1r[NI][4], w2r[NI][4], b2r[NI], b1r = 0.0f;
+  if constexpr (SMALL) {
+    // Reducing conv: this wave's rows j0 .. j0 + 3 (j0 = 4 wave < 64),
+    // inputs lane + 64 it.  Expanding conv: rows 4 wave + 64 it .. + 3,
+    // input lane.  Waves without rows load nothing; rows past the matrix
+    // read row 0 (ignored), inputs past it read zero.
+    const int j0 = wave * 4;
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const int i = lane + 64 * it, c0 = j0 + 64 * it;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r1 = j0 + q < p.Cr ? j0 + q : 0, r2 = c0 + q < p.C ? c0 + q : 0;
+        w1r[it][q] = j0 < p.Cr && i < p.C ? p.w1[(size_t)r1 * p.C + i] : 0.0f;
+        w2r[it][q] = c0 < p.C && lane < p.Cr ? p.w2[(size_t)r2 * p.Cr + lane] : 0.0f;
+      }
+      b2r[it] = lane < 4 && c0 + lane < p.C ? p.b2[c0 + lane] : 0.0f;
+    }
+    if (lane < 4 && j0 + lane < p.Cr) b1r = p.b1[j0 + lane];
+  }
   float4 s = f4_zero();
   if (pl < lanes_p) {
     if constexpr (PARTIALS)
@@ -891,9 +919,19 @@ __global__ __launch_bounds__(1024) void se_fused_kernel(SeParams p) {
   }
   red[tid] = s;
   __syncthreads();
+  // Two-level sum of the lanes_p phases of each channel quad: G partial
+  // sums of every G-th phase (in place: slot g of quad cq is read only by
+  // its own thread), then the G partials in order.
+  const int G = lanes_p < 16 ? lanes_p : 16;
+  if (tid < G * C4) {
+    float4 t = red[tid];
+    for (int k = pl + G; k < lanes_p; k += G) t = f4_sum(t, red[k * C4 + cq]);
+    red[tid] = t;
+  }
+  __syncthreads();
   if (tid < C4) {
     float4 t = red[tid];
-    for (int k = 1; k < lanes_p; ++k) t = f4_sum(t, red[k * C4 + tid]);
+    for (int k = 1; k < G; ++k) t = f4_sum(t, red[k * C4 + tid]);
     const float count = (float)p.HW;
     mean[tid * 4 + 0] = t.x / count;
     mean[tid * 4 + 1] = t.y / count;
@@ -901,7 +939,44 @@ __global__ __launch_bounds__(1024) void se_fused_kernel(SeParams p) {
     mean[tid * 4 + 3] = t.w / count;
   }
   __syncthreads();
-  const int wave = tid >> 6, lane = tid & 63;
+  if constexpr (SMALL) {
+    const int j0 = wave * 4;
+    if (j0 < p.Cr) {
+      float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int it = 0; it < NI; ++it) {
+        const int i = lane + 64 * it;
+        if (i < p.C) {  // the terms wave_dot4 takes, in its order
+          const float x = mean[i];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) a[q] = fmaf(w1r[it][q], x, a[q]);
+        }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[q] += __shfl_xor(a[q], o);
+      const float mine = lane == 0 ? a[0] : lane == 1 ? a[1] : lane == 2 ? a[2] : a[3];
+      if (lane < 4 && j0 + lane < p.Cr) hid[j0 + lane] = fmaxf(mine + b1r, 0.0f);
+    }
+    __syncthreads();
+    const float x = lane < p.Cr ? hid[lane] : 0.0f;
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const int c0 = wave * 4 + 64 * it;
+      if (c0 >= p.C) break;
+      float a[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a[q] = lane < p.Cr ? fmaf(w2r[it][q], x, 0.0f) : 0.0f;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[q] += __shfl_xor(a[q], o);
+      const float mine = lane == 0 ? a[0] : lane == 1 ? a[1] : lane == 2 ? a[2] : a[3];
+      if (lane < 4 && c0 + lane < p.C) p.gate[(size_t)n * p.C + c0 + lane] = act_apply(p.gate_act, mine + b2r[it]);
+    }
+    return;
+  }
   for (int j0 = wave * 4; j0 < p.Cr; j0 += 64) {
     const float4 acc = wave_dot4(p.w1, j0, p.Cr, mean, p.C, lane);
     const float a[4] = {acc.x, acc.y, acc.z, acc.w};
@@ -933,7 +1008,10 @@ static bool se_gate_one_block(const SeParams& p) {
 void launch_se_from_partials(const SeParams& p, hipStream_t s) {
   if (se_gate_one_block(p)) {
     const size_t lds = ((size_t)p.C + ((p.Cr + 3) & ~3)) * sizeof(float) + 1024 * sizeof(float4);
-    hipLaunchKernelGGL((se_fused_kernel<float, true>), dim3(p.N), dim3(1024), lds, s, p);
+    if (p.C <= kSeSmallC && p.Cr <= kSeSmallCr)
+      hipLaunchKernelGGL((se_fused_kernel<float, true, true>), dim3(p.N), dim3(1024), lds, s, p);
+    else
+      hipLaunchKernelGGL((se_fused_kernel<float, true, false>), dim3(p.N), dim3(1024), lds, s, p);
     return;
   }
   size_t lds = (size_t)p.C * sizeof(float) + 256 * sizeof(float4);
@@ -944,7 +1022,10 @@ void launch_se_from_partials(const SeParams& p, hipStream_t s) {
 void launch_se(const SeParams& p, hipStream_t s) {
   if (se_fused(p)) {
     const size_t lds = ((size_t)p.C + ((p.Cr + 3) & ~3)) * sizeof(float) + 1024 * sizeof(float4);
-    DISPATCH_DT(p.dt, hipLaunchKernelGGL((se_fused_kernel<T, false>), dim3(p.N), dim3(1024), lds, s, p));
+    if (p.C <= kSeSmallC && p.Cr <= kSeSmallCr)
+      DISPATCH_DT(p.dt, hipLaunchKernelGGL((se_fused_kernel<T, false, true>), dim3(p.N), dim3(1024), lds, s, p));
+    else
+      DISPATCH_DT(p.dt, hipLaunchKernelGGL((se_fused_kernel<T, false, false>), dim3(p.N), dim3(1024), lds, s, p));
     return;
   }
   int chunk = (p.HW + p.P - 1) / p.P;

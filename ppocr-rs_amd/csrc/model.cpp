@@ -245,19 +245,33 @@ class Builder {
   // non-null aligned values.
   static constexpr unsigned kTermRes = 1, kTermResGate = 2, kTermUp = 4, kTermCtc = 8;
   static std::string conv_kernel(const ConvParams& base, const View& x, size_t wo, bool gated, unsigned terms = 0) {
+    return conv_kernel_name(stand_in(base, x, wo, gated, terms));
+  }
+  // `base` with its pointers stood in for as above.
+  static ConvParams stand_in(const ConvParams& base, const View& x, size_t wo, bool gated, unsigned terms) {
     ConvParams probe = base;
     probe.in = reinterpret_cast<const void*>((uintptr_t)(x.off * dtype_size(x.dt)));
     probe.wt = reinterpret_cast<const void*>((uintptr_t)wo);
     probe.in_gate = gated ? reinterpret_cast<const float*>((uintptr_t)16) : nullptr;
-    const uintptr_t stand_in = 256;
-    if (terms & kTermRes) probe.res = reinterpret_cast<const void*>(stand_in);
-    if (terms & kTermResGate) probe.res_gate = reinterpret_cast<const float*>(stand_in);
-    if (terms & kTermUp) probe.up = reinterpret_cast<const void*>(stand_in);
-    if (terms & kTermCtc) probe.ctc_part = reinterpret_cast<float*>(stand_in);
-    return conv_kernel_name(probe);
+    const uintptr_t nonnull = 256;
+    if (terms & kTermRes) probe.res = reinterpret_cast<const void*>(nonnull);
+    if (terms & kTermResGate) probe.res_gate = reinterpret_cast<const float*>(nonnull);
+    if (terms & kTermUp) probe.up = reinterpret_cast<const void*>(nonnull);
+    if (terms & kTermCtc) probe.ctc_part = reinterpret_cast<float*>(nonnull);
+    return probe;
   }
 
-  View conv(const View& x, const ConvW& w, const Epi& e, const std::string& name) {
+  // Channel sums of a layer's output left by the depthwise or conv kernel
+  // that writes it, for the squeeze-excitation that reads it next: [N][P][C]
+  // fp32.
+  struct SePartial {
+    View part;
+    int P = 0;
+  };
+
+  // With sp, the conv also leaves the channel sums of its output in *sp
+  // where its kernel can (sp->P = 0 otherwise).
+  View conv(const View& x, const ConvW& w, const Epi& e, const std::string& name, SePartial* sp = nullptr) {
     if (x.c != w.ci_pad) raise(PPOCR_ERR_INVALID_MODEL, name + ": input has " + std::to_string(x.c) + " channels");
     const int Ho = (x.h + w.pt + w.pb - w.kh) / w.sh + 1;
     const int Wo = (x.w + w.pl + w.pr - w.kw) / w.sw + 1;
@@ -307,10 +321,22 @@ class Builder {
     View ws;
     if (splits > 1) ws = alloc(1, splits, x.n * Ho * Wo, w.co, name + ".split_k", DT_F32);
     base.splits = splits;
+    const unsigned terms = (has_res ? kTermRes : 0u) | (has_rg ? kTermResGate : 0u) | (has_up ? kTermUp : 0u);
+    View part;
+    bool has_part = false;
+    if (sp) {
+      sp->P = 0;
+      const int P = conv_se_blocks(stand_in(base, a_src, wo, has_ig && !prescale, terms));
+      if (P > 0) {
+        part = alloc(1, P, 1, w.co, name + ".se_partial", DT_F32);
+        has_part = true;
+        sp->part = part;
+        sp->P = P;
+      }
+    }
     Op op;
     op.name = name;
-    op.kernel = conv_kernel(base, a_src, wo, has_ig && !prescale,
-                            (has_res ? kTermRes : 0u) | (has_rg ? kTermResGate : 0u) | (has_up ? kTermUp : 0u));
+    op.kernel = conv_kernel(base, a_src, wo, has_ig && !prescale, terms);
     if (prescale) op.kernel += "+gate_pass";
     if (splits > 1) op.kernel += "+split_k" + std::to_string(splits);
     op.bound = 1;
@@ -330,6 +356,7 @@ class Builder {
     op.writes = {out.buf};
     if (splits > 1) op.writes.push_back(ws.buf);
     if (prescale) op.writes.push_back(xs.buf);
+    if (has_part) op.writes.push_back(part.buf);
     op.launch = [=](const Exec& ex, hipStream_t s) {
       ConvParams p = base;
       if (prescale) {
@@ -347,18 +374,13 @@ class Builder {
       p.res_gate = has_rg ? ex.fptr(rg) : nullptr;
       p.up = has_up ? ex.ptr(up) : nullptr;
       p.split_ws = splits > 1 ? ex.fptr(ws) : nullptr;
+      p.se_part = has_part ? ex.fptr(part) : nullptr;
       launch_conv(p, s);
     };
     add_op(std::move(op));
     return out;
   }
 
-  // Channel sums of a depthwise output left by the depthwise kernel for the
-  // squeeze-excitation that reads it: [N][P][C] fp32.
-  struct SePartial {
-    View part;
-    int P = 0;
-  };
 
   // Depthwise conv.  With se_cr > 0 a squeeze-excitation of reduction width
   // se_cr reads the output next; when the kernel can, and the gate is not
@@ -517,7 +539,7 @@ class Builder {
 
   // Squeeze-excitation gate [N,1,1,C] (fp32) of x (src/cpu/model.rs:456-493,
   // :1069-1105).
-  // With sp->P > 0 the channel sums come from the depthwise that wrote x.
+  // With sp->P > 0 the channel sums come from the kernel that wrote x.
   View se(const View& x, const SeW& w, const std::string& name, const SePartial* sp = nullptr) {
     int HW = x.h * x.w;
     const bool given = sp && sp->P > 0;
@@ -540,7 +562,7 @@ class Builder {
     SeW ww = w;
     Op op;
     op.name = name;
-    op.kernel = fused ? "se_fused" : given ? "se_gate+dw_sums" : "se_gate";
+    op.kernel = fused ? "se_fused" : given ? "se_gate+sums" : "se_gate";
     op.flops = 2.0 * x.n * ((double)HW * x.c + 2.0 * x.c * w.cr);
     op.bytes = (given ? 4.0 * x.n * P * x.c : (double)dtype_size(x.dt) * x.pixels() * x.c) +
                4.0 * (2.0 * x.c * w.cr + x.n * x.c);
@@ -941,10 +963,11 @@ View rep_lk_fpn(Builder& B, const std::vector<View>& st, const int chans[4], int
   for (int i = 0; i < 4; ++i) {
     std::string p = "model.neck.insert_conv." + std::to_string(i);
     ConvW w = B.conv_w(p + ".in_conv", chans[i], nc, 1, 1, 1, 1, {0, 0, 0, 0}, false);
-    h[i] = B.conv(st[i], w, Epi{}, p + ".in_conv");
+    Builder::SePartial sums;
+    h[i] = B.conv(st[i], w, Epi{}, p + ".in_conv", &sums);
     SeW sw = B.se_w(p + ".squeeze_excitation_block.conv1", p + ".squeeze_excitation_block.conv2", nc, nc / 4,
                     ACT_HSIG5);
-    g[i] = B.se(h[i], sw, p + ".se");
+    g[i] = B.se(h[i], sw, p + ".se", &sums);
   }
   // fused[i] = h + h * g (+ up2(fused[i + 1])) feeds input_conv i's
   // depthwise and level i - 1.  Where the depthwise can form it from h in its
@@ -982,10 +1005,11 @@ View rep_lk_fpn(Builder& B, const std::vector<View>& st, const int chans[4], int
     std::string p = "model.neck.input_conv." + std::to_string(i);
     if (!gr_fused) d[i] = B.depthwise(fused[i], dws[i], ACT_NONE, nullptr, p + ".depthwise_convolution");
     ConvW pw = B.conv_w(p + ".pointwise_convolution", nc, q, 1, 1, 1, 1, {0, 0, 0, 0}, false);
-    View pt = B.conv(d[i], pw, Epi{}, p + ".pointwise_convolution");
+    Builder::SePartial sums;
+    View pt = B.conv(d[i], pw, Epi{}, p + ".pointwise_convolution", &sums);
     SeW sw = B.se_w(p + ".squeeze_excitation_module.conv1", p + ".squeeze_excitation_module.conv2", q, q / 4,
                     ACT_HSIG5);
-    View gi = B.se(pt, sw, p + ".se");
+    View gi = B.se(pt, sw, p + ".se", &sums);
     View slot = Builder::slice(cat, (3 - i) * q, q);
     B.gate_residual(pt, gi, nullptr, slot, 1 << i, p + ".out");
   }

@@ -43,17 +43,11 @@ void* upload(const float* src, size_t n, int dt) {
   return d;
 }
 
-}  // namespace
-
-extern "C" {
-
-// x [n][h][w][c] (c % 4 == 0), weight [co][c][kh][kw], bias [co] (or null),
-// gate [n][c] (or null): out [n][ho][wo][co] = act(conv(x * gate) + bias),
-// computed with `splits` K splits (1: none) in storage type dt (0 fp32,
-// 1 bf16; bf16 output is returned widened).  Returns 0, or 1 on a HIP error.
-int ppocr_probe_conv(const float* x, int n, int h, int w, int c, const float* weight, const float* bias, int co,
-                     int kh, int kw, int sh, int sw, int pt, int pl, int pb, int pr, int act, const float* gate,
-                     int splits, int dt, float* out) {
+// ppocr_probe_conv, and with se_rows the SE channel sums the conv leaves:
+// *se_rows = conv_se_blocks() and se_part [*se_rows][co] (when non-zero).
+int run_conv(const float* x, int n, int h, int w, int c, const float* weight, const float* bias, int co, int kh,
+             int kw, int sh, int sw, int pt, int pl, int pb, int pr, int act, const float* gate, int splits, int dt,
+             float* out, int* se_rows, float* se_part) {
   const int ho = (h + pt + pb - kh) / sh + 1, wo = (w + pl + pr - kw) / sw + 1;
   const size_t K = (size_t)kh * kw * c, M = (size_t)n * ho * wo;
   std::vector<float> packed((size_t)co * K);
@@ -66,7 +60,7 @@ int ppocr_probe_conv(const float* x, int n, int h, int w, int c, const float* we
   void* d_wt = upload(packed.data(), packed.size(), dt);
   void* d_bias = bias ? upload(bias, co, ppocr::DT_F32) : nullptr;
   void* d_gate = gate ? upload(gate, (size_t)n * c, ppocr::DT_F32) : nullptr;
-  void *d_out = nullptr, *d_ws = nullptr;
+  void *d_out = nullptr, *d_ws = nullptr, *d_se = nullptr;
   int rc = 0;
   const size_t es = dt == ppocr::DT_BF16 ? 2 : 4;
   if (!d_in || !d_wt || (bias && !d_bias) || (gate && !d_gate) || hipMalloc(&d_out, M * co * es) != hipSuccess ||
@@ -90,8 +84,17 @@ int ppocr_probe_conv(const float* x, int n, int h, int w, int c, const float* we
     p.dt = dt;
     p.split_ws = static_cast<float*>(d_ws);
     p.splits = splits;
-    ppocr::launch_conv(p, nullptr);
-    if (hipDeviceSynchronize() != hipSuccess) rc = 1;
+    if (se_rows) {
+      *se_rows = ppocr::conv_se_blocks(p);
+      if (*se_rows > 0 && hipMalloc(&d_se, (size_t)*se_rows * co * 4) != hipSuccess) rc = 1;
+      p.se_part = static_cast<float*>(d_se);
+    }
+    if (rc == 0) {
+      ppocr::launch_conv(p, nullptr);
+      if (hipDeviceSynchronize() != hipSuccess) rc = 1;
+    }
+    if (rc == 0 && d_se && hipMemcpy(se_part, d_se, (size_t)*se_rows * co * 4, hipMemcpyDeviceToHost) != hipSuccess)
+      rc = 1;
     if (rc == 0) {
       if (dt == ppocr::DT_BF16) {
         std::vector<uint16_t> hb(M * co);
@@ -102,9 +105,35 @@ int ppocr_probe_conv(const float* x, int n, int h, int w, int c, const float* we
       }
     }
   }
-  for (void* ptr : {d_in, d_wt, d_bias, d_gate, d_out, static_cast<void*>(d_ws)})
+  for (void* ptr : {d_in, d_wt, d_bias, d_gate, d_out, d_ws, d_se})
     if (ptr) (void)hipFree(ptr);
   return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+// x [n][h][w][c] (c % 4 == 0), weight [co][c][kh][kw], bias [co] (or null),
+// gate [n][c] (or null): out [n][ho][wo][co] = act(conv(x * gate) + bias),
+// computed with `splits` K splits (1: none) in storage type dt (0 fp32,
+// 1 bf16; bf16 output is returned widened).  Returns 0, or 1 on a HIP error.
+int ppocr_probe_conv(const float* x, int n, int h, int w, int c, const float* weight, const float* bias, int co,
+                     int kh, int kw, int sh, int sw, int pt, int pl, int pb, int pr, int act, const float* gate,
+                     int splits, int dt, float* out) {
+  return run_conv(x, n, h, w, c, weight, bias, co, kh, kw, sh, sw, pt, pl, pb, pr, act, gate, splits, dt, out,
+                  nullptr, nullptr);
+}
+
+// ppocr_probe_conv without K splits, also asking for the squeeze-excitation
+// channel sums of the output: *rows = conv_se_blocks() (0: the kernel leaves
+// none), and se_part [rows][co] (room for ceil(ho*wo/64)*2 rows, the most
+// any tile gives) receives them.
+int ppocr_probe_conv_se(const float* x, int h, int w, int c, const float* weight, const float* bias, int co, int kh,
+                        int kw, int sh, int sw, int pt, int pl, int pb, int pr, int act, const float* gate, int dt,
+                        float* out, int* rows, float* se_part) {
+  return run_conv(x, 1, h, w, c, weight, bias, co, kh, kw, sh, sw, pt, pl, pb, pr, act, gate, 1, dt, out, rows,
+                  se_part);
 }
 
 // 1x1 conv with upsample-on-write (the medium neck's intraclass conv_final):

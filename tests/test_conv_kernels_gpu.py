@@ -349,3 +349,65 @@ def test_wide_bf16_1x1_matches_float64(name, n, h, w, c, co, kind, residual, f32
     tol = 1e-3 + (1e-5 if f32out else 8e-3) * np.abs(y)
     err = np.abs(out - y)
     assert np.all(err <= tol), f"{name} ({want_kernel}): max abs diff {err.max():.3e}"
+
+
+# (name, h, w, c, co, (kh, kw), pads, gated, dt, act, expected kernel, rows per tile row block or 0)
+SE_CASES = [
+    ("se sums 64x64 fp32", 23, 29, 64, 64, (1, 1), (0, 0, 0, 0), False, 0, ACT_RELU, "conv_gemm<64x64,1x1>", 2),
+    ("se sums 256x16", 19, 37, 32, 16, (1, 1), (0, 0, 0, 0), False, 0, ACT_NONE, "conv_gemm<256x16,1x1>", 4),
+    ("se sums 3x3 bf16 128x32", 17, 21, 32, 24, (3, 3), (1, 1, 1, 1), False, 1, ACT_HSWISH, "conv_gemm_bf16<128x32>",
+     4),
+    ("se sums gated", 13, 23, 64, 96, (1, 1), (0, 0, 0, 0), True, 0, ACT_NONE, "conv_gemm<64x64,1x1,gate>", 2),
+    ("no se sums: Co % 4 = 2", 9, 11, 16, 6, (1, 1), (0, 0, 0, 0), False, 0, ACT_NONE, "conv_gemm<256x16,1x1>", 0),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", SE_CASES, ids=[c[0] for c in SE_CASES])
+def test_conv_se_channel_sums(case):
+    """The squeeze-excitation channel sums a single-image conv leaves in its
+    register epilogue: summed over their rows they equal the column sums of
+    the output the conv stored (each row holds one wave's rows of one tile),
+    and the output itself still matches the float64 convolution."""
+    name, h, w, c, co, (kh, kw), pads, gated, dt, kind, want_kernel, per_block = case
+    lib = _lib()
+    f = ctypes.POINTER(ctypes.c_float)
+    i = ctypes.c_int
+    lib.ppocr_probe_conv_se.argtypes = [f, i, i, i, f, f, i, i, i, i, i, i, i, i, i, i, f, i, f,
+                                        ctypes.POINTER(i), f]
+    lib.ppocr_probe_conv_se.restype = i
+    kernel = lib.ppocr_probe_conv_kernel(1, h, w, c, co, kh, kw, 1, 1, *pads, int(gated), dt, None).decode()
+    assert kernel == want_kernel, f"{name}: runs {kernel}"
+
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    x = rng.standard_normal((1, h, w, c)).astype(np.float32)
+    wt = (rng.standard_normal((co, c, kh, kw)) / np.sqrt(c * kh * kw)).astype(np.float32)
+    b = rng.standard_normal(co).astype(np.float32) * 0.1
+    g = rng.uniform(0.0, 1.0, (1, c)).astype(np.float32) if gated else None
+    ho = h + pads[0] + pads[2] - kh + 1
+    wo = w + pads[1] + pads[3] - kw + 1
+    out = np.empty((1, ho, wo, co), dtype=np.float32)
+    cap = (ho * wo + 31) // 32 + 4
+    part = np.full((cap, co), np.nan, dtype=np.float32)
+    rows = ctypes.c_int(-1)
+    rc = lib.ppocr_probe_conv_se(_ptr(x), h, w, c, _ptr(wt), _ptr(b), co, kh, kw, 1, 1, *pads, kind, _ptr(g), dt,
+                                 _ptr(out), ctypes.byref(rows), _ptr(part))
+    assert rc == 0
+    bm = int(want_kernel.split("<")[1].split("x")[0])
+    assert rows.value == ((ho * wo + bm - 1) // bm) * per_block, f"{name}: {rows.value} rows"
+
+    if dt == 1:
+        xs = bf16_round(x)
+        ref = conv_ref(xs.astype(np.float64), bf16_round(wt).astype(np.float64), b, (1, 1), pads, kind)
+        tol = 1e-3 + 8e-3 * np.abs(ref)
+    else:
+        xs = x * g[:, None, None, :] if gated else x
+        ref = conv_ref(xs.astype(np.float64), wt.astype(np.float64), b, (1, 1), pads, kind)
+        tol = 1e-4 + 1e-5 * np.abs(ref)
+    assert np.all(np.abs(out - ref) <= tol), f"{name}: output differs"
+    if rows.value == 0:
+        return
+    sums = part[:rows.value].astype(np.float64).sum(axis=0)
+    want = out.astype(np.float64).sum(axis=(0, 1, 2))
+    scale = np.abs(out).astype(np.float64).sum(axis=(0, 1, 2))
+    assert np.all(np.abs(sums - want) <= 1e-5 * scale + 1e-6), f"{name}: sums differ by {np.abs(sums - want).max():.3e}"
