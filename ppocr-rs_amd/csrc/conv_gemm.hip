@@ -1658,20 +1658,20 @@ static int conv_variant(const ConvParams& p, int BM) {
 // Whether the direct kernel finishes its tiles from registers (finish_regs,
 // or finish_db_regs for the DB head with 16-column taps) rather than through
 // LDS (finish_tile): it can with whole float4 column groups (Co and out_ps
-// multiples of 4) and without the greedy-CTC epilogue.  Measured on the detector and recognizer layers:
-// the register epilogue is faster for fp32 and for bf16 up to K = 512; the
-// LDS one writes longer row segments per store, which wins for bf16 layers
-// of deeper K (1-4 %) and for upsample-on-write (2x at 8x8 blocks).
+// multiples of 4) and without the greedy-CTC epilogue.  Measured on the
+// detector and recognizer layers: the register epilogue is faster for fp32;
+// for bf16 the LDS one, whose stores write whole 128-byte row segments
+// where a register store writes 32 bytes of each of 16 rows (2-20 % per
+// layer on the batch-8 detector, up to 2x for upsample-on-write at 8x8
+// blocks).
 static bool regs_epilogue(const ConvParams& p) {
-  const int K = p.kh * p.kw * p.C;
   if (p.ctc_part) return false;
   if (p.db_ch) return p.db_ch % 16 == 0;
-  if (p.dt != DT_F32 && K > 512) return false;
+  if (p.dt != DT_F32) return false;
   // Even channel counts with an fp32 output and no epilogue terms (the
   // recognizer classifiers' logits, 6906 and 18710 columns) store column
   // pairs from registers.
-  const bool pairs = p.Co % 2 == 0 && p.out_ps % 2 == 0 && (p.dt == DT_F32 || p.out_f32) && !p.res && !p.up &&
-                     p.rep == 1;
+  const bool pairs = p.Co % 2 == 0 && p.out_ps % 2 == 0 && !p.res && !p.up && p.rep == 1;
   return (p.Co % 4 == 0 && p.out_ps % 4 == 0 && p.rep == 1) || pairs;
 }
 

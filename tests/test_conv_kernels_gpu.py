@@ -355,8 +355,9 @@ def test_wide_bf16_1x1_matches_float64(name, n, h, w, c, co, kind, residual, f32
 SE_CASES = [
     ("se sums 64x64 fp32", 23, 29, 64, 64, (1, 1), (0, 0, 0, 0), False, 0, ACT_RELU, "conv_gemm<64x64,1x1>", 2),
     ("se sums 256x16", 19, 37, 32, 16, (1, 1), (0, 0, 0, 0), False, 0, ACT_NONE, "conv_gemm<256x16,1x1>", 4),
-    ("se sums 3x3 bf16 128x32", 17, 21, 32, 24, (3, 3), (1, 1, 1, 1), False, 1, ACT_HSWISH, "conv_gemm_bf16<128x32>",
-     4),
+    ("se sums 3x3 128x32", 17, 21, 32, 24, (3, 3), (1, 1, 1, 1), False, 0, ACT_HSWISH, "conv_gemm<128x32>", 4),
+    ("no se sums: bf16 (LDS epilogue)", 17, 21, 32, 24, (3, 3), (1, 1, 1, 1), False, 1, ACT_HSWISH,
+     "conv_gemm_bf16<128x32>", 0),
     ("se sums gated", 13, 23, 64, 96, (1, 1), (0, 0, 0, 0), True, 0, ACT_NONE, "conv_gemm<64x64,1x1,gate>", 2),
     ("no se sums: Co % 4 = 2", 9, 11, 16, 6, (1, 1), (0, 0, 0, 0), False, 0, ACT_NONE, "conv_gemm<256x16,1x1>", 0),
 ]
