@@ -704,7 +704,9 @@ __device__ __forceinline__ int regs_col(int n0, int j) {
 // finish_tile without LDS: the split-K workspace store or the epilogue
 // straight from the accumulators.  bias[j]: bias of column group
 // regs_col(n0, j), loaded ahead.
-template <typename T, int BM, int BN, int WM, int WN>
+// SE: also leave the SE channel sums of the stored output in p.se_part
+// (single-image layers).
+template <typename T, int BM, int BN, int WM, int WN, bool SE = false>
 __device__ __forceinline__ void finish_regs(const ConvParams& p, floatx4 (&acc)[BM / (WM * 16)][BN / (WN * 16)],
                                             int m0, int n0, int M, const float4 (&bias)[BN / (WN * 16)]) {
   constexpr int TM = BM / (WM * 16);
@@ -775,10 +777,10 @@ __device__ __forceinline__ void finish_regs(const ConvParams& p, floatx4 (&acc)[
         continue;
       }
       const float4 stored = epilogue_store<T>(p, v, bias[j], t[j], m, col, img, oy, ox);
-      if (p.se_part) se_sum[j] = f4_add(se_sum[j], stored);
+      if constexpr (SE) se_sum[j] = f4_add(se_sum[j], stored);
     }
   }
-  if (p.se_part) {
+  if constexpr (SE) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       float4 a = se_sum[j];
@@ -989,6 +991,7 @@ __device__ __forceinline__ void lds_wait(floatx4& v) { asm volatile("s_waitcnt l
 enum DirectEpi : int {
   EPI_LDS = 0,   // finish_tile: staged through LDS (every epilogue)
   EPI_REGS = 1,  // finish_regs
+  EPI_REGS_SE = 3,  // finish_regs leaving SE channel sums (fp32 1x1 layers with se_part)
   EPI_DB = 2,    // finish_db_regs (DB head tail)
 };
 
@@ -1314,8 +1317,8 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
     finish_db_regs<T, BM, BN, WM, WN>(p, acc, m0, n0, M, bias_pre, reinterpret_cast<float4*>(st0));
     return;
   }
-  if constexpr (EPI == EPI_REGS) {
-    finish_regs<T, BM, BN, WM, WN>(p, acc, m0, n0, M, bias_pre);
+  if constexpr (EPI == EPI_REGS || EPI == EPI_REGS_SE) {
+    finish_regs<T, BM, BN, WM, WN, EPI == EPI_REGS_SE>(p, acc, m0, n0, M, bias_pre);
     return;
   }
   __syncthreads();
@@ -1713,6 +1716,9 @@ static void launch_tile_kernel(const ConvParams& p, dim3 grid, hipStream_t s) {
       if (regs && p.db_ch)
         hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, false, EPI_DB>), grid, dim3(256), 0,
                            s, p);
+      else if (regs && p.se_part && sizeof(T) == 4)
+        hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, false, EPI_REGS_SE>), grid, dim3(256),
+                           0, s, p);
       else if (regs)
         hipLaunchKernelGGL((conv_gemm_direct_kernel<T, BM, BN, WM, WN, true, S, false, EPI_REGS>), grid, dim3(256), 0,
                            s, p);
@@ -1856,8 +1862,7 @@ int conv_se_blocks(const ConvParams& p) {
   const int M = p.Ho * p.Wo;
   const int t = pick_tile(M, p.Co, p.dt);
   const int v = conv_variant(p, bm[t]);
-  if (v != CV_DIRECT_1X1 && v != CV_DIRECT && v != CV_DIRECT_GATE) return 0;
-  if (t == 3 && ((v == CV_DIRECT_1X1 && rows128_layer(p)) || (v == CV_DIRECT && rows128_kxk(p)))) return 0;
+  if (v != CV_DIRECT_1X1) return 0;
   return (M + bm[t] - 1) / bm[t] * wm[t];
 }
 

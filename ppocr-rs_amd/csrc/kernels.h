@@ -196,7 +196,7 @@ std::string conv_kernel_name(const ConvParams& p);
 // Column width of that instance's tiles.
 int conv_tile_cols(int M, int cols, int dt);
 // Rows of the SE channel-sum array the conv leaves in se_part (single-image
-// layers finished from registers), or 0 where it cannot.
+// fp32 1x1 layers finished from registers), or 0 where it cannot.
 int conv_se_blocks(const ConvParams& p);
 // K splits for a convolution of M rows, Co columns and reduction depth K:
 // more than 1 when its tiles alone would leave most of the 256 CUs idle and

@@ -355,10 +355,11 @@ def test_wide_bf16_1x1_matches_float64(name, n, h, w, c, co, kind, residual, f32
 SE_CASES = [
     ("se sums 64x64 fp32", 23, 29, 64, 64, (1, 1), (0, 0, 0, 0), False, 0, ACT_RELU, "conv_gemm<64x64,1x1>", 2),
     ("se sums 256x16", 19, 37, 32, 16, (1, 1), (0, 0, 0, 0), False, 0, ACT_NONE, "conv_gemm<256x16,1x1>", 4),
-    ("se sums 3x3 128x32", 17, 21, 32, 24, (3, 3), (1, 1, 1, 1), False, 0, ACT_HSWISH, "conv_gemm<128x32>", 4),
+    ("se sums 128x32", 17, 21, 32, 24, (1, 1), (0, 0, 0, 0), False, 0, ACT_HSWISH, "conv_gemm<128x32,1x1>", 4),
+    ("no se sums: 3x3", 17, 21, 32, 24, (3, 3), (1, 1, 1, 1), False, 0, ACT_HSWISH, "conv_gemm<128x32>", 0),
     ("no se sums: bf16 (LDS epilogue)", 17, 21, 32, 24, (3, 3), (1, 1, 1, 1), False, 1, ACT_HSWISH,
      "conv_gemm_bf16<128x32>", 0),
-    ("se sums gated", 13, 23, 64, 96, (1, 1), (0, 0, 0, 0), True, 0, ACT_NONE, "conv_gemm<64x64,1x1,gate>", 2),
+    ("no se sums: gated", 13, 23, 64, 96, (1, 1), (0, 0, 0, 0), True, 0, ACT_NONE, "conv_gemm<64x64,1x1,gate>", 0),
     ("no se sums: Co % 4 = 2", 9, 11, 16, 6, (1, 1), (0, 0, 0, 0), False, 0, ACT_NONE, "conv_gemm<256x16,1x1>", 0),
 ]
 
@@ -366,10 +367,11 @@ SE_CASES = [
 @pytest.mark.gpu
 @pytest.mark.parametrize("case", SE_CASES, ids=[c[0] for c in SE_CASES])
 def test_conv_se_channel_sums(case):
-    """The squeeze-excitation channel sums a single-image conv leaves in its
-    register epilogue: summed over their rows they equal the column sums of
-    the output the conv stored (each row holds one wave's rows of one tile),
-    and the output itself still matches the float64 convolution."""
+    """The squeeze-excitation channel sums a single-image fp32 1x1 conv
+    leaves in its register epilogue: summed over their rows they equal the
+    column sums of the output the conv stored (each row holds one wave's rows
+    of one tile), and the output itself still matches the float64
+    convolution.  Other layers report no sums."""
     name, h, w, c, co, (kh, kw), pads, gated, dt, kind, want_kernel, per_block = case
     lib = _lib()
     f = ctypes.POINTER(ctypes.c_float)
