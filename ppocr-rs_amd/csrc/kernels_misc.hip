@@ -286,40 +286,66 @@ __global__ __launch_bounds__(256) void depthwise_wave_kernel(DwParams p) {
 
   {
     // A lane keeps one channel group and steps through the tile's pixels 64
-    // at a time; the image base and channel test are hoisted.
+    // at a time; the image base and channel test are hoisted, and the loads
+    // of all its pixels are issued before the first LDS write.
+    constexpr int NPX = IH * IW, PPI = 256 / G, IT = (NPX + PPI - 1) / PPI;
     const int g = tid & (G - 1);
     const int c = ch0 + g * 4;
     const bool cok = c < p.C;
     const T* base = in + (size_t)n * p.H * p.W * p.in_ps + c;
+    float4 v[IT];
     if (p.gr_gate) {
       // x = in + in * gate (+ up2(upper)), rounded as gate_residual_kernel
       // stores it; pixels of the tile's output block also go to gr_out.
       const float4 gt = cok ? *reinterpret_cast<const float4*>(p.gr_gate + (size_t)n * p.C + c) : f4_zero();
       const int uh = p.H / 2, uw = p.W / 2;
       const T* up = p.gr_up ? static_cast<const T*>(p.gr_up) + (size_t)n * uh * uw * p.gr_up_ps + c : nullptr;
-      for (int px = tid / G; px < IH * IW; px += 256 / G) {
+      float4 u[IT];
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int px = tid / G + PPI * it;
         const int iy = px / IW, ix = px - iy * IW;
         const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
-        float4 v = f4_zero();
-        if (cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W) {
-          const float4 h = ld4<T>(base + ((size_t)gy * p.W + gx) * p.in_ps);
-          v = make_float4(residual_mul(h.x, gt.x), residual_mul(h.y, gt.y), residual_mul(h.z, gt.z),
-                          residual_mul(h.w, gt.w));
-          if (up) v = f4_sum(v, ld4<T>(up + ((size_t)(gy / 2) * uw + gx / 2) * p.gr_up_ps));
-          v = round4<T>(v);
-          if (p.gr_out && (unsigned)(iy - p.pt) < (unsigned)TY && (unsigned)(ix - p.pl) < (unsigned)TX)
-            st4<T>(static_cast<T*>(p.gr_out) + ((size_t)(n * p.H + gy) * p.W + gx) * p.gr_out_ps + c, v);
+        v[it] = u[it] = f4_zero();
+        if (px < NPX && cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W) {
+          v[it] = ld4<T>(base + ((size_t)gy * p.W + gx) * p.in_ps);
+          if (up) u[it] = ld4<T>(up + ((size_t)(gy / 2) * uw + gx / 2) * p.gr_up_ps);
         }
-        tile[(g * IH + iy) * IWP + ix] = v;
+      }
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int px = tid / G + PPI * it;
+        if (px >= NPX) break;
+        const int iy = px / IW, ix = px - iy * IW;
+        const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
+        float4 x = f4_zero();
+        if (cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W) {
+          const float4 h = v[it];
+          x = make_float4(residual_mul(h.x, gt.x), residual_mul(h.y, gt.y), residual_mul(h.z, gt.z),
+                          residual_mul(h.w, gt.w));
+          if (up) x = f4_sum(x, u[it]);
+          x = round4<T>(x);
+          if (p.gr_out && (unsigned)(iy - p.pt) < (unsigned)TY && (unsigned)(ix - p.pl) < (unsigned)TX)
+            st4<T>(static_cast<T*>(p.gr_out) + ((size_t)(n * p.H + gy) * p.W + gx) * p.gr_out_ps + c, x);
+        }
+        tile[(g * IH + iy) * IWP + ix] = x;
       }
     } else {
-      for (int px = tid / G; px < IH * IW; px += 256 / G) {
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int px = tid / G + PPI * it;
         const int iy = px / IW, ix = px - iy * IW;
         const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
-        float4 v = f4_zero();
-        if (cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W)
-          v = ld4<T>(base + ((size_t)gy * p.W + gx) * p.in_ps);
-        tile[(g * IH + iy) * IWP + ix] = v;
+        v[it] = f4_zero();
+        if (px < NPX && cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W)
+          v[it] = ld4<T>(base + ((size_t)gy * p.W + gx) * p.in_ps);
+      }
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int px = tid / G + PPI * it;
+        if (px >= NPX) break;
+        const int iy = px / IW, ix = px - iy * IW;
+        tile[(g * IH + iy) * IWP + ix] = v[it];
       }
     }
   }
