@@ -110,6 +110,15 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
   const int oy0 = blk / tiles_x * TY, ox0 = blk % tiles_x * TX;
   const int tid = threadIdx.x;
 
+  // Tap vector of this lane (one per lane at most), loaded with the tile so
+  // that both wait on one memory latency.
+  static_assert(KH * KW * C4B <= 256, "one tap vector per lane");
+  float4 tap = f4_zero();
+  if (tid < KH * KW * C4B) {
+    const int c = ch0 + (tid % C4B) * 4;
+    if (c < p.C) tap = *reinterpret_cast<const float4*>(p.wt + (size_t)(tid / C4B) * p.C + c);
+  }
+
   {
     // A lane keeps one channel group (256 is a multiple of C4B) and steps
     // through the tile's pixels; the image base and channel test are hoisted.
@@ -175,11 +184,7 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
     }
     }
   }
-  for (int i = tid; i < KH * KW * C4B; i += 256) {
-    int c = ch0 + (i % C4B) * 4;
-    int t = i / C4B;
-    taps[i] = c < p.C ? *reinterpret_cast<const float4*>(p.wt + (size_t)t * p.C + c) : f4_zero();
-  }
+  if (tid < KH * KW * C4B) taps[tid] = tap;
   __syncthreads();
 
   // Channel groups fastest, then rows, then x groups: with C4B * TY = 64 a
