@@ -127,8 +127,8 @@ int ppocr_probe_conv(const float* x, int n, int h, int w, int c, const float* we
 
 // ppocr_probe_conv without K splits, also asking for the squeeze-excitation
 // channel sums of the output: *rows = conv_se_blocks() (0: the kernel leaves
-// none), and se_part [rows][co] (room for ceil(ho*wo/64)*2 rows, the most
-// any tile gives) receives them.
+// none), and se_part [rows][co] (room for ceil(ho*wo/16) + 4 rows, the
+// most any tile gives) receives them.
 int ppocr_probe_conv_se(const float* x, int h, int w, int c, const float* weight, const float* bias, int co, int kh,
                         int kw, int sh, int sw, int pt, int pl, int pb, int pr, int act, const float* gate, int dt,
                         float* out, int* rows, float* se_part) {

@@ -81,7 +81,10 @@ CASES = [
     ("3x3 K tail", 1, 11, 13, 20, 24, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 0, ACT_HSWISH, "conv_gemm<128x32>"),
     ("3x3 stride 2", 2, 12, 10, 16, 64, (3, 3), (2, 2), (1, 1, 1, 1), False, 1, 0, ACT_NONE, "conv_gemm<64x64>"),
     ("7x1 asymmetric", 1, 9, 6, 8, 24, (7, 1), (1, 1), (3, 0, 3, 0), False, 1, 0, ACT_RELU, "conv_gemm<128x32>"),
-    ("1x1 narrow Co", 1, 5, 6, 12, 10, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_SIGMOID, "conv_gemm<256x16,1x1>"),
+    ("1x1 narrow Co", 1, 5, 6, 12, 10, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_SIGMOID, "conv_gemm<64x16,1x1>"),
+    ("1x1 narrow Co, 257 row tiles", 1, 257, 256, 16, 12, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_RELU,
+     "conv_gemm<256x16,1x1>"),
+    ("3x3 narrow Co", 2, 13, 11, 8, 12, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 0, ACT_HSWISH, "conv_gemm<64x16>"),
     ("gated 1x1 direct", 3, 8, 10, 64, 64, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 0, ACT_RELU,
      "conv_gemm<64x64,1x1,gate>"),
     ("gated 1x1 small images", 5, 3, 5, 64, 64, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 0, ACT_NONE,
@@ -354,13 +357,13 @@ def test_wide_bf16_1x1_matches_float64(name, n, h, w, c, co, kind, residual, f32
 # (name, h, w, c, co, (kh, kw), pads, gated, dt, act, expected kernel, rows per tile row block or 0)
 SE_CASES = [
     ("se sums 64x64 fp32", 23, 29, 64, 64, (1, 1), (0, 0, 0, 0), False, 0, ACT_RELU, "conv_gemm<64x64,1x1>", 2),
-    ("se sums 256x16", 19, 37, 32, 16, (1, 1), (0, 0, 0, 0), False, 0, ACT_NONE, "conv_gemm<256x16,1x1>", 4),
+    ("se sums 64x16", 19, 37, 32, 16, (1, 1), (0, 0, 0, 0), False, 0, ACT_NONE, "conv_gemm<64x16,1x1>", 4),
     ("se sums 128x32", 17, 21, 32, 24, (1, 1), (0, 0, 0, 0), False, 0, ACT_HSWISH, "conv_gemm<128x32,1x1>", 4),
     ("no se sums: 3x3", 17, 21, 32, 24, (3, 3), (1, 1, 1, 1), False, 0, ACT_HSWISH, "conv_gemm<128x32>", 0),
     ("no se sums: bf16 (LDS epilogue)", 17, 21, 32, 24, (3, 3), (1, 1, 1, 1), False, 1, ACT_HSWISH,
      "conv_gemm_bf16<128x32>", 0),
     ("no se sums: gated", 13, 23, 64, 96, (1, 1), (0, 0, 0, 0), True, 0, ACT_NONE, "conv_gemm<64x64,1x1,gate>", 0),
-    ("no se sums: Co % 4 = 2", 9, 11, 16, 6, (1, 1), (0, 0, 0, 0), False, 0, ACT_NONE, "conv_gemm<256x16,1x1>", 0),
+    ("no se sums: Co % 4 = 2", 9, 11, 16, 6, (1, 1), (0, 0, 0, 0), False, 0, ACT_NONE, "conv_gemm<64x16,1x1>", 0),
 ]
 
 
@@ -390,7 +393,7 @@ def test_conv_se_channel_sums(case):
     ho = h + pads[0] + pads[2] - kh + 1
     wo = w + pads[1] + pads[3] - kw + 1
     out = np.empty((1, ho, wo, co), dtype=np.float32)
-    cap = (ho * wo + 31) // 32 + 4
+    cap = (ho * wo + 15) // 16 + 4
     part = np.full((cap, co), np.nan, dtype=np.float32)
     rows = ctypes.c_int(-1)
     rc = lib.ppocr_probe_conv_se(_ptr(x), h, w, c, _ptr(wt), _ptr(b), co, kh, kw, 1, 1, *pads, kind, _ptr(g), dt,
