@@ -78,20 +78,22 @@ def conv_ref(x, w, b, stride, pads, kind):
 # (name, n, h, w, c, co, (kh, kw), (sh, sw), (pt, pl, pb, pr), gated, splits, dt, act, expected kernel)
 CASES = [
     ("1x1 M/N tails", 2, 7, 9, 64, 96, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_RELU, "conv_gemm<64x64,1x1>"),
-    ("3x3 K tail", 1, 11, 13, 20, 24, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 0, ACT_HSWISH, "conv_gemm<128x32>"),
+    ("3x3 K tail", 1, 11, 13, 20, 24, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 0, ACT_HSWISH, "conv_gemm<64x32>"),
     ("3x3 stride 2", 2, 12, 10, 16, 64, (3, 3), (2, 2), (1, 1, 1, 1), False, 1, 0, ACT_NONE, "conv_gemm<64x64>"),
-    ("7x1 asymmetric", 1, 9, 6, 8, 24, (7, 1), (1, 1), (3, 0, 3, 0), False, 1, 0, ACT_RELU, "conv_gemm<128x32>"),
+    ("7x1 asymmetric", 1, 9, 6, 8, 24, (7, 1), (1, 1), (3, 0, 3, 0), False, 1, 0, ACT_RELU, "conv_gemm<64x32>"),
     ("1x1 narrow Co", 1, 5, 6, 12, 10, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_SIGMOID, "conv_gemm<64x16,1x1>"),
     ("1x1 narrow Co, 257 row tiles", 1, 257, 256, 16, 12, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_RELU,
      "conv_gemm<256x16,1x1>"),
     ("3x3 narrow Co", 2, 13, 11, 8, 12, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 0, ACT_HSWISH, "conv_gemm<64x16>"),
+    ("1x1 Co 24, 256 row tiles", 1, 181, 181, 8, 24, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_NONE,
+     "conv_gemm<128x32,1x1>"),
     ("gated 1x1 direct", 3, 8, 10, 64, 64, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 0, ACT_RELU,
      "conv_gemm<64x64,1x1,gate>"),
     ("gated 1x1 small images", 5, 3, 5, 64, 64, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 0, ACT_NONE,
      "conv_gemm<64x64,1x1,reg>"),
     ("split K 1x1", 1, 5, 7, 256, 64, (1, 1), (1, 1), (0, 0, 0, 0), False, 4, 0, ACT_RELU, "conv_gemm<64x64,1x1>"),
     ("split K 3x3 uneven", 2, 6, 5, 32, 32, (3, 3), (1, 1), (1, 1, 1, 1), False, 5, 0, ACT_HSWISH,
-     "conv_gemm<128x32>"),
+     "conv_gemm<64x32>"),
     ("split K gated", 2, 6, 12, 128, 64, (1, 1), (1, 1), (0, 0, 0, 0), True, 3, 0, ACT_NONE,
      "conv_gemm<64x64,1x1,gate>"),
     ("bf16 1x1", 2, 9, 7, 64, 96, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 1, ACT_RELU, "conv_gemm_bf16<64x64,1x1>"),
@@ -358,10 +360,10 @@ def test_wide_bf16_1x1_matches_float64(name, n, h, w, c, co, kind, residual, f32
 SE_CASES = [
     ("se sums 64x64 fp32", 23, 29, 64, 64, (1, 1), (0, 0, 0, 0), False, 0, ACT_RELU, "conv_gemm<64x64,1x1>", 2),
     ("se sums 64x16", 19, 37, 32, 16, (1, 1), (0, 0, 0, 0), False, 0, ACT_NONE, "conv_gemm<64x16,1x1>", 4),
-    ("se sums 128x32", 17, 21, 32, 24, (1, 1), (0, 0, 0, 0), False, 0, ACT_HSWISH, "conv_gemm<128x32,1x1>", 4),
-    ("no se sums: 3x3", 17, 21, 32, 24, (3, 3), (1, 1, 1, 1), False, 0, ACT_HSWISH, "conv_gemm<128x32>", 0),
+    ("se sums 64x32", 17, 21, 32, 24, (1, 1), (0, 0, 0, 0), False, 0, ACT_HSWISH, "conv_gemm<64x32,1x1>", 4),
+    ("no se sums: 3x3", 17, 21, 32, 24, (3, 3), (1, 1, 1, 1), False, 0, ACT_HSWISH, "conv_gemm<64x32>", 0),
     ("no se sums: bf16 (LDS epilogue)", 17, 21, 32, 24, (3, 3), (1, 1, 1, 1), False, 1, ACT_HSWISH,
-     "conv_gemm_bf16<128x32>", 0),
+     "conv_gemm_bf16<64x32>", 0),
     ("no se sums: gated", 13, 23, 64, 96, (1, 1), (0, 0, 0, 0), True, 0, ACT_NONE, "conv_gemm<64x64,1x1,gate>", 0),
     ("no se sums: Co % 4 = 2", 9, 11, 16, 6, (1, 1), (0, 0, 0, 0), False, 0, ACT_NONE, "conv_gemm<64x16,1x1>", 0),
 ]
