@@ -127,9 +127,10 @@ def test_matrix_core_depthwise_needs_whole_channel_groups():
 
 @pytest.mark.gpu
 def test_fp32_depthwise_probe_matches_float64():
-    """The probe's fp32 path (VALU kernels) against float64: pins the probe."""
+    """The probe's fp32 path (VALU kernels: tiled 3x3 and 7x7, wave 5x5 and
+    9x9) against float64: pins the probe."""
     lib = _lib()
-    for k in (5, 7, 9):
+    for k in (3, 5, 7, 9):
         n, h, wd, c = 1, 23, 35, 8
         rng = np.random.default_rng(50 + k)
         x = rng.uniform(-1, 1, (n, h, wd, c)).astype(np.float32)
