@@ -989,10 +989,10 @@ __device__ __forceinline__ void lds_wait(floatx4& v) { asm volatile("s_waitcnt l
 // Epilogue of the direct kernel, fixed per instantiation so each keeps only
 // the registers its own epilogue needs.
 enum DirectEpi : int {
-  EPI_LDS = 0,   // finish_tile: staged through LDS (every epilogue)
-  EPI_REGS = 1,  // finish_regs
+  EPI_LDS = 0,      // finish_tile: staged through LDS (every epilogue)
+  EPI_REGS = 1,     // finish_regs
+  EPI_DB = 2,       // finish_db_regs (DB head tail)
   EPI_REGS_SE = 3,  // finish_regs leaving SE channel sums (fp32 1x1 layers with se_part)
-  EPI_DB = 2,    // finish_db_regs (DB head tail)
 };
 
 // RB: bytes of one operand row per K slice, 64 (half a cache line, key
@@ -1829,17 +1829,23 @@ static bool wide_layer(const ConvParams& p) {
          p.splits <= 1 && p.out_ps % (f32 ? 2 : 4) == 0 && (!p.res || p.res_ps % 4 == 0);
 }
 
-// Tile choice (0 256x16, 1 128x32, 2 128x64, 3 64x64, 4 64x16, 5 64x32):
-// narrow output channel counts get tall tiles so no MFMA column is wasted,
-// except that layers of at most 16 (32) columns take 64-row tiles while
-// 256-row (128-row) ones would not give every CU one (the tiny detector's
-// 16-channel FPN convs at 19136 pixels: 75 workgroups of 256 rows, 299 of
-// 64; 1.3-1.4x per layer, and without the split of K the few big tiles
-// needed; the 32-column tiles 0.6-2.2 % on every batch-1 plan).  Wide
-// layers: fp32
-// takes 64x64 (its MFMA is slow enough that the smaller tile's occupancy
-// wins); bf16 takes 128x64 when that still gives every CU several blocks
-// (its faster MFMA needs the operand reuse of the taller tile).
+// Tile shapes of the direct and register kernels, indexed by pick_tile
+// (rows, columns, waves along the rows; four waves per workgroup).
+constexpr int kTileBM[] = {256, 128, 128, 64, 64, 64};
+constexpr int kTileBN[] = {16, 32, 64, 64, 16, 32};
+constexpr int kTileWM[] = {4, 4, 2, 2, 4, 4};
+constexpr const char* kTileName[] = {"256x16", "128x32", "128x64", "64x64", "64x16", "64x32"};
+
+// Tile choice: narrow output channel counts get tall tiles so no MFMA
+// column is wasted, except that layers of at most 16 (32) columns take
+// 64-row tiles while 256-row (128-row) ones would not give every CU one
+// (the tiny detector's 16-channel FPN convs at 19136 pixels: 75 workgroups
+// of 256 rows, 299 of 64; 1.3-1.4x per layer, and without the split of K
+// the few big tiles needed; the 32-column tiles 0.6-2.2 % on every batch-1
+// plan).  Wide layers: fp32 takes 64x64 (its MFMA is slow enough that the
+// smaller tile's occupancy wins); bf16 takes 128x64 when that still gives
+// every CU several blocks (its faster MFMA needs the operand reuse of the
+// taller tile).
 static int pick_tile(int M, int cols, int dt) {
   if (cols <= 16) return (M + 255) / 256 < 256 ? 4 : 0;
   if (cols <= 32) return (M + 127) / 128 < 256 ? 5 : 1;
@@ -1849,13 +1855,11 @@ static int pick_tile(int M, int cols, int dt) {
 
 std::string conv_kernel_name(const ConvParams& p) {
   if (wide_layer(p)) return "conv_gemm_bf16<256x256,1x1>";
-  static const char* tiles[] = {"256x16", "128x32", "128x64", "64x64", "64x16", "64x32"};
-  static const int bm[] = {256, 128, 128, 64, 64, 64};
   static const char* variants[] = {",1x1", "", ",1x1,gate", ",1x1,reg", ",reg", ",1x1,reg4", ",reg4"};
   const int t = pick_tile(p.N * p.Ho * p.Wo, p.Co, p.dt);
-  const int v = conv_variant(p, bm[t]);
+  const int v = conv_variant(p, kTileBM[t]);
   const bool r128 = t == 3 && ((v == CV_DIRECT_1X1 && rows128_layer(p)) || (v == CV_DIRECT && rows128_kxk(p)));
-  return std::string(p.dt == DT_BF16 ? "conv_gemm_bf16<" : "conv_gemm<") + tiles[t] + variants[v] +
+  return std::string(p.dt == DT_BF16 ? "conv_gemm_bf16<" : "conv_gemm<") + kTileName[t] + variants[v] +
          (r128 ? ",r128" : "") + ">";
 }
 
@@ -1863,18 +1867,14 @@ int conv_se_blocks(const ConvParams& p) {
   if (p.N != 1 || p.splits > 1 || p.Co % 4 || p.out_ps % 4 || p.rep != 1 || p.db_ch || p.ctc_part || wide_layer(p) ||
       !regs_epilogue(p))
     return 0;
-  static const int bm[] = {256, 128, 128, 64, 64, 64};
-  static const int wm[] = {4, 4, 2, 2, 4, 4};
   const int M = p.Ho * p.Wo;
   const int t = pick_tile(M, p.Co, p.dt);
-  const int v = conv_variant(p, bm[t]);
-  if (v != CV_DIRECT_1X1) return 0;
-  return (M + bm[t] - 1) / bm[t] * wm[t];
+  if (conv_variant(p, kTileBM[t]) != CV_DIRECT_1X1) return 0;
+  return (M + kTileBM[t] - 1) / kTileBM[t] * kTileWM[t];
 }
 
 int conv_tile_cols(int M, int cols, int dt) {
-  static const int bn[] = {16, 32, 64, 64, 16, 32};
-  return bn[pick_tile(M, cols, dt)];
+  return kTileBN[pick_tile(M, cols, dt)];
 }
 
 // Split K when the tiles fill fewer than 192 of the 256 CUs: enough splits
@@ -1886,10 +1886,8 @@ int conv_tile_cols(int M, int cols, int dt) {
 // slower).  Each split keeps at least 8 K slices (the load pipeline is 3-4
 // slices deep), at most 16 splits.
 int conv_split_k(int M, int Co, int K, int dt) {
-  static const int bm[] = {256, 128, 128, 64, 64, 64};
-  static const int bn[] = {16, 32, 64, 64, 16, 32};
   const int t = pick_tile(M, Co, dt);
-  const long tiles = (long)((M + bm[t] - 1) / bm[t]) * ((Co + bn[t] - 1) / bn[t]);
+  const long tiles = (long)((M + kTileBM[t] - 1) / kTileBM[t]) * ((Co + kTileBN[t] - 1) / kTileBN[t]);
   const int bk = dt == DT_BF16 ? GemmTraits<bf16>::BK : GemmTraits<float>::BK;
   const int nk = (K + bk - 1) / bk;
   if (Co % 4 != 0 || wide_shape(M, Co, K, dt)) return 1;
@@ -1903,6 +1901,11 @@ int conv_split_k(int M, int Co, int K, int dt) {
   s = std::min<long>(s, nk / 8);
   s = std::min<long>(s, kMaxSplits);
   return s >= 2 ? (int)s : 1;
+}
+
+template <typename T, int I>
+static void launch_tile_shape(const ConvParams& p, int M, hipStream_t s) {
+  launch_tile<T, kTileBM[I], kTileBN[I], kTileWM[I], 4 / kTileWM[I]>(p, M, s);
 }
 
 template <typename T>
@@ -1939,12 +1942,12 @@ static void launch_typed(const ConvParams& p, hipStream_t s) {
     }
   }
   switch (pick_tile(M, p.Co, p.dt)) {
-    case 0: launch_tile<T, 256, 16, 4, 1>(p, M, s); break;
-    case 4: launch_tile<T, 64, 16, 4, 1>(p, M, s); break;
-    case 5: launch_tile<T, 64, 32, 4, 1>(p, M, s); break;
-    case 1: launch_tile<T, 128, 32, 4, 1>(p, M, s); break;
-    case 2: launch_tile<T, 128, 64, 2, 2>(p, M, s); break;
-    default: launch_tile<T, 64, 64, 2, 2>(p, M, s); break;
+    case 0: launch_tile_shape<T, 0>(p, M, s); break;
+    case 1: launch_tile_shape<T, 1>(p, M, s); break;
+    case 2: launch_tile_shape<T, 2>(p, M, s); break;
+    case 3: launch_tile_shape<T, 3>(p, M, s); break;
+    case 4: launch_tile_shape<T, 4>(p, M, s); break;
+    default: launch_tile_shape<T, 5>(p, M, s); break;
   }
 }
 
