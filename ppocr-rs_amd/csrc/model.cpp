@@ -381,7 +381,6 @@ class Builder {
     return out;
   }
 
-
   // Depthwise conv.  With se_cr > 0 a squeeze-excitation of reduction width
   // se_cr reads the output next; when the kernel can, and the gate is not
   // small enough for its one-kernel form, it also leaves the gate's channel
