@@ -423,6 +423,8 @@ __global__ __launch_bounds__(256) void depthwise_wave_kernel(DwParams p) {
 // read touches on distinct banks, and the columns past the tile's input
 // (read as the zero-weight tail of the last K group) are written as zeros.
 // Outputs are staged in the same LDS as four planes of channel pairs.
+// Registers are held to four waves per SIMD, what the LDS allows (the tile
+// loads issued ahead would otherwise cost a wave: three measured slower).
 constexpr int kDwMfmaT = 32, kDwMfmaP = 28, kDwMfmaC = 8;  // tile side, LDS row pitch (dwords), channels
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
