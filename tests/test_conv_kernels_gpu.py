@@ -85,7 +85,7 @@ CASES = [
     ("1x1 narrow Co, 257 row tiles", 1, 257, 256, 16, 12, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_RELU,
      "conv_gemm<256x16,1x1>"),
     ("3x3 narrow Co", 2, 13, 11, 8, 12, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 0, ACT_HSWISH, "conv_gemm<64x16>"),
-    ("1x1 Co 24, 256 row tiles", 1, 181, 181, 8, 24, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_NONE,
+    ("1x1 Co 24, 512 row tiles", 1, 256, 256, 8, 24, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_NONE,
      "conv_gemm<128x32,1x1>"),
     ("gated 1x1 direct", 3, 8, 10, 64, 64, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 0, ACT_RELU,
      "conv_gemm<64x64,1x1,gate>"),
