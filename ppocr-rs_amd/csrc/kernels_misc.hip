@@ -247,10 +247,12 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
   }
 }
 
-// LDS-tiled stride-1 depthwise for large kernels with the taps in scalar
-// registers: a block computes a 16 x 16 output tile of 16 channels and each
-// wave one group of 4 channels, so a wave's taps are uniform and come from
-// scalar loads (one tap row of KW float4 at a time) instead of LDS reads.
+// LDS-tiled stride-1 depthwise for large kernels with wave-uniform taps: a
+// block computes a 16 x 16 output tile of 16 channels and each wave one
+// group of 4 channels, so all lanes of a wave read the same tap vector (an
+// LDS broadcast: the block's taps are staged in LDS with the tile; read from
+// memory per tap row they cost the 9x9 layers 1.1x, the 5x5 even, although
+// staging them takes the 9x9 from four workgroups per CU to three).
 // Lane (ty, xg) = (lane / 4, lane % 4) slides a window of 4 + KW - 1 pixels
 // of tile row ty + ky for 4 outputs; a tap row costs 4 + KW - 1 LDS reads for
 // 4 * KW * 4 FMAs.  The input tile is stored per channel group with an odd
@@ -274,7 +276,9 @@ __global__ __launch_bounds__(256) void depthwise_wave_kernel(DwParams p) {
   constexpr int IWP = IW | 1;                  // odd pitch
   constexpr int OPX = 5, OROW = TX * OPX + 1;  // staged output pitch (float4)
   static_assert(G * IH * IWP >= TY * OROW, "output staging fits the tile");
+  constexpr int NT = KH * KW * G, TIT = (NT + 255) / 256;  // tap vectors of the block
   __shared__ float4 tile[G * IH * IWP];
+  __shared__ float4 taps[NT];
   const T* in = static_cast<const T*>(p.in);
 
   const int cblocks = (p.C + 4 * G - 1) / (4 * G);
@@ -289,6 +293,14 @@ __global__ __launch_bounds__(256) void depthwise_wave_kernel(DwParams p) {
   const int oy0 = (txy / tiles_x) % tiles_y * TY, ox0 = txy % tiles_x * TX;
   const int tid = threadIdx.x;
 
+  // The block's taps go to LDS with the tile (loaded with it).
+  float4 tv[TIT];
+#pragma unroll
+  for (int it = 0; it < TIT; ++it) {
+    const int i = tid + 256 * it;
+    const int c = ch0 + (i % G) * 4;
+    tv[it] = i < NT && c < p.C ? *reinterpret_cast<const float4*>(p.wt + (size_t)(i / G) * p.C + c) : f4_zero();
+  }
   {
     // A lane keeps one channel group and steps through the tile's pixels 64
     // at a time; the image base and channel test are hoisted, and the loads
@@ -354,6 +366,9 @@ __global__ __launch_bounds__(256) void depthwise_wave_kernel(DwParams p) {
       }
     }
   }
+#pragma unroll
+  for (int it = 0; it < TIT; ++it)
+    if (tid + 256 * it < NT) taps[tid + 256 * it] = tv[it];
   __syncthreads();
 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's channel group
@@ -361,18 +376,17 @@ __global__ __launch_bounds__(256) void depthwise_wave_kernel(DwParams p) {
   const int ty = lane >> 2, xg = lane & 3;
   const int c = ch0 + wave * 4;
   const bool cin = c < p.C;
-  const float* wt = p.wt + (cin ? c : 0);  // uniform: taps come through scalar loads
   float4 acc[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) acc[r] = f4_zero();
   const float4* trow = tile + (wave * IH + ty) * IWP + xg * 4;
-  // Three tap rows per iteration let a row's tap loads issue under the
-  // previous row's FMAs (5x5 layers 1.04x, 9x9 even, registers unchanged).
+  // Three tap rows per iteration (5x5 layers 1.04x with the taps read from
+  // memory, registers unchanged).
 #pragma unroll 3
   for (int ky = 0; ky < KH; ++ky) {
     float4 w[KW];
 #pragma unroll
-    for (int kx = 0; kx < KW; ++kx) w[kx] = *reinterpret_cast<const float4*>(wt + (size_t)(ky * KW + kx) * p.C);
+    for (int kx = 0; kx < KW; ++kx) w[kx] = taps[(ky * KW + kx) * G + wave];
     float4 win[4 + KW - 1];
 #pragma unroll
     for (int j = 0; j < 4 + KW - 1; ++j) win[j] = trow[ky * IWP + j];
@@ -746,7 +760,7 @@ static void launch_dw_typed(const DwParams& p, hipStream_t s) {
     return p.Ho == 3 ? launch_dw_strip<T, 3, 3, 3, 1>(p, s) : launch_dw_strip<T, 3, 3, 4, 1>(p, s);
   if (p.sh == 1 && p.sw == 1) {
     if (p.kh == 3 && p.kw == 3) return launch_dw_tiled<T, 3, 3, kDw3TY, dw3_xr(sizeof(T) == 2 ? DT_BF16 : DT_F32), kDw3C4B>(p, s);
-    // 5x5 and 9x9: taps in scalar registers (1.1-1.2x the LDS-tap kernel);
+    // 5x5 and 9x9: wave-uniform taps (1.1-1.2x the tiled kernel's per-lane taps);
     // 7x7 (32 channels here) measured even: 16-row tiles of 16 channels.
     if (p.kh == 5 && p.kw == 5) return launch_dw_wave<T, 5, 5>(p, s);
     if (p.kh == 7 && p.kw == 7) return launch_dw_tiled<T, 7, 7, 16, 4, 4>(p, s);
