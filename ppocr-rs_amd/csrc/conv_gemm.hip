@@ -1837,19 +1837,19 @@ constexpr int kTileWM[] = {4, 4, 2, 2, 4, 4};
 constexpr const char* kTileName[] = {"256x16", "128x32", "128x64", "64x64", "64x16", "64x32"};
 
 // Tile choice: narrow output channel counts get tall tiles so no MFMA
-// column is wasted, except that layers of at most 16 columns take 64-row
-// tiles while 256-row ones would not give every CU one, and layers of at
-// most 32 while 128-row ones would not give every CU two (the tiny
-// detector's 16-channel FPN convs at 19136 pixels: 75 workgroups of 256
-// rows, 299 of 64, 1.3-1.4x per layer and without the split of K the few
-// big tiles needed; the 32-column tiles 0.6-2.2 % on every batch-1 plan
-// and 0.2-0.6 % on the batch-8 detectors, where taller tiles stay faster
-// from about two per CU).  Wide layers: fp32 takes 64x64 (its MFMA is slow enough that the
+// column is wasted, except that layers of at most 16 (32) columns take
+// 64-row tiles while 256-row (128-row) ones would not give every CU two
+// (the tiny detector's 16-channel FPN convs at 19136 pixels: 75 workgroups
+// of 256 rows, 299 of 64, 1.3-1.4x per layer and without the split of K the
+// few big tiles needed; its stem and head convs at 832x1472 2.5 % of the
+// pass; the 32-column tiles 0.6-2.2 % on every batch-1 plan and 0.2-0.6 %
+// on the batch-8 detectors, where taller tiles stay faster from about two
+// per CU).  Wide layers: fp32 takes 64x64 (its MFMA is slow enough that the
 // smaller tile's occupancy wins); bf16 takes 128x64 when that still gives
 // every CU several blocks (its faster MFMA needs the operand reuse of the
 // taller tile).
 static int pick_tile(int M, int cols, int dt) {
-  if (cols <= 16) return (M + 255) / 256 < 256 ? 4 : 0;
+  if (cols <= 16) return (M + 255) / 256 < 512 ? 4 : 0;
   if (cols <= 32) return (M + 127) / 128 < 512 ? 5 : 1;
   if (dt == DT_BF16 && (long)((M + 127) / 128) * ((cols + 63) / 64) >= 2048) return 2;
   return 3;

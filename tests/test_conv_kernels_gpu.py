@@ -82,7 +82,7 @@ CASES = [
     ("3x3 stride 2", 2, 12, 10, 16, 64, (3, 3), (2, 2), (1, 1, 1, 1), False, 1, 0, ACT_NONE, "conv_gemm<64x64>"),
     ("7x1 asymmetric", 1, 9, 6, 8, 24, (7, 1), (1, 1), (3, 0, 3, 0), False, 1, 0, ACT_RELU, "conv_gemm<64x32>"),
     ("1x1 narrow Co", 1, 5, 6, 12, 10, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_SIGMOID, "conv_gemm<64x16,1x1>"),
-    ("1x1 narrow Co, 257 row tiles", 1, 257, 256, 16, 12, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_RELU,
+    ("1x1 narrow Co, 512 row tiles", 1, 512, 256, 16, 12, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_RELU,
      "conv_gemm<256x16,1x1>"),
     ("3x3 narrow Co", 2, 13, 11, 8, 12, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 0, ACT_HSWISH, "conv_gemm<64x16>"),
     ("1x1 Co 24, 512 row tiles", 1, 256, 256, 8, 24, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_NONE,
