@@ -164,8 +164,21 @@ struct PairParams {
   int dw_ps, dw_h, dw_w, dw_wo, dw_sh, dw_sw, dw_pt, dw_pl;
   const float* dw_wt;
   const float* dw_b;
+  // SE gate formed in the prologue (gate null, se_part set; one image,
+  // pair_se_fold_supported): the channel means of x from its partial sums
+  // se_part [se_P][C] over HW pixels, then act(W2 relu(W1 mean + b1) + b2)
+  // with W1 [se_Cr][C] and W2 [C][se_Cr] packed densely.
+  const float* se_part;
+  int se_P, se_Cr, se_act;
+  const float* se_w1;
+  const float* se_b1;
+  const float* se_w2;
+  const float* se_b2;
 };
 bool pointwise_pair_supported(int C, int H2, int Co, int dt);
+// Whether the pair kernel can form the SE gate of its input itself from P
+// partial channel sums (N images, C channels, H2 hidden, Cr reduced ones).
+bool pair_se_fold_supported(int N, int C, int H2, int Cr, int P);
 
 // LayerNorm fused into the linear layer that reads it (pair_gemm.hip), fp32:
 // out[m][n] = act(sum_k LN(x[m])[k] w[n][k] + b[n]), LN with eps over K

@@ -383,8 +383,8 @@ class Builder {
 
   // Depthwise conv.  With se_cr > 0 a squeeze-excitation of reduction width
   // se_cr reads the output next; when the kernel can, and the gate is not
-  // small enough for its one-kernel form, it also leaves the gate's channel
-  // sums in *sp (sp->P = 0 otherwise).
+  // small enough for its one-kernel form (or sums_always), it also leaves
+  // the gate's channel sums in *sp (sp->P = 0 otherwise).
   // The FPN gate-residual x = h + h * g (+ up2(upper)) applied as the
   // depthwise conv's input prologue: `x` passed to depthwise() is h, and
   // `out` (when set) receives x itself for the layers that read it next.
@@ -395,7 +395,7 @@ class Builder {
   };
 
   View depthwise(const View& x, const DwW& w, int act, const View* res, const std::string& name, int se_cr = 0,
-                 SePartial* sp = nullptr, const GateResidual* gr = nullptr) {
+                 SePartial* sp = nullptr, const GateResidual* gr = nullptr, bool sums_always = false) {
     if (x.c != w.c) raise(PPOCR_ERR_INVALID_MODEL, name + ": channel mismatch");
     if (gr && (res || se_cr || !depthwise_gate_residual_supported(w.kh, w.kw, w.sh, w.sw) || w.pt != w.kh / 2 ||
                w.pl != w.kw / 2 || (gr->upper && (x.h != 2 * gr->upper->h || x.w != 2 * gr->upper->w))))
@@ -416,7 +416,7 @@ class Builder {
       SeParams se{};
       se.N = x.n, se.HW = Ho * Wo, se.C = w.c, se.Cr = se_cr, se.dt = x.dt;
       const int P = depthwise_se_blocks(base);
-      if (se_cr > 0 && P > 0 && !se_fused(se)) {
+      if (se_cr > 0 && P > 0 && (sums_always || !se_fused(se))) {
         part = alloc(x.n, P, 1, w.c, name + ".se_partial", DT_F32);
         has_part = true;
         sp->part = part;
@@ -479,10 +479,16 @@ class Builder {
   // gate of x (or null) and `residual` adds the gated x.  With `dw` (no
   // gate), x is the input of the block's 3x3 depthwise token conv `dw`,
   // which the op computes per tile instead of reading its stored output.
+  // With se_sums and se (no gate view), the kernel forms x's SE gate itself
+  // from the channel sums the token conv left (pair_se_fold_supported).
   View pointwise_pair(const View& x, const ConvW& w1, const ConvW& w2, const View* gate, bool residual,
-                      const std::string& name, const DwW* dw = nullptr) {
-    if (dw && (gate || dw->kh != 3 || dw->kw != 3 || dw->c != x.c))
+                      const std::string& name, const DwW* dw = nullptr, const SePartial* se_sums = nullptr,
+                      const SeW* se = nullptr) {
+    if (dw && (gate || se_sums || dw->kh != 3 || dw->kw != 3 || dw->c != x.c))
       raise(PPOCR_ERR_INVALID_MODEL, name + ": depthwise prologue needs an ungated 3x3 depthwise");
+    const bool fold = se_sums && se;
+    if (fold && (gate || !pair_se_fold_supported(x.n, x.c, w1.co, se->cr, se_sums->P) || se->c != x.c))
+      raise(PPOCR_ERR_INVALID_MODEL, name + ": SE gate in the pair prologue is not supported for this shape");
     const int h = dw ? (x.h + dw->pt + dw->pb - 3) / dw->sh + 1 : x.h;
     const int w = dw ? (x.w + dw->pl + dw->pr - 3) / dw->sw + 1 : x.w;
     if (x.c != w1.ci_pad || w2.ci_pad != w1.co || w1.kh * w1.kw * w2.kh * w2.kw != 1)
@@ -491,8 +497,11 @@ class Builder {
     View out = alloc(x.n, h, w, w2.co, name);
     View in = x;
     View g = gate ? *gate : View();
-    const bool has_gate = gate;
+    const bool has_gate = gate || fold;
+    const View part = fold ? se_sums->part : View();
+    const SeW sw = fold ? *se : SeW();
     PairParams base{};
+    if (fold) base.se_P = se_sums->P, base.se_Cr = sw.cr, base.se_act = sw.act;
     base.in_ps = x.ps;
     base.HW = h * w;
     base.M = x.n * h * w;
@@ -509,14 +518,19 @@ class Builder {
     const bool has_dw = dw;
     Op op;
     op.name = name;
-    op.kernel = std::string("pointwise_pair") + (has_gate ? "<gate>" : has_dw ? "<dw3x3>" : "");
+    op.kernel = std::string("pointwise_pair") + (has_gate ? "<gate>" : has_dw ? "<dw3x3>" : "") + (fold ? "+se" : "");
     op.bound = 1;
     const double M = (double)base.M;
     op.flops = 2.0 * M * ((double)x.c * w1.co + (double)w1.co * w2.co + (has_dw ? 9.0 * x.c : 0.0));
     op.bytes = 4.0 * ((double)x.pixels() * x.c + (double)x.c * w1.co + (double)w1.co * w2.co + M * w2.co +
                       (has_dw ? 10.0 * x.c : 0.0));
+    if (fold) {
+      op.flops += 2.0 * 2.0 * x.c * sw.cr;
+      op.bytes += 4.0 * ((double)se_sums->P * x.c + 2.0 * x.c * sw.cr);
+    }
     op.reads = {x.buf};
-    if (has_gate) op.reads.push_back(g.buf);
+    if (gate) op.reads.push_back(g.buf);
+    if (fold) op.reads.push_back(part.buf);
     op.writes = {out.buf};
     op.launch = [=](const Exec& ex, hipStream_t s) {
       PairParams p = base;
@@ -524,7 +538,14 @@ class Builder {
       p.dw_in = has_dw ? ex.fptr(in) : nullptr;
       p.dw_wt = ex.w(dwo);
       p.dw_b = ex.w(dbo);
-      p.gate = has_gate ? ex.fptr(g) : nullptr;
+      p.gate = has_gate && !fold ? ex.fptr(g) : nullptr;
+      if (fold) {
+        p.se_part = ex.fptr(part);
+        p.se_w1 = ex.w(sw.w1);
+        p.se_b1 = ex.w(sw.b1);
+        p.se_w2 = ex.w(sw.w2);
+        p.se_b2 = ex.w(sw.b2);
+      }
       p.w1 = ex.w(w1o);
       p.b1 = ex.w(b1o);
       p.w2 = ex.w(w2o);
@@ -848,16 +869,22 @@ View lcnet_block(Builder& B, const View& x, const std::string& p, BlockSpec s) {
   // computes it per tile (src/cpu/backend.rs:697-816).
   if (!has_se && pair_fusion_pays(x, s.ci, s.co, B.dt()))
     return B.pointwise_pair(x, c1, c2, nullptr, residual, p + ".channel_conv", &tw);
+  // A single image's fused pair forms the SE gate in its own prologue from
+  // the token conv's channel sums (no gate launch) where the sums are few.
+  const bool pays = pair_fusion_pays(x, s.ci, s.co, B.dt());
+  const bool fold = has_se && pays && x.n == 1;
   Builder::SePartial sums;
-  View t = B.depthwise(x, tw, ACT_NONE, nullptr, p + ".token_conv", has_se ? s.ci / 4 : 0, &sums);
+  View t = B.depthwise(x, tw, ACT_NONE, nullptr, p + ".token_conv", has_se ? s.ci / 4 : 0, &sums, nullptr, fold);
   View gate;
+  SeW sw;
   if (has_se) {
     std::string q = p + ".token_squeeze_excitation.convolutions";
-    SeW sw = B.se_w(q + ".0", q + ".2", s.ci, s.ci / 4, ACT_HSIG6);
+    sw = B.se_w(q + ".0", q + ".2", s.ci, s.ci / 4, ACT_HSIG6);
+    if (fold && sums.P > 0 && pair_se_fold_supported(t.n, s.ci, 2 * s.ci, s.ci / 4, sums.P))
+      return B.pointwise_pair(t, c1, c2, nullptr, residual, p + ".channel_conv", nullptr, &sums, &sw);
     gate = B.se(t, sw, p + ".se", &sums);
   }
-  if (pair_fusion_pays(t, s.ci, s.co, B.dt()))
-    return B.pointwise_pair(t, c1, c2, has_se ? &gate : nullptr, residual, p + ".channel_conv");
+  if (pays) return B.pointwise_pair(t, c1, c2, has_se ? &gate : nullptr, residual, p + ".channel_conv");
   Epi e1;
   e1.act = ACT_GELU;
   if (has_se) e1.in_gate = &gate;

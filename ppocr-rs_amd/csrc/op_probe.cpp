@@ -413,6 +413,56 @@ int ppocr_probe_pointwise_pair(const float* x, int m, int hw, int c, const float
   return rc;
 }
 
+// ppocr_probe_pointwise_pair for one image (m pixels) whose SE gate the
+// kernel forms itself: part [P][c] partial channel sums of x, se_w1 [cr][c],
+// se_b1 [cr], se_w2 [c][cr], se_b2 [c], gate act(W2 relu(W1 sum/m + b1) +
+// b2) with activation se_act.  Returns 0, 1 on a HIP error, 2 when the
+// shape is outside pair_se_fold_supported.
+int ppocr_probe_pointwise_pair_se(const float* x, int m, int c, const float* part, int P, const float* se_w1,
+                                  const float* se_b1, int cr, const float* se_w2, const float* se_b2, int se_act,
+                                  const float* w1, const float* b1, int h2, const float* w2, const float* b2, int co,
+                                  int residual, float* out) {
+  if (!ppocr::pair_se_fold_supported(1, c, h2, cr, P)) return 2;
+  void* d_in = upload(x, (size_t)m * c, ppocr::DT_F32);
+  void* d_part = upload(part, (size_t)P * c, ppocr::DT_F32);
+  void* d_sw1 = upload(se_w1, (size_t)cr * c, ppocr::DT_F32);
+  void* d_sb1 = upload(se_b1, cr, ppocr::DT_F32);
+  void* d_sw2 = upload(se_w2, (size_t)c * cr, ppocr::DT_F32);
+  void* d_sb2 = upload(se_b2, c, ppocr::DT_F32);
+  void* d_w1 = upload(w1, (size_t)h2 * c, ppocr::DT_F32);
+  void* d_b1 = upload(b1, h2, ppocr::DT_F32);
+  void* d_w2 = upload(w2, (size_t)co * h2, ppocr::DT_F32);
+  void* d_b2 = upload(b2, co, ppocr::DT_F32);
+  void* d_out = nullptr;
+  int rc = 0;
+  if (!d_in || !d_part || !d_sw1 || !d_sb1 || !d_sw2 || !d_sb2 || !d_w1 || !d_b1 || !d_w2 || !d_b2 ||
+      hipMalloc(&d_out, (size_t)m * co * 4) != hipSuccess || !ppocr::pointwise_pair_supported(c, h2, co, 0)) {
+    rc = 1;
+  } else {
+    ppocr::PairParams p{};
+    p.in = static_cast<const float*>(d_in);
+    p.in_ps = c;
+    p.HW = m;
+    p.M = m, p.C = c, p.H2 = h2, p.Co = co;
+    p.w1 = static_cast<const float*>(d_w1), p.ldw1 = c, p.b1 = static_cast<const float*>(d_b1);
+    p.w2 = static_cast<const float*>(d_w2), p.ldw2 = h2, p.b2 = static_cast<const float*>(d_b2);
+    p.residual = residual;
+    p.out = static_cast<float*>(d_out);
+    p.out_ps = co;
+    p.se_part = static_cast<const float*>(d_part);
+    p.se_P = P, p.se_Cr = cr, p.se_act = se_act;
+    p.se_w1 = static_cast<const float*>(d_sw1), p.se_b1 = static_cast<const float*>(d_sb1);
+    p.se_w2 = static_cast<const float*>(d_sw2), p.se_b2 = static_cast<const float*>(d_sb2);
+    ppocr::launch_pointwise_pair(p, nullptr);
+    if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(out, d_out, (size_t)m * co * 4, hipMemcpyDeviceToHost) != hipSuccess)
+      rc = 1;
+  }
+  for (void* d : {d_in, d_part, d_sw1, d_sb1, d_sw2, d_sb2, d_w1, d_b1, d_w2, d_b2, d_out})
+    if (d) (void)hipFree(d);
+  return rc;
+}
+
 // Fused 3x3 depthwise -> pointwise pair (the pair kernel's depthwise
 // prologue) on host arrays: x [n][h][w][c], dw [9][c] taps, dwb [c], stride
 // (sh, sw), pads 1; then as ppocr_probe_pointwise_pair on the depthwise

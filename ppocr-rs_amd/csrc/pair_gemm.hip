@@ -91,6 +91,76 @@ __global__ __launch_bounds__(256) void pointwise_pair_kernel(PairParams p) {
   const int lrow = lane & 15, g = lane >> 4;
   const int m0 = blockIdx.x * PB_M;
 
+  // SE gate formed here (GATE with se_part, one image): gs[c] in the hidden
+  // tile's LDS, free until the hidden products.  Lane (ph, q) sums partial
+  // rows ph, ph + PH, ... of channel group q (at most 8: P <= 128, PH >= 16),
+  // the PH phase sums are added in order, then the two small convs run one
+  // output per lane with their weights staged in LDS; every load is issued
+  // before the first barrier.
+  const float* gs = nullptr;
+  if constexpr (GATE) {
+    if (p.se_part) {
+      float* g_lds = hs;             // [C]
+      float* mean = hs + 64;         // [C]
+      float* hid = hs + 128;         // [Cr]
+      float* w1s = hs + 144;         // [Cr][C]
+      float* w2s = w1s + p.se_Cr * p.C;  // [C][Cr]
+      float4* red = reinterpret_cast<float4*>(xs);  // [PH][C / 4], free until the input tile
+      const int C4 = p.C >> 2, PH = 256 / C4;
+      const int nw1 = p.se_Cr * p.C / 4, nw2 = p.C * p.se_Cr / 4;  // float4 of W1, W2 (<= 256 each)
+      // (Loads under if, not ?:, which the compiler turns into a load from
+      // either the buffer or a zero on the stack.)
+      float4 w1v = make_float4(0.f, 0.f, 0.f, 0.f), w2v = w1v;
+      if (tid < nw1) w1v = reinterpret_cast<const float4*>(p.se_w1)[tid];
+      if (tid < nw2) w2v = reinterpret_cast<const float4*>(p.se_w2)[tid];
+      float b1v = 0.0f, b2v = 0.0f;
+      if (tid < p.se_Cr) b1v = p.se_b1[tid];
+      if (tid < p.C) b2v = p.se_b2[tid];
+      const int q = tid % C4, ph = tid / C4;
+      float4 v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int row = ph + k * PH;
+        v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (ph < PH && row < p.se_P) v[k] = *reinterpret_cast<const float4*>(p.se_part + (size_t)row * p.C + 4 * q);
+      }
+      float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        sum = make_float4(sum.x + v[k].x, sum.y + v[k].y, sum.z + v[k].z, sum.w + v[k].w);
+      if (ph < PH) red[ph * C4 + q] = sum;
+      if (tid < nw1) reinterpret_cast<float4*>(w1s)[tid] = w1v;
+      if (tid < nw2) reinterpret_cast<float4*>(w2s)[tid] = w2v;
+      __syncthreads();
+      if (tid < C4) {
+        float4 t = red[tid];
+        for (int k = 1; k < PH; ++k) {
+          const float4 r = red[k * C4 + tid];
+          t = make_float4(t.x + r.x, t.y + r.y, t.z + r.z, t.w + r.w);
+        }
+        const float count = (float)p.HW;
+        mean[4 * tid + 0] = t.x / count;
+        mean[4 * tid + 1] = t.y / count;
+        mean[4 * tid + 2] = t.z / count;
+        mean[4 * tid + 3] = t.w / count;
+      }
+      __syncthreads();
+      if (tid < p.se_Cr) {
+        float a = 0.0f;
+        for (int c = 0; c < p.C; ++c) a = fmaf(w1s[tid * p.C + c], mean[c], a);
+        hid[tid] = fmaxf(a + b1v, 0.0f);
+      }
+      __syncthreads();
+      if (tid < p.C) {
+        float a = 0.0f;
+        for (int j = 0; j < p.se_Cr; ++j) a = fmaf(w2s[tid * p.se_Cr + j], hid[j], a);
+        g_lds[tid] = act_apply(p.se_act, a + b2v);
+      }
+      __syncthreads();
+      gs = g_lds;
+    }
+  }
+
   // Input tile, gated; rows past M are zero.
   const int c4 = p.C >> 2;
   for (int i = tid; i < PB_M * c4; i += 256) {
@@ -124,7 +194,8 @@ __global__ __launch_bounds__(256) void pointwise_pair_kernel(PairParams p) {
     } else if (m < p.M) {
       v = *reinterpret_cast<const float4*>(p.in + (size_t)m * p.in_ps + c);
       if constexpr (GATE) {
-        const float4 gt = *reinterpret_cast<const float4*>(p.gate + (size_t)(m / p.HW) * p.C + c);
+        const float4 gt = gs ? *reinterpret_cast<const float4*>(gs + c)
+                             : *reinterpret_cast<const float4*>(p.gate + (size_t)(m / p.HW) * p.C + c);
         v = make_float4(__fmul_rn(v.x, gt.x), __fmul_rn(v.y, gt.y), __fmul_rn(v.z, gt.z), __fmul_rn(v.w, gt.w));
       }
     }
@@ -273,12 +344,19 @@ bool pointwise_pair_supported(int C, int H2, int Co, int dt) {
   return dt == DT_F32 && C % 16 == 0 && H2 % 16 == 0 && Co % 16 == 0 && pointwise_pair_lds(C, H2) <= (160u << 10);
 }
 
+bool pair_se_fold_supported(int N, int C, int H2, int Cr, int P) {
+  // The phase sums fit the input tile's LDS (C >= 32), the staged weights,
+  // means and gate the hidden tile's, and a lane sums at most 8 rows.
+  return N == 1 && C >= 32 && C <= 64 && C % 4 == 0 && Cr >= 1 && Cr <= 16 && (C * Cr) % 4 == 0 && P >= 1 &&
+         P <= 8 * (256 / (C / 4)) && 144 + 2 * C * Cr <= PB_M * (H2 + 4);
+}
+
 size_t pointwise_pair_lds(int C, int H2) { return (size_t)PB_M * ((C + 4) + (H2 + 4)) * sizeof(float); }
 
 void launch_pointwise_pair(const PairParams& p, hipStream_t s) {
   const dim3 grid((unsigned)((p.M + PB_M - 1) / PB_M));
   const size_t lds = pointwise_pair_lds(p.C, p.H2);
-  const bool gate = p.gate != nullptr, res = p.residual != 0;
+  const bool gate = p.gate != nullptr || p.se_part != nullptr, res = p.residual != 0;
   if (p.dw_in) {
     if (res)
       hipLaunchKernelGGL((pointwise_pair_kernel<false, true, true>), grid, dim3(256), lds, s, p);

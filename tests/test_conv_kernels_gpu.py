@@ -218,6 +218,61 @@ def test_pointwise_pair_matches_float64(name, m, hw, c, co, gated, residual):
     assert np.all(err <= 1e-4 + 1e-5 * np.abs(want)), f"max err {err.max()}"
 
 
+# (name, m, c, co, partial rows, residual): one image whose SE gate the pair
+# kernel forms from partial channel sums, up to the most rows a lane sums.
+PAIR_SE_CASES = [
+    ("C32, 250 partial rows, residual", 900, 32, 32, 250, True),
+    ("C48, 84 partial rows", 333, 48, 96, 84, False),
+    ("C64, 128 partial rows, residual", 1000, 64, 64, 128, True),
+    ("C64, one partial row", 40, 64, 64, 1, False),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,m,c,co,P,residual", PAIR_SE_CASES, ids=[c[0] for c in PAIR_SE_CASES])
+def test_pointwise_pair_forms_se_gate(name, m, c, co, P, residual):
+    """The pair kernel's SE prologue: channel means from P partial sums, the
+    two small convs (ReLU, then hard-sigmoid(x/6 + 0.5)), x * gate, then the
+    pair, against float64 (the gate's sums run in another order than the
+    gate kernel's, within fp32 rounding)."""
+    from scipy.special import erf
+
+    lib = _lib()
+    f = ctypes.POINTER(ctypes.c_float)
+    i = ctypes.c_int
+    lib.ppocr_probe_pointwise_pair_se.argtypes = [f, i, i, f, i, f, f, i, f, f, i, f, f, i, f, f, i, i, f]
+    lib.ppocr_probe_pointwise_pair_se.restype = i
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    h2, cr = 2 * c, c // 4
+    x = rng.standard_normal((m, c)).astype(np.float32)
+    part = rng.standard_normal((P, c)).astype(np.float32) * np.float32(m / P)
+    sw1 = (rng.standard_normal((cr, c)) / np.sqrt(c)).astype(np.float32)
+    sb1 = rng.standard_normal(cr).astype(np.float32) * 0.1
+    sw2 = (rng.standard_normal((c, cr)) / np.sqrt(cr)).astype(np.float32)
+    sb2 = rng.standard_normal(c).astype(np.float32) * 0.1
+    w1 = (rng.standard_normal((h2, c)) / np.sqrt(c)).astype(np.float32)
+    b1 = rng.standard_normal(h2).astype(np.float32) * 0.1
+    w2 = (rng.standard_normal((co, h2)) / np.sqrt(h2)).astype(np.float32)
+    b2 = rng.standard_normal(co).astype(np.float32) * 0.1
+    out = np.empty((m, co), np.float32)
+    ACT_HSIG6 = 4
+    rc = lib.ppocr_probe_pointwise_pair_se(_ptr(x), m, c, _ptr(part), P, _ptr(sw1), _ptr(sb1), cr, _ptr(sw2),
+                                           _ptr(sb2), ACT_HSIG6, _ptr(w1), _ptr(b1), h2, _ptr(w2), _ptr(b2), co,
+                                           int(residual), _ptr(out))
+    assert rc == 0
+    mean = part.astype(np.float64).sum(axis=0) / m
+    hid = np.maximum(sw1.astype(np.float64) @ mean + sb1, 0.0)
+    gate = np.clip((sw2.astype(np.float64) @ hid + sb2) / 6.0 + 0.5, 0.0, 1.0)
+    xg = x.astype(np.float64) * gate
+    h = xg @ w1.T.astype(np.float64) + b1
+    h = 0.5 * h * (1.0 + erf(h / np.sqrt(2.0)))
+    want = h @ w2.T.astype(np.float64) + b2
+    if residual:
+        want = want + xg
+    err = np.abs(out - want)
+    assert np.all(err <= 1e-4 + 1e-5 * np.abs(want)), f"max err {err.max()}"
+
+
 # (name, n, h, w, c, stride, co, residual): maps whose pixel count is not a
 # multiple of the 32-pixel tile, strides 1 and 2, a tile spanning two images.
 PAIR_DW_CASES = [
