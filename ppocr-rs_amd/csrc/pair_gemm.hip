@@ -14,7 +14,10 @@
 // h W2^T + b2 (+ x for a residual block) from that, 16 output channels at a
 // time.  Weights stream from L2.  The sums run in the order of the unfused
 // kernel (K slices of 16 ascending, four MFMAs per slice), so results match
-// it up to its split-K choices.
+// it up to its split-K choices.  For one image the SE gate itself can be
+// formed in the prologue from the token conv's partial channel sums (the
+// squeeze-excitation's mean and two small convs, src/cpu/model.rs:456-493),
+// so no separate gate launch precedes the pair.
 #include "device_math.h"
 #include "kernels.h"
 
