@@ -96,7 +96,7 @@ __global__ __launch_bounds__(256) void pointwise_pair_kernel(PairParams p) {
 
   // SE gate formed here (GATE with se_part, one image): gs[c] in the hidden
   // tile's LDS, free until the hidden products.  Lane (ph, q) sums partial
-  // rows ph, ph + PH, ... of channel group q (at most 8: P <= 128, PH >= 16),
+  // rows ph, ph + PH, ... of channel group q (eight loads in flight at a time),
   // the PH phase sums are added in order, then the two small convs run one
   // output per lane with their weights staged in LDS; every load is issued
   // before the first barrier.
@@ -120,17 +120,20 @@ __global__ __launch_bounds__(256) void pointwise_pair_kernel(PairParams p) {
       if (tid < p.se_Cr) b1v = p.se_b1[tid];
       if (tid < p.C) b2v = p.se_b2[tid];
       const int q = tid % C4, ph = tid / C4;
-      float4 v[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int row = ph + k * PH;
-        v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (ph < PH && row < p.se_P) v[k] = *reinterpret_cast<const float4*>(p.se_part + (size_t)row * p.C + 4 * q);
-      }
       float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int r0 = 0; r0 < p.se_P; r0 += 8 * PH) {  // eight rows per lane in flight at a time
+        float4 v[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
-        sum = make_float4(sum.x + v[k].x, sum.y + v[k].y, sum.z + v[k].z, sum.w + v[k].w);
+        for (int k = 0; k < 8; ++k) {
+          const int row = r0 + ph + k * PH;
+          v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (ph < PH && row < p.se_P)
+            v[k] = *reinterpret_cast<const float4*>(p.se_part + (size_t)row * p.C + 4 * q);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          sum = make_float4(sum.x + v[k].x, sum.y + v[k].y, sum.z + v[k].z, sum.w + v[k].w);
+      }
       if (ph < PH) red[ph * C4 + q] = sum;
       if (tid < nw1) reinterpret_cast<float4*>(w1s)[tid] = w1v;
       if (tid < nw2) reinterpret_cast<float4*>(w2s)[tid] = w2v;
@@ -349,9 +352,9 @@ bool pointwise_pair_supported(int C, int H2, int Co, int dt) {
 
 bool pair_se_fold_supported(int N, int C, int H2, int Cr, int P) {
   // The phase sums fit the input tile's LDS (C >= 32), the staged weights,
-  // means and gate the hidden tile's, and a lane sums at most 8 rows.
+  // means and gate the hidden tile's, and a lane sums at most 32 rows.
   return N == 1 && C >= 32 && C <= 64 && C % 4 == 0 && Cr >= 1 && Cr <= 16 && (C * Cr) % 4 == 0 && P >= 1 &&
-         P <= 8 * (256 / (C / 4)) && 144 + 2 * C * Cr <= PB_M * (H2 + 4);
+         P <= 32 * (256 / (C / 4)) && 144 + 2 * C * Cr <= PB_M * (H2 + 4);
 }
 
 size_t pointwise_pair_lds(int C, int H2) { return (size_t)PB_M * ((C + 4) + (H2 + 4)) * sizeof(float); }

@@ -219,12 +219,14 @@ def test_pointwise_pair_matches_float64(name, m, hw, c, co, gated, residual):
 
 
 # (name, m, c, co, partial rows, residual): one image whose SE gate the pair
-# kernel forms from partial channel sums, up to the most rows a lane sums.
+# kernel forms from partial channel sums, one to three rounds of eight rows
+# per lane.
 PAIR_SE_CASES = [
     ("C32, 250 partial rows, residual", 900, 32, 32, 250, True),
     ("C48, 84 partial rows", 333, 48, 96, 84, False),
     ("C64, 128 partial rows, residual", 1000, 64, 64, 128, True),
     ("C64, one partial row", 40, 64, 64, 1, False),
+    ("C32, 600 partial rows in three rounds", 2000, 32, 32, 600, True),
 ]
 
 
