@@ -48,8 +48,8 @@ METRIC = "detector images/s @416×736 + rec lines/s @48×320; % HBM/MFMA rooflin
 PEAK_F32_TFLOPS = 157.3
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
-# fp32 FMAs on the vector ALU without packed-fp32 instructions (this build
-# disables them): 256 CUs x 4 SIMDs x 16 lanes x 2 FLOP x 2.4 GHz.
+# fp32 FMAs on the vector ALU without packed-fp32 instructions (the HIP code
+# is compiled without them): 256 CUs x 4 SIMDs x 16 lanes x 2 FLOP x 2.4 GHz.
 PEAK_VALU_F32_TFLOPS = 78.6
 TMP = pathlib.Path(tempfile.gettempdir()) / "ppocr_bench_models"
 
@@ -369,7 +369,7 @@ def main():
         only(args.only, args.warmup, args.steps)
         return
     if args.gpus != 1:
-        print("bench.py measures one GPU: the detector/recognizer path has no multi-GPU form in this build "
+        print("bench.py measures one GPU: the detector/recognizer path has no multi-GPU form in this library "
               "(independent images shard across GPUs without communication); run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)

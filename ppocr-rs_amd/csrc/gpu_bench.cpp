@@ -12,7 +12,7 @@
 // Differences, all additive: `--batch N` (the reference benchmarks batch 1
 // only) and `--precision f32|bf16`.  Models resolve from `--model`, or from
 // `<model-dir>/<size>-<kind>/model.safetensors` (src/models.rs:325-344)
-// when that file is already cached: this build never downloads, so
+// when that file is already cached: this program never downloads, so
 // `--offline` changes nothing and `--verify-models`, which needs the pinned
 // catalog's digests, is refused.
 #include <algorithm>
@@ -277,11 +277,11 @@ std::string resolve_model_path(const Args& a) {
   if (!a.model.empty()) return a.model;
   const std::string name = a.model_size + "-" + a.kind;
   if (a.verify_models)
-    throw Fail("--verify-models needs the pinned model catalog, which this build does not carry; pass --model");
+    throw Fail("--verify-models needs the pinned model catalog, which this program does not carry; pass --model");
   const std::string path = a.model_dir + "/" + name + "/model.safetensors";
   if (!is_file(path))
     throw Fail(name + " is missing in " + a.model_dir + "/" + name +
-               "; this build does not download models: pass --model or fill the cache");
+               "; this program does not download models: pass --model or fill the cache");
   return path;
 }
 
