@@ -30,18 +30,28 @@ __device__ __forceinline__ void lse_merge(float& m, float& s, int& i, float om, 
   s = a + b;
 }
 
-__device__ __forceinline__ float erf_as(float value) {
-  float sign = value < 0.0f ? -1.0f : 1.0f;
-  float x = fabsf(value);
-  float t = fast_rcp(fmaf(x, 0.3275911f, 1.0f));
-  float poly = t * (0.2548296f + t * (-0.28449672f + t * (1.4214138f + t * (-1.4531521f + t * 1.0614054f))));
-  return sign * (1.0f - poly * fast_exp(-x * x));
+// GELU(v) = v/2 (1 + erf(v / sqrt 2)) with the A-S 7.1.26 erf: for
+// x = |v| / sqrt 2, t = 1 / (1 + p x) and E = poly(t) exp(-x^2),
+// erf(v / sqrt 2) = sign(v) (1 - E).  With h = v/2, h sign(v) = |h|, so
+// GELU(v) = h + |h| (1 - E): one fused multiply-add and an add in place of
+// the sign select and three products.  The 1/sqrt 2 scaling is folded into
+// the constants (p / sqrt 2 in the t denominator; the exp2 argument
+// x^2 log2(e) is y^2 with y = |v| sqrt(log2(e) / 2)).  Thirteen vector
+// operations per element, two of them transcendental.
+__device__ __forceinline__ float gelu_as(float v) {
+  const float a = fabsf(v);
+  const float t = fast_rcp(fmaf(a, 0.3275911f * 0.70710678118654752f, 1.0f));
+  const float poly = t * (0.2548296f + t * (-0.28449672f + t * (1.4214138f + t * (-1.4531521f + t * 1.0614054f))));
+  const float y = a * 0.84932180028801904f;
+  const float e = poly * __builtin_amdgcn_exp2f(-(y * y));
+  const float h = 0.5f * v, ha = fabsf(h);
+  return h + fmaf(-ha, e, ha);
 }
 
 __device__ __forceinline__ float act_apply(int act, float v) {
   switch (act) {
     case ACT_RELU: return fmaxf(v, 0.0f);
-    case ACT_GELU: return 0.5f * v * (1.0f + erf_as(v * 0.70710678118654752f));
+    case ACT_GELU: return gelu_as(v);
     case ACT_SILU: return v * fast_rcp(1.0f + fast_exp(-v));
     case ACT_HSIG6: return fminf(fmaxf(fmaf(v, 1.0f / 6.0f, 0.5f), 0.0f), 1.0f);
     case ACT_HSIG5: return fminf(fmaxf(fmaf(v, 0.2f, 0.5f), 0.0f), 1.0f);
