@@ -242,6 +242,17 @@ void launch_se(const SeParams& p, hipStream_t s);
 // Stages 2 and 3 of launch_se from partial sums already in p.partial
 // ([N][P][C], e.g. from the producing depthwise).
 void launch_se_from_partials(const SeParams& p, hipStream_t s);
+// Up to four gates from given partial sums in one launch (grid y = gate),
+// for the FPN's per-level gates: each gate must take the one-workgroup path
+// (se_multi_kind) and all of them the same kind.
+constexpr int kSeMultiMax = 4;
+struct SeMulti {
+  SeParams p[kSeMultiMax];
+  int count;
+};
+// 1 (small weights), 2 (one workgroup, larger weights) or 0 (not batchable).
+int se_multi_kind(const SeParams& p);
+void launch_se_multi(const SeMulti& m, hipStream_t s);
 // Whether launch_se runs the gate as one kernel (small maps and weights; the
 // partial and hidden arrays are then unused).
 bool se_fused(const SeParams& p);
@@ -257,6 +268,20 @@ void launch_maxpool_same(const void* in, int N, int H, int W, int C, int in_ps, 
 // rep x rep blocks (rep = 1: plain) into a tensor of pixel stride out_ps.
 void launch_gate_residual(const void* in, int N, int H, int W, int C, int in_ps, const float* gate,
                           const void* upper, int up_ps, void* out, int out_ps, int rep, int dt, hipStream_t s);
+// Up to four gate_residual writes without an upper level (same N and
+// storage type) in one launch: part i takes blocks first[i] .. first[i+1]-1.
+struct GateResidualPart {
+  const void* in;
+  int H, W, C, in_ps;
+  const float* gate;
+  void* out;
+  int out_ps, rep;
+};
+struct GateResidualMulti {
+  GateResidualPart part[4];
+  int count, N, dt;
+};
+void launch_gate_residual_multi(const GateResidualMulti& m, hipStream_t s);
 
 // out[n, p, c] = x[n, p, c] * gate[n, c] rounded to the storage type; out is
 // packed (pixel stride C).

@@ -6,7 +6,9 @@
 // (16 B as fp32, 8 B as bf16) and consecutive lanes touch consecutive
 // segments: every global access of these kernels is coalesced.  Arithmetic
 // is fp32 for both storage types.
+#include <algorithm>
 #include <cstring>
+#include <stdexcept>
 #include <type_traits>
 
 #include "device_math.h"
@@ -925,14 +927,13 @@ __global__ __launch_bounds__(256) void se_expand_kernel(SeParams p) {
 constexpr int kSeSmallC = 256, kSeSmallCr = 64;
 
 template <typename T, bool PARTIALS, bool SMALL>
-__global__ __launch_bounds__(1024) void se_fused_kernel(SeParams p) {
+__device__ __forceinline__ void se_fused_body(const SeParams& p, const int n) {
   extern __shared__ float sm[];
   const int cr4 = (p.Cr + 3) & ~3;
   float* mean = sm;                                          // [C]
   float* hid = sm + p.C;                                     // [Cr]
   float4* red = reinterpret_cast<float4*>(sm + p.C + cr4);  // [1024]
   const T* in = static_cast<const T*>(p.in);
-  const int n = blockIdx.x;
   const int tid = threadIdx.x;
   const int C4 = p.C >> 2;
   const int lanes_p = 1024 / C4;
@@ -1040,6 +1041,23 @@ __global__ __launch_bounds__(1024) void se_fused_kernel(SeParams p) {
   }
 }
 
+template <typename T, bool PARTIALS, bool SMALL>
+__global__ __launch_bounds__(1024) void se_fused_kernel(SeParams p) {
+  se_fused_body<T, PARTIALS, SMALL>(p, blockIdx.x);
+}
+
+// Several gates from given partial sums, one per grid row (the cases index
+// the parameter array with constants, so it stays in kernel arguments).
+template <bool SMALL>
+__global__ __launch_bounds__(1024) void se_multi_kernel(SeMulti m) {
+  switch (blockIdx.y) {
+    case 0: se_fused_body<float, true, SMALL>(m.p[0], blockIdx.x); break;
+    case 1: se_fused_body<float, true, SMALL>(m.p[1], blockIdx.x); break;
+    case 2: se_fused_body<float, true, SMALL>(m.p[2], blockIdx.x); break;
+    default: se_fused_body<float, true, SMALL>(m.p[3], blockIdx.x); break;
+  }
+}
+
 bool se_fused(const SeParams& p) {
   const size_t es = p.dt == DT_BF16 ? 2 : 4;
   return p.C % 4 == 0 && p.C <= 4096 && (size_t)p.HW * p.C * es <= (256u << 10) &&
@@ -1066,6 +1084,31 @@ void launch_se_from_partials(const SeParams& p, hipStream_t s) {
   size_t lds = (size_t)p.C * sizeof(float) + 256 * sizeof(float4);
   hipLaunchKernelGGL(se_reduce_kernel, dim3(p.N, (p.Cr + 15) / 16), dim3(256), lds, s, p);
   hipLaunchKernelGGL(se_expand_kernel, dim3(p.N, (p.C + 15) / 16), dim3(256), (size_t)p.Cr * sizeof(float), s, p);
+}
+
+static size_t se_one_block_lds(const SeParams& p) {
+  return ((size_t)p.C + ((p.Cr + 3) & ~3)) * sizeof(float) + 1024 * sizeof(float4);
+}
+
+int se_multi_kind(const SeParams& p) {
+  if (!se_gate_one_block(p) || p.C % 4 || p.P < 1) return 0;
+  return p.C <= kSeSmallC && p.Cr <= kSeSmallCr ? 1 : 2;
+}
+
+void launch_se_multi(const SeMulti& m, hipStream_t s) {
+  if (m.count < 1 || m.count > kSeMultiMax) throw std::runtime_error("launch_se_multi: 1 to 4 gates");
+  const int kind = se_multi_kind(m.p[0]);
+  size_t lds = 0;
+  for (int i = 0; i < m.count; ++i) {
+    if (se_multi_kind(m.p[i]) != kind || kind == 0 || m.p[i].N != m.p[0].N)
+      throw std::runtime_error("launch_se_multi: gates of different kinds or image counts");
+    lds = std::max(lds, se_one_block_lds(m.p[i]));
+  }
+  const dim3 grid((unsigned)m.p[0].N, (unsigned)m.count);
+  if (kind == 1)
+    hipLaunchKernelGGL(se_multi_kernel<true>, grid, dim3(1024), lds, s, m);
+  else
+    hipLaunchKernelGGL(se_multi_kernel<false>, grid, dim3(1024), lds, s, m);
 }
 
 void launch_se(const SeParams& p, hipStream_t s) {
@@ -1192,10 +1235,10 @@ void launch_avgpool32(const void* in, int N, int H, int W, int C, int in_ps, voi
 // (upsample_and_cat_nchw, :1322-1417): each input pixel is written as a
 // rep x rep block into its channel slice of the concat tensor.
 template <typename T>
-__global__ void gate_residual_kernel(const T* in, int N, int H, int W, int C, int in_ps, const float* gate,
-                                     const T* upper, int up_ps, T* out, int out_ps, int rep) {
+__device__ __forceinline__ void gate_residual_at(long idx, const T* in, int N, int H, int W, int C, int in_ps,
+                                                 const float* gate, const T* upper, int up_ps, T* out, int out_ps,
+                                                 int rep) {
   const int C4 = C >> 2;
-  long idx = (long)blockIdx.x * 256 + threadIdx.x;
   long total = (long)N * H * W * C4;
   if (idx >= total) return;
   int c = (int)(idx % C4) * 4;
@@ -1222,12 +1265,52 @@ __global__ void gate_residual_kernel(const T* in, int N, int H, int W, int C, in
   }
 }
 
+template <typename T>
+__global__ void gate_residual_kernel(const T* in, int N, int H, int W, int C, int in_ps, const float* gate,
+                                     const T* upper, int up_ps, T* out, int out_ps, int rep) {
+  gate_residual_at<T>((long)blockIdx.x * 256 + threadIdx.x, in, N, H, W, C, in_ps, gate, upper, up_ps, out, out_ps,
+                      rep);
+}
+
+// Several gate_residual writes in one launch: block b belongs to the last
+// part whose first block is <= b (constant indices into the kernel
+// arguments, as in se_multi_kernel).
+template <typename T>
+__global__ void gate_residual_multi_kernel(GateResidualMulti m, int first1, int first2, int first3) {
+  const int b = blockIdx.x;
+  const int i = (b >= first1) + (b >= first2) + (b >= first3);
+  const int first = i == 0 ? 0 : i == 1 ? first1 : i == 2 ? first2 : first3;
+  const long idx = (long)(b - first) * 256 + threadIdx.x;
+  auto run = [&](const GateResidualPart& q) {
+    gate_residual_at<T>(idx, static_cast<const T*>(q.in), m.N, q.H, q.W, q.C, q.in_ps, q.gate, nullptr, 0,
+                        static_cast<T*>(q.out), q.out_ps, q.rep);
+  };
+  switch (i) {
+    case 0: run(m.part[0]); break;
+    case 1: run(m.part[1]); break;
+    case 2: run(m.part[2]); break;
+    default: run(m.part[3]); break;
+  }
+}
+
 void launch_gate_residual(const void* in, int N, int H, int W, int C, int in_ps, const float* gate,
                           const void* upper, int up_ps, void* out, int out_ps, int rep, int dt, hipStream_t s) {
   long total = (long)N * H * W * (C / 4);
   DISPATCH_DT(dt, hipLaunchKernelGGL(gate_residual_kernel<T>, dim3(blocks_for(total)), dim3(256), 0, s,
                                      static_cast<const T*>(in), N, H, W, C, in_ps, gate,
                                      static_cast<const T*>(upper), up_ps, static_cast<T*>(out), out_ps, rep));
+}
+
+void launch_gate_residual_multi(const GateResidualMulti& m, hipStream_t s) {
+  if (m.count < 1 || m.count > 4) throw std::runtime_error("launch_gate_residual_multi: 1 to 4 parts");
+  int first[4] = {0, INT32_MAX, INT32_MAX, INT32_MAX};
+  long blocks = 0;
+  for (int i = 0; i < m.count; ++i) {
+    first[i] = (int)blocks;
+    blocks += blocks_for((long)m.N * m.part[i].H * m.part[i].W * (m.part[i].C / 4));
+  }
+  DISPATCH_DT(m.dt, hipLaunchKernelGGL(gate_residual_multi_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s, m,
+                                       first[1], first[2], first[3]));
 }
 
 // SE gate applied to a whole tensor: out = x * g[n, c] rounded to the

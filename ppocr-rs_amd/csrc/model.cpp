@@ -611,6 +611,93 @@ class Builder {
     return gate;
   }
 
+  // The gates of several maps, each with the channel sums its producing conv
+  // left: one launch where every gate takes the one-workgroup path with the
+  // same kernel, otherwise one se() op per map.
+  std::vector<View> se_levels(const std::vector<View>& xs, const std::vector<SeW>& ws, const std::string& name,
+                              const std::vector<SePartial>& sps) {
+    const int count = (int)xs.size();
+    bool batch = count >= 2 && count <= kSeMultiMax;
+    int kind = -1;
+    std::vector<SeParams> ps(count);
+    for (int i = 0; batch && i < count; ++i) {
+      const View& x = xs[i];
+      SeParams& b = ps[i];
+      b = SeParams{};
+      b.N = x.n, b.HW = x.h * x.w, b.C = x.c, b.in_ps = x.ps, b.P = sps[i].P, b.Cr = ws[i].cr;
+      b.gate_act = ws[i].act, b.dt = x.dt;
+      const int k = sps[i].P > 0 ? se_multi_kind(b) : 0;
+      batch = k != 0 && (kind < 0 || k == kind) && x.n == xs[0].n;
+      kind = k;
+    }
+    std::vector<View> gates(count);
+    if (!batch) {
+      for (int i = 0; i < count; ++i) gates[i] = se(xs[i], ws[i], name + "." + std::to_string(i), &sps[i]);
+      return gates;
+    }
+    std::vector<View> parts(count);
+    std::vector<SeW> wv = ws;
+    Op op;
+    op.name = name;
+    op.kernel = "se_gates+sums";
+    op.flops = op.bytes = 0.0;
+    for (int i = 0; i < count; ++i) {
+      const View& x = xs[i];
+      gates[i] = alloc(x.n, 1, 1, x.c, name + "." + std::to_string(i), DT_F32);
+      parts[i] = sps[i].part;
+      op.flops += 2.0 * x.n * ((double)x.h * x.w * x.c + 2.0 * x.c * ws[i].cr);
+      op.bytes += 4.0 * x.n * sps[i].P * x.c + 4.0 * (2.0 * x.c * ws[i].cr + x.n * x.c);
+      op.reads.push_back(parts[i].buf);
+      op.writes.push_back(gates[i].buf);
+    }
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      SeMulti m{};
+      m.count = count;
+      for (int i = 0; i < count; ++i) {
+        SeParams p = ps[i];
+        p.partial = ex.fptr(parts[i]);
+        p.w1 = ex.w(wv[i].w1);
+        p.b1 = ex.w(wv[i].b1);
+        p.w2 = ex.w(wv[i].w2);
+        p.b2 = ex.w(wv[i].b2);
+        p.gate = ex.fptr(gates[i]);
+        m.p[i] = p;
+      }
+      launch_se_multi(m, s);
+    };
+    add_op(std::move(op));
+    return gates;
+  }
+
+  // x_i + x_i*g_i written replicated (rep_i) into dst_i for several maps of
+  // the same image count and storage type, in one launch.
+  void gate_residual_levels(const std::vector<View>& xs, const std::vector<View>& gs, const std::vector<View>& dsts,
+                            const std::vector<int>& reps, const std::string& name) {
+    const int count = (int)xs.size();
+    Op op;
+    op.name = name;
+    op.kernel = "gate_residual";
+    op.bytes = 0.0;
+    for (int i = 0; i < count; ++i) {
+      op.bytes += (double)dtype_size(xs[i].dt) * xs[i].pixels() * xs[i].c * (1 + reps[i] * reps[i]);
+      op.reads.push_back(xs[i].buf);
+      op.reads.push_back(gs[i].buf);
+      op.writes.push_back(dsts[i].buf);
+    }
+    std::vector<View> in = xs, gate = gs, out = dsts;
+    std::vector<int> rep = reps;
+    const int n = xs[0].n, dt = xs[0].dt;
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      GateResidualMulti m{};
+      m.count = count, m.N = n, m.dt = dt;
+      for (int i = 0; i < count; ++i)
+        m.part[i] = GateResidualPart{ex.ptr(in[i]), in[i].h,          in[i].w, in[i].c, in[i].ps,
+                                     ex.fptr(gate[i]), ex.ptr(out[i]), out[i].ps, rep[i]};
+      launch_gate_residual_multi(m, s);
+    };
+    add_op(std::move(op));
+  }
+
   // x + x*g [+ up2(upper)], written (optionally replicated) into dst.
   void gate_residual(const View& x, const View& g, const View* upper, const View& dst, int rep,
                      const std::string& name) {
@@ -985,16 +1072,18 @@ std::vector<std::vector<BlockSpec>> recognizer_stages(int size) {
 // channel slot 3 - i (deepest first) upsampled by 2^i.
 View rep_lk_fpn(Builder& B, const std::vector<View>& st, const int chans[4], int nc, int k) {
   const int q = nc / 4;
-  std::vector<View> h(4), g(4), fused(4);
+  std::vector<View> h(4), fused(4);
+  std::vector<Builder::SePartial> sums(4);
+  std::vector<SeW> sws(4);
   for (int i = 0; i < 4; ++i) {
     std::string p = "model.neck.insert_conv." + std::to_string(i);
     ConvW w = B.conv_w(p + ".in_conv", chans[i], nc, 1, 1, 1, 1, {0, 0, 0, 0}, false);
-    Builder::SePartial sums;
-    h[i] = B.conv(st[i], w, Epi{}, p + ".in_conv", &sums);
-    SeW sw = B.se_w(p + ".squeeze_excitation_block.conv1", p + ".squeeze_excitation_block.conv2", nc, nc / 4,
+    h[i] = B.conv(st[i], w, Epi{}, p + ".in_conv", &sums[i]);
+    sws[i] = B.se_w(p + ".squeeze_excitation_block.conv1", p + ".squeeze_excitation_block.conv2", nc, nc / 4,
                     ACT_HSIG5);
-    g[i] = B.se(h[i], sw, p + ".se", &sums);
   }
+  // The four levels' gates (each from its conv's channel sums) in one launch.
+  std::vector<View> g = B.se_levels(h, sws, "model.neck.insert_conv.se", sums);
   // fused[i] = h + h * g (+ up2(fused[i + 1])) feeds input_conv i's
   // depthwise and level i - 1.  Where the depthwise can form it from h in its
   // tile loads, levels run deepest first and the depthwise also stores it for
@@ -1027,18 +1116,24 @@ View rep_lk_fpn(Builder& B, const std::vector<View>& st, const int chans[4], int
       d[i] = B.depthwise(h[i], dws[i], ACT_NONE, nullptr, "model.neck.input_conv." + std::to_string(i) +
                          ".depthwise_convolution", 0, nullptr, &gr);
     }
+  std::vector<View> pt(4), slots(4);
+  std::vector<Builder::SePartial> psums(4);
+  std::vector<SeW> psw(4);
+  std::vector<int> reps(4);
   for (int i = 0; i < 4; ++i) {
     std::string p = "model.neck.input_conv." + std::to_string(i);
     if (!gr_fused) d[i] = B.depthwise(fused[i], dws[i], ACT_NONE, nullptr, p + ".depthwise_convolution");
     ConvW pw = B.conv_w(p + ".pointwise_convolution", nc, q, 1, 1, 1, 1, {0, 0, 0, 0}, false);
-    Builder::SePartial sums;
-    View pt = B.conv(d[i], pw, Epi{}, p + ".pointwise_convolution", &sums);
-    SeW sw = B.se_w(p + ".squeeze_excitation_module.conv1", p + ".squeeze_excitation_module.conv2", q, q / 4,
+    pt[i] = B.conv(d[i], pw, Epi{}, p + ".pointwise_convolution", &psums[i]);
+    psw[i] = B.se_w(p + ".squeeze_excitation_module.conv1", p + ".squeeze_excitation_module.conv2", q, q / 4,
                     ACT_HSIG5);
-    View gi = B.se(pt, sw, p + ".se", &sums);
-    View slot = Builder::slice(cat, (3 - i) * q, q);
-    B.gate_residual(pt, gi, nullptr, slot, 1 << i, p + ".out");
+    slots[i] = Builder::slice(cat, (3 - i) * q, q);
+    reps[i] = 1 << i;
   }
+  // Every level's gate, then every level's x + x*g written upsampled into
+  // its concat slot (deepest first in the channels): one launch each.
+  std::vector<View> gi = B.se_levels(pt, psw, "model.neck.input_conv.se", psums);
+  B.gate_residual_levels(pt, gi, slots, reps, "model.neck.input_conv.out");
   return cat;
 }
 
