@@ -513,4 +513,95 @@ const char* ppocr_probe_depthwise_kernel(int h, int c, int k, int dt, int table)
   return ppocr::depthwise_kernel_name(k, k, 1, 1, h, dt, table != 0, c);
 }
 
+// Batched FPN gates on host arrays.  Gate i (dims[4i..4i+3] = HW, C, P, Cr)
+// takes its partial sums [n][P][C], w1 [Cr][C], b1 [Cr], w2 [C][Cr], b2 [C]
+// from the concatenation of the per-gate arrays, in gate order; gates [n][C]
+// are written the same way.  Returns 0, 1 on a HIP error, 2 when the gates
+// cannot share one launch.
+int ppocr_probe_se_multi(int count, int n, const int* dims, const float* part, const float* w1, const float* b1,
+                         const float* w2, const float* b2, int act, float* gates) {
+  if (count < 1 || count > ppocr::kSeMultiMax) return 2;
+  ppocr::SeMulti m{};
+  m.count = count;
+  std::vector<void*> bufs;
+  size_t op = 0, ow1 = 0, ob1 = 0, ow2 = 0, ob2 = 0, og = 0;
+  int rc = 0;
+  int kind = -1;
+  for (int i = 0; i < count && rc == 0; ++i) {
+    const int HW = dims[4 * i], C = dims[4 * i + 1], P = dims[4 * i + 2], Cr = dims[4 * i + 3];
+    ppocr::SeParams q{};
+    q.N = n, q.HW = HW, q.C = C, q.in_ps = C, q.P = P, q.Cr = Cr, q.gate_act = act, q.dt = ppocr::DT_F32;
+    const int k = ppocr::se_multi_kind(q);
+    if (k == 0 || (kind >= 0 && k != kind)) rc = 2;
+    kind = k;
+    void* d[6] = {upload(part + op, (size_t)n * P * C, ppocr::DT_F32), upload(w1 + ow1, (size_t)Cr * C, ppocr::DT_F32),
+                  upload(b1 + ob1, Cr, ppocr::DT_F32),                upload(w2 + ow2, (size_t)C * Cr, ppocr::DT_F32),
+                  upload(b2 + ob2, C, ppocr::DT_F32),                 nullptr};
+    if (hipMalloc(&d[5], (size_t)n * C * 4) != hipSuccess) d[5] = nullptr;
+    for (void* b : d) {
+      bufs.push_back(b);
+      if (!b) rc = rc ? rc : 1;
+    }
+    q.partial = static_cast<float*>(d[0]);
+    q.w1 = static_cast<const float*>(d[1]), q.b1 = static_cast<const float*>(d[2]);
+    q.w2 = static_cast<const float*>(d[3]), q.b2 = static_cast<const float*>(d[4]);
+    q.gate = static_cast<float*>(d[5]);
+    m.p[i] = q;
+    op += (size_t)n * P * C, ow1 += (size_t)Cr * C, ob1 += Cr, ow2 += (size_t)C * Cr, ob2 += C;
+  }
+  if (rc == 0) {
+    ppocr::launch_se_multi(m, nullptr);
+    if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess) rc = 1;
+    for (int i = 0; i < count && rc == 0; ++i) {
+      const size_t bytes = (size_t)n * m.p[i].C * 4;
+      if (hipMemcpy(gates + og, m.p[i].gate, bytes, hipMemcpyDeviceToHost) != hipSuccess) rc = 1;
+      og += (size_t)n * m.p[i].C;
+    }
+  }
+  for (void* b : bufs)
+    if (b) (void)hipFree(b);
+  return rc;
+}
+
+// Batched gate_residual writes on host arrays: part i (dims[4i..4i+3] = H,
+// W, C, rep) reads x [n][H][W][C] and gate [n][C] and writes out
+// [n][H rep][W rep][C], each array the concatenation of the per-part ones.
+// Returns 0, or 1 on a HIP error.
+int ppocr_probe_gate_residual_multi(int count, int n, const int* dims, const float* x, const float* gate,
+                                    float* out) {
+  if (count < 1 || count > 4) return 1;
+  ppocr::GateResidualMulti m{};
+  m.count = count, m.N = n, m.dt = ppocr::DT_F32;
+  std::vector<void*> bufs;
+  size_t ox = 0, og = 0;
+  int rc = 0;
+  for (int i = 0; i < count; ++i) {
+    const int H = dims[4 * i], W = dims[4 * i + 1], C = dims[4 * i + 2], rep = dims[4 * i + 3];
+    void* dx = upload(x + ox, (size_t)n * H * W * C, ppocr::DT_F32);
+    void* dg = upload(gate + og, (size_t)n * C, ppocr::DT_F32);
+    void* dout = nullptr;
+    if (hipMalloc(&dout, (size_t)n * H * rep * W * rep * C * 4) != hipSuccess) dout = nullptr;
+    for (void* b : {dx, dg, dout}) {
+      bufs.push_back(b);
+      if (!b) rc = 1;
+    }
+    m.part[i] = ppocr::GateResidualPart{dx, H, W, C, C, static_cast<const float*>(dg), dout, C, rep};
+    ox += (size_t)n * H * W * C, og += (size_t)n * C;
+  }
+  if (rc == 0) {
+    ppocr::launch_gate_residual_multi(m, nullptr);
+    if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess) rc = 1;
+    size_t oo = 0;
+    for (int i = 0; i < count && rc == 0; ++i) {
+      const ppocr::GateResidualPart& q = m.part[i];
+      const size_t cnt = (size_t)n * q.H * q.rep * q.W * q.rep * q.C;
+      if (hipMemcpy(out + oo, q.out, cnt * 4, hipMemcpyDeviceToHost) != hipSuccess) rc = 1;
+      oo += cnt;
+    }
+  }
+  for (void* b : bufs)
+    if (b) (void)hipFree(b);
+  return rc;
+}
+
 }  // extern "C"
