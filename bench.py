@@ -1,5 +1,10 @@
 #!/usr/bin/env python3
-"""Throughput benchmark of the MI355X backend (one JSON line on stdout).
+"""Throughput benchmark of the MI355X backend.
+
+The LAST stdout line is the headline JSON record (under 8 KB); detail
+records (per-configuration kernel tables, pass rates, host pipeline timings,
+CPU sample descriptions) come first, one JSON line each, as
+``{"detail": name, "data": ...}``.
 
 Workload (the headline configuration that fits one GPU): the PP-OCRv6
 medium detector, fp32, batch 8 of 3x416x736 seeded-pixel images with seeded
@@ -15,7 +20,7 @@ Alongside ``value`` the line carries:
   bf16 matrix 2.5 PFLOP/s, fp32 vector 78.6 TFLOP/s without packed fp32,
   HBM 8 TB/s); ``traffic`` is its measured HBM bytes per launch from the
   committed counter summary, when one covers this kernel and workload;
-* ``kernels``: the same measure for the twelve kernel instances with the
+* (detail line) the same measure for the twelve kernel instances with the
   most device time (the depthwise and elementwise ones against HBM);
 * ``pass``: the whole pass's algorithmic FLOPs and bytes per step over the
   step time;
@@ -25,7 +30,8 @@ Alongside ``value`` the line carries:
   src/cpu/model.rs:19-27); ``others`` holds the same at every CPU this
   process may use and for the tiny and medium recognizers;
 * ``also``: the other benchmark configurations, measured after the timed
-  region, each with its own dominant-kernel roofline and pass rates.
+  region: value, step time and the dominant kernel's roofline fraction
+  (their full records, with pass rates and kernel tables, are detail lines).
 """
 
 import argparse
@@ -215,13 +221,23 @@ def cpu_time(kind, size, threads, budget_s):
 def cpu_baseline(kind, size):
     """The oracle at the reference's default thread count, min(cores, 4)
     (src/cpu/model.rs:19-27), with the same at every usable CPU and for the
-    tiny and medium recognizers under ``others``."""
+    tiny and medium recognizers under ``others`` (value, unit, threads and
+    workload only; the full sample descriptions go to an earlier line)."""
     cpus, how = usable_cpus()
     base = cpu_time(kind, size, min(cpus, 4), 10.0)
     base["cpus"] = how
-    base["others"] = [cpu_time(kind, size, cpus, 8.0), cpu_time("rec", "tiny", min(cpus, 4), 3.0),
-                      cpu_time("rec", "tiny", cpus, 3.0), cpu_time("rec", "medium", min(cpus, 4), 4.0)]
+    others = [("det", size, cpu_time(kind, size, cpus, 8.0)), ("rec", "tiny", cpu_time("rec", "tiny", min(cpus, 4), 3.0)),
+              ("rec", "tiny", cpu_time("rec", "tiny", cpus, 3.0)),
+              ("rec", "medium", cpu_time("rec", "medium", min(cpus, 4), 4.0))]
+    emit("cpu_baseline_samples", [o["sample"] for _, _, o in others])
+    base["others"] = [{"workload": f"{sz} {'detector 1x3x416x736' if k == 'det' else 'recognizer 1x3x48x320'}",
+                       "value": o["value"], "unit": o["unit"], "cores": o["cores"]} for k, sz, o in others]
     return base
+
+
+def emit(name, payload):
+    """One detail line (JSON) on stdout ahead of the headline line."""
+    print(json.dumps({"detail": name, "data": payload}), flush=True)
 
 
 def config_key(kind, size, shape, precision, greedy=False):
@@ -260,30 +276,32 @@ def measure(gpu, kind, size, shape, precision, greedy, warmup, steps, top=5):
             "kernels": kernel_table(stats, top, precision)}
 
 
+ALSO_CONFIGS = [
+    ("det", "tiny", (1, 3, 416, 736), "f32"),
+    ("det", "small", (1, 3, 416, 736), "f32"),
+    ("det", "small", (8, 3, 416, 736), "f32"),
+    ("det", "medium", (1, 3, 416, 736), "f32"),
+    ("det", "tiny", (1, 3, 832, 1472), "f32"),
+    ("rec", "tiny", (1, 3, 48, 320), "f32"),
+    ("rec", "small", (1, 3, 48, 320), "f32"),
+    ("rec", "medium", (1, 3, 48, 320), "f32"),
+    ("rec", "tiny", (64, 3, 48, 320), "f32"),
+    ("rec", "small", (64, 3, 48, 320), "f32"),
+    ("rec", "medium", (256, 3, 48, 320), "f32"),
+    ("det", "medium", (1, 3, 416, 736), "bf16"),
+    ("det", "medium", (8, 3, 416, 736), "bf16"),
+    ("rec", "medium", (256, 3, 48, 320), "bf16"),
+    # Recognizers with the classifier fused with greedy CTC step decoding
+    # (per-step class + probability instead of [N, T, V] probabilities).
+    ("rec", "tiny", (64, 3, 48, 320), "f32", "greedy"),
+    ("rec", "medium", (256, 3, 48, 320), "f32", "greedy"),
+    ("rec", "medium", (256, 3, 48, 320), "bf16", "greedy"),
+]
+
+
 def also(gpu, warmup, steps):
     out = {}
-    configs = [
-        ("det", "tiny", (1, 3, 416, 736), "f32"),
-        ("det", "small", (1, 3, 416, 736), "f32"),
-        ("det", "small", (8, 3, 416, 736), "f32"),
-        ("det", "medium", (1, 3, 416, 736), "f32"),
-        ("det", "tiny", (1, 3, 832, 1472), "f32"),
-        ("rec", "tiny", (1, 3, 48, 320), "f32"),
-        ("rec", "small", (1, 3, 48, 320), "f32"),
-        ("rec", "medium", (1, 3, 48, 320), "f32"),
-        ("rec", "tiny", (64, 3, 48, 320), "f32"),
-        ("rec", "small", (64, 3, 48, 320), "f32"),
-        ("rec", "medium", (256, 3, 48, 320), "f32"),
-        ("det", "medium", (1, 3, 416, 736), "bf16"),
-        ("det", "medium", (8, 3, 416, 736), "bf16"),
-        ("rec", "medium", (256, 3, 48, 320), "bf16"),
-        # Recognizers with the classifier fused with greedy CTC step decoding
-        # (per-step class + probability instead of [N, T, V] probabilities).
-        ("rec", "tiny", (64, 3, 48, 320), "f32", "greedy"),
-        ("rec", "medium", (256, 3, 48, 320), "f32", "greedy"),
-        ("rec", "medium", (256, 3, 48, 320), "bf16", "greedy"),
-    ]
-    for kind, size, shape, precision, *mode in configs:
+    for kind, size, shape, precision, *mode in ALSO_CONFIGS:
         greedy = mode == ["greedy"]
         key = config_key(kind, size, shape, precision, greedy)
         try:
@@ -351,6 +369,49 @@ def pipeline(gpu, reps=20):
     return out
 
 
+def compact_also(extra):
+    """Per configuration only value, step time and the dominant kernel's
+    roofline fraction: the full records go to earlier detail lines."""
+    out = {}
+    for key, r in extra.items():
+        if "error" in r:
+            out[key] = {"error": r["error"][:120]}
+            continue
+        out[key] = {"value": r["value"], "unit": r["unit"], "ms_per_step": r["ms_per_step"],
+                    "frac": r["roofline"]["frac"]}
+    return out
+
+
+def headline(value, steps, warmup, ms_per_step, shape, roof, pass_, cpu=None, extra=None):
+    """The last stdout line: the metric, its roofline and CPU baseline, and a
+    compact summary of the other configurations (kept well under 8 KB so a
+    tail of the output always holds it whole)."""
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded uniform RGB8 pixels (BGR-normalised as the reference preprocess), "
+                "seeded weights at the reference tensor names/shapes",
+        "config": {"workload": "PP-OCRv6 medium detector, fp32, batch 8, input 8x3x416x736",
+                   "model_size": "medium", "batch": shape[0], "height": shape[2], "width": shape[3]},
+        "roofline": roof,
+        "pass": pass_,
+    }
+    if cpu is not None:
+        line["cpu_baseline"] = cpu
+    if extra is not None:
+        line["also"] = compact_also(extra)
+    return json.dumps(line, separators=(",", ":"))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -384,34 +445,18 @@ def main():
     stats = model.profile(x, runs=max(3, min(args.steps, 10)))
     roof = roofline(stats, HEADLINE_KEY, precision)
     model.close()
+    emit(HEADLINE_KEY + "_kernels", kernel_table(stats))
 
-    line = {
-        "metric": METRIC,
-        "value": round(value, 3),
-        "unit": "images/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic: seeded uniform RGB8 pixels (BGR-normalised as the reference preprocess), "
-                "seeded weights at the reference tensor names/shapes",
-        "config": {"workload": "PP-OCRv6 medium detector, fp32, batch 8, input 8x3x416x736",
-                   "model_size": "medium", "batch": shape[0], "height": shape[2], "width": shape[3]},
-        "roofline": roof,
-        "kernels": kernel_table(stats),
-        "pass": pass_rates(stats, ms_per_step, precision),
-    }
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(kind, size)
+    cpu = None if args.no_cpu else cpu_baseline(kind, size)
+    extra = None
     if not args.no_extra:
-        line["also"] = also(gpu, args.warmup, max(5, args.steps // 2))
-        line["pipeline"] = pipeline(gpu)
+        extra = also(gpu, args.warmup, max(5, args.steps // 2))
+        for key, r in extra.items():
+            emit(key, r)
+        emit("pipeline", pipeline(gpu))
     gpu.close()
-    print(json.dumps(line), flush=True)
+    print(headline(value, args.steps, args.warmup, ms_per_step, shape, roof,
+                   pass_rates(stats, ms_per_step, precision), cpu, extra), flush=True)
 
 
 if __name__ == "__main__":

@@ -60,6 +60,23 @@ const char* ppocr_hip_last_error(void);
 ppocr_status ppocr_hip_create(int device, ppocr_hip_ctx** out);
 void ppocr_hip_destroy(ppocr_hip_ctx* ctx);
 
+/* `GpuInfo` (src/gpu/runtime.rs:17-21): the adapter's name, backend and
+ * device type, plus what a HIP device adds (architecture, compute units,
+ * memory).  Strings are NUL-terminated and cut to fit. */
+typedef struct ppocr_gpu_info {
+  char name[256];    /* marketing name, e.g. "AMD Instinct MI355X" */
+  char backend[16];  /* "HIP" (the reference reports its wgpu backend) */
+  char arch[64];     /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int device;        /* HIP device index of the context */
+  int integrated;    /* 1 for an integrated GPU (wgpu DeviceType::IntegratedGpu), 0 for a discrete one */
+  int compute_units;
+  int wavefront_size;
+  size_t total_memory; /* bytes of device memory */
+} ppocr_gpu_info;
+
+/* Replaces `Gpu::info` (src/gpu/runtime.rs:169-171). */
+ppocr_status ppocr_hip_device_info(const ppocr_hip_ctx* ctx, ppocr_gpu_info* out);
+
 /* Replaces `Detector::load` (src/gpu/model.rs:50-93): loads a safetensors
  * file, checks the tier's tensor count (350/271/271), folds BatchNorm, packs
  * the weights, and plans the graph for the fixed input shape `nchw`
@@ -216,8 +233,9 @@ ppocr_status ppocr_hip_db_postprocess(ppocr_hip_ctx* ctx, const float* prob, siz
  * of 64 MiB per GPU, held until the process ends; it calls no hipMalloc or
  * hipFree.  Maps needing more scratch (about 51 bytes per pixel, e.g. four
  * 416 x 736 maps) are rejected with PPOCR_ERR_INVALID_INPUT.  All calls on
- * one GPU share its scratch: calls that overlap on one GPU (from different
- * contexts; one context serialises its own calls) race. */
+ * one GPU share its scratch, so calls on one GPU serialise (also across
+ * contexts): a call holds the device's scratch from staging the maps until
+ * its detections are read back. */
 ppocr_status ppocr_hip_db_postprocess_static(ppocr_hip_ctx* ctx, const float* prob, size_t n, size_t height,
                                              size_t width, const ppocr_detector_transform* transforms,
                                              const ppocr_db_options* options, ppocr_detection* out, size_t cap,

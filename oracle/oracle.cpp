@@ -96,13 +96,26 @@ enum Fault {
 
 inline bool fault(int f) { return g_fault == f; }
 
-// bf16 storage emulation (tests of the bf16 path): when on, the tensors a
-// bf16 plan stores are rounded to bf16 (nearest even) as they are produced,
-// and so are the weights it feeds to the matrix cores (after BN folding);
-// sums, SE gates, LayerNorm parameters, biases and the outputs stay fp32.
-// The error of this emulation against the fp32 oracle is the yardstick of
-// the bf16 path's tolerances.
+// bf16 storage emulation (tests of the bf16 path): when on, the values a
+// bf16 plan rounds to bf16 (nearest even) are rounded where they are
+// produced, and so are the weights it feeds to the matrix cores (dense convs
+// and linear layers, depthwise 5x5 and wider, the head's transposed conv;
+// after BN folding); sums, SE gates, LayerNorm parameters, biases and the
+// outputs stay fp32.  A sum that a bf16 plan forms in one kernel epilogue
+// (a residual or upsampled add after a conv or linear layer, the LightSVTR
+// skip after the final LayerNorm, the FPN's x + x*g + up2(upper)) is rounded
+// once, after the add.  Every rounding point is named (the value, or "W"
+// and the layer for weights) and logged, so a test can compare the list
+// with the plan's own.  The error of this emulation against the fp32
+// oracle is the yardstick of the bf16 path's tolerances.
 bool g_bf16 = false;
+std::vector<std::string> g_bf16_log;
+
+// Summation order (tests only): with g_reverse_sums the matrix products,
+// depthwise convs and attention sums accumulate their terms last to first.
+// Under the bf16 emulation, the spread between the two orders measures how
+// far fp32 summation order alone moves outputs of a bf16-storage network.
+bool g_reverse_sums = false;
 
 inline float round_bf16(float f) {
   uint32_t u;
@@ -113,18 +126,23 @@ inline float round_bf16(float f) {
   return f;
 }
 
-// Rounds t in place when the emulation is on; returns it.
-Tensor& bf(Tensor& t) {
-  if (g_bf16)
+// Rounds t (the value `name`) in place when the emulation is on; returns it.
+Tensor& bf(Tensor& t, const std::string& name) {
+  if (g_bf16) {
+    g_bf16_log.push_back("A " + name);
     for (float& v : t.v) v = round_bf16(v);
+  }
   return t;
 }
 
-// w itself, or with the emulation on a bf16-rounded copy of it held in tmp.
-const Tensor& bf_weights(const Tensor& w, Tensor& tmp) {
+// w (the weights of layer `name`) itself, or with the emulation on a
+// bf16-rounded copy of it held in tmp.
+const Tensor& bf_weights(const Tensor& w, Tensor& tmp, const std::string& name) {
   if (!g_bf16) return w;
+  g_bf16_log.push_back("W " + name);
   tmp = w;
-  return bf(tmp);
+  for (float& v : tmp.v) v = round_bf16(v);
+  return tmp;
 }
 
 void trace(const std::string& name, const Tensor& t) {
@@ -379,7 +397,8 @@ void gemm(float* C, const float* A, const float* B, int M, int K, int N, long ld
       float acc[MB][NB];
       for (int m = m0; m < m1; ++m)
         for (int j = 0; j < nn; ++j) acc[m - m0][j] = 0.0f;
-      for (int k = 0; k < K; ++k) {
+      for (int kk = 0; kk < K; ++kk) {
+        const int k = g_reverse_sums ? K - 1 - kk : kk;
         const float* b = B + (long)k * ldb + n0;
         for (int m = m0; m < m1; ++m) {
           float a = A[(long)m * K + k];
@@ -449,10 +468,12 @@ Tensor conv2d(const Tensor& x, const Tensor& W, const float* bias, int sh, int s
       for (int oy = 0; oy < Ho; ++oy) {
         for (int ox = 0; ox < Wo; ++ox) {
           float acc = 0.0f;
-          for (int ky = 0; ky < kh; ++ky) {
+          for (int kyy = 0; kyy < kh; ++kyy) {
+            const int ky = g_reverse_sums ? kh - 1 - kyy : kyy;
             int iy = oy * sh + ky - pads[0];
             if (iy < 0 || iy >= H) continue;
-            for (int kx = 0; kx < kw; ++kx) {
+            for (int kxx = 0; kxx < kw; ++kxx) {
+              const int kx = g_reverse_sums ? kw - 1 - kxx : kxx;
               int ix = ox * sw + kx - pads[1];
               if (ix < 0 || ix >= Wd) continue;
               acc = std::fma(src[(long)iy * Wd + ix], wk[ky * kw + kx], acc);
@@ -528,7 +549,7 @@ Tensor max_pool_2x2_same(const Tensor& x) {
 
 // Average pool, kernel [3,2], stride [3,2], no pad, count_include_pad=false
 // (src/cpu/ops.rs:1537-1604).
-Tensor avg_pool_3x2(const Tensor& x) {
+Tensor avg_pool_3x2(const Tensor& x, const std::string& name = "pool") {
   int H = x.h(), W = x.w();
   int Ho = (H - 3) / 3 + 1, Wo = (W - 2) / 2 + 1;
   Tensor y({x.n(), x.c(), Ho, Wo});
@@ -545,7 +566,7 @@ Tensor avg_pool_3x2(const Tensor& x) {
         d[(long)oy * Wo + ox] = v / 6.0f;
       }
   }
-  return bf(y);
+  return bf(y, name);
 }
 
 // global_average_pool: mean over the plane (src/cpu/ops.rs:1480-1495).
@@ -563,39 +584,41 @@ Tensor global_mean(const Tensor& x) {
   return y;
 }
 
-Tensor add(const Tensor& a, const Tensor& b) {
+Tensor add(const Tensor& a, const Tensor& b, const std::string& name = "") {
   ENSURE(a.shape == b.shape, "add shape mismatch");
   Tensor y(a.shape);
   long n = (long)a.count();
 #pragma omp parallel for schedule(static)
   for (long i = 0; i < n; ++i) y.v[i] = a.v[i] + b.v[i];
-  return bf(y);
+  return bf(y, name);
 }
 
 // x * gate[n, c] (plain SE, src/cpu/model.rs:487-492).
-Tensor mul_gate(const Tensor& x, const Tensor& g) {
+Tensor mul_gate(const Tensor& x, const Tensor& g, const std::string& name = "") {
   Tensor y(x.shape);
   long plane = (long)x.h() * x.w();
   long planes = (long)x.n() * x.c();
 #pragma omp parallel for schedule(static)
   for (long p = 0; p < planes; ++p)
     for (long i = 0; i < plane; ++i) y.v[p * plane + i] = x.v[p * plane + i] * g.v[p];
-  return bf(y);
+  return bf(y, name);
 }
 
 // into_residual_mul (src/cpu/backend.rs:180-199).
-Tensor residual_mul_gate(const Tensor& x, const Tensor& g) {
+// With `round` false the result stays fp32 (an add follows in the same
+// kernel of a bf16 plan).
+Tensor residual_mul_gate(const Tensor& x, const Tensor& g, const std::string& name = "", bool round = true) {
   Tensor y(x.shape);
   long plane = (long)x.h() * x.w();
   long planes = (long)x.n() * x.c();
 #pragma omp parallel for schedule(static)
   for (long p = 0; p < planes; ++p)
     for (long i = 0; i < plane; ++i) y.v[p * plane + i] = residual_mul(x.v[p * plane + i], g.v[p]);
-  return bf(y);
+  return round ? bf(y, name) : y;
 }
 
 // upsample_add_nchw: feature[y][x] += upper[y/s][x/s] (src/cpu/model.rs:1265-1320).
-Tensor upsample_add(Tensor feature, const Tensor& upper, int s) {
+Tensor upsample_add(Tensor feature, const Tensor& upper, int s, const std::string& name = "") {
   ENSURE(feature.n() == upper.n() && feature.c() == upper.c() && feature.h() == upper.h() * s &&
              feature.w() == upper.w() * s,
          "upsample-add shape mismatch");
@@ -606,7 +629,7 @@ Tensor upsample_add(Tensor feature, const Tensor& upper, int s) {
     for (int y = 0; y < H; ++y)
       for (int x = 0; x < W; ++x)
         feature.v[(p * H + y) * W + x] += upper.v[(p * uh + y / s) * uw + x / s];
-  return bf(feature);
+  return bf(feature, name);
 }
 
 // upsample_and_cat_nchw: nearest integer upsample then channel concat
@@ -639,9 +662,13 @@ Tensor upsample_cat(const std::vector<Tensor>& fs, const std::vector<int>& scale
 
 // Linear::run: y = x W^T + b, optional activation / row softmax
 // (src/cpu/backend.rs:1292-1370).
-Tensor linear(const Tensor& x, const Tensor& W_, const Tensor* b, int act, bool softmax) {
+// `name` names the layer (its weights) and its output value; with `round`
+// false the output stays fp32 (an add follows in the same kernel of a bf16
+// plan).
+Tensor linear(const Tensor& x, const Tensor& W_, const Tensor* b, int act, bool softmax, const std::string& name = "",
+              bool round = true) {
   Tensor tmp;
-  const Tensor& W = bf_weights(W_, tmp);
+  const Tensor& W = bf_weights(W_, tmp, name);
   int K = W.shape[1], M = W.shape[0];
   ENSURE(x.shape.back() == K, "Linear input feature count");
   long rows = (long)x.count() / K;
@@ -655,21 +682,25 @@ Tensor linear(const Tensor& x, const Tensor& W_, const Tensor* b, int act, bool 
     for (int m = 0; m < M; ++m) {
       const float* wr = W.data() + (size_t)m * K;
       float acc = 0.0f;
-      for (int k = 0; k < K; ++k) acc = std::fma(xi[k], wr[k], acc);
+      for (int kk = 0; kk < K; ++kk) {
+        const int k = g_reverse_sums ? K - 1 - kk : kk;
+        acc = std::fma(xi[k], wr[k], acc);
+      }
       yo[m] = apply_act(act, acc + (b ? b->v[m] : 0.0f));
     }
     if (softmax) softmax_row(yo, M);
   }
-  return softmax ? y : bf(y);
+  return softmax || !round ? y : bf(y, name);
 }
 
-Tensor layer_norm(const Tensor& x, const Tensor& w, const Tensor& b, float eps) {
+Tensor layer_norm(const Tensor& x, const Tensor& w, const Tensor& b, float eps, const std::string& name = "",
+                  bool round = true) {
   int F = w.shape[0];
   Tensor y = x;
   long rows = (long)x.count() / F;
 #pragma omp parallel for schedule(static)
   for (long r = 0; r < rows; ++r) layer_norm_row(y.data() + r * F, w.data(), b.data(), F, eps);
-  return bf(y);
+  return round ? bf(y, name) : y;
 }
 
 // ---------------------------------------------------------------- layers
@@ -696,14 +727,17 @@ struct Conv {
   int sh = 1, sw = 1, pads[4] = {0, 0, 0, 0}, groups = 1;
   int act = ACT_NONE;
   bool fp32_only = false;  // SE 1x1 convs: fp32 weights and outputs in every plan
-  Tensor forward(const Tensor& x, int a = -1) const {
+  std::string name;        // module path: names the weights and the output value
+  // With `round` false the output stays fp32: an add follows in the same
+  // kernel of a bf16 plan.
+  Tensor forward(const Tensor& x, int a = -1, bool round = true) const {
     // Matrix-core layers (dense convs, depthwise 5x5 and wider) take bf16
     // weights in a bf16 plan.
     const bool mfma = groups == 1 || (W.shape[2] >= 5 && W.shape[3] >= 5);
     Tensor tmp;
-    const Tensor& w = !fp32_only && mfma ? bf_weights(W, tmp) : W;
+    const Tensor& w = !fp32_only && mfma ? bf_weights(W, tmp, name) : W;
     Tensor y = conv2d(x, w, b.empty() ? nullptr : b.data(), sh, sw, pads, groups, a < 0 ? act : a);
-    return fp32_only ? y : bf(y);
+    return fp32_only || !round ? y : bf(y, name);
   }
 };
 
@@ -711,6 +745,7 @@ struct Conv {
 Conv load_conv(const Weights& wt, const std::string& p, int ci, int co, int kh, int kw, int sh, int sw,
                std::vector<int> pads, bool bias, int groups, int act = ACT_NONE) {
   Conv c;
+  c.name = p;
   c.W = wt.get(p + ".weight", {co, ci / groups, kh, kw});
   if (bias) c.b = wt.get(p + ".bias", {co}).v;
   c.sh = sh;
@@ -725,6 +760,7 @@ Conv load_conv(const Weights& wt, const std::string& p, int ci, int co, int kh, 
 Conv load_conv_bn(const Weights& wt, const std::string& p, int ci, int co, int kh, int kw, int sh, int sw,
                   std::vector<int> pads, bool bias, int groups, const std::string& norm, int act) {
   Conv c = load_conv(wt, p + ".convolution", ci, co, kh, kw, sh, sw, pads, bias, groups, act);
+  c.name = p;
   fold_bn(c.W, c.b, wt, p + "." + norm, co);
   return c;
 }
@@ -754,11 +790,11 @@ struct LcNetBlock {
   SE se;
   Tensor forward(const Tensor& x) const {
     Tensor t = token.forward(x);
-    if (has_se) t = mul_gate(t, se.gate(t));
+    if (has_se) t = mul_gate(t, se.gate(t), conv1.name + ".gated");
     Tensor h = conv1.forward(t, fault(FAULT_MISSING_GELU) ? ACT_NONE : ACT_GELU);
-    Tensor o = conv2.forward(h, ACT_NONE);
-    if (residual) return add(fault(FAULT_LCNET_RESIDUAL_FROM_BLOCK_INPUT) ? x : t, o);
-    return o;
+    if (!residual) return conv2.forward(h, ACT_NONE);
+    Tensor o = conv2.forward(h, ACT_NONE, false);
+    return add(fault(FAULT_LCNET_RESIDUAL_FROM_BLOCK_INPUT) ? x : t, o, conv2.name);
   }
 };
 
@@ -997,6 +1033,8 @@ struct RankOne {
 RankOne load_rank_one(const Weights& wt, const std::string& p, int ci, int co, int k) {
   Tensor W = wt.get(p + ".weight", {co, ci, k, k});
   RankOne r;
+  r.dw.name = p + ".depthwise";
+  r.pw.name = p + ".pointwise";
   factor_rank_one(W, ci, co, k, r.dw.W, r.pw.W);
   r.dw.groups = ci;
   for (int i = 0; i < 4; ++i) r.dw.pads[i] = k / 2;
@@ -1018,17 +1056,22 @@ struct RepLkFpn {
     for (int i = 0; i < 4; ++i) {
       Tensor h = in_conv[i].forward(st[i]);
       Tensor g = in_se[i].gate(h);
-      fused.push_back(fault(FAULT_NECK_SE_PLAIN_GATE) ? mul_gate(h, g) : residual_mul_gate(h, g));
+      // Levels above the deepest add the upsampled level below before a
+      // bf16 plan rounds them.
+      const std::string name = "model.neck.fused." + std::to_string(i);
+      fused.push_back(fault(FAULT_NECK_SE_PLAIN_GATE) ? mul_gate(h, g, name) : residual_mul_gate(h, g, name, i == 3));
       trace("fpn.insert" + std::to_string(i), fused.back());
     }
     const std::vector<Tensor> inserted = fused;
     for (int i = 2; i >= 0; --i)
-      fused[i] = upsample_add(fused[i], fault(FAULT_TOPDOWN_NOT_CASCADED) ? inserted[i + 1] : fused[i + 1], 2);
+      fused[i] = upsample_add(fused[i], fault(FAULT_TOPDOWN_NOT_CASCADED) ? inserted[i + 1] : fused[i + 1], 2,
+                              "model.neck.fused." + std::to_string(i));
     std::vector<Tensor> feats;
     for (int i = 0; i < 4; ++i) {
       Tensor h = pwc[i].forward(dwc[i].forward(fused[i]));
       Tensor g = dw_se[i].gate(h);
-      feats.push_back(fault(FAULT_NECK_SE_PLAIN_GATE) ? mul_gate(h, g) : residual_mul_gate(h, g));
+      const std::string name = "model.neck.input_conv." + std::to_string(i) + ".out";
+      feats.push_back(fault(FAULT_NECK_SE_PLAIN_GATE) ? mul_gate(h, g, name) : residual_mul_gate(h, g, name));
       trace("fpn.feature" + std::to_string(i), feats.back());
     }
     if (fault(FAULT_NECK_CONCAT_SHALLOW_FIRST)) return upsample_cat(feats, {1, 2, 4, 8});
@@ -1068,13 +1111,14 @@ struct Intraclass {
     Tensor l7 = lng.forward(r);
     Tensor l5 = mid.forward(l7);
     Tensor l3 = sht.forward(l5);
-    return add(x, fin.forward(l3));
+    return add(x, fin.forward(l3, -1, false), fin.name);
   }
 };
 
 Conv load_fused_intraclass(const Weights& wt, const std::string& p, const std::string& ratio, int k) {
   Conv sym = load_conv(wt, p + ".symmetric_conv_long_" + ratio, 32, 32, k, k, 1, 1, {k / 2, k / 2, k / 2, k / 2},
                        true, 1);
+  sym.name = p + (ratio == "longratio" ? ".long" : ratio == "midratio" ? ".mid" : ".short");
   Tensor vw = wt.get(p + ".vertical_long_to_small_conv_" + ratio + ".weight", {32, 32, k, 1});
   auto vb = wt.get(p + ".vertical_long_to_small_conv_" + ratio + ".bias", {32}).v;
   Tensor hw = wt.get(p + ".horizontal_small_to_long_conv_" + ratio + ".weight", {32, 32, 1, k});
@@ -1091,16 +1135,20 @@ struct MediumNeck {
   Intraclass intra[4];
   Tensor forward(const std::vector<Tensor>& st) const {
     std::vector<Tensor> adj;
-    for (int i = 0; i < 4; ++i) adj.push_back(adjust[i].forward(st[i]));
+    // Levels above the deepest add the upsampled level below before a bf16
+    // plan rounds them.
+    for (int i = 0; i < 4; ++i) adj.push_back(adjust[i].forward(st[i], -1, i == 3));
     std::vector<Tensor> td(4);
     td[3] = adj[3];
     for (int i = 2; i >= 0; --i)
-      td[i] = upsample_add(adj[i], fault(FAULT_TOPDOWN_NOT_CASCADED) ? adj[i + 1] : td[i + 1], 2);
+      td[i] = upsample_add(adj[i], fault(FAULT_TOPDOWN_NOT_CASCADED) ? adj[i + 1] : td[i + 1], 2, adjust[i].name);
     std::vector<Tensor> bu, projected;
     for (int i = 0; i < 4; ++i) {
       Tensor p = project[i].forward(td[i]);
       projected.push_back(p);
-      if (i > 0) p = add(p, pan[i - 1].forward(fault(FAULT_PAN_FROM_PROJECTION) ? projected[i - 1] : bu[i - 1]));
+      if (i > 0)
+        p = add(p, pan[i - 1].forward(fault(FAULT_PAN_FROM_PROJECTION) ? projected[i - 1] : bu[i - 1], -1, false),
+                pan[i - 1].name);
       bu.push_back(p);
       trace("neck.bottom_up" + std::to_string(i), p);
     }
@@ -1150,7 +1198,7 @@ struct DetHead {
     Tensor d = down.forward(x);
     trace("head.down", d);
     Tensor tmp;
-    Tensor u = conv_transpose2x2(d, bf_weights(upW, tmp), upb.data());
+    Tensor u = conv_transpose2x2(d, bf_weights(upW, tmp, "head.conv_up"), upb.data());
     act_in_place(u, ACT_RELU);
     trace("head.up", u);
     Tensor f = conv_transpose2x2(u, finW, finb.data());
@@ -1210,9 +1258,11 @@ struct Detector : Model {
 struct RecBlock {
   Tensor ln1w, ln1b, ln2w, ln2b, qkvW, qkvB, projW, projB, fc1W, fc1B, fc2W, fc2B;
   int hidden = 0, heads = 8;
+  std::string p;  // module path head.encoder.svtr_block.<i>
+  // The attention context, before its projection.
   Tensor attention(const Tensor& x) const {
     int B = x.shape[0], T = x.shape[1], hd = hidden / heads;
-    Tensor qkv = linear(x, qkvW, &qkvB, ACT_NONE, false);
+    Tensor qkv = linear(x, qkvW, &qkvB, ACT_NONE, false, p + ".self_attn.qkv");
     Tensor out({B, T, hidden});
     float scale = std::pow((float)(fault(FAULT_ATTENTION_SCALE_HIDDEN) ? hidden : hd), -0.5f);
     // Column of part (q, k, v) for head h, dimension d within a qkv row: the
@@ -1230,27 +1280,36 @@ struct RecBlock {
           for (int u = 0; u < T; ++u) {
             const float* k = qkv.data() + ((size_t)b * T + u) * 3 * hidden;
             float acc = 0.0f;
-            for (int d = 0; d < hd; ++d) acc = std::fma(q[col(0, h, d)], k[col(1, h, d)], acc);
+            for (int dd = 0; dd < hd; ++dd) {
+              const int d = g_reverse_sums ? hd - 1 - dd : dd;
+              acc = std::fma(q[col(0, h, d)], k[col(1, h, d)], acc);
+            }
             s[u] = std::fma(acc, scale, 0.0f);
           }
           softmax_row(s.data(), T);
           float* o = out.data() + ((size_t)b * T + t) * hidden + h * hd;
           for (int d = 0; d < hd; ++d) {
             float acc = 0.0f;
-            for (int u = 0; u < T; ++u)
+            for (int uu = 0; uu < T; ++uu) {
+              const int u = g_reverse_sums ? T - 1 - uu : uu;
               acc = std::fma(s[u], qkv.v[((size_t)b * T + u) * 3 * hidden + col(2, h, d)], acc);
+            }
             o[d] = acc;
           }
         }
       }
-    return linear(bf(out), projW, &projB, ACT_NONE, false);
+    return bf(out, p + ".self_attn");
   }
+  // The projection and fc2 sums with their residuals are rounded once, after
+  // the add, as a bf16 plan's epilogues do.
   Tensor forward(const Tensor& x) const {
-    Tensor n1 = layer_norm(x, ln1w, ln1b, 1e-6f);
-    Tensor o = add(fault(FAULT_RECBLOCK_RESIDUAL_NORMED) ? n1 : x, attention(n1));
-    Tensor m = linear(linear(layer_norm(o, ln2w, ln2b, 1e-6f), fc1W, &fc1B, ACT_SILU, false), fc2W, &fc2B, ACT_NONE,
-                      false);
-    return add(o, m);
+    Tensor n1 = layer_norm(x, ln1w, ln1b, 1e-6f, p + ".layer_norm1");
+    Tensor a = linear(attention(n1), projW, &projB, ACT_NONE, false, p + ".self_attn.projection", false);
+    Tensor o = add(fault(FAULT_RECBLOCK_RESIDUAL_NORMED) ? n1 : x, a, p + ".self_attn.projection");
+    Tensor h = linear(layer_norm(o, ln2w, ln2b, 1e-6f, p + ".layer_norm2"), fc1W, &fc1B, ACT_SILU, false,
+                      p + ".mlp.fc1");
+    Tensor m = linear(h, fc2W, &fc2B, ACT_NONE, false, p + ".mlp.fc2", false);
+    return add(o, m, p + ".mlp.fc2");
   }
 };
 
@@ -1268,7 +1327,7 @@ struct Recognizer : Model {
 
   Tensor forward(const Tensor& x) const override {
     std::vector<Tensor> st = bb.forward(x);
-    Tensor pooled = avg_pool_3x2(st.back());  // [N, C, 1, T]
+    Tensor pooled = avg_pool_3x2(st.back(), "pool");  // [N, C, 1, T]
     trace("pool", pooled);
     int N = pooled.n(), C = pooled.c(), T = pooled.w();
     ENSURE(pooled.h() == 1, "recognizer pooling must produce height 1");
@@ -1281,14 +1340,14 @@ struct Recognizer : Model {
       for (int n = 0; n < N; ++n)
         for (int c = 0; c < C; ++c)
           for (int t = 0; t < T; ++t) seq.v[((size_t)n * T + t) * C + c] = h.v[((size_t)n * C + c) * T + t];
-      return linear(linear(seq, fc1W, &fc1B, ACT_NONE, false), fc2W, &fc2B, ACT_NONE, true);
+      return linear(linear(seq, fc1W, &fc1B, ACT_NONE, false, "head.fc1"), fc2W, &fc2B, ACT_NONE, true, "head.fc2");
     }
     // RecEncoder::forward (src/cpu/model.rs:1825-1842)
     Tensor res = skip.forward(pooled);
     trace("svtr.skip", res);
     Tensor h = reduce.forward(pooled);
-    Tensor loc = local.forward(h);
-    h = add(h, loc);
+    Tensor loc = local.forward(h, -1, false);
+    h = add(h, loc, local.name);
     trace("svtr.hidden", h);
     int Hc = h.c();
     Tensor seq({N, T, Hc});
@@ -1300,17 +1359,17 @@ struct Recognizer : Model {
       trace("svtr.block" + std::to_string(i), seq);
     }
     const bool skip_first = fault(FAULT_SVTR_SKIP_BEFORE_NORM);
-    if (!skip_first) seq = layer_norm(seq, normW, normB, 1e-6f);
+    if (!skip_first) seq = layer_norm(seq, normW, normB, 1e-6f, "", false);
     for (int n = 0; n < N; ++n)
       for (int t = 0; t < T; ++t)
         for (int c = 0; c < Hc; ++c) {
           float& v = seq.v[((size_t)n * T + t) * Hc + c];
           v = v + res.v[((size_t)n * Hc + c) * T + t];
         }
-    if (skip_first) seq = layer_norm(seq, normW, normB, 1e-6f);
-    bf(seq);  // stored in bf16 by a bf16 plan
+    if (skip_first) seq = layer_norm(seq, normW, normB, 1e-6f, "", false);
+    bf(seq, "head.encoder.norm");  // LayerNorm + skip, stored in bf16 by a bf16 plan
     trace("svtr.encoder", seq);
-    return linear(seq, clsW, &clsB, ACT_NONE, true);
+    return linear(seq, clsW, &clsB, ACT_NONE, true, "head.head");
   }
 };
 
@@ -1349,6 +1408,7 @@ std::unique_ptr<Model> load_detector(const std::string& path, int size) {
 
 RecBlock load_rec_block(const Weights& wt, const std::string& p, int h, int mlp) {
   RecBlock b;
+  b.p = p;
   b.hidden = h;
   b.ln1w = wt.get(p + ".layer_norm1.weight", {h});
   b.ln1b = wt.get(p + ".layer_norm1.bias", {h});
@@ -1381,6 +1441,7 @@ std::unique_ptr<Model> load_recognizer(const std::string& path, int size) {
     w1.shape = {160, 1, 1, 5};
     std::vector<float> b1;
     fold_bn(w1, b1, wt, "head.norm1", 160);
+    r->tconv1.name = "head.conv1";
     r->tconv1.W = w1;
     r->tconv1.b = b1;
     r->tconv1.groups = 160;
@@ -1390,6 +1451,7 @@ std::unique_ptr<Model> load_recognizer(const std::string& path, int size) {
     w2.shape = {160, 160, 1, 1};
     std::vector<float> b2;
     fold_bn(w2, b2, wt, "head.norm2", 160);
+    r->tconv2.name = "head.conv2";
     r->tconv2.W = w2;
     r->tconv2.b = b2;
     r->fc1W = wt.get("head.fc1.weight", {80, 160});
@@ -1507,6 +1569,27 @@ void oracle_model_free(void* m) { delete static_cast<Model*>(m); }
 int oracle_fault_count(void) { return FAULT_COUNT; }
 void oracle_set_fault(int f) { g_fault = f; }
 void oracle_set_bf16(int on) { g_bf16 = on != 0; }
+void oracle_set_reverse_sums(int on) { g_reverse_sums = on != 0; }
+
+// The emulation's rounding of n floats (tests pin it against a library
+// bf16 conversion).
+void oracle_round_bf16(const float* in, float* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = round_bf16(in[i]);
+}
+
+// The rounding points of the last forward run with the bf16 emulation on,
+// one per line ("A <value>" or "W <layer>"), into `out` (NUL terminated, cut
+// at `cap`); returns the bytes needed with the terminator.
+long oracle_bf16_log(char* out, size_t cap) {
+  std::string text;
+  for (const std::string& r : g_bf16_log) text += r + "\n";
+  if (out && cap) {
+    const size_t k = std::min(cap - 1, text.size());
+    memcpy(out, text.data(), k);
+    out[k] = 0;
+  }
+  return (long)text.size() + 1;
+}
 void oracle_set_tracing(int on) {
   g_tracing = on != 0;
   g_trace.clear();
@@ -1539,7 +1622,8 @@ int oracle_forward(void* handle, const float* in, const int shape[4], float* out
     }
     Tensor x({shape[0], shape[1], shape[2], shape[3]});
     memcpy(x.data(), in, x.count() * 4);
-    bf(x);  // a bf16 plan stores its input in bf16
+    g_bf16_log.clear();
+    bf(x, "input");  // a bf16 plan stores its input in bf16
     Tensor y = m->forward(x);
     ENSURE(y.count() <= cap, "output buffer too small");
     memcpy(out, y.data(), y.count() * 4);

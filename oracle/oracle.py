@@ -372,3 +372,38 @@ def set_bf16(on):
     L = lib()
     L.oracle_set_bf16.argtypes = [ctypes.c_int]
     L.oracle_set_bf16(int(bool(on)))
+
+
+def bf16_log():
+    """The rounding points of the last forward run with the bf16 emulation
+    on, in order: "A <value>" (an activation value rounded to bf16) and
+    "W <layer>" (a layer's weights rounded to bf16)."""
+    L = lib()
+    fn = L.oracle_bf16_log
+    fn.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
+    fn.restype = ctypes.c_long
+    n = fn(None, 0)
+    buf = ctypes.create_string_buffer(n)
+    fn(buf, n)
+    return buf.value.decode().splitlines()
+
+
+def round_bf16(values):
+    """The emulation's float32 -> bf16 rounding (nearest even; NaN kept),
+    elementwise, as float32."""
+    L = lib()
+    fn = L.oracle_round_bf16
+    fn.argtypes = [_F, _F, ctypes.c_size_t]
+    fn.restype = None
+    x = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.empty_like(x)
+    fn(_f(x), _f(out), x.size)
+    return out
+
+
+def set_reverse_sums(on):
+    """Accumulate matrix products, depthwise convs and attention sums last
+    term first, for models run afterwards (tests only)."""
+    L = lib()
+    L.oracle_set_reverse_sums.argtypes = [ctypes.c_int]
+    L.oracle_set_reverse_sums(int(bool(on)))

@@ -34,6 +34,11 @@ static __device__ __align__(256) unsigned char scratch[kDbScratchBytes];
 
 size_t db_scratch_bytes() { return kDbScratchBytes; }
 
+std::mutex* db_scratch_mutex(int device) {
+  static std::mutex mus[64];
+  return device >= 0 && device < 64 ? &mus[device] : nullptr;
+}
+
 hipError_t db_scratch(int device, void** ptr) {
   static std::mutex mu;
   static void* cached[64] = {};

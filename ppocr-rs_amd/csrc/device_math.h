@@ -36,8 +36,11 @@ __device__ __forceinline__ void lse_merge(float& m, float& s, int& i, float om, 
 // GELU(v) = h + |h| (1 - E): one fused multiply-add and an add in place of
 // the sign select and three products.  The 1/sqrt 2 scaling is folded into
 // the constants (p / sqrt 2 in the t denominator; the exp2 argument
-// x^2 log2(e) is y^2 with y = |v| sqrt(log2(e) / 2)).  Thirteen vector
-// operations per element, two of them transcendental.
+// x^2 log2(e) is y^2 with y = |v| sqrt(log2(e) / 2)).  Fourteen vector
+// operations per element, two of them transcendental, one of them the
+// clamp: at v = +inf, E is 0 and |h| infinite, so the product's factor is
+// clamped to the largest finite float, -|h| E is 0 rather than NaN, and the
+// result is +inf, as v/2 (1 + erf) gives (at -inf both forms give NaN).
 __device__ __forceinline__ float gelu_as(float v) {
   const float a = fabsf(v);
   const float t = fast_rcp(fmaf(a, 0.3275911f * 0.70710678118654752f, 1.0f));
@@ -45,7 +48,7 @@ __device__ __forceinline__ float gelu_as(float v) {
   const float y = a * 0.84932180028801904f;
   const float e = poly * __builtin_amdgcn_exp2f(-(y * y));
   const float h = 0.5f * v, ha = fabsf(h);
-  return h + fmaf(-ha, e, ha);
+  return h + fmaf(-fminf(ha, 3.40282347e38f), e, ha);
 }
 
 __device__ __forceinline__ float act_apply(int act, float v) {

@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime.h>
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 namespace ppocr {
@@ -342,8 +343,11 @@ void launch_db_postprocess(const DbParams& p, hipStream_t s);
 // (db_scratch_bytes() bytes per device, held until the process ends).
 // db_scratch looks its address up once per device (with that device made
 // current for the lookup) and returns the cached address afterwards.
+// db_scratch_mutex(device) serialises every use of one device's scratch
+// (null for a device index outside [0, 64)).
 size_t db_scratch_bytes();
 hipError_t db_scratch(int device, void** ptr);
+std::mutex* db_scratch_mutex(int device);
 
 // Quad-bilinear RGB8 sampling -> rounded -> normalised NCHW fp32 planes.  One
 // geometry per image: corners [N][8], content widths [N].

@@ -31,6 +31,14 @@ uint16_t to_bf16(float f) {
   return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
+// f rounded to bf16 (nearest even), as a float.
+float bf16_value(float f) {
+  const uint32_t u = (uint32_t)to_bf16(f) << 16;
+  float r;
+  memcpy(&r, &u, 4);
+  return r;
+}
+
 struct ConvW {
   size_t w = NOW, b = NOW;  // byte offsets into the weight blob
   int ldw = 0;
@@ -151,6 +159,12 @@ class Builder {
     std::vector<float> packed((size_t)kh * kw * c);
     for (int ch = 0; ch < c; ++ch)
       for (int t = 0; t < kh * kw; ++t) packed[(size_t)t * c + ch] = W[(size_t)ch * kh * kw + t];
+    // bf16 plans take 5x5 and wider taps in bf16 (the matrix-core form's
+    // operand type) on every kernel: the vector-ALU kernels, which run the
+    // maps too small for the matrix cores and the gate-residual layers, read
+    // the same bf16-valued taps in fp32.
+    if (dt_ == DT_BF16 && kh >= 5 && kw >= 5)
+      for (float& v : packed) v = bf16_value(v);
     d.w = put(packed);
     if (!b.empty()) d.b = put(b);
     if (depthwise_uses_mfma(kh, kw, sh, sw, dt_, 16, c)) {
@@ -212,6 +226,7 @@ class Builder {
     Buffer b;
     b.bytes = (size_t)n * h * w * v.ps * dtype_size(v.dt);
     b.name = name;
+    b.dt = v.dt;
     plan_.bufs.push_back(b);
     v.buf = (int)plan_.bufs.size() - 1;
     return v;
@@ -336,6 +351,7 @@ class Builder {
     }
     Op op;
     op.name = name;
+    if (dt_ == DT_BF16) op.bf16_weights = {name};
     op.kernel = conv_kernel(base, a_src, wo, has_ig && !prescale, terms);
     if (prescale) op.kernel += "+gate_pass";
     if (splits > 1) op.kernel += "+split_k" + std::to_string(splits);
@@ -392,6 +408,7 @@ class Builder {
     View gate;
     const View* upper = nullptr;
     const View* out = nullptr;
+    std::string name;  // of the value x, rounded to the storage type also where it is not stored
   };
 
   View depthwise(const View& x, const DwW& w, int act, const View* res, const std::string& name, int se_cr = 0,
@@ -430,6 +447,11 @@ class Builder {
     size_t wo = w.w, bo = w.b, to = w.tab;
     Op op;
     op.name = name;
+    if (dt_ == DT_BF16 && w.kh >= 5 && w.kw >= 5) op.bf16_weights = {name};
+    if (dt_ == DT_BF16 && gr) {
+      op.rounds = {name, gr->name};
+      op.rounds_set = true;
+    }
     op.kernel = depthwise_kernel_name(w.kh, w.kw, w.sh, w.sw, Ho, x.dt, w.tab != NOW && x.ps % 8 == 0, w.c);
     op.flops = 2.0 * out.pixels() * w.c * w.kh * w.kw;
     op.bytes = (double)dtype_size(x.dt) * ((double)x.pixels() * w.c + (double)out.pixels() * w.c * (has_res ? 2 : 1)) +
@@ -670,12 +692,18 @@ class Builder {
   }
 
   // x_i + x_i*g_i written replicated (rep_i) into dst_i for several maps of
-  // the same image count and storage type, in one launch.
+  // the same image count and storage type, in one launch; level i's value is
+  // named names[i].
   void gate_residual_levels(const std::vector<View>& xs, const std::vector<View>& gs, const std::vector<View>& dsts,
-                            const std::vector<int>& reps, const std::string& name) {
+                            const std::vector<int>& reps, const std::string& name,
+                            const std::vector<std::string>& names) {
     const int count = (int)xs.size();
     Op op;
     op.name = name;
+    if (dt_ == DT_BF16) {
+      op.rounds = names;
+      op.rounds_set = true;
+    }
     op.kernel = "gate_residual";
     op.bytes = 0.0;
     for (int i = 0; i < count; ++i) {
@@ -724,6 +752,7 @@ class Builder {
     Op op;
     op.name = name;
     op.kernel = "maxpool_same";
+    op.exact = true;
     op.bytes = 2.0 * dtype_size(x.dt) * x.pixels() * x.c;
     op.reads = {x.buf};
     op.writes = {dst.buf};
@@ -1113,6 +1142,7 @@ View rep_lk_fpn(Builder& B, const std::vector<View>& st, const int chans[4], int
       gr.gate = g[i];
       gr.upper = i < 3 ? &fused[i + 1] : nullptr;
       gr.out = i > 0 ? &fused[i] : nullptr;
+      gr.name = "model.neck.fused." + std::to_string(i);
       d[i] = B.depthwise(h[i], dws[i], ACT_NONE, nullptr, "model.neck.input_conv." + std::to_string(i) +
                          ".depthwise_convolution", 0, nullptr, &gr);
     }
@@ -1133,7 +1163,9 @@ View rep_lk_fpn(Builder& B, const std::vector<View>& st, const int chans[4], int
   // Every level's gate, then every level's x + x*g written upsampled into
   // its concat slot (deepest first in the channels): one launch each.
   std::vector<View> gi = B.se_levels(pt, psw, "model.neck.input_conv.se", psums);
-  B.gate_residual_levels(pt, gi, slots, reps, "model.neck.input_conv.out");
+  std::vector<std::string> level_names;
+  for (int i = 0; i < 4; ++i) level_names.push_back("model.neck.input_conv." + std::to_string(i) + ".out");
+  B.gate_residual_levels(pt, gi, slots, reps, "model.neck.input_conv.out", level_names);
   return cat;
 }
 
@@ -1298,6 +1330,11 @@ void detector_head(Builder& B, const View& x, int nc) {
   std::vector<float> wu = B.get("head.conv_up.convolution.weight", {h, h, 2, 2}).v;
   std::vector<float> bu = B.get("head.conv_up.convolution.bias", {h}).v;
   B.fold_bn(wu, bu, "head.conv_up.norm", h, true, h);
+  // conv_up's weights are bf16 in a bf16 plan on both of its kernels (the
+  // matrix-core GEMM takes them so; the vector-ALU kernel reads the same
+  // bf16 values in fp32).
+  if (B.dt() == DT_BF16)
+    for (float& v : wu) v = bf16_value(v);
   std::vector<float> wf = B.get("head.conv_final.weight", {h, 1, 2, 2}).v;
   float bf = B.get("head.conv_final.bias", {1}).v[0];
   size_t owu = B.put(wu), obu = B.put(bu), owf = B.put(wf);
@@ -1309,6 +1346,7 @@ void detector_head(Builder& B, const View& x, int nc) {
   View in = d;
   Op op;
   op.name = "head.conv_up+conv_final";
+  if (B.dt() == DT_BF16) op.bf16_weights = {"head.conv_up"};
   op.flops = 2.0 * d.pixels() * (4.0 * h * h + 16.0 * h);
   op.bytes = (double)dtype_size(d.dt) * d.pixels() * h + 4.0 * ((double)out.pixels() + 4.0 * h * h + 4.0 * h);
   op.reads = {d.buf};
@@ -1554,6 +1592,24 @@ void plan_arena(Plan& plan) {
   }
   plan.arena_bytes = total;
   plan.unplanned_bytes = unplanned;
+}
+
+std::vector<std::string> plan_rounding_points(const Plan& plan) {
+  std::vector<std::string> out;
+  if (plan.dt != DT_BF16) return out;
+  std::vector<int> writers(plan.bufs.size(), 0);
+  for (const Op& op : plan.ops)
+    for (int b : op.writes) ++writers[b];
+  for (const Op& op : plan.ops) {
+    if (op.rounds_set) {
+      for (const std::string& r : op.rounds) out.push_back("A " + r);
+    } else if (!op.exact) {
+      for (int b : op.writes)
+        if (plan.bufs[b].dt == DT_BF16) out.push_back("A " + (writers[b] == 1 ? plan.bufs[b].name : op.name));
+    }
+    for (const std::string& w : op.bf16_weights) out.push_back("W " + w);
+  }
+  return out;
 }
 
 }  // namespace ppocr

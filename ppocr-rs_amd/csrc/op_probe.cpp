@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "kernels.h"
+#include "runtime.h"
 
 namespace {
 
@@ -602,6 +603,31 @@ int ppocr_probe_gate_residual_multi(int count, int n, const int* dims, const flo
   for (void* b : bufs)
     if (b) (void)hipFree(b);
   return rc;
+}
+
+
+// The bf16 rounding points of a model's bf16 plan (plan_rounding_points),
+// built on the host from a safetensors file (no device work): one per line,
+// "A <value>" or "W <layer>", into `out` (NUL terminated, cut at `cap`).
+// kind 0 detector, 1 recognizer.  Returns the bytes needed (with the
+// terminator), or -1 on an error.
+long ppocr_probe_plan_rounding(const char* path, int kind, int size, int n, int h, int w, char* out, size_t cap) {
+  try {
+    ppocr::SafeTensors st = ppocr::SafeTensors::load(path);
+    const size_t nchw[4] = {(size_t)n, 3, (size_t)h, (size_t)w};
+    ppocr::Plan plan = kind == 0 ? ppocr::build_detector(st, size, nchw, ppocr::DT_BF16)
+                                 : ppocr::build_recognizer(st, size, nchw, ppocr::DT_BF16, false);
+    std::string text;
+    for (const std::string& r : ppocr::plan_rounding_points(plan)) text += r + "\n";
+    if (out && cap) {
+      const size_t k = std::min(cap - 1, text.size());
+      memcpy(out, text.data(), k);
+      out[k] = 0;
+    }
+    return (long)text.size() + 1;
+  } catch (...) {
+    return -1;
+  }
 }
 
 }  // extern "C"

@@ -344,6 +344,24 @@ ppocr_status ppocr_hip_create(int device, ppocr_hip_ctx** out) {
 
 void ppocr_hip_destroy(ppocr_hip_ctx* ctx) { delete ctx; }
 
+ppocr_status ppocr_hip_device_info(const ppocr_hip_ctx* ctx, ppocr_gpu_info* out) {
+  return guarded([&] {
+    if (!ctx || !out) raise(PPOCR_ERR_INVALID_INPUT, "null argument");
+    hipDeviceProp_t prop{};
+    HIP_OK(hipGetDeviceProperties(&prop, ctx->device));
+    ppocr_gpu_info info{};
+    snprintf(info.name, sizeof info.name, "%.255s", prop.name);
+    snprintf(info.backend, sizeof info.backend, "HIP");
+    snprintf(info.arch, sizeof info.arch, "%.63s", prop.gcnArchName);
+    info.device = ctx->device;
+    info.integrated = prop.integrated ? 1 : 0;
+    info.compute_units = prop.multiProcessorCount;
+    info.wavefront_size = prop.warpSize;
+    info.total_memory = prop.totalGlobalMem;
+    *out = info;
+  });
+}
+
 ppocr_status ppocr_hip_detector_load(ppocr_hip_ctx* ctx, const char* path, ppocr_model_size size, const size_t nchw[4],
                                      ppocr_precision precision, ppocr_hip_model** out) {
   return guarded([&] {
@@ -988,6 +1006,11 @@ ppocr_status ppocr_hip_db_postprocess_static(ppocr_hip_ctx* ctx, const float* pr
       raise(PPOCR_ERR_INVALID_INPUT, "maps need " + std::to_string(need) + " bytes of postprocess scratch; the static "
                                      "scratch holds " + std::to_string(db_scratch_bytes()) + " bytes");
     std::lock_guard<std::mutex> lock(ctx->mu);
+    // Every context on this device shares its scratch: hold the device's
+    // scratch lock from staging the maps until the detections are read back.
+    std::mutex* device_mu = db_scratch_mutex(ctx->device);
+    if (!device_mu) raise(PPOCR_ERR_GPU, "postprocess scratch unavailable for this device index");
+    std::lock_guard<std::mutex> scratch_lock(*device_mu);
     HIP_OK(hipSetDevice(ctx->device));
     char* base = static_cast<char*>(ctx->db_scratch_ptr);
     if (!base) raise(PPOCR_ERR_GPU, "postprocess scratch address unknown for this device");

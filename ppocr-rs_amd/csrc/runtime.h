@@ -101,6 +101,7 @@ struct Buffer {
   size_t arena_off = 0;  // bytes
   int first = -1, last = -1;
   std::string name;
+  int dt = DT_F32;  // element storage type
 };
 
 struct Exec {
@@ -121,6 +122,12 @@ struct Op {
   int bound = 0;  // 0 HBM, 1 matrix cores, 2 fp32 vector ALU
   std::vector<int> reads, writes;
   std::function<void(const Exec&, hipStream_t)> launch;
+  // bf16 plans: the values this op rounds to bf16 and the weights it takes
+  // in bf16, by name.  With rounds_set false the rounded values are the bf16
+  // buffers the op writes (plan_rounding_points); `exact` ops (maxima,
+  // copies) round nothing.
+  std::vector<std::string> rounds, bf16_weights;
+  bool rounds_set = false, exact = false;
 };
 
 struct Plan {
@@ -144,6 +151,13 @@ struct Plan {
 // pack the same weight blob.
 Plan build_detector(const SafeTensors& st, int size, const size_t nchw[4], int dt);
 Plan build_recognizer(const SafeTensors& st, int size, const size_t nchw[4], int dt, bool greedy);
+
+// Every point where a plan rounds to its bf16 storage type, in op order:
+// "A <value>" for each activation value rounded (a bf16 buffer's name when
+// one op writes it, else the writing op's name, or the op's explicit list)
+// and "W <layer>" for each layer whose weights are bf16.  Empty for fp32
+// plans.
+std::vector<std::string> plan_rounding_points(const Plan& plan);
 
 // Postprocess options (defaults when null) after
 // DetectorPostprocessOptions::validate (src/ocr.rs:250-268).

@@ -33,7 +33,7 @@ STATUS = {
 
 # Every symbol include/ppocr_hip.h declares.
 EXPORTS = (
-    "ppocr_hip_last_error", "ppocr_hip_create", "ppocr_hip_destroy", "ppocr_hip_detector_load",
+    "ppocr_hip_last_error", "ppocr_hip_create", "ppocr_hip_destroy", "ppocr_hip_device_info", "ppocr_hip_detector_load",
     "ppocr_hip_recognizer_load", "ppocr_hip_model_free", "ppocr_hip_output_shape", "ppocr_hip_forward",
     "ppocr_hip_upload_rgb", "ppocr_hip_image_free", "ppocr_hip_forward_image", "ppocr_hip_preprocess",
     "ppocr_hip_benchmark", "ppocr_hip_benchmark_stream", "ppocr_hip_profile", "ppocr_hip_memory_report",
@@ -66,6 +66,29 @@ class DetectorTransform(ctypes.Structure):
 
     _fields_ = [("source_width", ctypes.c_uint32), ("source_height", ctypes.c_uint32),
                 ("content_width", ctypes.c_uint32), ("content_height", ctypes.c_uint32)]
+
+
+class GpuInfoStruct(ctypes.Structure):
+    """``ppocr_gpu_info``: ``GpuInfo`` (src/gpu/runtime.rs:17-21) plus HIP device facts."""
+
+    _fields_ = [("name", ctypes.c_char * 256), ("backend", ctypes.c_char * 16), ("arch", ctypes.c_char * 64),
+                ("device", ctypes.c_int), ("integrated", ctypes.c_int), ("compute_units", ctypes.c_int),
+                ("wavefront_size", ctypes.c_int), ("total_memory", ctypes.c_size_t)]
+
+
+@dataclass
+class GpuInfo:
+    """``GpuInfo`` (src/gpu/runtime.rs:17-21): name, backend, device type, and
+    the HIP architecture, compute units, wavefront size and memory."""
+
+    name: str
+    backend: str
+    device_type: str
+    arch: str
+    device: int
+    compute_units: int
+    wavefront_size: int
+    total_memory: int
 
 
 class _Detection(ctypes.Structure):
@@ -132,6 +155,7 @@ def lib():
         L.ppocr_hip_last_error.restype = ctypes.c_char_p
         L.ppocr_hip_create.argtypes = [ctypes.c_int, ctypes.POINTER(_VP)]
         L.ppocr_hip_destroy.argtypes = [_VP]
+        L.ppocr_hip_device_info.argtypes = [_VP, _VP]
         L.ppocr_hip_detector_load.argtypes = [_VP, ctypes.c_char_p, ctypes.c_int, _SZ, ctypes.c_int,
                                               ctypes.POINTER(_VP)]
         L.ppocr_hip_recognizer_load.argtypes = [_VP, ctypes.c_char_p, ctypes.c_int, _SZ, ctypes.c_int, _VP,
@@ -207,6 +231,14 @@ class Gpu:
         _check(lib().ppocr_hip_create(int(device), ctypes.byref(h)))
         self.handle = h
         self._children = []
+
+    def info(self):
+        """``Gpu::info`` (src/gpu/runtime.rs:169-171)."""
+        s = GpuInfoStruct()
+        _check(lib().ppocr_hip_device_info(self.handle, ctypes.byref(s)))
+        return GpuInfo(s.name.decode(errors="replace"), s.backend.decode(), "IntegratedGpu" if s.integrated else
+                       "DiscreteGpu", s.arch.decode(errors="replace"), s.device, s.compute_units, s.wavefront_size,
+                       s.total_memory)
 
     def upload_rgb(self, rgb):
         """``Gpu::upload_rgb``: RGB8 HWC array -> device image."""

@@ -35,6 +35,13 @@ def test_null_arguments_are_rejected_without_device_work():
     rank = ctypes.c_size_t()
     assert lib.ppocr_hip_output_shape(None, shape, ctypes.byref(rank)) == 10
     assert lib.ppocr_hip_forward(None, None, 0, None, 0) == 10
+    assert lib.ppocr_hip_device_info(None, None) == 10
+
+
+def test_gpu_info_struct_layout_matches_the_header():
+    # char[256] + char[16] + char[64] + 4 ints + size_t (8-aligned)
+    assert ctypes.sizeof(ppocr_hip.GpuInfoStruct) == 256 + 16 + 64 + 4 * 4 + 8
+    assert ppocr_hip.GpuInfoStruct.total_memory.offset == 352
 
 
 def test_missing_device_reports_a_gpu_error():

@@ -40,10 +40,12 @@ def _ptr(a):
 
 
 def bf16_round(a):
-    """Round float32 values to bfloat16 (nearest even), returned as float32."""
-    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
-    return r.astype(np.uint32).view(np.float32)
+    """Round float32 values to bfloat16 (nearest even; NaN stays NaN),
+    returned as float32."""
+    x = np.ascontiguousarray(a, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    r = (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(x), x, r)
 
 
 def act(y, kind):

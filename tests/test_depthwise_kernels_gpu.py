@@ -184,3 +184,35 @@ def test_gate_residual_prologue_matches_float64(case):
     want += b
     err = np.abs(out - want)
     assert np.all(err <= 1e-5 + 1e-5 * np.abs(want)), f"max err {err.max()}"
+
+
+@pytest.mark.gpu
+def test_gelu_epilogue_at_infinities_and_large_values():
+    """The device GELU (A-S erf form, shared by every kernel's epilogue)
+    follows v/2 (1 + erf(v / sqrt 2)) where it overflows: +inf stays +inf,
+    -inf gives NaN (-inf times 0), NaN stays NaN, large finite values give v
+    (positive) or 0 (negative).  Run as a 3x3 depthwise with only its centre
+    tap set, over 1x1 maps, so each value meets only zero padding."""
+    ACT_GELU = 2
+    lib = _lib()
+    vals = np.array([np.inf, -np.inf, np.nan, 3.0e38, -3.0e38, 1.0e30, -1.0e30, 1.0e6, -1.0e6, 40.0, -40.0, 0.0,
+                     1.0, -1.0, 0.5, -0.5], np.float32)
+    n, c = 4, 16
+    x = np.resize(vals, n * c).reshape(n, 1, 1, c).astype(np.float32)
+    w = np.zeros((c, 3, 3), np.float32)
+    w[:, 1, 1] = 1.0
+    out = np.empty_like(x)
+    assert lib.ppocr_probe_depthwise(_ptr(x), n, 1, 1, c, _ptr(w), None, 3, ACT_GELU, None, 0, 0, _ptr(out)) == 0
+    v = x.ravel().astype(np.float64)
+    got = out.ravel()
+    import math
+
+    exact = np.array([0.5 * t * (1.0 + math.erf(t / math.sqrt(2.0))) if np.isfinite(t) else np.nan for t in v])
+    for t, g, e in zip(v, got, exact):
+        if np.isnan(t) or t == -np.inf:
+            assert np.isnan(g), (t, g)
+        elif t == np.inf:
+            assert g == np.inf, (t, g)
+        else:
+            assert np.isfinite(g), (t, g)
+            assert abs(g - e) <= 1e-6 * abs(e) + 1e-6, (t, g, e)

@@ -53,6 +53,9 @@ SE_CASES = [
     ("input convs", 1, [(19136, 16, 1196, 4), (4784, 16, 300, 4), (1196, 16, 76, 4), (299, 16, 20, 4)]),
     ("two images, three gates", 2, [(900, 32, 57, 8), (225, 32, 15, 8), (64, 32, 4, 8)]),
     ("one gate", 1, [(4000, 128, 250, 32)]),
+    # Gates over 256 channels (or 64 reduced ones) whose weights still fit one
+    # workgroup take the general body (se_multi_kind 2).
+    ("general body", 2, [(4000, 512, 250, 32), (1000, 384, 63, 32)]),
 ]
 
 
@@ -81,16 +84,26 @@ def test_se_multi_matches_float64(name, n, dims):
 
 
 def test_se_multi_refuses_mixed_kinds():
-    # A 16-channel gate (small-weight kernel) and a 512-channel one with 128
-    # hidden units (the general one-workgroup kernel) cannot share a launch.
+    # A 16-channel gate (small-weight body, kind 1) and a 384-channel one with
+    # 32 hidden units (the general one-workgroup body, kind 2) cannot share a
+    # launch; each alone can.
     lib = _lib()
-    dims = [(100, 16, 4, 4), (100, 512, 4, 128)]
-    flat = [d for g in dims for d in g]
     z = lambda k: np.zeros(k, np.float32)  # noqa: E731
-    rc = lib.ppocr_probe_se_multi(2, 1, _ints(flat), _ptr(z(4 * 16 + 4 * 512)), _ptr(z(4 * 16 + 128 * 512)),
-                                  _ptr(z(4 + 128)), _ptr(z(16 * 4 + 512 * 128)), _ptr(z(16 + 512)), ACT_HSIG5,
-                                  _ptr(z(16 + 512)))
-    assert rc == 2
+
+    def run(dims):
+        flat = [d for g in dims for d in g]
+        part = sum(p * c for _, c, p, _ in dims)
+        w = sum(c * cr for _, c, _, cr in dims)
+        return lib.ppocr_probe_se_multi(len(dims), 1, _ints(flat), _ptr(z(part)), _ptr(z(w)),
+                                        _ptr(z(sum(cr for *_, cr in dims))), _ptr(z(w)),
+                                        _ptr(z(sum(c for _, c, _, _ in dims))), ACT_HSIG5,
+                                        _ptr(z(sum(c for _, c, _, _ in dims))))
+
+    small, general = (100, 16, 4, 4), (100, 384, 4, 32)
+    assert run([small, general]) == 2
+    assert run([general, small]) == 2
+    assert run([small]) == 0
+    assert run([general]) == 0
 
 
 # (n, [(H, W, C, rep) per level]): the FPN's input-conv outputs into the

@@ -15,7 +15,7 @@ import pytest
 import oracle
 import ppocr_hip
 import seeded
-from helpers import (argmax_last, band_mismatches, ctc_greedy, model_path, quad_corners,
+from helpers import (argmax_last, band_mismatches, ctc_greedy, edit_distance, model_path, quad_corners,
                      synthetic_dictionary)
 
 pytestmark = pytest.mark.gpu
@@ -112,24 +112,35 @@ def test_recognizer_matches_oracle(gpu, size, batch, width):
 
 
 # bf16 storage (activations and matrix-core weights in bf16, fp32 accumulate
-# and epilogues) against the fp32 oracle.  The tolerances are derived, per
-# input, from the error that bf16 storage alone causes: the oracle's bf16
-# emulation (the tensors a bf16 plan stores and its matrix-core weights
-# rounded to bf16, everything else as the fp32 oracle) against the fp32
-# oracle gives E = |emulation - fp32| on the same input.  With F = 2 (the
-# device rounds at slightly different points, e.g. once after a fused
-# residual add where the emulation rounds twice):
+# and epilogues) against the fp32 oracle.  The yardstick is the oracle's bf16
+# emulation: the same network with the values a bf16 plan rounds to bf16
+# rounded at the same points, and the same weights taken in bf16 (the
+# rounding function and the list of rounding points are pinned on the CPU,
+# tests/test_bf16_emulation.py).  E = |emulation - fp32| on the same input
+# is what bf16 storage alone costs.  The seeded networks amplify a rounding
+# difference by ~10x per few layers, so a rounding that the device's fp32
+# summation order flips and the emulation's does not moves an output by as
+# much as E itself (measured: reversing the emulation's summation order
+# moves the tiny detector's map by 0.053 against E = 0.080); the bars are
+# therefore statistical in E, not bit-level:
 #   max and mean |device - fp32| <= F x (max, mean) of E, plus 1e-3 / 1e-4
-#     (detector / recognizer) for the fp32 kernels' own rounding;
+#     (detector / recognizer) for the fp32 kernels' own rounding, F = 2;
 #   detector: the DB masks at 0.2 and 0.5 identical wherever the fp32 value
-#     is further than that max bound from the threshold;
+#     is further than that max bound from the threshold, and over the whole
+#     map the device's mask pixels that differ from fp32's at most 1.5x the
+#     emulation's (plus 0.05 % of the pixels);
 #   recognizer: in logit space (log p of the fp32 top-2 classes), G = F x
 #     the largest change the emulation makes to any step's top-2 logit gap;
 #     the argmax is identical on every step whose fp32 logit gap exceeds G
 #     (at least half the steps), and the greedy CTC string is identical on
-#     every line all of whose steps do.  (The seeded recognizers leave some
-#     near-tied steps on most lines, so few lines qualify for the string
-#     check; the step check carries the weight.)
+#     every line all of whose steps do; over all steps, the device's argmax
+#     disagreements with fp32 are at most 1.5x the emulation's (plus 10), and
+#     over all lines the edit distance of the device's CTC strings to fp32's
+#     at most 1.5x the emulation's (plus 5 tokens).  (Line-level string
+#     equality on every line cannot be asked of a random-weight network in
+#     bf16: its encoder features carry ~1.6 % RMS noise from bf16 storage,
+#     and the seeded recognizers whose every step clears that noise are the
+#     collapsed ones that emit one or two classes.)
 BF16_F = 2.0
 
 
@@ -173,6 +184,10 @@ def test_bf16_storage_within_derived_tolerance(gpu, kind, size, shape):
             far = np.abs(ref - thr) > band
             assert np.all((y >= thr)[far] == (ref >= thr)[far]), f"mask differs outside the {band:.3f} band at {thr}"
             assert far.mean() > 0.5  # the check covers most of the map
+            mis_dev = int(np.count_nonzero((y >= thr) != (ref >= thr)))
+            mis_emu = int(np.count_nonzero((emu >= thr) != (ref >= thr)))
+            print(f"  mask at {thr}: device differs from fp32 on {mis_dev} pixels, emulation on {mis_emu}")
+            assert mis_dev <= 1.5 * mis_emu + 5e-4 * ref.size, (thr, mis_dev, mis_emu)
     else:
         top = np.argsort(ref, axis=-1)[..., -2:]
 
@@ -186,12 +201,24 @@ def test_bf16_storage_within_derived_tolerance(gpu, kind, size, shape):
         print(f"  logit-gap bound {bound:.3f}: {confident.mean():.1%} of steps confident")
         assert confident.mean() >= 0.5
         assert np.all(argmax_last(y)[confident] == argmax_last(ref)[confident])
+        am_ref = argmax_last(ref)
+        dis_dev = int(np.count_nonzero(argmax_last(y) != am_ref))
+        dis_emu = int(np.count_nonzero(argmax_last(emu) != am_ref))
+        print(f"  step argmax differs from fp32: device {dis_dev}, emulation {dis_emu} of {am_ref.size}")
+        assert dis_dev <= 1.5 * dis_emu + 10, (dis_dev, dis_emu)
         dictionary = synthetic_dictionary(ref.shape[-1])
         width = shape[3]
         lines = [i for i in range(shape[0]) if confident[i].all()]
         print(f"  {len(lines)} of {shape[0]} lines fully confident")
+        tokens = lambda p: oracle.ctc_greedy_decode(p, len(dictionary), width, width)[0]  # noqa: E731
         for i in lines:
             assert ctc_greedy(y[i], dictionary, width, width)[0] == ctc_greedy(ref[i], dictionary, width, width)[0]
+        want = [tokens(ref[i]) for i in range(shape[0])]
+        d_dev = sum(edit_distance(tokens(y[i]), want[i]) for i in range(shape[0]))
+        d_emu = sum(edit_distance(tokens(emu[i]), want[i]) for i in range(shape[0]))
+        print(f"  CTC edit distance to fp32 over {shape[0]} lines ({sum(map(len, want))} tokens): device {d_dev}, "
+              f"emulation {d_emu}")
+        assert d_dev <= 1.5 * d_emu + 5, (d_dev, d_emu)
 
 
 def test_preprocess_is_bit_exact(gpu):

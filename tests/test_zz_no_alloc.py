@@ -69,3 +69,37 @@ def test_static_postprocess_rejects_maps_beyond_its_scratch(gpu):
     maps = blob_maps(3, 2, 96, 128, blobs=5)
     tr = [(128, 96, 128, 96)] * 2
     same(gpu.db_postprocess_static(maps, tr), gpu.db_postprocess(maps, tr))
+
+
+def _free_device_bytes():
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def test_static_postprocess_allocates_no_device_memory():
+    """Device memory is unchanged across a static call on maps larger than
+    any before it.  That the measure sees allocations of this size is shown
+    by a device image of 24 MB held across a second reading."""
+    g = ppocr_hip.Gpu(0)
+    try:
+        warm = blob_maps(4, 1, 64, 96, blobs=3)
+        g.db_postprocess_static(warm, [(96, 64, 96, 64)])
+        maps = blob_maps(5, 2, 416, 736)
+        tr = [(736, 416, 736, 416)] * 2
+        before = _free_device_bytes()
+        got = g.db_postprocess_static(maps, tr)
+        after_static = _free_device_bytes()
+        image = g.upload_rgb(np.zeros((2000, 4000, 3), np.uint8))
+        with_image = _free_device_bytes()
+        image.close()
+        print(f"free device bytes: {before} -> {after_static} (static call) -> {with_image} (24 MB image held)",
+              flush=True)
+        same(got, g.db_postprocess(maps, tr))
+        assert after_static == before
+        assert after_static - with_image >= 8 << 20
+    finally:
+        g.close()
