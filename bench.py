@@ -412,6 +412,35 @@ def headline(value, steps, warmup, ms_per_step, shape, roof, pass_, cpu=None, ex
     return json.dumps(line, separators=(",", ":"))
 
 
+def db_profile(reps=10):
+    """The tiny detector's forward + device DB postprocess at 416x736 with the
+    postprocess's per-step breakdown (PPOCR_HIP_DB_PROFILE: host steps by
+    wall clock, kernels by HIP events; the library prints one JSON line per
+    call on stderr) for a page of ~9000 components cut to 1000 detections and
+    for the default thresholds, next to the forward with the map read back."""
+    os.environ["PPOCR_HIP_DB_PROFILE"] = "1"
+    gpu = ppocr_hip.Gpu(0)
+    shape = (1, 3, 416, 736)
+    det = load(gpu, "det", "tiny", shape)
+    x = inputs("det", shape)
+    tr = [(736, 416, 736, 416)]
+    for thr, box in ((0.5, 0.6), (0.2, 0.4)):
+        for _ in range(3):
+            d = det.detect(x, tr, binary_threshold=thr, box_threshold=box)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            d = det.detect(x, tr, binary_threshold=thr, box_threshold=box)
+        t1 = time.perf_counter()
+        for _ in range(reps):
+            det.forward(x)
+        t2 = time.perf_counter()
+        print(json.dumps({"binary_threshold": thr, "box_threshold": box, "detections": len(d[0]),
+                          "detect_ms": round((t1 - t0) / reps * 1e3, 3),
+                          "forward_map_to_host_ms": round((t2 - t1) / reps * 1e3, 3)}), flush=True)
+    det.close()
+    gpu.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -422,7 +451,12 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a known-size copy kernel (for rocprofv3 counter scaling)")
     ap.add_argument("--only", metavar="KEY", help="run only this configuration's timed loop (rocprofv3 runs)")
+    ap.add_argument("--db-profile", action="store_true",
+                    help="only the device DB postprocess breakdown (JSON lines on stdout and stderr)")
     args = ap.parse_args()
+    if args.db_profile:
+        db_profile()
+        return
     if args.copy_calibration:
         copy_calibration()
         return

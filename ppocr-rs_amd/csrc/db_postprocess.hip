@@ -116,6 +116,19 @@ __device__ __forceinline__ int wave_sum(int v) {
   for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
   return v;
 }
+// Slot of this lane among the lanes of its wave that ask for one (`want`):
+// one atomic per wave on *counter instead of one per lane.
+__device__ __forceinline__ int wave_claim(int* counter, bool want) {
+  const uint64_t mask = __ballot(want);
+  if (!want) return -1;
+  const int leader = __ffsll((unsigned long long)mask) - 1;
+  const int lane = threadIdx.x & 63;
+  int base = 0;
+  if (lane == leader) base = atomicAdd(counter, __popcll(mask));
+  base = __shfl(base, leader);
+  return base + __popcll(mask & ((1ull << lane) - 1));
+}
+
 __device__ __forceinline__ float wave_min(float v) {
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) v = fminf(v, __shfl_xor(v, o));
@@ -131,6 +144,17 @@ struct PixelPos {
   int n, x, y;
   bool inside;
 };
+
+// The next pixel's position (raster order over images).
+__device__ __forceinline__ void advance(const DbParams& p, PixelPos& q) {
+  if (++q.x == p.W) {
+    q.x = 0;
+    if (++q.y == p.H) {
+      q.y = 0;
+      ++q.n;
+    }
+  }
+}
 
 __device__ __forceinline__ PixelPos locate(const DbParams& p, long i) {
   PixelPos q;
@@ -216,12 +240,21 @@ __global__ __launch_bounds__(256) void db_union_kernel(DbParams p) {
 }
 
 // label = root; each root takes a component slot and clears its moments.
+// No union runs any more, so the parent links are followed with plain loads
+// (a link another thread has just shortened still points at an ancestor).
 __global__ __launch_bounds__(256) void db_flatten_kernel(DbParams p) {
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= p.total || p.label[i] < 0) return;
-  const int root = find_root(p.label, (int)i);
+  int parent = i < p.total ? p.label[i] : -1;
+  int root = (int)i;
+  if (parent >= 0)
+    while (parent != root) {
+      root = parent;
+      parent = p.label[root];
+    }
+  // Every lane takes part in the wave's slot claim (ballot and shuffle).
+  const int id = wave_claim(&p.counters[0], parent >= 0 && root == (int)i);
+  if (parent < 0) return;
   if (root == (int)i) {
-    const int id = atomicAdd(&p.counters[0], 1);
     p.slot[i] = id;
     if (id < p.max_comp) {
       p.count[id] = 0;
@@ -249,7 +282,8 @@ __global__ __launch_bounds__(256) void db_moments_kernel(DbParams p) {
   const int lane = threadIdx.x & 63;
   int id = -1, c = 0;
   double v[6] = {0, 0, 0, 0, 0, 0};
-  for (long i = i0; i < i0 + PPT && i < p.total; ++i) {
+  PixelPos q = locate(p, i0);
+  for (long i = i0; i < i0 + PPT && i < p.total; ++i, advance(p, q)) {
     const int r = p.label[i];
     const int pid = r >= 0 ? p.slot[r] : -1;
     if (pid < 0 || pid >= p.max_comp) continue;
@@ -260,7 +294,6 @@ __global__ __launch_bounds__(256) void db_moments_kernel(DbParams p) {
 #pragma unroll
       for (int k = 0; k < 6; ++k) v[k] = 0.0;
     }
-    const PixelPos q = locate(p, i);
     const double x = q.x + 0.5, y = q.y + 0.5;
     c += 1;
     v[0] += (double)p.prob[i];
@@ -270,9 +303,11 @@ __global__ __launch_bounds__(256) void db_moments_kernel(DbParams p) {
     v[4] += x * y;
     v[5] += y * y;
   }
+  // Up to two wave-level combines (a large component's pixels fill whole
+  // waves); lanes still pending after them flush on their own.
   const bool active = id >= 0;
   uint64_t pending = __ballot(active);
-  while (pending) {
+  for (int round = 0; round < 2 && pending; ++round) {
     const int leader = __ffsll((unsigned long long)pending) - 1;
     const int lid = __shfl(id, leader);
     const bool mine = active && id == lid && ((pending >> lane) & 1);
@@ -283,6 +318,7 @@ __global__ __launch_bounds__(256) void db_moments_kernel(DbParams p) {
     for (int k = 0; k < 6; ++k) s[k] = wave_sum(mine ? v[k] : 0.0);
     if (lane == leader) flush_moments(p, lid, cs, s);
   }
+  if ((pending >> lane) & 1) flush_moments(p, id, c, v);
 }
 
 // Per component: score and area filters, centre and principal axis
@@ -334,7 +370,8 @@ __global__ __launch_bounds__(256) void db_extent_kernel(DbParams p) {
   const int lane = threadIdx.x & 63;
   int id = -1;
   float m[4] = {INFINITY, -INFINITY, INFINITY, -INFINITY};
-  for (long i = i0; i < i0 + PPT && i < p.total; ++i) {
+  PixelPos q = locate(p, i0);
+  for (long i = i0; i < i0 + PPT && i < p.total; ++i, advance(p, q)) {
     const int r = p.label[i];
     const int pid = r >= 0 ? p.slot[r] : -1;
     if (pid < 0 || pid >= p.max_comp || !p.keep[pid]) continue;
@@ -344,7 +381,6 @@ __global__ __launch_bounds__(256) void db_extent_kernel(DbParams p) {
       m[0] = m[2] = INFINITY;
       m[1] = m[3] = -INFINITY;
     }
-    const PixelPos q = locate(p, i);
     const float* g = p.geom + 8 * (size_t)id;
     const float dx = (float)q.x + 0.5f - g[0], dy = (float)q.y + 0.5f - g[1];
     const float a = dx * g[2] + dy * g[3];
@@ -356,7 +392,7 @@ __global__ __launch_bounds__(256) void db_extent_kernel(DbParams p) {
   }
   const bool active = id >= 0;
   uint64_t pending = __ballot(active);
-  while (pending) {
+  for (int round = 0; round < 2 && pending; ++round) {
     const int leader = __ffsll((unsigned long long)pending) - 1;
     const int lid = __shfl(id, leader);
     const bool mine = active && id == lid && ((pending >> lane) & 1);
@@ -368,6 +404,7 @@ __global__ __launch_bounds__(256) void db_extent_kernel(DbParams p) {
     s[3] = wave_max(mine ? m[3] : -INFINITY);
     if (lane == leader) flush_extent(p, lid, s);
   }
+  if ((pending >> lane) & 1) flush_extent(p, id, m);
 }
 
 // Unclipped box in content coordinates, mapped to the source image
@@ -377,7 +414,9 @@ __global__ __launch_bounds__(256) void db_emit_kernel(DbParams p) {
 #pragma clang fp contract(off)
   const int id = blockIdx.x * 256 + threadIdx.x;
   const int n_comp = min(p.counters[0], p.max_comp);
-  if (id >= n_comp || !p.keep[id]) return;
+  const bool emit = id < n_comp && p.keep[id];
+  const int slot = wave_claim(&p.counters[1], emit);
+  if (!emit) return;
   const float* g = p.geom + 8 * (size_t)id;
   const int* e = p.extent + 4 * (size_t)id;
   const float min_a = unordered(e[0]), max_a = unordered(e[1]);
@@ -393,7 +432,6 @@ __global__ __launch_bounds__(256) void db_emit_kernel(DbParams p) {
   const int n = root / (p.H * p.W);
   const float sw = (float)p.source[2 * n], sh = (float)p.source[2 * n + 1];
   const float cw = (float)p.content_scale[2 * n], ch = (float)p.content_scale[2 * n + 1];
-  const int slot = atomicAdd(&p.counters[1], 1);
   float* o = p.out + 12 * (size_t)slot;
   const float sa[4] = {-1.0f, 1.0f, 1.0f, -1.0f}, sn[4] = {-1.0f, -1.0f, 1.0f, 1.0f};
 #pragma unroll
@@ -409,18 +447,34 @@ __global__ __launch_bounds__(256) void db_emit_kernel(DbParams p) {
   o[11] = 0.0f;
 }
 
-void launch_db_postprocess(const DbParams& p, hipStream_t s) {
+const char* const kDbKernelNames[kDbKernels] = {"reset", "runs", "union", "flatten",
+                                                 "moments", "axis", "extent", "emit"};
+
+void launch_db_postprocess(const DbParams& p, hipStream_t s, hipEvent_t* marks) {
   const unsigned px_blocks = (unsigned)((p.total + 255) / 256);
   const unsigned chunk_blocks = (unsigned)((p.total + 256L * PPT - 1) / (256L * PPT));
   const unsigned comp_blocks = (unsigned)((p.max_comp + 255) / 256);
+  int k = 0;
+  auto mark = [&] {
+    if (marks) (void)hipEventRecord(marks[k++], s);
+  };
+  mark();
   hipLaunchKernelGGL(db_reset_kernel, dim3(1), dim3(64), 0, s, p.counters);
+  mark();
   hipLaunchKernelGGL(db_runs_kernel, dim3((unsigned)(p.N * p.H)), dim3(256), 0, s, p);
+  mark();
   hipLaunchKernelGGL(db_union_kernel, dim3(px_blocks), dim3(256), 0, s, p);
+  mark();
   hipLaunchKernelGGL(db_flatten_kernel, dim3(px_blocks), dim3(256), 0, s, p);
+  mark();
   hipLaunchKernelGGL(db_moments_kernel, dim3(chunk_blocks), dim3(256), 0, s, p);
+  mark();
   hipLaunchKernelGGL(db_axis_kernel, dim3(comp_blocks), dim3(256), 0, s, p);
+  mark();
   hipLaunchKernelGGL(db_extent_kernel, dim3(chunk_blocks), dim3(256), 0, s, p);
+  mark();
   hipLaunchKernelGGL(db_emit_kernel, dim3(comp_blocks), dim3(256), 0, s, p);
+  mark();
 }
 
 }  // namespace ppocr

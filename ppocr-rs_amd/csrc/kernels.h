@@ -337,7 +337,11 @@ struct DbParams {
   int* extent;
   float* out;
 };
-void launch_db_postprocess(const DbParams& p, hipStream_t s);
+// The postprocess's kernels in launch order.  With `marks` (kDbKernels + 1
+// events) an event is recorded before each kernel and after the last.
+constexpr int kDbKernels = 8;
+extern const char* const kDbKernelNames[kDbKernels];
+void launch_db_postprocess(const DbParams& p, hipStream_t s, hipEvent_t* marks = nullptr);
 
 // Static device scratch of the no-allocation postprocess entry point
 // (db_scratch_bytes() bytes per device, held until the process ends).

@@ -7,6 +7,7 @@
 // redone whenever the arena had to move.
 #include <chrono>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <thread>
 
@@ -790,20 +791,12 @@ void polygon_center(const ppocr_detection& d, float* cx, float* cy) {
   *cy = sy / 4.0f;
 }
 
-// f32::total_cmp for finite values.
-int total_cmp(float a, float b) {
-  if (a < b) return -1;
-  if (a > b) return 1;
-  return (int)std::signbit(b) - (int)std::signbit(a);
-}
-
-// sort_detections (src/ocr.rs:1120-1131): centre y, centre x, score; the
-// reference's stable sort keeps raster order (root pixel) among equals.
-bool detection_before(const HostDetection& l, const HostDetection& r) {
-  if (int c = total_cmp(l.cy, r.cy)) return c < 0;
-  if (int c = total_cmp(l.cx, r.cx)) return c < 0;
-  if (int c = total_cmp(l.det.score, r.det.score)) return c < 0;
-  return l.root < r.root;
+// A key whose unsigned order is f32::total_cmp's order (negative values
+// below -0, below +0, below positive values).
+uint32_t total_key(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
 // Byte offsets of the postprocess work arrays of N maps of H x W in one
@@ -842,6 +835,52 @@ DbLayout db_layout(int N, int H, int W) {
 }
 
 // Grows a model's or call's postprocess work buffer to `bytes`.
+// PPOCR_HIP_DB_PROFILE set: each postprocess run prints one JSON line to
+// stderr with the wall time of its host steps and the HIP-event time of each
+// of its kernels (ms), like the reference's PPOCR_GPU_PROFILE dispatch
+// profile (src/gpu/runtime.rs:1815-1817).
+class DbProfile {
+ public:
+  DbProfile() : on_(std::getenv("PPOCR_HIP_DB_PROFILE") != nullptr) {
+    if (!on_) return;
+    for (hipEvent_t& e : ev_) HIP_OK(hipEventCreate(&e));
+    last_ = std::chrono::steady_clock::now();
+  }
+  ~DbProfile() {
+    if (on_)
+      for (hipEvent_t e : ev_) (void)hipEventDestroy(e);
+  }
+  hipEvent_t* marks() { return on_ ? ev_ : nullptr; }
+  void step(const char* name) {
+    if (!on_) return;
+    const auto now = std::chrono::steady_clock::now();
+    steps_.push_back({name, std::chrono::duration<double, std::milli>(now - last_).count()});
+    last_ = now;
+  }
+  void report(int detections, int n, int h, int w) {
+    if (!on_) return;
+    std::string line = "{\"db_profile\": {\"maps\": [" + std::to_string(n) + ", " + std::to_string(h) + ", " +
+                       std::to_string(w) + "], \"components_emitted\": " + std::to_string(detections) +
+                       ", \"host_ms\": {";
+    for (size_t i = 0; i < steps_.size(); ++i)
+      line += (i ? ", \"" : "\"") + steps_[i].first + "\": " + std::to_string(steps_[i].second);
+    line += "}, \"kernel_ms\": {";
+    for (int i = 0; i < kDbKernels; ++i) {
+      float ms = 0.0f;
+      HIP_OK(hipEventElapsedTime(&ms, ev_[i], ev_[i + 1]));
+      line += (i ? ", \"" : "\"") + std::string(kDbKernelNames[i]) + "\": " + std::to_string(ms);
+    }
+    line += "}}}\n";
+    fputs(line.c_str(), stderr);
+  }
+
+ private:
+  bool on_;
+  hipEvent_t ev_[kDbKernels + 1] = {};
+  std::chrono::steady_clock::time_point last_;
+  std::vector<std::pair<std::string, double>> steps_;
+};
+
 char* db_work(ppocr_hip_ctx* ctx, std::shared_ptr<DeviceBuffer>& work, size_t bytes) {
   if (!work || work->bytes < bytes) work = device_alloc(ctx->device, bytes);
   return static_cast<char*>(work->ptr);
@@ -857,6 +896,7 @@ std::vector<std::vector<HostDetection>> run_db(ppocr_hip_ctx* ctx, const float* 
   const long total = (long)N * H * W;
   if (total >= (long)INT32_MAX) raise(PPOCR_ERR_INVALID_INPUT, "probability maps too large for the postprocess");
   const DbLayout L = db_layout(N, H, W);
+  DbProfile prof;
   std::vector<int> tables(6 * (size_t)N);
   for (int n = 0; n < N; ++n) {
     const ppocr_detector_transform& t = tr[n];
@@ -870,6 +910,7 @@ std::vector<std::vector<HostDetection>> run_db(ppocr_hip_ctx* ctx, const float* 
     tables[4 * N + 2 * n + 1] = (int)std::min<uint32_t>(t.content_height, INT32_MAX);
   }
   HIP_OK(hipMemcpyAsync(base + L.tables, tables.data(), 4 * tables.size(), hipMemcpyHostToDevice, ctx->stream));
+  prof.step("tables_h2d");
   DbParams p{};
   p.prob = prob;
   p.N = N, p.H = H, p.W = W;
@@ -892,46 +933,87 @@ std::vector<std::vector<HostDetection>> run_db(ppocr_hip_ctx* ctx, const float* 
   p.geom = reinterpret_cast<float*>(base + L.geom);
   p.extent = reinterpret_cast<int*>(base + L.ext);
   p.out = reinterpret_cast<float*>(base + L.out);
-  launch_db_postprocess(p, ctx->stream);
+  launch_db_postprocess(p, ctx->stream, prof.marks());
   HIP_OK(hipGetLastError());
+  prof.step("launch");
+  // The counters and a first block of records come back in one round trip;
+  // more records (a page with over kDbFirstRecords components) in a second.
+  constexpr int kDbFirstRecords = 1024;
+  const int first = (int)std::min<long>(kDbFirstRecords, p.max_comp);
   int counters[3] = {0, 0, 0};
+  std::vector<float> rec(12 * (size_t)first);
   HIP_OK(hipMemcpyAsync(counters, p.counters, sizeof counters, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_OK(hipMemcpyAsync(rec.data(), p.out, rec.size() * 4, hipMemcpyDeviceToHost, ctx->stream));
   HIP_OK(hipStreamSynchronize(ctx->stream));
+  prof.step("kernels_and_first_records_d2h");
   // src/ocr.rs:731-733
   if (counters[2]) raise(non_finite_status, "detector output contains non-finite values");
   const int n_det = std::max(0, std::min(counters[1], p.max_comp));
-  std::vector<float> rec(12 * (size_t)n_det);
-  if (n_det) {
-    HIP_OK(hipMemcpyAsync(rec.data(), p.out, rec.size() * 4, hipMemcpyDeviceToHost, ctx->stream));
+  if (n_det > first) {
+    rec.resize(12 * (size_t)n_det);
+    HIP_OK(hipMemcpyAsync(rec.data() + 12 * (size_t)first, p.out + 12 * (size_t)first,
+                          12 * sizeof(float) * (size_t)(n_det - first), hipMemcpyDeviceToHost, ctx->stream));
     HIP_OK(hipStreamSynchronize(ctx->stream));
   }
-  std::vector<std::vector<HostDetection>> per(N);
+  prof.step("more_records_d2h");
+  // sort_detections, and the max_boxes cut by score (src/ocr.rs:775-788):
+  // the kept detections are the first max_boxes under (score descending,
+  // centre y, centre x, raster order), selected in linear time from packed
+  // keys, and only those are sorted into (centre y, centre x, score, raster
+  // order) and built.  The keys order as f32::total_cmp does.
+  struct Key {
+    uint64_t hi, lo;
+    uint32_t i;
+  };
+  auto before = [](const Key& a, const Key& b) { return a.hi != b.hi ? a.hi < b.hi : a.lo < b.lo; };
+  std::vector<std::vector<Key>> keys(N);
+  std::vector<float> cx(n_det), cy(n_det);
   for (int i = 0; i < n_det; ++i) {
     const float* r = rec.data() + 12 * (size_t)i;
-    HostDetection d;
-    memcpy(d.det.polygon, r, 8 * sizeof(float));
-    d.det.score = r[8];
-    memcpy(&d.image, r + 9, 4);
-    memcpy(&d.root, r + 10, 4);
-    if (d.image < 0 || d.image >= N) raise(PPOCR_ERR_GPU, "postprocess produced an invalid image index");
-    polygon_center(d.det, &d.cx, &d.cy);
-    per[d.image].push_back(d);
+    int image;
+    memcpy(&image, r + 9, 4);
+    if (image < 0 || image >= N) raise(PPOCR_ERR_GPU, "postprocess produced an invalid image index");
+    ppocr_detection d;
+    memcpy(d.polygon, r, 8 * sizeof(float));
+    polygon_center(d, &cx[i], &cy[i]);
+    keys[image].push_back({0, 0, (uint32_t)i});
   }
-  for (auto& v : per) {
-    std::sort(v.begin(), v.end(), detection_before);
-    if (v.size() > o.max_boxes) {
-      // Keep the highest scores (ties: centre y, then x), then restore the
-      // positional order (src/ocr.rs:775-788).
-      std::sort(v.begin(), v.end(), [](const HostDetection& l, const HostDetection& r) {
-        if (int c = total_cmp(r.det.score, l.det.score)) return c < 0;
-        if (int c = total_cmp(l.cy, r.cy)) return c < 0;
-        if (int c = total_cmp(l.cx, r.cx)) return c < 0;
-        return l.root < r.root;
-      });
-      v.resize(o.max_boxes);
-      std::sort(v.begin(), v.end(), detection_before);
+  auto root_of = [&](uint32_t i) {
+    int root;
+    memcpy(&root, rec.data() + 12 * (size_t)i + 10, 4);
+    return (uint32_t)root;
+  };
+  auto score_of = [&](uint32_t i) { return rec[12 * (size_t)i + 8]; };
+  std::vector<std::vector<HostDetection>> per(N);
+  for (int n = 0; n < N; ++n) {
+    std::vector<Key>& k = keys[n];
+    if (k.size() > o.max_boxes) {
+      for (Key& e : k) {
+        e.hi = ((uint64_t)~total_key(score_of(e.i)) << 32) | total_key(cy[e.i]);
+        e.lo = ((uint64_t)total_key(cx[e.i]) << 32) | root_of(e.i);
+      }
+      std::nth_element(k.begin(), k.begin() + (long)o.max_boxes, k.end(), before);
+      k.resize(o.max_boxes);
+    }
+    for (Key& e : k) {
+      e.hi = ((uint64_t)total_key(cy[e.i]) << 32) | total_key(cx[e.i]);
+      e.lo = ((uint64_t)total_key(score_of(e.i)) << 32) | root_of(e.i);
+    }
+    std::sort(k.begin(), k.end(), before);
+    per[n].reserve(k.size());
+    for (const Key& e : k) {
+      HostDetection d;
+      memcpy(d.det.polygon, rec.data() + 12 * (size_t)e.i, 8 * sizeof(float));
+      d.det.score = score_of(e.i);
+      d.image = n;
+      d.root = (int)root_of(e.i);
+      d.cx = cx[e.i];
+      d.cy = cy[e.i];
+      per[n].push_back(d);
     }
   }
+  prof.step("host_sort");
+  prof.report(n_det, N, H, W);
   return per;
 }
 

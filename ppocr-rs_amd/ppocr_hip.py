@@ -122,14 +122,14 @@ def _collect(call, n, max_boxes):
     total = ctypes.c_size_t()
     buf = (_Detection * (n * max_boxes))()
     _check(call(buf, n * max_boxes, counts, ctypes.byref(total)))
+    rows = np.frombuffer(buf, dtype=np.float32).reshape(n * max_boxes, 9)[:total.value].copy()
+    polygons = rows[:, :8].reshape(-1, 4, 2)
+    scores = rows[:, 8].tolist()
     out, k = [], 0
     for i in range(n):
-        items = []
-        for _ in range(counts[i]):
-            d = buf[k]
-            items.append(Detection(np.array(d.polygon[:], np.float32).reshape(4, 2), float(d.score)))
-            k += 1
-        out.append(items)
+        c = counts[i]
+        out.append([Detection(polygons[j], scores[j]) for j in range(k, k + c)])
+        k += c
     return out
 
 
