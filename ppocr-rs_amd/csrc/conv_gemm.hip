@@ -69,8 +69,7 @@ __device__ __forceinline__ float4 f4_add(float4 a, float4 b) {
 }
 
 __device__ __forceinline__ uint32_t gate_pair(uint32_t v, float g0, float g1) {
-  return f32_to_bf16_bits(bf16_bits_to_f32(v & 0xFFFFu) * g0) |
-         (f32_to_bf16_bits(bf16_bits_to_f32(v >> 16) * g1) << 16);
+  return pack_bf16x2(bf16_bits_to_f32(v & 0xFFFFu) * g0, bf16_bits_to_f32(v >> 16) * g1);
 }
 
 // v * g elementwise (the SE gate applied while gathering A); g points at the

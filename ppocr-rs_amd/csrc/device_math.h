@@ -85,12 +85,24 @@ typedef __bf16 bf16;
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-// Round to nearest even; a NaN stays a (quiet) NaN instead of carrying into
-// the exponent, so non-finite values still reach the output checks.
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-  return f != f ? ((u >> 16) | 0x40u) : r;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// lo and hi rounded to bf16 and packed as (hi << 16) | lo: one
+// v_cvt_pk_bf16_f32, which rounds to nearest even (denormals kept) and
+// keeps a NaN a NaN, so non-finite values still reach the output checks.
+// (Its results equal the integer form (u + 0x7FFF + ((u >> 16) & 1)) >> 16,
+// with NaN mapped to a quiet NaN, on all 2^32 inputs.)
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return pack_bf16x2(f, 0.0f) & 0xFFFFu; }
+
+// Four bf16 values packed low half first in a and b, as floats.
+__device__ __forceinline__ float4 unpack_bf16x4(uint32_t a, uint32_t b) {
+  return make_float4(__uint_as_float(a << 16), __uint_as_float(a & 0xFFFF0000u), __uint_as_float(b << 16),
+                     __uint_as_float(b & 0xFFFF0000u));
 }
 
 // v rounded to the storage type T (what st4 stores and ld4 reads back).
@@ -102,8 +114,9 @@ __device__ __forceinline__ float4 round4<float>(float4 v) {
 }
 template <>
 __device__ __forceinline__ float4 round4<bf16>(float4 v) {
-  return make_float4(bf16_bits_to_f32(f32_to_bf16_bits(v.x)), bf16_bits_to_f32(f32_to_bf16_bits(v.y)),
-                     bf16_bits_to_f32(f32_to_bf16_bits(v.z)), bf16_bits_to_f32(f32_to_bf16_bits(v.w)));
+  const uint32_t a = pack_bf16x2(v.x, v.y), b = pack_bf16x2(v.z, v.w);
+  return make_float4(__uint_as_float(a << 16), __uint_as_float(a & 0xFFFF0000u), __uint_as_float(b << 16),
+                     __uint_as_float(b & 0xFFFF0000u));
 }
 
 // Four consecutive values (16 B as fp32, 8 B as bf16).
@@ -129,8 +142,8 @@ __device__ __forceinline__ void st4<float>(float* p, float4 v) {
 template <>
 __device__ __forceinline__ void st4<bf16>(bf16* p, float4 v) {
   uint2 u;
-  u.x = f32_to_bf16_bits(v.x) | (f32_to_bf16_bits(v.y) << 16);
-  u.y = f32_to_bf16_bits(v.z) | (f32_to_bf16_bits(v.w) << 16);
+  u.x = pack_bf16x2(v.x, v.y);
+  u.y = pack_bf16x2(v.z, v.w);
   *reinterpret_cast<uint2*>(p) = u;
 }
 

@@ -223,9 +223,11 @@ void launch_depthwise(const DwParams& p, hipStream_t s);
 // Blocks per image of the depthwise launch when it can leave the channel
 // sums of its output for a squeeze-excitation (p.se_part), else 0.
 int depthwise_se_blocks(const DwParams& p);
-// Name of the kernel instance launch_depthwise picks.
+// Name of the kernel instance launch_depthwise picks; `groups8`: every
+// pixel access (input, output, residual) starts on a whole group of 8
+// channels.
 const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho, int dt = DT_F32, bool table = false,
-                                  int C = 0);
+                                  int C = 0, bool groups8 = true);
 // bf16 layers with square stride-1 5x5, 7x7 or 9x9 kernels, at least 16
 // output rows and a multiple of 8 channels run on the matrix cores when their
 // taps come packed by depthwise_mfma_table (pack for Ho = 16: the rows are

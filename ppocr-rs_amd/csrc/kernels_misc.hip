@@ -249,6 +249,159 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
   }
 }
 
+// The bf16 form of depthwise_tiled_kernel for channel counts in groups of 8
+// with 16-byte-aligned pixels: a lane owns 8 channels (16-byte loads and
+// stores, half the lanes and workgroups per pixel of the 4-channel form),
+// the input tile is staged in LDS as packed bf16 and unpacked as a lane
+// reads its window.  The 4-channel form ran as long as the fp32 kernel on
+// the same maps (its cost is per lane and workgroup, not per byte); this one
+// measured 1.31-1.37x on the recognizer's 6- and 12-row maps and 1.28x on
+// the detector's 104 x 184 map, with bit-identical outputs (same taps in the
+// same (ky, kx) order).  SE partial sums as the 4-channel form leaves them.
+template <int KH, int KW, int TY, int XR, int C8B>
+__global__ __launch_bounds__(256) void depthwise_tiled8_kernel(DwParams p) {
+  constexpr int XG = 256 / (C8B * TY);  // lane groups along x
+  constexpr int TX = XG * XR;
+  constexpr int IH = TY + KH - 1, IW = TX + KW - 1;
+  constexpr int IWP = IW | 1;  // odd row pitch (pixels)
+  static_assert(IH * IWP * C8B >= 512, "the SE reduction reuses the tile");
+  __shared__ uint4 tile[IH * IWP * C8B];
+  constexpr int NT = KH * KW * C8B * 2;  // tap float4s of the block
+  constexpr int TIT = (NT + 255) / 256;
+  __shared__ float4 taps[NT];
+  const bf16* in = static_cast<const bf16*>(p.in);
+
+  const int cblocks = (p.C + 8 * C8B - 1) / (8 * C8B);
+  const int tiles_x = (p.Wo + TX - 1) / TX, tiles_y = (p.Ho + TY - 1) / TY;
+  const int total = tiles_x * tiles_y * cblocks * p.N;
+  const int t = (blockIdx.x & 7) * ((total + 7) / 8) + (blockIdx.x >> 3);
+  if (t >= total) return;  // grid padding, before any barrier
+  const int txy = t / cblocks;
+  const int n = txy / (tiles_x * tiles_y);
+  const int blk = txy - n * tiles_x * tiles_y;  // tile within the image
+  const int ch0 = (t - txy * cblocks) * 8 * C8B;
+  const int oy0 = blk / tiles_x * TY, ox0 = blk % tiles_x * TX;
+  const int tid = threadIdx.x;
+
+  // The block's taps, loaded with the tile.
+  float4 tv[TIT];
+#pragma unroll
+  for (int it = 0; it < TIT; ++it) {
+    const int i = tid + 256 * it;
+    const int c = ch0 + (i % (2 * C8B)) * 4;
+    tv[it] = i < NT && c < p.C ? *reinterpret_cast<const float4*>(p.wt + (size_t)(i / (2 * C8B)) * p.C + c) : f4_zero();
+  }
+  {
+    static_assert(256 % C8B == 0, "fixed channel group per lane");
+    const int c8 = tid % C8B;
+    const int c = ch0 + c8 * 8;
+    const bool cok = c < p.C;
+    const bf16* base = in + (size_t)n * p.H * p.W * p.in_ps + c;
+    constexpr int STEP = 256 / C8B, NL = (IH * IW + STEP - 1) / STEP;
+    uint4 v[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int px = tid / C8B + i * STEP;
+      const int iy = px / IW, ix = px - iy * IW;
+      const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
+      v[i] = make_uint4(0, 0, 0, 0);
+      if (px < IH * IW && cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W)
+        v[i] = *reinterpret_cast<const uint4*>(base + ((size_t)gy * p.W + gx) * p.in_ps);
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int px = tid / C8B + i * STEP;
+      const int iy = px / IW, ix = px - iy * IW;
+      if (px < IH * IW) tile[(iy * IWP + ix) * C8B + c8] = v[i];
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < TIT; ++it)
+    if (tid + 256 * it < NT) taps[tid + 256 * it] = tv[it];
+  __syncthreads();
+
+  // Channel groups fastest, then rows, then x groups (as the 4-channel form).
+  const int c8 = tid % C8B;
+  const int ty = (tid / C8B) % TY;
+  const int xg = tid / (C8B * TY);
+  float4 acc[XR][2];
+#pragma unroll
+  for (int r = 0; r < XR; ++r) acc[r][0] = acc[r][1] = f4_zero();
+#pragma unroll 1
+  for (int ky = 0; ky < KH; ++ky) {
+    float4 win[XR + KW - 1][2];
+#pragma unroll
+    for (int j = 0; j < XR + KW - 1; ++j) {
+      const uint4 u = tile[((ty + ky) * IWP + xg * XR + j) * C8B + c8];
+      win[j][0] = unpack_bf16x4(u.x, u.y);
+      win[j][1] = unpack_bf16x4(u.z, u.w);
+    }
+#pragma unroll
+    for (int kx = 0; kx < KW; ++kx) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float4 w = taps[((ky * KW + kx) * C8B + c8) * 2 + h];
+#pragma unroll
+        for (int r = 0; r < XR; ++r) {
+          acc[r][h].x = fmaf(win[r + kx][h].x, w.x, acc[r][h].x);
+          acc[r][h].y = fmaf(win[r + kx][h].y, w.y, acc[r][h].y);
+          acc[r][h].z = fmaf(win[r + kx][h].z, w.z, acc[r][h].z);
+          acc[r][h].w = fmaf(win[r + kx][h].w, w.w, acc[r][h].w);
+        }
+      }
+    }
+  }
+  const int c = ch0 + c8 * 8;
+  const int oy = oy0 + ty;
+  const bool cin = c < p.C;
+  float4 b0 = f4_zero(), b1 = f4_zero();
+  if (p.bias && cin) {
+    b0 = *reinterpret_cast<const float4*>(p.bias + c);
+    b1 = *reinterpret_cast<const float4*>(p.bias + c + 4);
+  }
+  float4 sum0 = f4_zero(), sum1 = f4_zero();  // this lane's stored outputs, for the SE partial sums
+#pragma unroll
+  for (int r = 0; r < XR; ++r) {
+    const int ox = ox0 + xg * XR + r;
+    if (!cin || oy >= p.Ho || ox >= p.Wo) break;
+    float4 v0 = acc[r][0], v1 = acc[r][1];
+    if (p.bias) {
+      v0 = f4_sum(v0, b0);
+      v1 = f4_sum(v1, b1);
+    }
+    v0 = f4_act(p.act, v0);
+    v1 = f4_act(p.act, v1);
+    const size_t pix = (size_t)(n * p.Ho + oy) * p.Wo + ox;
+    if (p.res) {
+      const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const bf16*>(p.res) + pix * p.res_ps + c);
+      v0 = f4_sum(unpack_bf16x4(u.x, u.y), v0);
+      v1 = f4_sum(unpack_bf16x4(u.z, u.w), v1);
+    }
+    const uint4 o = make_uint4(pack_bf16x2(v0.x, v0.y), pack_bf16x2(v0.z, v0.w), pack_bf16x2(v1.x, v1.y),
+                               pack_bf16x2(v1.z, v1.w));
+    *reinterpret_cast<uint4*>(static_cast<bf16*>(p.out) + pix * p.out_ps + c) = o;
+    if (p.se_part) {
+      sum0 = f4_sum(sum0, unpack_bf16x4(o.x, o.y));
+      sum1 = f4_sum(sum1, unpack_bf16x4(o.z, o.w));
+    }
+  }
+  if (p.se_part) {
+    // Channel sums of the block's outputs as stored; lanes of one channel
+    // group add in a fixed order.
+    __syncthreads();  // every lane is done with the input tile
+    float4* red = reinterpret_cast<float4*>(tile);
+    red[2 * tid] = sum0;
+    red[2 * tid + 1] = sum1;
+    __syncthreads();
+    if (tid < 2 * C8B && ch0 + tid * 4 < p.C) {
+      // tid = 2 * (channel group) + half
+      float4 sums = red[tid];
+      for (int k = 1; k < 256 / C8B; ++k) sums = f4_sum(sums, red[k * 2 * C8B + tid]);
+      *reinterpret_cast<float4*>(p.se_part + ((size_t)n * tiles_x * tiles_y + blk) * p.C + ch0 + tid * 4) = sums;
+    }
+  }
+}
+
 // LDS-tiled stride-1 depthwise for large kernels with wave-uniform taps: a
 // block computes a 16 x 16 output tile of 16 channels and each wave one
 // group of 4 channels, so all lanes of a wave read the same tap vector (an
@@ -584,10 +737,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
       v1 = f4_sum(ld4<bf16>(rp + 4), v1);
     }
     uint4 o;
-    o.x = f32_to_bf16_bits(v0.x) | (f32_to_bf16_bits(v0.y) << 16);
-    o.y = f32_to_bf16_bits(v0.z) | (f32_to_bf16_bits(v0.w) << 16);
-    o.z = f32_to_bf16_bits(v1.x) | (f32_to_bf16_bits(v1.y) << 16);
-    o.w = f32_to_bf16_bits(v1.z) | (f32_to_bf16_bits(v1.w) << 16);
+    o.x = pack_bf16x2(v0.x, v0.y);
+    o.y = pack_bf16x2(v0.z, v0.w);
+    o.z = pack_bf16x2(v1.x, v1.y);
+    o.w = pack_bf16x2(v1.z, v1.w);
     *reinterpret_cast<uint4*>(static_cast<bf16*>(p.out) + pix * p.out_ps + ch0) = o;
   }
 }
@@ -719,20 +872,36 @@ static void launch_dw_wave(const DwParams& p, hipStream_t s) {
   hipLaunchKernelGGL((depthwise_wave_kernel<T, KH, KW>), dim3((unsigned)((tiles + 7) / 8 * 8)), dim3(256), 0, s, p);
 }
 
-// The launch shape of the tiled 3x3 kernel, the one that can leave SE
-// partial sums (stride 1 and more than 4 output rows): 8-row tiles of 32
-// channels, 2 outputs per lane along x for fp32 (8-pixel-wide tiles: 1.03-
-// 1.22x over 4 outputs on the detector's maps, more blocks for the same
-// work and less tail) and 4 for bf16 (16-pixel-wide; 2 measured 0.94-0.96x
-// on the recognizer's 6- and 12-row maps).
+// The launch shape of the tiled 3x3 kernels, the ones that can leave SE
+// partial sums (stride 1 and more than 4 output rows): 8-row tiles, 8 lanes
+// per pixel (32 fp32 or 64 bf16 channels), 2 outputs per lane along x
+// (8-pixel-wide tiles: 1.03-1.22x over 4 outputs on the detector's fp32
+// maps, more blocks for the same work and less tail) except for bf16 maps
+// of at most 16 rows (the recognizer's), which take 4 (16-pixel-wide: 1.1x
+// on its 6- and 12-row maps, 0.95x on the detector's).
 constexpr int kDw3TY = 8, kDw3C4B = 8;
-constexpr int dw3_xr(int dt) { return dt == DT_BF16 ? 4 : 2; }
-static int dw3_tx(int dt) { return 256 / (kDw3C4B * kDw3TY) * dw3_xr(dt); }
+constexpr int dw3_xr(int dt, int ho) { return dt == DT_BF16 && ho <= 16 ? 4 : 2; }
+static int dw3_tx(int dt, int ho) { return 256 / (kDw3C4B * kDw3TY) * dw3_xr(dt, ho); }
 
 int depthwise_se_blocks(const DwParams& p) {
   if (!(p.kh == 3 && p.kw == 3 && p.sh == 1 && p.sw == 1 && p.Ho > 4)) return 0;
-  const int tx = dw3_tx(p.dt);
+  const int tx = dw3_tx(p.dt, p.Ho);
   return ((p.Wo + tx - 1) / tx) * ((p.Ho + kDw3TY - 1) / kDw3TY);
+}
+
+// bf16 3x3 stride-1 layers take the 8-channel tiled kernel when every pixel
+// access is a whole 16-byte group.
+static bool dw3_tiled8(const DwParams& p) {
+  return p.dt == DT_BF16 && p.C % 8 == 0 && p.in_ps % 8 == 0 && p.out_ps % 8 == 0 && (!p.res || p.res_ps % 8 == 0) &&
+         (((uintptr_t)p.in | (uintptr_t)p.out | (uintptr_t)p.res) & 15) == 0;
+}
+
+template <int KH, int KW, int TY, int XR, int C8B>
+static void launch_dw_tiled8(const DwParams& p, hipStream_t s) {
+  constexpr int TX = 256 / (C8B * TY) * XR;
+  const long tiles = (long)((p.Wo + TX - 1) / TX) * ((p.Ho + TY - 1) / TY) * p.N * ((p.C + 8 * C8B - 1) / (8 * C8B));
+  hipLaunchKernelGGL((depthwise_tiled8_kernel<KH, KW, TY, XR, C8B>), dim3((unsigned)((tiles + 7) / 8 * 8)),
+                     dim3(256), 0, s, p);
 }
 
 template <typename T>
@@ -761,7 +930,15 @@ static void launch_dw_typed(const DwParams& p, hipStream_t s) {
   if (p.kh == 3 && p.kw == 3 && p.sh == 1 && p.Ho <= 4)
     return p.Ho == 3 ? launch_dw_strip<T, 3, 3, 3, 1>(p, s) : launch_dw_strip<T, 3, 3, 4, 1>(p, s);
   if (p.sh == 1 && p.sw == 1) {
-    if (p.kh == 3 && p.kw == 3) return launch_dw_tiled<T, 3, 3, kDw3TY, dw3_xr(sizeof(T) == 2 ? DT_BF16 : DT_F32), kDw3C4B>(p, s);
+    if (p.kh == 3 && p.kw == 3) {
+      if constexpr (sizeof(T) == 2) {
+        const bool wide = dw3_xr(DT_BF16, p.Ho) == 4;
+        if (dw3_tiled8(p))
+          return wide ? launch_dw_tiled8<3, 3, kDw3TY, 4, kDw3C4B>(p, s) : launch_dw_tiled8<3, 3, kDw3TY, 2, kDw3C4B>(p, s);
+        return wide ? launch_dw_tiled<T, 3, 3, kDw3TY, 4, kDw3C4B>(p, s) : launch_dw_tiled<T, 3, 3, kDw3TY, 2, kDw3C4B>(p, s);
+      }
+      return launch_dw_tiled<T, 3, 3, kDw3TY, 2, kDw3C4B>(p, s);
+    }
     // 5x5 and 9x9: wave-uniform taps (1.1-1.2x the tiled kernel's per-lane taps);
     // 7x7 (32 channels here) measured even: 16-row tiles of 16 channels.
     if (p.kh == 5 && p.kw == 5) return launch_dw_wave<T, 5, 5>(p, s);
@@ -780,13 +957,13 @@ bool depthwise_gate_residual_supported(int kh, int kw, int sh, int sw) {
   return kh == kw && (kh == 5 || kh == 7 || kh == 9) && sh == 1 && sw == 1;
 }
 
-const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho, int dt, bool table, int C) {
+const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho, int dt, bool table, int C, bool groups8) {
   if (table && depthwise_uses_mfma(kh, kw, sh, sw, dt, Ho, C))
     return kh == 5 ? "depthwise_mfma<5x5>" : kh == 7 ? "depthwise_mfma<7x7>" : "depthwise_mfma<9x9>";
   if (kh == 3 && kw == 3 && sh == 2) return "depthwise_strip<3x3,s2>";
   if (kh == 3 && kw == 3 && sh == 1 && Ho <= 4) return "depthwise_strip<3x3>";
   if (sh == 1 && sw == 1) {
-    if (kh == 3 && kw == 3) return "depthwise_tiled<3x3>";
+    if (kh == 3 && kw == 3) return dt == DT_BF16 && C % 8 == 0 && groups8 ? "depthwise_tiled8<3x3>" : "depthwise_tiled<3x3>";
     if (kh == kw && (kh == 5 || kh == 7 || kh == 9))
       return kh == 5 ? "depthwise_wave<5x5>" : kh == 7 ? "depthwise_tiled<7x7>" : "depthwise_wave<9x9>";
     if (kh == 1 && (kw == 5 || kw == 7) && Ho == 1) return kw == 5 ? "depthwise_tiled<1x5>" : "depthwise_tiled<1x7>";

@@ -452,7 +452,8 @@ class Builder {
       op.rounds = {name, gr->name};
       op.rounds_set = true;
     }
-    op.kernel = depthwise_kernel_name(w.kh, w.kw, w.sh, w.sw, Ho, x.dt, w.tab != NOW && x.ps % 8 == 0, w.c);
+    op.kernel = depthwise_kernel_name(w.kh, w.kw, w.sh, w.sw, Ho, x.dt, w.tab != NOW && x.ps % 8 == 0, w.c,
+                                      x.ps % 8 == 0 && out.ps % 8 == 0 && (!res || res->ps % 8 == 0));
     op.flops = 2.0 * out.pixels() * w.c * w.kh * w.kw;
     op.bytes = (double)dtype_size(x.dt) * ((double)x.pixels() * w.c + (double)out.pixels() * w.c * (has_res ? 2 : 1)) +
                4.0 * w.kh * w.kw * w.c;

@@ -216,3 +216,40 @@ def test_gelu_epilogue_at_infinities_and_large_values():
         else:
             assert np.isfinite(g), (t, g)
             assert abs(g - e) <= 1e-6 * abs(e) + 1e-6, (t, g, e)
+
+
+# (n, h, w, c, act, bias, residual): the bf16 3x3 tiled kernel with 8
+# channels per lane, on maps of at most 16 rows (16-pixel-wide tiles) and
+# taller ones (8-pixel-wide), with row, column and channel-block tails.
+TILED8_CASES = [
+    (2, 6, 80, 64, ACT_NONE, True, False),
+    (1, 12, 37, 72, ACT_HSWISH, True, True),
+    (3, 7, 21, 8, ACT_RELU, False, True),
+    (1, 29, 45, 136, ACT_NONE, True, False),
+    (2, 17, 9, 16, ACT_HSWISH, False, False),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", TILED8_CASES, ids=lambda c: "x".join(map(str, c[:4])))
+def test_bf16_tiled8_depthwise_matches_float64(case):
+    """bf16 activations (rounded on store), fp32 taps and sums: against the
+    float64 depthwise of the bf16-rounded input the error is the output
+    rounding (2^-9 relative) plus the fp32 sums of nine products."""
+    n, h, wd, c, kind, has_bias, has_res = case
+    lib = _lib()
+    kernel = lib.ppocr_probe_depthwise_kernel(h, c, 3, 1, 0).decode()
+    assert kernel == "depthwise_tiled8<3x3>", kernel
+    rng = np.random.default_rng(77 + 3 * h + wd + c)
+    x = rng.uniform(-1, 1, (n, h, wd, c)).astype(np.float32)
+    w = rng.uniform(-0.5, 0.5, (c, 3, 3)).astype(np.float32)
+    b = rng.uniform(-0.5, 0.5, c).astype(np.float32) if has_bias else None
+    res = rng.uniform(-1, 1, (n, h, wd, c)).astype(np.float32) if has_res else None
+    out = np.empty_like(x)
+    assert lib.ppocr_probe_depthwise(_ptr(x), n, h, wd, c, _ptr(w), _ptr(b), 3, kind, _ptr(res), 1, 0, _ptr(out)) == 0
+    ref = depthwise_ref(bf16_round(x), w, b, kind, None if res is None else bf16_round(res))
+    err = np.abs(out - ref)
+    tol = 2.0 ** -8 * np.abs(ref) + 1e-5
+    assert np.all(err <= tol), (float(err.max()), np.unravel_index(np.argmax(err - tol), err.shape))
+    # Every output is finite and written (no stale pixels past the tiles).
+    assert np.all(np.isfinite(out))
