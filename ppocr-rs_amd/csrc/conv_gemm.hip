@@ -28,6 +28,8 @@
 //     nearest-upsample add and an upsample-on-write.
 #include <type_traits>
 
+#include <stdexcept>
+
 #include "device_math.h"
 
 namespace ppocr {
@@ -1001,8 +1003,10 @@ __device__ __forceinline__ int direct_key(int r) {
   return RB == 64 ? swizzle_key(r) : (r >> 1) & 7;
 }
 
-template <typename T, int BM, int BN, int WM, int WN, bool PW, int S, bool GATE, int EPI, int RB = 64>
-__global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
+// The direct kernel's work for output tile t of layer p (t in [0, M tiles x
+// N tiles); other values return at once).
+template <typename T, int BM, int BN, int WM, int WN, bool PW, int S, bool GATE, int EPI, int RB>
+__device__ __forceinline__ void conv_gemm_direct_tile(const ConvParams& p, int t) {
   constexpr int BK = RB / sizeof(T);  // k values of one row per K slice
   constexpr int VE = 16 / sizeof(T);
   constexpr int TM = BM / (WM * 16);
@@ -1039,11 +1043,8 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
   const int K = p.kh * p.kw * p.C;
   constexpr int ES = sizeof(T);
 
-  // XCD-aware tile order (as conv_gemm_kernel).
   const int n_tiles = (p.Co + BN - 1) / BN;
   const int m_tiles = (M + BM - 1) / BM;
-  const int per_xcd = gridDim.x / 8;
-  const int t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   if (t >= m_tiles * n_tiles) return;
   const int m0 = (t / n_tiles) * BM;
   const int n0 = (t % n_tiles) * BN;
@@ -1330,6 +1331,29 @@ __global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
         return reinterpret_cast<float*>(base) + (row - part * RPA) * LDE;
       },
       m0, n0, M, n_tiles, &bias_pre[0]);
+}
+
+// XCD-aware tile order (as conv_gemm_kernel): workgroup b takes tile
+// (b % 8) * (grid / 8) + b / 8 (the grid is a multiple of 8).
+__device__ __forceinline__ int xcd_tile() {
+  const int per_xcd = gridDim.x / 8;
+  return (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+}
+
+template <typename T, int BM, int BN, int WM, int WN, bool PW, int S, bool GATE, int EPI, int RB = 64>
+__global__ __launch_bounds__(256) void conv_gemm_direct_kernel(ConvParams p) {
+  conv_gemm_direct_tile<T, BM, BN, WM, WN, PW, S, GATE, EPI, RB>(p, xcd_tile());
+}
+
+// Up to kConvMultiMax independent layers of one kernel instance in one
+// launch (the FPN's per-level convs): the tiles of layer i follow those of
+// layers 0 .. i - 1 in the XCD-aware order.
+template <typename T, int BM, int BN, int WM, int WN, bool PW, int S, bool GATE, int EPI, int RB = 64>
+__global__ __launch_bounds__(256) void conv_gemm_direct_multi_kernel(ConvMulti m) {
+  int t = xcd_tile();
+  int i = 0;
+  while (i + 1 < m.count && t >= m.first[i + 1]) ++i;
+  conv_gemm_direct_tile<T, BM, BN, WM, WN, PW, S, GATE, EPI, RB>(m.p[i], t - m.first[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -1950,6 +1974,102 @@ static void launch_typed(const ConvParams& p, hipStream_t s) {
     case 4: launch_tile_shape<T, 4>(p, M, s); break;
     default: launch_tile_shape<T, 5>(p, M, s); break;
   }
+}
+
+bool conv_multi_supported(const ConvParams* p, int count) {
+  if (count < 1 || count > kConvMultiMax) return false;
+  const std::string name = conv_kernel_name(p[0]);
+  for (int i = 0; i < count; ++i) {
+    const ConvParams& q = p[i];
+    const int t = pick_tile(q.N * q.Ho * q.Wo, q.Co, q.dt);
+    const int v = conv_variant(q, kTileBM[t]);
+    if (q.dt != p[0].dt || q.splits > 1 || q.rep != 1 || q.db_ch || q.ctc_part || q.in_gate || wide_layer(q) ||
+        (v != CV_DIRECT_1X1 && v != CV_DIRECT) || conv_kernel_name(q) != name ||
+        regs_epilogue(q) != regs_epilogue(p[0]) || (q.se_part != nullptr) != (p[0].se_part != nullptr))
+      return false;
+  }
+  return true;
+}
+
+// The instance launch_tile_kernel would pick for layer m.p[0] (which every
+// layer shares), over all the layers' tiles.
+template <typename T, int BM, int BN, int WM, int WN>
+static void launch_multi_kernel(const ConvMulti& m, dim3 grid, hipStream_t s) {
+  const ConvParams& p = m.p[0];
+  constexpr int S = sizeof(T) == 2 && (BM + BN) * 64 <= 10240 ? 4 : 3;
+  const bool regs = regs_epilogue(p);
+  switch (conv_variant(p, BM)) {
+    case CV_DIRECT_1X1:
+      if constexpr (sizeof(T) == 2 && BM == 64 && BN == 64) {
+        if (rows128_layer(p)) {
+          hipLaunchKernelGGL((conv_gemm_direct_multi_kernel<T, BM, BN, WM, WN, true, 3, false, EPI_LDS, 128>), grid,
+                             dim3(256), 0, s, m);
+          return;
+        }
+      }
+      if (regs && p.se_part && sizeof(T) == 4)
+        hipLaunchKernelGGL((conv_gemm_direct_multi_kernel<T, BM, BN, WM, WN, true, S, false, EPI_REGS_SE>), grid,
+                           dim3(256), 0, s, m);
+      else if (regs)
+        hipLaunchKernelGGL((conv_gemm_direct_multi_kernel<T, BM, BN, WM, WN, true, S, false, EPI_REGS>), grid,
+                           dim3(256), 0, s, m);
+      else
+        hipLaunchKernelGGL((conv_gemm_direct_multi_kernel<T, BM, BN, WM, WN, true, S, false, EPI_LDS>), grid,
+                           dim3(256), 0, s, m);
+      return;
+    case CV_DIRECT:
+      if constexpr (sizeof(T) == 2 && BM == 64 && BN == 64) {
+        if (rows128_kxk(p)) {
+          hipLaunchKernelGGL((conv_gemm_direct_multi_kernel<T, BM, BN, WM, WN, false, 3, false, EPI_LDS, 128>),
+                             grid, dim3(256), 0, s, m);
+          return;
+        }
+      }
+      if (regs)
+        hipLaunchKernelGGL((conv_gemm_direct_multi_kernel<T, BM, BN, WM, WN, false, S, false, EPI_REGS>), grid,
+                           dim3(256), 0, s, m);
+      else
+        hipLaunchKernelGGL((conv_gemm_direct_multi_kernel<T, BM, BN, WM, WN, false, S, false, EPI_LDS>), grid,
+                           dim3(256), 0, s, m);
+      return;
+    default:
+      throw std::runtime_error("launch_conv_multi: unsupported kernel variant");
+  }
+}
+
+template <typename T>
+static void launch_multi_typed(const ConvMulti& m, hipStream_t s) {
+  const int t = pick_tile(m.p[0].N * m.p[0].Ho * m.p[0].Wo, m.p[0].Co, m.p[0].dt);
+  long total = 0;
+  for (int i = 0; i < m.count; ++i) {
+    const ConvParams& q = m.p[i];
+    total += (long)((q.N * q.Ho * q.Wo + kTileBM[t] - 1) / kTileBM[t]) * ((q.Co + kTileBN[t] - 1) / kTileBN[t]);
+  }
+  const dim3 grid((unsigned)((total + 7) / 8 * 8));
+  switch (t) {
+    case 0: launch_multi_kernel<T, kTileBM[0], kTileBN[0], kTileWM[0], 4 / kTileWM[0]>(m, grid, s); break;
+    case 1: launch_multi_kernel<T, kTileBM[1], kTileBN[1], kTileWM[1], 4 / kTileWM[1]>(m, grid, s); break;
+    case 2: launch_multi_kernel<T, kTileBM[2], kTileBN[2], kTileWM[2], 4 / kTileWM[2]>(m, grid, s); break;
+    case 3: launch_multi_kernel<T, kTileBM[3], kTileBN[3], kTileWM[3], 4 / kTileWM[3]>(m, grid, s); break;
+    case 4: launch_multi_kernel<T, kTileBM[4], kTileBN[4], kTileWM[4], 4 / kTileWM[4]>(m, grid, s); break;
+    default: launch_multi_kernel<T, kTileBM[5], kTileBN[5], kTileWM[5], 4 / kTileWM[5]>(m, grid, s); break;
+  }
+}
+
+void launch_conv_multi(const ConvMulti& mm, hipStream_t s) {
+  if (!conv_multi_supported(mm.p, mm.count)) throw std::runtime_error("launch_conv_multi: layers cannot share a launch");
+  ConvMulti m = mm;
+  const int t = pick_tile(m.p[0].N * m.p[0].Ho * m.p[0].Wo, m.p[0].Co, m.p[0].dt);
+  int first = 0;
+  for (int i = 0; i < m.count; ++i) {
+    const ConvParams& q = m.p[i];
+    m.first[i] = first;
+    first += ((q.N * q.Ho * q.Wo + kTileBM[t] - 1) / kTileBM[t]) * ((q.Co + kTileBN[t] - 1) / kTileBN[t]);
+  }
+  if (m.p[0].dt == DT_BF16)
+    launch_multi_typed<bf16>(m, s);
+  else
+    launch_multi_typed<float>(m, s);
 }
 
 void launch_conv(const ConvParams& p, hipStream_t s) {

@@ -132,6 +132,19 @@ struct SeParams {
 };
 
 void launch_conv(const ConvParams& p, hipStream_t s);
+// Up to kConvMultiMax independent layers in one launch (first[i]: index of
+// layer i's first tile, set by launch_conv_multi).  conv_multi_supported
+// tells whether a set of layers can share one: the same kernel instance,
+// no split K, upsample-on-write or DB-head / greedy-CTC epilogue, and no SE
+// input gate.
+constexpr int kConvMultiMax = 4;
+struct ConvMulti {
+  ConvParams p[kConvMultiMax];
+  int first[kConvMultiMax];
+  int count;
+};
+bool conv_multi_supported(const ConvParams* p, int count);
+void launch_conv_multi(const ConvMulti& m, hipStream_t s);
 // Layers whose depthwise launch can take the gate-residual prologue
 // (DwParams::gr_gate): 5x5 / 7x7 / 9x9, stride 1 (with gr_up the map sides must
 // be twice gr_up's).

@@ -284,9 +284,20 @@ class Builder {
     int P = 0;
   };
 
+  // A conv op not yet added: its op and the function that fills its launch
+  // parameters (for merging independent layers into one launch).
+  struct Deferred {
+    Op op;
+    std::function<ConvParams(const Exec&)> fill;
+    ConvParams shape;  // its parameters with stand-in pointers
+  };
+
   // With sp, the conv also leaves the channel sums of its output in *sp
-  // where its kernel can (sp->P = 0 otherwise).
-  View conv(const View& x, const ConvW& w, const Epi& e, const std::string& name, SePartial* sp = nullptr) {
+  // where its kernel can (sp->P = 0 otherwise).  With `gated`, a bf16 layer
+  // with an SE input gate returns there the x * g tensor its gate pass stores.
+  // With `defer`, the op is returned there instead of added.
+  View conv(const View& x, const ConvW& w, const Epi& e, const std::string& name, SePartial* sp = nullptr,
+            View* gated = nullptr, Deferred* defer = nullptr) {
     if (x.c != w.ci_pad) raise(PPOCR_ERR_INVALID_MODEL, name + ": input has " + std::to_string(x.c) + " channels");
     const int Ho = (x.h + w.pt + w.pb - w.kh) / w.sh + 1;
     const int Wo = (x.w + w.pl + w.pr - w.kw) / w.sw + 1;
@@ -316,6 +327,7 @@ class Builder {
     const bool prescale = has_ig && x.dt == DT_BF16;
     View xs;
     if (prescale) xs = alloc(x.n, x.h, x.w, x.c, name + ".gated");
+    if (gated) *gated = xs;
     const View& a_src = prescale ? xs : x;
     ConvParams base{};
     base.N = x.n, base.H = x.h, base.W = x.w, base.C = x.c, base.in_ps = a_src.ps;
@@ -373,16 +385,10 @@ class Builder {
     if (splits > 1) op.writes.push_back(ws.buf);
     if (prescale) op.writes.push_back(xs.buf);
     if (has_part) op.writes.push_back(part.buf);
-    op.launch = [=](const Exec& ex, hipStream_t s) {
+    auto fill = [=](const Exec& ex) {
       ConvParams p = base;
-      if (prescale) {
-        launch_scale_channels(ex.ptr(in), in.n, in.h * in.w, in.c, in.ps, ex.fptr(ig), ex.ptr(xs), in.dt, s);
-        p.in = ex.ptr(xs);
-        p.in_gate = nullptr;
-      } else {
-        p.in = ex.ptr(in);
-        p.in_gate = has_ig ? ex.fptr(ig) : nullptr;
-      }
+      p.in = prescale ? ex.ptr(xs) : ex.ptr(in);
+      p.in_gate = has_ig && !prescale ? ex.fptr(ig) : nullptr;
       p.out = ex.ptr(out);
       p.wt = ex.wv(wo);
       p.bias = ex.w(bo);
@@ -391,10 +397,62 @@ class Builder {
       p.up = has_up ? ex.ptr(up) : nullptr;
       p.split_ws = splits > 1 ? ex.fptr(ws) : nullptr;
       p.se_part = has_part ? ex.fptr(part) : nullptr;
-      launch_conv(p, s);
+      return p;
+    };
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      if (prescale)
+        launch_scale_channels(ex.ptr(in), in.n, in.h * in.w, in.c, in.ps, ex.fptr(ig), ex.ptr(xs), in.dt, s);
+      launch_conv(fill(ex), s);
+    };
+    if (defer) {
+      ConvParams shape = stand_in(base, a_src, wo, has_ig && !prescale, terms);
+      shape.splits = splits;
+      shape.se_part = has_part ? reinterpret_cast<float*>((uintptr_t)256) : nullptr;
+      *defer = Deferred{std::move(op), fill, shape};
+    } else {
+      add_op(std::move(op));
+    }
+    return out;
+  }
+
+  // Independent conv layers (the FPN levels), as one launch where they can
+  // share one (conv_multi_supported), else one op each.
+  std::vector<View> conv_levels(const std::vector<const View*>& xs, const std::vector<ConvW>& ws, const Epi& e,
+                                const std::vector<std::string>& names, const std::string& name,
+                                std::vector<SePartial>* sps = nullptr) {
+    const int n = (int)xs.size();
+    std::vector<View> outs(n);
+    std::vector<Deferred> d(n);
+    std::vector<ConvParams> shapes(n);
+    for (int i = 0; i < n; ++i) {
+      outs[i] = conv(*xs[i], ws[i], e, names[i], sps ? &(*sps)[i] : nullptr, nullptr, &d[i]);
+      shapes[i] = d[i].shape;
+    }
+    if (n < 2 || n > kConvMultiMax || !conv_multi_supported(shapes.data(), n)) {
+      for (Deferred& q : d) add_op(std::move(q.op));
+      return outs;
+    }
+    Op op;
+    op.name = name;
+    op.kernel = d[0].op.kernel + "x" + std::to_string(n);
+    op.bound = 1;
+    std::vector<std::function<ConvParams(const Exec&)>> fills;
+    for (Deferred& q : d) {
+      op.flops += q.op.flops;
+      op.bytes += q.op.bytes;
+      op.reads.insert(op.reads.end(), q.op.reads.begin(), q.op.reads.end());
+      op.writes.insert(op.writes.end(), q.op.writes.begin(), q.op.writes.end());
+      op.bf16_weights.insert(op.bf16_weights.end(), q.op.bf16_weights.begin(), q.op.bf16_weights.end());
+      fills.push_back(q.fill);
+    }
+    op.launch = [fills](const Exec& ex, hipStream_t s) {
+      ConvMulti m{};
+      m.count = (int)fills.size();
+      for (int i = 0; i < m.count; ++i) m.p[i] = fills[i](ex);
+      launch_conv_multi(m, s);
     };
     add_op(std::move(op));
-    return out;
+    return outs;
   }
 
   // Depthwise conv.  With se_cr > 0 a squeeze-excitation of reduction width
@@ -1005,11 +1063,19 @@ View lcnet_block(Builder& B, const View& x, const std::string& p, BlockSpec s) {
   Epi e1;
   e1.act = ACT_GELU;
   if (has_se) e1.in_gate = &gate;
-  View h = B.conv(t, c1, e1, p + ".channel_conv1");
+  View gated;
+  View h = B.conv(t, c1, e1, p + ".channel_conv1", nullptr, &gated);
   Epi e2;
   if (residual) {
-    e2.res = &t;
-    if (has_se) e2.res_gate = &gate;
+    // The residual is the post-SE tensor: in a bf16 plan the stored
+    // (rounded) x * g of channel_conv1's gate pass, else t gated in the
+    // epilogue.
+    if (has_se && gated.buf >= 0) {
+      e2.res = &gated;
+    } else {
+      e2.res = &t;
+      if (has_se) e2.res_gate = &gate;
+    }
   }
   return B.conv(h, c2, e2, p + ".channel_conv2");
 }
@@ -1105,13 +1171,19 @@ View rep_lk_fpn(Builder& B, const std::vector<View>& st, const int chans[4], int
   std::vector<View> h(4), fused(4);
   std::vector<Builder::SePartial> sums(4);
   std::vector<SeW> sws(4);
+  // The four levels' insert convs in one launch where they share a kernel.
+  std::vector<const View*> ins(4);
+  std::vector<ConvW> iw(4);
+  std::vector<std::string> inames(4);
   for (int i = 0; i < 4; ++i) {
     std::string p = "model.neck.insert_conv." + std::to_string(i);
-    ConvW w = B.conv_w(p + ".in_conv", chans[i], nc, 1, 1, 1, 1, {0, 0, 0, 0}, false);
-    h[i] = B.conv(st[i], w, Epi{}, p + ".in_conv", &sums[i]);
+    ins[i] = &st[i];
+    iw[i] = B.conv_w(p + ".in_conv", chans[i], nc, 1, 1, 1, 1, {0, 0, 0, 0}, false);
+    inames[i] = p + ".in_conv";
     sws[i] = B.se_w(p + ".squeeze_excitation_block.conv1", p + ".squeeze_excitation_block.conv2", nc, nc / 4,
                     ACT_HSIG5);
   }
+  h = B.conv_levels(ins, iw, Epi{}, inames, "model.neck.insert_conv.in_conv", &sums);
   // The four levels' gates (each from its conv's channel sums) in one launch.
   std::vector<View> g = B.se_levels(h, sws, "model.neck.insert_conv.se", sums);
   // fused[i] = h + h * g (+ up2(fused[i + 1])) feeds input_conv i's
@@ -1151,16 +1223,22 @@ View rep_lk_fpn(Builder& B, const std::vector<View>& st, const int chans[4], int
   std::vector<Builder::SePartial> psums(4);
   std::vector<SeW> psw(4);
   std::vector<int> reps(4);
+  std::vector<const View*> pin(4);
+  std::vector<ConvW> pws(4);
+  std::vector<std::string> pnames(4);
   for (int i = 0; i < 4; ++i) {
     std::string p = "model.neck.input_conv." + std::to_string(i);
     if (!gr_fused) d[i] = B.depthwise(fused[i], dws[i], ACT_NONE, nullptr, p + ".depthwise_convolution");
-    ConvW pw = B.conv_w(p + ".pointwise_convolution", nc, q, 1, 1, 1, 1, {0, 0, 0, 0}, false);
-    pt[i] = B.conv(d[i], pw, Epi{}, p + ".pointwise_convolution", &psums[i]);
+    pin[i] = &d[i];
+    pws[i] = B.conv_w(p + ".pointwise_convolution", nc, q, 1, 1, 1, 1, {0, 0, 0, 0}, false);
+    pnames[i] = p + ".pointwise_convolution";
     psw[i] = B.se_w(p + ".squeeze_excitation_module.conv1", p + ".squeeze_excitation_module.conv2", q, q / 4,
                     ACT_HSIG5);
     slots[i] = Builder::slice(cat, (3 - i) * q, q);
     reps[i] = 1 << i;
   }
+  // The four pointwise convs in one launch where they share a kernel.
+  pt = B.conv_levels(pin, pws, Epi{}, pnames, "model.neck.input_conv.pointwise_convolution", &psums);
   // Every level's gate, then every level's x + x*g written upsampled into
   // its concat slot (deepest first in the channels): one launch each.
   std::vector<View> gi = B.se_levels(pt, psw, "model.neck.input_conv.se", psums);
