@@ -415,29 +415,55 @@ class Builder {
     return out;
   }
 
-  // Independent conv layers (the FPN levels), as one launch where they can
-  // share one (conv_multi_supported), else one op each.
+  // Independent conv layers (the levels of a neck), each set of them that
+  // can share a launch (conv_multi_supported) as one op, the others one op
+  // each; a set is named after `name` with its first layer's index.
   std::vector<View> conv_levels(const std::vector<const View*>& xs, const std::vector<ConvW>& ws, const Epi& e,
                                 const std::vector<std::string>& names, const std::string& name,
                                 std::vector<SePartial>* sps = nullptr) {
     const int n = (int)xs.size();
     std::vector<View> outs(n);
     std::vector<Deferred> d(n);
-    std::vector<ConvParams> shapes(n);
-    for (int i = 0; i < n; ++i) {
+    for (int i = 0; i < n; ++i)
       outs[i] = conv(*xs[i], ws[i], e, names[i], sps ? &(*sps)[i] : nullptr, nullptr, &d[i]);
-      shapes[i] = d[i].shape;
+    // Greedy sets in layer order: a layer joins the first set it can share a
+    // launch with.
+    std::vector<std::vector<int>> sets;
+    for (int i = 0; i < n; ++i) {
+      bool placed = false;
+      for (auto& set : sets) {
+        if ((int)set.size() >= kConvMultiMax) continue;
+        std::vector<ConvParams> shapes;
+        for (int j : set) shapes.push_back(d[j].shape);
+        shapes.push_back(d[i].shape);
+        if (conv_multi_supported(shapes.data(), (int)shapes.size())) {
+          set.push_back(i);
+          placed = true;
+          break;
+        }
+      }
+      if (!placed) sets.push_back({i});
     }
-    if (n < 2 || n > kConvMultiMax || !conv_multi_supported(shapes.data(), n)) {
-      for (Deferred& q : d) add_op(std::move(q.op));
-      return outs;
+    for (auto& set : sets) {
+      if (set.size() == 1) {
+        add_op(std::move(d[set[0]].op));
+        continue;
+      }
+      std::vector<Deferred*> members;
+      for (int j : set) members.push_back(&d[j]);
+      add_multi(members, sets.size() == 1 ? name : name + "." + std::to_string(set[0]));
     }
+    return outs;
+  }
+
+  void add_multi(const std::vector<Deferred*>& d, const std::string& name) {
     Op op;
     op.name = name;
-    op.kernel = d[0].op.kernel + "x" + std::to_string(n);
+    op.kernel = d[0]->op.kernel + "x" + std::to_string(d.size());
     op.bound = 1;
     std::vector<std::function<ConvParams(const Exec&)>> fills;
-    for (Deferred& q : d) {
+    for (Deferred* qp : d) {
+      Deferred& q = *qp;
       op.flops += q.op.flops;
       op.bytes += q.op.bytes;
       op.reads.insert(op.reads.end(), q.op.reads.begin(), q.op.reads.end());
@@ -452,7 +478,6 @@ class Builder {
       launch_conv_multi(m, s);
     };
     add_op(std::move(op));
-    return outs;
   }
 
   // Depthwise conv.  With se_cr > 0 a squeeze-excitation of reduction width
@@ -1318,15 +1343,39 @@ void factor_rank_one(const std::string& name, const std::vector<float>& W, int c
 }
 
 // RankOneConv2d (src/cpu/model.rs:165-219): depthwise k x k then 1x1 + bias.
-View rank_one(Builder& B, const View& x, const std::string& p, int ci, int co, int k, const Epi& e) {
+struct RankOneW {
+  DwW dw;
+  ConvW pw;
+};
+
+RankOneW rank_one_w(Builder& B, const std::string& p, int ci, int co, int k) {
   std::vector<float> W = B.get(p + ".weight", {co, ci, k, k}).v;
   std::vector<float> dwv, pwv;
   factor_rank_one(p, W, ci, co, k, dwv, pwv);
   int pd = k / 2;
-  DwW dw = B.pack_dw(dwv, {}, ci, k, k, 1, 1, {pd, pd, pd, pd});
-  View d = B.depthwise(x, dw, ACT_NONE, nullptr, p + ".depthwise");
-  ConvW pw = B.pack_conv(pwv, B.get(p + ".bias", {co}).v, ci, co, 1, 1, 1, 1, {0, 0, 0, 0});
-  return B.conv(d, pw, e, p + ".pointwise");
+  RankOneW r;
+  r.dw = B.pack_dw(dwv, {}, ci, k, k, 1, 1, {pd, pd, pd, pd});
+  r.pw = B.pack_conv(pwv, B.get(p + ".bias", {co}).v, ci, co, 1, 1, 1, 1, {0, 0, 0, 0});
+  return r;
+}
+
+// The rank-one convs of the four neck levels: the depthwise layers one by
+// one, the pointwise layers as one launch where they can share one.
+std::vector<View> rank_one_levels(Builder& B, const std::vector<View>& xs, const std::string& prefix, int ci, int co,
+                                  int k) {
+  std::vector<View> d(4);
+  std::vector<const View*> dp(4);
+  std::vector<ConvW> pws(4);
+  std::vector<std::string> names(4);
+  for (int i = 0; i < 4; ++i) {
+    const std::string p = prefix + "." + std::to_string(i);
+    const RankOneW r = rank_one_w(B, p, ci, co, k);
+    d[i] = B.depthwise(xs[i], r.dw, ACT_NONE, nullptr, p + ".depthwise");
+    dp[i] = &d[i];
+    pws[i] = r.pw;
+    names[i] = p + ".pointwise";
+  }
+  return B.conv_levels(dp, pws, Epi{}, names, prefix + ".pointwise");
 }
 
 // fuse_intraclass_conv (src/cpu/model.rs:819-906).
@@ -1363,37 +1412,56 @@ View medium_neck(Builder& B, const std::vector<View>& st) {
     if (i < 3) e.up = &td[i + 1];
     td[i] = B.conv(st[i], w, e, p);
   }
+  // The projections of the four levels, then the bottom-up chain
+  // p[i] += conv3x3s2(p[i - 1]) (the projection added in the pan conv's
+  // epilogue).
+  std::vector<View> proj = rank_one_levels(B, td, n + ".input_feature_projection_convolution", 256, 64, 9);
   std::vector<View> bu(4);
   for (int i = 0; i < 4; ++i) {
-    View proj = rank_one(B, td[i], n + ".input_feature_projection_convolution." + std::to_string(i), 256, 64, 9, Epi{});
     if (i == 0) {
-      bu[i] = proj;
+      bu[i] = proj[0];
     } else {
       std::string p = n + ".path_aggregation_head_convolution." + std::to_string(i - 1);
       ConvW w = B.conv_w(p, 64, 64, 3, 3, 2, 2, {1, 1, 1, 1}, false);
       Epi e;
-      e.res = &proj;
+      e.res = &proj[i];
       bu[i] = B.conv(bu[i - 1], w, e, p);
     }
   }
   const View& b0 = bu[0];
   View cat = B.alloc(b0.n, b0.h, b0.w, 256, n + ".concat");
+  std::vector<View> lat = rank_one_levels(B, bu, n + ".path_aggregation_lateral_convolution", 64, 64, 9);
+  // IntraclassBlock per level, each step of the four levels as one launch
+  // where they can share one: 1x1 64 -> 32, the fused 7x7, 5x5 and 3x3, then
+  // conv_final (upsampled into the concat slot, one launch per level).
+  auto step = [&](const std::vector<View>& xs, auto make_w, const std::string& suffix) {
+    std::vector<const View*> xp(4);
+    std::vector<ConvW> ws(4);
+    std::vector<std::string> names(4);
+    for (int i = 0; i < 4; ++i) {
+      const std::string p = n + ".intraclass_blocks." + std::to_string(i);
+      xp[i] = &xs[i];
+      ws[i] = make_w(p);
+      names[i] = p + suffix;
+    }
+    return B.conv_levels(xp, ws, Epi{}, names, n + ".intraclass_blocks" + suffix);
+  };
+  std::vector<View> r = step(lat, [&](const std::string& p) {
+    return B.conv_w(p + ".conv_reduce_channel", 64, 32, 1, 1, 1, 1, {0, 0, 0, 0}, true);
+  }, ".conv_reduce_channel");
+  std::vector<View> l7 = step(r, [&](const std::string& p) { return intraclass_conv(B, p, "longratio", 7); }, ".long");
+  std::vector<View> l5 = step(l7, [&](const std::string& p) { return intraclass_conv(B, p, "midratio", 5); }, ".mid");
+  std::vector<View> l3 = step(l5, [&](const std::string& p) { return intraclass_conv(B, p, "shortratio", 3); }, ".short");
   for (int i = 0; i < 4; ++i) {
-    View lat = rank_one(B, bu[i], n + ".path_aggregation_lateral_convolution." + std::to_string(i), 64, 64, 9, Epi{});
     std::string p = n + ".intraclass_blocks." + std::to_string(i);
-    ConvW red = B.conv_w(p + ".conv_reduce_channel", 64, 32, 1, 1, 1, 1, {0, 0, 0, 0}, true);
-    View r = B.conv(lat, red, Epi{}, p + ".conv_reduce_channel");
-    View l7 = B.conv(r, intraclass_conv(B, p, "longratio", 7), Epi{}, p + ".long");
-    View l5 = B.conv(l7, intraclass_conv(B, p, "midratio", 5), Epi{}, p + ".mid");
-    View l3 = B.conv(l5, intraclass_conv(B, p, "shortratio", 3), Epi{}, p + ".short");
     ConvW fin = B.conv_w(p + ".conv_final", 32, 64, 1, 1, 1, 1, {0, 0, 0, 0}, true, "norm");
     View slot = Builder::slice(cat, (3 - i) * 64, 64);
     Epi e;
     e.act = ACT_RELU;
-    e.res = &lat;
+    e.res = &lat[i];
     e.rep = 1 << i;
     e.dst = &slot;
-    B.conv(l3, fin, e, p + ".conv_final");
+    B.conv(l3[i], fin, e, p + ".conv_final");
   }
   return cat;
 }
