@@ -16,9 +16,11 @@ Alongside ``value`` the line carries:
 * ``roofline``: the dominant kernel (most device time per step), its
   algorithmic FLOPs (2 x MACs) or bytes per step over its HIP-event-timed
   duration (events recorded on the stream the kernels run on), against the
-  MI355X peak for its bound and storage type (fp32 matrix 157.3 TFLOP/s,
-  bf16 matrix 2.5 PFLOP/s, fp32 vector 78.6 TFLOP/s without packed fp32,
-  HBM 8 TB/s); ``traffic`` is its measured HBM bytes per launch from the
+  MI355X peak of the roof it runs under (fp32 matrix 157.3 TFLOP/s, bf16
+  matrix 2.5 PFLOP/s, fp32 vector 78.6 TFLOP/s without packed fp32, HBM
+  8 TB/s; a compute kernel whose algorithmic FLOPs per byte stay below that
+  compute peak's ridge point is measured in bytes against HBM, the roofline
+  model's lower roof, see bound_of); ``traffic`` is its measured HBM bytes per launch from the
   committed counter summary, when one covers this kernel and workload;
 * (detail line) the same measure for the twelve kernel instances with the
   most device time (the depthwise and elementwise ones against HBM);
@@ -96,13 +98,33 @@ def kernel_groups(stats):
     return groups
 
 
+def compute_peak(bound, precision="f32"):
+    """Peak TFLOP/s of a compute roof (matrix or vector)."""
+    if bound == "mfma":
+        return PEAK_BF16_TFLOPS if precision == "bf16" else PEAK_F32_TFLOPS
+    return PEAK_VALU_F32_TFLOPS
+
+
+def bound_of(g, precision="f32"):
+    """The roof a kernel group runs under (the roofline model): the compute
+    roof its kernel is built for (matrix cores or vector ALUs) when its
+    arithmetic intensity, algorithmic FLOPs per algorithmic HBM byte, reaches
+    that roof's ridge point (peak FLOP/s over the 8 TB/s of HBM; 19.7 FLOP/B
+    for fp32 matrix products, 312.5 for bf16); below the ridge HBM is the
+    lower roof, and the group is measured against it (achieved bytes / 8 TB/s
+    equals achieved FLOPs over the attainable intensity x bandwidth)."""
+    if g["bound"] not in ("mfma", "valu") or g["bytes"] <= 0:
+        return g["bound"]
+    ridge = compute_peak(g["bound"], precision) * 1e12 / (PEAK_HBM_GBS * 1e9)
+    return g["bound"] if g["flops"] / g["bytes"] >= ridge else "hbm"
+
+
 def rate(g, precision="f32"):
-    """(achieved, peak, unit) of a kernel group against its bound's peak."""
+    """(achieved, peak, unit) of a kernel group against its roof (bound_of)."""
     secs = g["ms"] * 1e-3
-    if g["bound"] == "mfma":
-        return g["flops"] / secs / 1e12, PEAK_BF16_TFLOPS if precision == "bf16" else PEAK_F32_TFLOPS, "TFLOP/s"
-    if g["bound"] == "valu":
-        return g["flops"] / secs / 1e12, PEAK_VALU_F32_TFLOPS, "TFLOP/s"
+    bound = bound_of(g, precision)
+    if bound in ("mfma", "valu"):
+        return g["flops"] / secs / 1e12, compute_peak(bound, precision), "TFLOP/s"
     return g["bytes"] / secs / 1e9, PEAK_HBM_GBS, "GB/s"
 
 
@@ -113,7 +135,7 @@ def kernel_table(stats, top=12, precision="f32"):
     rows = []
     for name, g in sorted(groups.items(), key=lambda kv: -kv[1]["ms"])[:top]:
         achieved, peak, unit = rate(g, precision)
-        rows.append({"kernel": name, "bound": g["bound"],
+        rows.append({"kernel": name, "bound": bound_of(g, precision),
                      "launches_per_step": g["launches"], "ms_per_step": round(g["ms"], 4),
                      "share_of_device_time": round(g["ms"] / total_ms, 3) if total_ms else None,
                      "achieved": round(achieved, 2), "unit": unit, "frac": round(achieved / peak, 3)})
@@ -127,7 +149,7 @@ def roofline(stats, key, precision="f32"):
     achieved, peak, unit = rate(g, precision)
     total_ms = sum(v["ms"] for v in groups.values())
     return {
-        "bound": g["bound"],
+        "bound": bound_of(g, precision),
         "achieved": round(achieved, 3),
         "peak": peak,
         "unit": unit,

@@ -64,3 +64,29 @@ def test_detail_lines_are_json(capsys):
     bench.emit("probe", {"a": [1, 2, 3]})
     out = capsys.readouterr().out.strip().splitlines()
     assert json.loads(out[-1]) == {"detail": "probe", "data": {"a": [1, 2, 3]}}
+
+
+def test_roof_follows_arithmetic_intensity():
+    """A matrix-core group is measured against the matrix peak only from the
+    ridge point (peak FLOP/s / 8 TB/s) up, against HBM below it."""
+    bench = _bench()
+
+    def group(flops, nbytes, bound="mfma"):
+        return {"ms": 0.05, "flops": flops, "bytes": nbytes, "launches": 1, "bound": bound}
+
+    # fp32 ridge 157.3e12 / 8e12 = 19.66 FLOP/B; bf16 ridge 312.5 FLOP/B.
+    assert bench.bound_of(group(6.4e9, 1.055e8), "f32") == "mfma"  # 60.7 FLOP/B
+    assert bench.bound_of(group(1.9e9, 1.055e8), "f32") == "hbm"  # 18.0 FLOP/B
+    assert bench.bound_of(group(6.4e9, 1.055e8), "bf16") == "hbm"
+    assert bench.bound_of(group(1.3e11, 3.77e8), "bf16") == "mfma"  # 345 FLOP/B
+    assert bench.bound_of(group(1e9, 1e8, "valu"), "f32") == "valu"  # 10 >= 9.83
+    assert bench.bound_of(group(9e8, 1e8, "valu"), "f32") == "hbm"
+    assert bench.bound_of(group(0.0, 1e8, "hbm"), "f32") == "hbm"
+    # Below the ridge the fraction is bytes over the HBM peak, which equals
+    # FLOPs over the attainable intensity x bandwidth.
+    g = group(6.4e9, 1.055e8)
+    achieved, peak, unit = bench.rate(g, "bf16")
+    assert unit == "GB/s" and peak == bench.PEAK_HBM_GBS
+    flops_rate = 6.4e9 / 0.05e-3
+    attainable = 6.4e9 / 1.055e8 * bench.PEAK_HBM_GBS * 1e9
+    assert abs(achieved / peak - flops_rate / attainable) < 1e-9

@@ -361,7 +361,8 @@ def test_upsample_on_write_matches_float64(name, n, h, w, c, co, rep):
 
 
 # Wide-tile bf16 1x1 kernel (256x256 tiles of 32x32x16 MFMAs): M, N and K
-# tails, plain and gated residual, and a layer just below its K threshold.
+# tails, plain and gated residual, and a layer just below its K threshold;
+# grids of fewer and of more tiles than the persistent workgroups.
 # (name, n, h, w, c, co, act, residual: 0 none / 1 plain / 2 gated, fp32 output, kernel)
 ACT_GELU = 2
 WIDE_CASES = [
@@ -371,6 +372,12 @@ WIDE_CASES = [
     ("K below threshold", 2, 65, 127, 256, 516, ACT_RELU, 1, False, "conv_gemm_bf16<64x64,1x1>"),
     # The classifier form: fp32 logits, Co % 4 == 2 (float2 stores), short K.
     ("wide fp32 out, Co % 4 = 2", 1, 61, 110, 200, 1030, ACT_NONE, 0, True, "conv_gemm_bf16<256x256,1x1>"),
+    # More tiles than compute units: each persistent workgroup walks several
+    # tiles, the next tile's first K slice loading during the epilogue.
+    ("wide persistent, 432 tiles", 4, 96, 96, 520, 520, ACT_GELU, 0, False, "conv_gemm_bf16<256x256,1x1>"),
+    ("wide persistent residual, 354 tiles", 3, 100, 100, 512, 768, ACT_NONE, 1, False, "conv_gemm_bf16<256x256,1x1>"),
+    ("wide persistent gated residual", 8, 64, 80, 576, 512, ACT_RELU, 2, False, "conv_gemm_bf16<256x256,1x1>"),
+    ("wide persistent fp32 out", 2, 100, 160, 192, 2050, ACT_NONE, 0, True, "conv_gemm_bf16<256x256,1x1>"),
 ]
 
 
