@@ -942,6 +942,12 @@ __device__ void llvm_raw_buffer_store_v2i32(u32x2 v, int32x4_t rsrc, int voffset
                                             int aux) __asm("llvm.amdgcn.raw.buffer.store.v2i32");
 __device__ void llvm_raw_buffer_store_v2f32(f32x2v v, int32x4_t rsrc, int voffset, int soffset,
                                             int aux) __asm("llvm.amdgcn.raw.buffer.store.v2f32");
+typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+__device__ void llvm_raw_buffer_store_v4i32(u32x4v v, int32x4_t rsrc, int voffset, int soffset,
+                                            int aux) __asm("llvm.amdgcn.raw.buffer.store.v4i32");
+// ds_swizzle offset in its 32-lane bit-mask mode: lane l reads lane l ^ 4
+// (and mask 0x1F, or mask 0, xor mask 4 in bits 10-14).
+constexpr int kSwizzleXor4 = 0x1F | (4 << 10);
 
 // One 16-byte buffer -> LDS load per lane from byte voffset + soffset of
 // the resource (LDS destination base + 16 * lane, base wave-uniform).
@@ -1531,7 +1537,7 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
   // Vector memory operations of one lane's epilogue (residual loads, gate
   // loads, stores; all issued unconditionally, masked lanes by offset), and
   // of one slice's loads: the waits below count them.
-  constexpr int E_OPS = (RES != 0 ? 32 : 0) + (RES == 2 ? 32 : 0) + (F32OUT ? 64 : 32);
+  constexpr int E_OPS = (RES != 0 ? 32 : 0) + (RES == 2 ? 32 : 0) + (F32OUT ? 64 : 16);
   constexpr int LP = AP + BP;
   constexpr int W0 = LP + E_OPS < 63 ? LP + E_OPS : 63;
   constexpr int W1 = E_OPS < 63 ? E_OPS : 63;
@@ -1643,6 +1649,7 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
           v[q] = quad_transpose(floatx4{acc[i][q][4 * g], acc[i][q][4 * g + 1], acc[i][q][4 * g + 2], acc[i][q][4 * g + 3]},
                                 lane);
         const int m = m0 + wm * 128 + i * 32 + 8 * g + rsub;
+        u32x2 packed[TN];
 #pragma unroll
         for (int q = 0; q < TN; ++q) {
           const int col = n0 + wn * 64 + q * 32 + ccol;
@@ -1661,18 +1668,34 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
             }
             x = f4_add(r, x);
           }
-          const bool mok = m < M;
           if constexpr (F32OUT) {
+            const bool mok = m < M;
             const size_t o = (size_t)m * p.out_ps + col;
             llvm_raw_buffer_store_v2f32(f32x2v{x.x, x.y}, out_rsrc, mok && col < p.Co ? (int)(o * 4) : (int)kOutOfRange, 0, 0);
             llvm_raw_buffer_store_v2f32(f32x2v{x.z, x.w}, out_rsrc, mok && col + 2 < p.Co ? (int)(o * 4 + 8) : (int)kOutOfRange,
                                         0, 0);
           } else {
-            const u32x2 w2{pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w)};
-            llvm_raw_buffer_store_v2i32(w2, out_rsrc,
-                                        mok && col < p.Co ? (int)(((size_t)m * p.out_ps + col) * 2) : (int)kOutOfRange, 0,
-                                        NT_STORE ? kAuxNontemporal : 0);
+            packed[q] = u32x2{pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w)};
           }
+        }
+        if constexpr (!F32OUT) {
+          // Lanes l and l ^ 4 trade halves: the even column group takes
+          // block 0's columns 8 c' .. + 7, the odd one block 1's, so one
+          // 16-byte store per lane writes each row's 64 columns (128 bytes,
+          // a whole line) at once: 1.02-1.17x against 8-byte stores of
+          // half lines, which the non-temporal stores also write to HBM as
+          // partial lines.  (Co and out_ps are multiples of 8 here.)
+          const bool odd = (lane >> 2) & 1;
+          const u32x2 give = odd ? packed[0] : packed[1];
+          u32x2 got;
+          got[0] = __builtin_amdgcn_ds_swizzle(give[0], kSwizzleXor4);
+          got[1] = __builtin_amdgcn_ds_swizzle(give[1], kSwizzleXor4);
+          const int colw = n0 + wn * 64 + (odd ? 32 : 0) + ((lr >> 2) & ~1) * 4;
+          const u32x4v w4 = odd ? u32x4v{got[0], got[1], packed[1][0], packed[1][1]}
+                                : u32x4v{packed[0][0], packed[0][1], got[0], got[1]};
+          llvm_raw_buffer_store_v4i32(w4, out_rsrc,
+                                      m < M && colw < p.Co ? (int)(((size_t)m * p.out_ps + colw) * 2) : (int)kOutOfRange,
+                                      0, NT_STORE ? kAuxNontemporal : 0);
         }
       }
     }
@@ -1925,7 +1948,10 @@ static bool wide_layer(const ConvParams& p) {
   // Epilogue buffer offsets are 32-bit with kOutOfRange as the masked offset.
   const size_t M = (size_t)p.N * p.Ho * p.Wo;
   const bool small = M * p.out_ps * (f32 ? 4 : 2) < kOutOfRange && (!p.res || M * p.res_ps * 2 < kOutOfRange);
-  return act && small && wide_shape(p.N * p.Ho * p.Wo, p.Co, p.C, p.dt, f32) && conv_variant(p, 128) == CV_DIRECT_1X1 &&
+  // bf16 outputs are stored 16 bytes (8 columns) at a time.
+  const bool whole8 = f32 || (p.Co % 8 == 0 && p.out_ps % 8 == 0);
+  return act && small && whole8 && wide_shape(p.N * p.Ho * p.Wo, p.Co, p.C, p.dt, f32) &&
+         conv_variant(p, 128) == CV_DIRECT_1X1 &&
          (!p.res_gate || p.res) && !p.up && p.rep == 1 && !(f32 && p.res) && !p.ctc_part && !p.db_ch &&
          p.splits <= 1 && p.out_ps % (f32 ? 2 : 4) == 0 && (!p.res || p.res_ps % 4 == 0);
 }

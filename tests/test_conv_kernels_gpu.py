@@ -386,9 +386,12 @@ def test_upsample_on_write_matches_float64(name, n, h, w, c, co, rep):
 # (name, n, h, w, c, co, act, residual: 0 none / 1 plain / 2 gated, fp32 output, kernel)
 ACT_GELU = 2
 WIDE_CASES = [
-    ("wide M/N/K tails", 2, 65, 127, 520, 516, ACT_HSWISH, 0, False, "conv_gemm_bf16<256x256,1x1>"),
+    ("wide M/N/K tails", 2, 65, 127, 520, 520, ACT_HSWISH, 0, False, "conv_gemm_bf16<256x256,1x1>"),
+    # bf16 outputs leave the wide kernel 8 columns at a time: Co % 8 = 4 runs
+    # on the direct kernel.
+    ("wide shape, Co % 8 = 4", 2, 65, 127, 520, 516, ACT_HSWISH, 0, False, "conv_gemm_bf16<64x64,1x1>"),
     ("wide residual", 1, 130, 127, 512, 512, ACT_NONE, 1, False, "conv_gemm_bf16<256x256,1x1>"),
-    ("wide gated residual", 4, 33, 128, 768, 260, ACT_GELU, 2, False, "conv_gemm_bf16<256x256,1x1>"),
+    ("wide gated residual", 4, 33, 128, 768, 264, ACT_GELU, 2, False, "conv_gemm_bf16<256x256,1x1>"),
     ("K below threshold", 2, 65, 127, 256, 516, ACT_RELU, 1, False, "conv_gemm_bf16<64x64,1x1>"),
     # The classifier form: fp32 logits, Co % 4 == 2 (float2 stores), short K.
     ("wide fp32 out, Co % 4 = 2", 1, 61, 110, 200, 1030, ACT_NONE, 0, True, "conv_gemm_bf16<256x256,1x1>"),
