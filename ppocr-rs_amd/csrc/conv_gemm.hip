@@ -943,6 +943,8 @@ __device__ void llvm_raw_buffer_store_v2i32(u32x2 v, int32x4_t rsrc, int voffset
 __device__ void llvm_raw_buffer_store_v2f32(f32x2v v, int32x4_t rsrc, int voffset, int soffset,
                                             int aux) __asm("llvm.amdgcn.raw.buffer.store.v2f32");
 typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+__device__ u32x4v llvm_raw_buffer_load_v4i32(int32x4_t rsrc, int voffset, int soffset,
+                                             int aux) __asm("llvm.amdgcn.raw.buffer.load.v4i32");
 __device__ void llvm_raw_buffer_store_v4i32(u32x4v v, int32x4_t rsrc, int voffset, int soffset,
                                             int aux) __asm("llvm.amdgcn.raw.buffer.store.v4i32");
 // ds_swizzle offset in its 32-lane bit-mask mode: lane l reads lane l ^ 4
@@ -1537,7 +1539,7 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
   // Vector memory operations of one lane's epilogue (residual loads, gate
   // loads, stores; all issued unconditionally, masked lanes by offset), and
   // of one slice's loads: the waits below count them.
-  constexpr int E_OPS = (RES != 0 ? 32 : 0) + (RES == 2 ? 32 : 0) + (F32OUT ? 64 : 16);
+  constexpr int E_OPS = (RES != 0 ? 16 : 0) + (RES == 2 ? 32 : 0) + (F32OUT ? 64 : 16);
   constexpr int LP = AP + BP;
   constexpr int W0 = LP + E_OPS < 63 ? LP + E_OPS : 63;
   constexpr int W1 = E_OPS < 63 ? E_OPS : 63;
@@ -1620,29 +1622,48 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
     // them; a row block's residual (and gate) loads are all issued before its
     // first store (a load cannot move above a store that may alias it).
     const int rsub = 4 * (lane >> 5) + (lane & 3);
+    // Lanes l and l ^ 4 (column groups c and c ^ 1 of both blocks) move
+    // whole 128-byte row lines between them: the even lane 8 columns of
+    // block 0, the odd one 8 of block 1, starting at colw.
+    const bool odd = (lane >> 2) & 1;
+    const int colw = n0 + wn * 64 + (odd ? 32 : 0) + ((lr >> 2) & ~1) * 4;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      u32x2 rraw[4][TN];
+      // Residual rows as whole lines: 16 bytes per lane at column colw, as
+      // the stores below; lane l ^ 4 holds the other block's 4 columns.
+      u32x4v rline[4];
       floatx4 rgate[4][TN];
       if constexpr (RES != 0) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int m = m0 + wm * 128 + i * 32 + 8 * g + rsub;
           const int img = RES == 2 ? min(m, M - 1) / (p.Ho * p.Wo) : 0;
+          rline[g] = llvm_raw_buffer_load_v4i32(
+              res_rsrc, m < M && colw < p.Co ? (int)(((size_t)m * p.res_ps + colw) * 2) : (int)kOutOfRange, 0,
+              kAuxNontemporal);
+          if constexpr (RES == 2) {
 #pragma unroll
-          for (int q = 0; q < TN; ++q) {
-            const int col = n0 + wn * 64 + q * 32 + ccol;
-            const bool ok = m < M && col < p.Co;
-            rraw[g][q] = llvm_raw_buffer_load_v2i32(res_rsrc, ok ? (int)(((size_t)m * p.res_ps + col) * 2) : (int)kOutOfRange,
-                                                    0, kAuxNontemporal);
-            if constexpr (RES == 2)
+            for (int q = 0; q < TN; ++q) {
+              const int col = n0 + wn * 64 + q * 32 + ccol;
+              const bool ok = m < M && col < p.Co;
               rgate[g][q] = llvm_raw_buffer_load_v4f32(gate_rsrc, ok ? (int)(((size_t)img * p.Co + col) * 4) : (int)kOutOfRange,
                                                        0, 0);
+            }
           }
         }
       }
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
+        u32x2 rq[TN];
+        if constexpr (RES != 0) {
+          const u32x2 keep = odd ? u32x2{rline[g][2], rline[g][3]} : u32x2{rline[g][0], rline[g][1]};
+          const u32x2 give = odd ? u32x2{rline[g][0], rline[g][1]} : u32x2{rline[g][2], rline[g][3]};
+          u32x2 got;
+          got[0] = __builtin_amdgcn_ds_swizzle(give[0], kSwizzleXor4);
+          got[1] = __builtin_amdgcn_ds_swizzle(give[1], kSwizzleXor4);
+          rq[0] = odd ? got : keep;
+          rq[1] = odd ? keep : got;
+        }
         floatx4 v[TN];
 #pragma unroll
         for (int q = 0; q < TN; ++q)
@@ -1660,7 +1681,7 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
           x.z = act_apply(ACT, x.z);
           x.w = act_apply(ACT, x.w);
           if constexpr (RES != 0) {
-            const u32x2 u = rraw[g][q];
+            const u32x2 u = rq[q];
             float4 r = unpack_bf16x4(u[0], u[1]);
             if constexpr (RES == 2) {
               const floatx4 gt = rgate[g][q];
@@ -1679,18 +1700,15 @@ __global__ __launch_bounds__(512) void conv1x1_wide_kernel(ConvParams p) {
           }
         }
         if constexpr (!F32OUT) {
-          // Lanes l and l ^ 4 trade halves: the even column group takes
-          // block 0's columns 8 c' .. + 7, the odd one block 1's, so one
-          // 16-byte store per lane writes each row's 64 columns (128 bytes,
-          // a whole line) at once: 1.02-1.17x against 8-byte stores of
-          // half lines, which the non-temporal stores also write to HBM as
-          // partial lines.  (Co and out_ps are multiples of 8 here.)
-          const bool odd = (lane >> 2) & 1;
+          // Lanes l and l ^ 4 trade halves so that one 16-byte store per
+          // lane writes each row's 64 columns (128 bytes, a whole line) at
+          // once: 1.02-1.17x against 8-byte stores of half lines, which the
+          // non-temporal stores also write to HBM as partial lines.  (Co and
+          // out_ps are multiples of 8 here.)
           const u32x2 give = odd ? packed[0] : packed[1];
           u32x2 got;
           got[0] = __builtin_amdgcn_ds_swizzle(give[0], kSwizzleXor4);
           got[1] = __builtin_amdgcn_ds_swizzle(give[1], kSwizzleXor4);
-          const int colw = n0 + wn * 64 + (odd ? 32 : 0) + ((lr >> 2) & ~1) * 4;
           const u32x4v w4 = odd ? u32x4v{got[0], got[1], packed[1][0], packed[1][1]}
                                 : u32x4v{packed[0][0], packed[0][1], got[0], got[1]};
           llvm_raw_buffer_store_v4i32(w4, out_rsrc,
@@ -1953,7 +1971,7 @@ static bool wide_layer(const ConvParams& p) {
   return act && small && whole8 && wide_shape(p.N * p.Ho * p.Wo, p.Co, p.C, p.dt, f32) &&
          conv_variant(p, 128) == CV_DIRECT_1X1 &&
          (!p.res_gate || p.res) && !p.up && p.rep == 1 && !(f32 && p.res) && !p.ctc_part && !p.db_ch &&
-         p.splits <= 1 && p.out_ps % (f32 ? 2 : 4) == 0 && (!p.res || p.res_ps % 4 == 0);
+         p.splits <= 1 && p.out_ps % (f32 ? 2 : 4) == 0 && (!p.res || p.res_ps % 8 == 0);
 }
 
 // Tile shapes of the direct and register kernels, indexed by pick_tile
