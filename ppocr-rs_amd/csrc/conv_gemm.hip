@@ -1992,17 +1992,19 @@ constexpr const char* kTileName[] = {"256x16", "128x32", "128x64", "64x64", "64x
 // per CU).  Wide layers: fp32 takes 64x64 (its MFMA is slow enough that the
 // smaller tile's occupancy wins); bf16 takes 128x64 when that still gives
 // every CU several blocks (its faster MFMA needs the operand reuse of the
-// taller tile).  Layers whose 64x64 tiles would number fewer than 512 (two
-// per CU; the batch-1 plans' deeper stages) take 64x32 tiles: twice the
-// workgroups to overlap each other's load latency, for less operand reuse
-// per tile (same-box A/B against 64x64: recognizers at batch 1 1.09-1.15x,
-// detectors at batch 1 1.03-1.07x, batch-8 detectors 0.99-1.02x; thresholds
-// of 256 and 384 tiles gave less at batch 1 and the same at batch 8).
+// taller tile).  Layers whose 64x64 tiles would number fewer than 1024
+// (four per CU; the batch-1 plans' deeper stages, the batch-8 plans'
+// deepest) take 64x32 tiles: twice the workgroups to overlap each other's
+// load latency, for less operand reuse per tile (same-box A/B against
+// 64x64 everywhere: recognizers at batch 1 1.09-1.15x, detectors at batch 1
+// 1.03-1.08x, batch-8 detectors 1.00-1.03x, tiny recognizer R64 1.03x;
+// thresholds of 256-768 tiles gave less, 1536 and 2048 lost 5-7 % on the
+// medium detector at batch 1).
 static int pick_tile(int M, int cols, int dt) {
   if (cols <= 16) return (M + 255) / 256 < 512 ? 4 : 0;
   if (cols <= 32) return (M + 127) / 128 < 512 ? 5 : 1;
   if (dt == DT_BF16 && (long)((M + 127) / 128) * ((cols + 63) / 64) >= 2048) return 2;
-  if ((long)((M + 63) / 64) * ((cols + 63) / 64) < 512) return 5;
+  if ((long)((M + 63) / 64) * ((cols + 63) / 64) < 1024) return 5;
   return 3;
 }
 

@@ -78,15 +78,15 @@ def conv_ref(x, w, b, stride, pads, kind):
 
 
 # (name, n, h, w, c, co, (kh, kw), (sh, sw), (pt, pl, pb, pr), gated, splits, dt, act, expected kernel)
-# Layers of fewer than 512 64x64 tiles take 64-row tiles of 32 columns; the
-# "64x64" cases are sized past that (>= 512 tiles).
+# Layers of fewer than 1024 64x64 tiles take 64-row tiles of 32 columns; the
+# "64x64" cases are sized past that (>= 1024 tiles).
 CASES = [
     ("1x1 M/N tails", 2, 7, 9, 64, 96, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_RELU, "conv_gemm<64x32,1x1>"),
-    ("1x1 M/N tails 64x64", 1, 129, 135, 64, 96, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_RELU,
+    ("1x1 M/N tails 64x64", 1, 181, 183, 64, 96, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_RELU,
      "conv_gemm<64x64,1x1>"),
     ("3x3 K tail", 1, 11, 13, 20, 24, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 0, ACT_HSWISH, "conv_gemm<64x32>"),
     ("3x3 stride 2", 2, 12, 10, 16, 64, (3, 3), (2, 2), (1, 1, 1, 1), False, 1, 0, ACT_NONE, "conv_gemm<64x32>"),
-    ("3x3 stride 2 64x64", 1, 257, 271, 16, 96, (3, 3), (2, 2), (1, 1, 1, 1), False, 1, 0, ACT_NONE,
+    ("3x3 stride 2 64x64", 1, 365, 363, 16, 96, (3, 3), (2, 2), (1, 1, 1, 1), False, 1, 0, ACT_NONE,
      "conv_gemm<64x64>"),
     ("7x1 asymmetric", 1, 9, 6, 8, 24, (7, 1), (1, 1), (3, 0, 3, 0), False, 1, 0, ACT_RELU, "conv_gemm<64x32>"),
     ("1x1 narrow Co", 1, 5, 6, 12, 10, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 0, ACT_SIGMOID, "conv_gemm<64x16,1x1>"),
@@ -97,40 +97,40 @@ CASES = [
      "conv_gemm<128x32,1x1>"),
     ("gated 1x1 direct", 3, 8, 10, 64, 64, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 0, ACT_RELU,
      "conv_gemm<64x32,1x1,gate>"),
-    ("gated 1x1 direct 64x64", 4, 64, 72, 64, 128, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 0, ACT_RELU,
+    ("gated 1x1 direct 64x64", 8, 64, 72, 64, 128, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 0, ACT_RELU,
      "conv_gemm<64x64,1x1,gate>"),
     ("gated 1x1 small images", 5, 3, 5, 64, 64, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 0, ACT_NONE,
      "conv_gemm<64x32,1x1,reg>"),
-    ("gated 1x1 small images 64x64", 1200, 3, 5, 64, 128, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 0, ACT_NONE,
+    ("gated 1x1 small images 64x64", 2400, 3, 5, 64, 128, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 0, ACT_NONE,
      "conv_gemm<64x64,1x1,reg>"),
     ("split K 1x1", 1, 5, 7, 256, 64, (1, 1), (1, 1), (0, 0, 0, 0), False, 4, 0, ACT_RELU, "conv_gemm<64x32,1x1>"),
-    ("split K 1x1 64x64", 1, 129, 135, 256, 96, (1, 1), (1, 1), (0, 0, 0, 0), False, 3, 0, ACT_RELU,
+    ("split K 1x1 64x64", 1, 181, 183, 256, 96, (1, 1), (1, 1), (0, 0, 0, 0), False, 3, 0, ACT_RELU,
      "conv_gemm<64x64,1x1>"),
     ("split K 3x3 uneven", 2, 6, 5, 32, 32, (3, 3), (1, 1), (1, 1, 1, 1), False, 5, 0, ACT_HSWISH,
      "conv_gemm<64x32>"),
     ("split K gated", 2, 6, 12, 128, 64, (1, 1), (1, 1), (0, 0, 0, 0), True, 3, 0, ACT_NONE,
      "conv_gemm<64x32,1x1,gate>"),
     ("bf16 1x1", 2, 9, 7, 64, 96, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 1, ACT_RELU, "conv_gemm_bf16<64x32,1x1>"),
-    ("bf16 1x1 64x64", 1, 129, 135, 64, 96, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 1, ACT_RELU,
+    ("bf16 1x1 64x64", 1, 181, 183, 64, 96, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 1, ACT_RELU,
      "conv_gemm_bf16<64x64,1x1>"),
     ("bf16 3x3", 1, 10, 12, 32, 64, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 1, ACT_NONE, "conv_gemm_bf16<64x32>"),
-    ("bf16 3x3 64x64", 1, 129, 135, 32, 96, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 1, ACT_NONE,
+    ("bf16 3x3 64x64", 1, 181, 183, 32, 96, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 1, ACT_NONE,
      "conv_gemm_bf16<64x64>"),
     ("bf16 C % 8 = 4", 1, 8, 9, 12, 48, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 1, ACT_RELU,
      "conv_gemm_bf16<64x32,reg4>"),
-    ("bf16 C % 8 = 4 64x64", 1, 129, 135, 12, 96, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 1, ACT_RELU,
+    ("bf16 C % 8 = 4 64x64", 1, 181, 183, 12, 96, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 1, ACT_RELU,
      "conv_gemm_bf16<64x64,reg4>"),
     ("bf16 gated", 2, 8, 10, 64, 64, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 1, ACT_NONE,
      "conv_gemm_bf16<64x32,1x1,reg>"),
-    ("bf16 gated 64x64", 1200, 3, 5, 64, 128, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 1, ACT_NONE,
+    ("bf16 gated 64x64", 2400, 3, 5, 64, 128, (1, 1), (1, 1), (0, 0, 0, 0), True, 1, 1, ACT_NONE,
      "conv_gemm_bf16<64x64,1x1,reg>"),
     ("bf16 split K", 1, 7, 5, 256, 64, (1, 1), (1, 1), (0, 0, 0, 0), False, 2, 1, ACT_RELU,
      "conv_gemm_bf16<64x32,1x1>"),
-    ("bf16 128-byte rows", 3, 37, 41, 776, 520, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 1, ACT_HSWISH,
+    ("bf16 128-byte rows", 5, 37, 41, 776, 520, (1, 1), (1, 1), (0, 0, 0, 0), False, 1, 1, ACT_HSWISH,
      "conv_gemm_bf16<64x64,1x1,r128>"),
-    ("bf16 3x3 128-byte rows", 19, 19, 23, 320, 200, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 1, ACT_RELU,
+    ("bf16 3x3 128-byte rows", 17, 19, 23, 320, 520, (3, 3), (1, 1), (1, 1, 1, 1), False, 1, 1, ACT_RELU,
      "conv_gemm_bf16<64x64,r128>"),
-    ("bf16 3x3 s2 128-byte rows", 104, 21, 17, 128, 200, (3, 3), (2, 2), (1, 1, 0, 0), False, 1, 1, ACT_NONE,
+    ("bf16 3x3 s2 128-byte rows", 208, 21, 17, 128, 200, (3, 3), (2, 2), (1, 1, 0, 0), False, 1, 1, ACT_NONE,
      "conv_gemm_bf16<64x64,r128>"),
 ]
 
@@ -447,7 +447,7 @@ def test_wide_bf16_1x1_matches_float64(name, n, h, w, c, co, kind, residual, f32
 
 # (name, h, w, c, co, (kh, kw), pads, gated, dt, act, expected kernel, rows per tile row block or 0)
 SE_CASES = [
-    ("se sums 64x64 fp32", 160, 208, 64, 64, (1, 1), (0, 0, 0, 0), False, 0, ACT_RELU, "conv_gemm<64x64,1x1>", 2),
+    ("se sums 64x64 fp32", 256, 260, 64, 64, (1, 1), (0, 0, 0, 0), False, 0, ACT_RELU, "conv_gemm<64x64,1x1>", 2),
     ("se sums 64x32 fp32, 64 columns", 23, 29, 64, 64, (1, 1), (0, 0, 0, 0), False, 0, ACT_RELU, "conv_gemm<64x32,1x1>",
      4),
     ("se sums 64x16", 19, 37, 32, 16, (1, 1), (0, 0, 0, 0), False, 0, ACT_NONE, "conv_gemm<64x16,1x1>", 4),
