@@ -194,6 +194,30 @@ bool pointwise_pair_supported(int C, int H2, int Co, int dt);
 // partial channel sums (N images, C channels, H2 hidden, Cr reduced ones).
 bool pair_se_fold_supported(int N, int C, int H2, int Cr, int P);
 
+// bf16 pointwise pair of an LCNet block (pair_bf16.hip): out = conv2(GELU(
+// conv1(x * gate))) (+ x * gate), conv1 C -> 2C, conv2 2C -> C, one launch.
+// x, out bf16 [M][ps]; gate fp32 [N][C] over HW pixels per image, or null;
+// weights bf16 packed [rows][ldw], biases fp32.
+struct PairBf16Params {
+  const void* in;
+  int in_ps;
+  const float* gate;
+  int HW;
+  int M, C;
+  const void* w1;  // [2C][ldw1]
+  int ldw1;
+  const float* b1;
+  const void* w2;  // [C][ldw2]
+  int ldw2;
+  const float* b2;
+  int residual;
+  void* out;
+  int out_ps;
+};
+bool pair_bf16_supported(int C, int H2, int Co);
+std::string pair_bf16_kernel_name(const PairBf16Params& p);
+void launch_pair_bf16(const PairBf16Params& p, hipStream_t s);
+
 // LayerNorm fused into the linear layer that reads it (pair_gemm.hip), fp32:
 // out[m][n] = act(sum_k LN(x[m])[k] w[n][k] + b[n]), LN with eps over K
 // features (K a multiple of 4); weights packed [N][ldw].

@@ -663,6 +663,61 @@ class Builder {
     return out;
   }
 
+  // bf16 plans: an LCNet block's pointwise pair x -> conv1 (GELU) -> conv2
+  // (+ residual) in one launch (pair_bf16_supported shapes), `gate` the SE
+  // gate of x or null.  It rounds where the unfused layers would (x * g,
+  // the GELU output, the result) and writes only the result, named as
+  // channel_conv2's output would be.
+  View pointwise_pair_bf16(const View& x, const ConvW& w1, const ConvW& w2, const View* gate, bool residual,
+                           const std::string& p) {
+    if (x.dt != DT_BF16 || x.c != w1.ci_pad || w2.ci_pad != w1.co || w1.kh * w1.kw * w2.kh * w2.kw != 1 ||
+        !pair_bf16_supported(x.c, w1.co, w2.co) || (residual && w2.co != x.c))
+      raise(PPOCR_ERR_INVALID_MODEL, p + ": bf16 pointwise pair shapes do not chain");
+    View out = alloc(x.n, x.h, x.w, w2.co, p + "2");
+    PairBf16Params base{};
+    base.in_ps = x.ps;
+    base.HW = x.h * x.w;
+    base.M = x.n * x.h * x.w;
+    base.C = x.c;
+    base.ldw1 = w1.ldw, base.ldw2 = w2.ldw;
+    base.residual = residual;
+    base.out_ps = out.ps;
+    const bool has_gate = gate;
+    const View in = x;
+    const View g = gate ? *gate : View();
+    const size_t w1o = w1.w, b1o = w1.b, w2o = w2.w, b2o = w2.b;
+    Op op;
+    op.name = p;
+    // Stand-in pointers (offsets, 16-byte aligned like the real ones) pick the instance name.
+    PairBf16Params probe = base;
+    probe.gate = has_gate ? reinterpret_cast<const float*>((uintptr_t)256) : nullptr;
+    op.kernel = pair_bf16_kernel_name(probe);
+    op.bound = 1;
+    const double M = (double)base.M, C = x.c, H = w1.co;
+    op.flops = 2.0 * M * (C * H + H * w2.co);
+    op.bytes = 2.0 * (M * C + C * H + H * w2.co + M * w2.co) + (has_gate ? 4.0 * x.n * C : 0.0);
+    op.rounds = {p + "1", p + "2"};
+    if (has_gate) op.rounds.push_back(p + "1.gated");
+    op.rounds_set = true;
+    op.bf16_weights = {p + "1", p + "2"};
+    op.reads = {x.buf};
+    if (has_gate) op.reads.push_back(g.buf);
+    op.writes = {out.buf};
+    op.launch = [=](const Exec& ex, hipStream_t s) {
+      PairBf16Params q = base;
+      q.in = ex.ptr(in);
+      q.gate = has_gate ? ex.fptr(g) : nullptr;
+      q.w1 = ex.wv(w1o);
+      q.b1 = ex.w(b1o);
+      q.w2 = ex.wv(w2o);
+      q.b2 = ex.w(b2o);
+      q.out = ex.ptr(out);
+      launch_pair_bf16(q, s);
+    };
+    add_op(std::move(op));
+    return out;
+  }
+
   // Squeeze-excitation gate [N,1,1,C] (fp32) of x (src/cpu/model.rs:456-493,
   // :1069-1105).
   // With sp->P > 0 the channel sums come from the kernel that wrote x.
@@ -1085,6 +1140,8 @@ View lcnet_block(Builder& B, const View& x, const std::string& p, BlockSpec s) {
     gate = B.se(t, sw, p + ".se", &sums);
   }
   if (pays) return B.pointwise_pair(t, c1, c2, has_se ? &gate : nullptr, residual, p + ".channel_conv");
+  if (B.dt() == DT_BF16 && pair_bf16_supported(s.ci, 2 * s.ci, s.co))
+    return B.pointwise_pair_bf16(t, c1, c2, has_se ? &gate : nullptr, residual, p + ".channel_conv");
   Epi e1;
   e1.act = ACT_GELU;
   if (has_se) e1.in_gate = &gate;

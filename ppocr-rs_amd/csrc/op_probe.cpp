@@ -509,6 +509,89 @@ int ppocr_probe_pointwise_pair_dw(const float* x, int n, int h, int w, int c, co
   return rc;
 }
 
+// The bf16 pointwise pair on host arrays, twice: fused (launch_pair_bf16)
+// into out_fused, and as the unfused bf16 plan runs it (the gate pass
+// storing x * g, then channel_conv1 and channel_conv2 on the direct conv
+// kernel with the stored x * g as residual) into out_unfused.  x [m][c]
+// (hw pixels per image), gate [m / hw][c] or null, w1 [2c][c], b1 [2c],
+// w2 [c][2c], b2 [c]; x and the weights are rounded to bf16, the outputs
+// [m][c] are returned widened.  *kernel (cap bytes) receives the fused
+// kernel's instance name.  Returns 0, 1 on a HIP error, 2 for a shape the
+// fused kernel does not take.
+int ppocr_probe_pair_bf16(const float* x, int m, int hw, int c, const float* gate, const float* w1, const float* b1,
+                          const float* w2, const float* b2, int residual, float* out_fused, float* out_unfused,
+                          char* kernel, size_t cap) {
+  if (!ppocr::pair_bf16_supported(c, 2 * c, c) || m <= 0 || hw <= 0) return 2;
+  const int n = (m + hw - 1) / hw;
+  const int BF = ppocr::DT_BF16, F = ppocr::DT_F32;
+  // The gate pass covers whole images (n * hw rows): x and x * g are
+  // allocated that long, x zero past row m.
+  const size_t rows = (size_t)n * hw;
+  std::vector<float> xpad(rows * c, 0.0f);
+  memcpy(xpad.data(), x, (size_t)m * c * sizeof(float));
+  void* d_in = upload(xpad.data(), rows * c, BF);
+  void* d_gate = gate ? upload(gate, (size_t)n * c, F) : nullptr;
+  void* d_w1 = upload(w1, (size_t)2 * c * c, BF);
+  void* d_b1 = upload(b1, 2 * c, F);
+  void* d_w2 = upload(w2, (size_t)2 * c * c, BF);
+  void* d_b2 = upload(b2, c, F);
+  void *d_xs = nullptr, *d_h = nullptr, *d_o1 = nullptr, *d_o2 = nullptr;
+  int rc = 0;
+  if (!d_in || (gate && !d_gate) || !d_w1 || !d_b1 || !d_w2 || !d_b2 || hipMalloc(&d_xs, rows * c * 2) ||
+      hipMalloc(&d_h, (size_t)m * 2 * c * 2) || hipMalloc(&d_o1, (size_t)m * c * 2) ||
+      hipMalloc(&d_o2, (size_t)m * c * 2)) {
+    rc = 1;
+  } else {
+    ppocr::PairBf16Params p{};
+    p.in = d_in, p.in_ps = c;
+    p.gate = static_cast<const float*>(d_gate), p.HW = hw;
+    p.M = m, p.C = c;
+    p.w1 = d_w1, p.ldw1 = c, p.b1 = static_cast<const float*>(d_b1);
+    p.w2 = d_w2, p.ldw2 = 2 * c, p.b2 = static_cast<const float*>(d_b2);
+    p.residual = residual;
+    p.out = d_o1, p.out_ps = c;
+    if (kernel && cap) {
+      const std::string name = ppocr::pair_bf16_kernel_name(p);
+      const size_t k = std::min(cap - 1, name.size());
+      memcpy(kernel, name.data(), k);
+      kernel[k] = 0;
+    }
+    ppocr::launch_pair_bf16(p, nullptr);
+    if (hipGetLastError() != hipSuccess) rc = 1;
+    // Unfused: x * g stored, conv1 (GELU), conv2 (+ residual).
+    const void* a = d_in;
+    if (gate) {
+      ppocr::launch_scale_channels(d_in, n, hw, c, c, static_cast<const float*>(d_gate), d_xs, BF, nullptr);
+      a = d_xs;
+    }
+    ppocr::ConvParams q{};
+    q.N = 1, q.H = m, q.W = 1, q.Ho = m, q.Wo = 1, q.out_h = m, q.out_w = 1;
+    q.kh = q.kw = q.sh = q.sw = 1;
+    q.up_s = 2, q.rep = 1, q.dt = BF, q.splits = 1;
+    ppocr::ConvParams q1 = q, q2 = q;
+    q1.in = a, q1.C = q1.in_ps = c, q1.wt = d_w1, q1.ldw = c, q1.bias = static_cast<const float*>(d_b1);
+    q1.Co = q1.out_ps = 2 * c, q1.act = ppocr::ACT_GELU, q1.out = d_h;
+    q2.in = d_h, q2.C = q2.in_ps = 2 * c, q2.wt = d_w2, q2.ldw = 2 * c, q2.bias = static_cast<const float*>(d_b2);
+    q2.Co = q2.out_ps = c, q2.out = d_o2;
+    if (residual) q2.res = a, q2.res_ps = c;
+    if (ppocr::conv_split_k(m, 2 * c, c, BF) > 1 || ppocr::conv_split_k(m, c, 2 * c, BF) > 1) rc = 2;
+    if (rc == 0) {
+      ppocr::launch_conv(q1, nullptr);
+      ppocr::launch_conv(q2, nullptr);
+      if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess) rc = 1;
+    }
+    std::vector<uint16_t> hb((size_t)m * c);
+    for (auto [d, o] : {std::pair<void*, float*>{d_o1, out_fused}, {d_o2, out_unfused}}) {
+      if (rc != 0) break;
+      if (hipMemcpy(hb.data(), d, hb.size() * 2, hipMemcpyDeviceToHost) != hipSuccess) rc = 1;
+      for (size_t i = 0; i < hb.size(); ++i) o[i] = from_bf16(hb[i]);
+    }
+  }
+  for (void* d : {d_in, d_gate, d_w1, d_b1, d_w2, d_b2, d_xs, d_h, d_o1, d_o2})
+    if (d) (void)hipFree(d);
+  return rc;
+}
+
 // The kernel instance ppocr_probe_depthwise runs.
 const char* ppocr_probe_depthwise_kernel(int h, int c, int k, int dt, int table) {
   return ppocr::depthwise_kernel_name(k, k, 1, 1, h, dt, table != 0, c);

@@ -240,6 +240,66 @@ def test_pointwise_pair_matches_float64(name, m, hw, c, co, gated, residual):
     assert np.all(err <= 1e-4 + 1e-5 * np.abs(want)), f"max err {err.max()}"
 
 
+# The fused bf16 pair (C -> 2C -> C) against the unfused bf16 plan's own
+# launches on the same device data, which it must equal bit for bit (same
+# MFMA instruction, k order and rounding points), and against a float64
+# evaluation with the plan's bf16 roundings (x, x * g, the GELU output and
+# the result rounded to bf16): within one bf16 ulp of the larger magnitude
+# (the final rounding, which can also cross a power of two) plus 2e-3 for
+# GELU outputs near a rounding tie that round the other way in float64.  Rows not a multiple
+# of the 16- or 32-row wave blocks, blocks straddling images, and row counts
+# on both sides of the 32-row threshold (a block per wave of 256 CUs x 8
+# waves: 65536 rows).
+PAIR_BF16_CASES = [
+    # name, rows, pixels per image, C, gate, residual, rows per wave block
+    ("C128 gated residual", 3000, 700, 128, True, True, 16),
+    ("C128 plain, one block", 9, 9, 128, False, False, 16),
+    ("C128 residual, 32-row blocks", 66001, 66001, 128, False, True, 32),
+    ("C128 gated, 32-row blocks", 70000, 9999, 128, True, False, 32),
+    ("C96 gated residual", 1999, 333, 96, True, True, 16),
+    ("C64 residual", 4097, 4097, 64, False, True, 16),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,m,hw,c,gated,residual,rows", PAIR_BF16_CASES, ids=[c[0] for c in PAIR_BF16_CASES])
+def test_pair_bf16_equals_unfused_bf16_plan(name, m, hw, c, gated, residual, rows):
+    from scipy.special import erf
+
+    lib = _lib()
+    f = ctypes.POINTER(ctypes.c_float)
+    i = ctypes.c_int
+    lib.ppocr_probe_pair_bf16.argtypes = [f, i, i, i, f, f, f, f, f, i, f, f, ctypes.c_char_p, ctypes.c_size_t]
+    lib.ppocr_probe_pair_bf16.restype = i
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    x = rng.standard_normal((m, c)).astype(np.float32)
+    n = (m + hw - 1) // hw
+    gate = rng.uniform(0, 1, (n, c)).astype(np.float32) if gated else None
+    w1 = (rng.standard_normal((2 * c, c)) / np.sqrt(c)).astype(np.float32)
+    b1 = rng.standard_normal(2 * c).astype(np.float32) * 0.1
+    w2 = (rng.standard_normal((c, 2 * c)) / np.sqrt(2 * c)).astype(np.float32)
+    b2 = rng.standard_normal(c).astype(np.float32) * 0.1
+    fused = np.full((m, c), np.nan, np.float32)
+    unfused = np.full((m, c), np.nan, np.float32)
+    kernel = ctypes.create_string_buffer(64)
+    rc = lib.ppocr_probe_pair_bf16(_ptr(x), m, hw, c, _ptr(gate), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2),
+                                   int(residual), _ptr(fused), _ptr(unfused), kernel, 64)
+    assert rc == 0
+    want_name = f"pair_bf16<{c},{rows}" + (",gate" if gated else "") + (",res" if residual else "") + ">"
+    assert kernel.value.decode() == want_name
+    diff = np.flatnonzero(fused.view(np.uint32) != unfused.view(np.uint32))
+    assert diff.size == 0, f"{diff.size} outputs differ from the unfused plan, first at {np.unravel_index(diff[0], fused.shape)}"
+    xb = bf16_round(x)
+    xg = bf16_round(xb * gate[np.arange(m) // hw]) if gated else xb
+    h = xg.astype(np.float64) @ bf16_round(w1).T.astype(np.float64) + b1
+    h = bf16_round((0.5 * h * (1.0 + erf(h / np.sqrt(2.0)))).astype(np.float32))
+    want = h.astype(np.float64) @ bf16_round(w2).T.astype(np.float64) + b2
+    if residual:
+        want = want + xg
+    err = np.abs(fused - want)
+    assert np.all(err <= 2.0 ** -7 * np.maximum(np.abs(want), np.abs(fused)) + 2e-3), f"max err {err.max()}"
+
+
 # (name, m, c, co, partial rows, residual): one image whose SE gate the pair
 # kernel forms from partial channel sums, one to three rounds of eight rows
 # per lane.
