@@ -75,7 +75,7 @@ __device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
 }
 
 template <int C, bool GATE, bool RES, int MB>
-__global__ __launch_bounds__(512) void pair_bf16_kernel(PairBf16Params p) {
+__global__ __launch_bounds__(64 * kPairWaves) void pair_bf16_kernel(PairBf16Params p) {
   constexpr int H = 2 * C;
   constexpr int KB = C / 32;   // GEMM1 k blocks (input channels)
   constexpr int KB2 = H / 32;  // GEMM2 k blocks (hidden channels)
