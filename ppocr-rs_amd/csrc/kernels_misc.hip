@@ -873,20 +873,22 @@ static void launch_dw_wave(const DwParams& p, hipStream_t s) {
 }
 
 // The launch shape of the tiled 3x3 kernels, the ones that can leave SE
-// partial sums (stride 1 and more than 4 output rows): 8-row tiles, 8 lanes
-// per pixel (32 fp32 or 64 bf16 channels), 2 outputs per lane along x
-// (8-pixel-wide tiles: 1.03-1.22x over 4 outputs on the detector's fp32
-// maps, more blocks for the same work and less tail) except for bf16 maps
-// of at most 16 rows (the recognizer's), which take 4 (16-pixel-wide: 1.1x
-// on its 6- and 12-row maps, 0.95x on the detector's).
-constexpr int kDw3TY = 8, kDw3C4B = 8;
-constexpr int dw3_xr(int dt, int ho) { return dt == DT_BF16 && ho <= 16 ? 4 : 2; }
-static int dw3_tx(int dt, int ho) { return 256 / (kDw3C4B * kDw3TY) * dw3_xr(dt, ho); }
+// partial sums (stride 1 and more than 4 output rows): 8 lanes per pixel
+// (32 fp32 or 64 bf16 channels), 2 outputs per lane along x (1.03-1.22x
+// over 4 outputs on the detector's fp32 maps, more blocks for the same
+// work and less tail; on bf16 maps 1.03-1.04x on the recognizer's 6- and
+// 12-row maps too), 8-row tiles except for bf16 maps whose height is a
+// multiple of 4 but not of 8, which take 4-row tiles and leave no lane row
+// idle (the recognizer's 12-row maps 1.23-1.25x, the detector's 52-row
+// map 1.03x; measured on the isolated layers, identical outputs).
+constexpr int kDw3C4B = 8, kDw3XR = 2;
+constexpr int dw3_ty(int dt, int ho) { return dt == DT_BF16 && ho % 8 != 0 && ho % 4 == 0 ? 4 : 8; }
+static int dw3_tx(int dt, int ho) { return 256 / (kDw3C4B * dw3_ty(dt, ho)) * kDw3XR; }
 
 int depthwise_se_blocks(const DwParams& p) {
   if (!(p.kh == 3 && p.kw == 3 && p.sh == 1 && p.sw == 1 && p.Ho > 4)) return 0;
-  const int tx = dw3_tx(p.dt, p.Ho);
-  return ((p.Wo + tx - 1) / tx) * ((p.Ho + kDw3TY - 1) / kDw3TY);
+  const int tx = dw3_tx(p.dt, p.Ho), ty = dw3_ty(p.dt, p.Ho);
+  return ((p.Wo + tx - 1) / tx) * ((p.Ho + ty - 1) / ty);
 }
 
 // bf16 3x3 stride-1 layers take the 8-channel tiled kernel when every pixel
@@ -932,12 +934,14 @@ static void launch_dw_typed(const DwParams& p, hipStream_t s) {
   if (p.sh == 1 && p.sw == 1) {
     if (p.kh == 3 && p.kw == 3) {
       if constexpr (sizeof(T) == 2) {
-        const bool wide = dw3_xr(DT_BF16, p.Ho) == 4;
+        const bool short_tiles = dw3_ty(DT_BF16, p.Ho) == 4;
         if (dw3_tiled8(p))
-          return wide ? launch_dw_tiled8<3, 3, kDw3TY, 4, kDw3C4B>(p, s) : launch_dw_tiled8<3, 3, kDw3TY, 2, kDw3C4B>(p, s);
-        return wide ? launch_dw_tiled<T, 3, 3, kDw3TY, 4, kDw3C4B>(p, s) : launch_dw_tiled<T, 3, 3, kDw3TY, 2, kDw3C4B>(p, s);
+          return short_tiles ? launch_dw_tiled8<3, 3, 4, kDw3XR, kDw3C4B>(p, s)
+                             : launch_dw_tiled8<3, 3, 8, kDw3XR, kDw3C4B>(p, s);
+        return short_tiles ? launch_dw_tiled<T, 3, 3, 4, kDw3XR, kDw3C4B>(p, s)
+                           : launch_dw_tiled<T, 3, 3, 8, kDw3XR, kDw3C4B>(p, s);
       }
-      return launch_dw_tiled<T, 3, 3, kDw3TY, 2, kDw3C4B>(p, s);
+      return launch_dw_tiled<T, 3, 3, 8, kDw3XR, kDw3C4B>(p, s);
     }
     // 5x5 and 9x9: wave-uniform taps (1.1-1.2x the tiled kernel's per-lane taps);
     // 7x7 (32 channels here) measured even: 16-row tiles of 16 channels.

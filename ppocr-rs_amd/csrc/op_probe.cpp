@@ -111,6 +111,70 @@ int run_conv(const float* x, int n, int h, int w, int c, const float* weight, co
   return rc;
 }
 
+// ppocr_probe_depthwise, and with se_rows the SE channel sums the layer
+// leaves: *se_rows = depthwise_se_blocks() and se_part [n][*se_rows][c].
+int run_depthwise(const float* x, int n, int h, int w, int c, const float* weight, const float* bias, int k, int act,
+                  const float* res, int dt, int table, float* out, int* se_rows, float* se_part) {
+  const size_t px = (size_t)n * h * w;
+  std::vector<float> packed((size_t)k * k * c);
+  for (int ch = 0; ch < c; ++ch)
+    for (int t = 0; t < k * k; ++t) packed[(size_t)t * c + ch] = weight[(size_t)ch * k * k + t];
+  void* d_in = upload(x, px * c, dt);
+  void* d_wt = upload(packed.data(), packed.size(), ppocr::DT_F32);
+  void* d_bias = bias ? upload(bias, c, ppocr::DT_F32) : nullptr;
+  void* d_res = res ? upload(res, px * c, dt) : nullptr;
+  void *d_out = nullptr, *d_tab = nullptr, *d_se = nullptr;
+  int rc = 0;
+  const size_t es = dt == ppocr::DT_BF16 ? 2 : 4;
+  if (table) {
+    std::vector<uint16_t> tab(ppocr::depthwise_mfma_table_size(c, k));
+    ppocr::depthwise_mfma_table(weight, c, k, tab.data());
+    if (hipMalloc(&d_tab, tab.size() * 2) != hipSuccess ||
+        hipMemcpy(d_tab, tab.data(), tab.size() * 2, hipMemcpyHostToDevice) != hipSuccess)
+      rc = 1;
+  }
+  if (rc || !d_in || !d_wt || (bias && !d_bias) || (res && !d_res) || hipMalloc(&d_out, px * c * es) != hipSuccess) {
+    rc = 1;
+  } else {
+    ppocr::DwParams p{};
+    p.in = d_in;
+    p.N = n, p.H = h, p.W = w, p.C = c, p.in_ps = c;
+    p.out = d_out;
+    p.Ho = h, p.Wo = w, p.out_ps = c;
+    p.wt = static_cast<const float*>(d_wt);
+    p.bias = static_cast<const float*>(d_bias);
+    p.kh = p.kw = k, p.sh = p.sw = 1, p.pt = p.pl = k / 2;
+    p.act = act;
+    p.res = d_res;
+    p.res_ps = c;
+    p.dt = dt;
+    p.wtab = d_tab;
+    if (se_rows) {
+      *se_rows = ppocr::depthwise_se_blocks(p);
+      if (*se_rows == 0) rc = 2;
+      else if (hipMalloc(&d_se, (size_t)n * *se_rows * c * 4) != hipSuccess) rc = 1;
+      p.se_part = static_cast<float*>(d_se);
+    }
+    if (rc == 0) ppocr::launch_depthwise(p, nullptr);
+    if (rc == 0 && hipDeviceSynchronize() != hipSuccess) rc = 1;
+    if (rc == 0 && d_se &&
+        hipMemcpy(se_part, d_se, (size_t)n * *se_rows * c * 4, hipMemcpyDeviceToHost) != hipSuccess)
+      rc = 1;
+    if (rc == 0) {
+      if (dt == ppocr::DT_BF16) {
+        std::vector<uint16_t> hb(px * c);
+        if (hipMemcpy(hb.data(), d_out, hb.size() * 2, hipMemcpyDeviceToHost) != hipSuccess) rc = 1;
+        for (size_t i = 0; i < hb.size(); ++i) out[i] = from_bf16(hb[i]);
+      } else if (hipMemcpy(out, d_out, px * c * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+        rc = 1;
+      }
+    }
+  }
+  for (void* ptr : {d_in, d_wt, d_bias, d_res, d_out, d_tab, d_se})
+    if (ptr) (void)hipFree(ptr);
+  return rc;
+}
+
 }  // namespace
 
 extern "C" {
@@ -266,55 +330,16 @@ const char* ppocr_probe_conv_kernel(int n, int h, int w, int c, int co, int kh, 
 // or 1 on a HIP error.
 int ppocr_probe_depthwise(const float* x, int n, int h, int w, int c, const float* weight, const float* bias, int k,
                           int act, const float* res, int dt, int table, float* out) {
-  const size_t px = (size_t)n * h * w;
-  std::vector<float> packed((size_t)k * k * c);
-  for (int ch = 0; ch < c; ++ch)
-    for (int t = 0; t < k * k; ++t) packed[(size_t)t * c + ch] = weight[(size_t)ch * k * k + t];
-  void* d_in = upload(x, px * c, dt);
-  void* d_wt = upload(packed.data(), packed.size(), ppocr::DT_F32);
-  void* d_bias = bias ? upload(bias, c, ppocr::DT_F32) : nullptr;
-  void* d_res = res ? upload(res, px * c, dt) : nullptr;
-  void *d_out = nullptr, *d_tab = nullptr;
-  int rc = 0;
-  const size_t es = dt == ppocr::DT_BF16 ? 2 : 4;
-  if (table) {
-    std::vector<uint16_t> tab(ppocr::depthwise_mfma_table_size(c, k));
-    ppocr::depthwise_mfma_table(weight, c, k, tab.data());
-    if (hipMalloc(&d_tab, tab.size() * 2) != hipSuccess ||
-        hipMemcpy(d_tab, tab.data(), tab.size() * 2, hipMemcpyHostToDevice) != hipSuccess)
-      rc = 1;
-  }
-  if (rc || !d_in || !d_wt || (bias && !d_bias) || (res && !d_res) || hipMalloc(&d_out, px * c * es) != hipSuccess) {
-    rc = 1;
-  } else {
-    ppocr::DwParams p{};
-    p.in = d_in;
-    p.N = n, p.H = h, p.W = w, p.C = c, p.in_ps = c;
-    p.out = d_out;
-    p.Ho = h, p.Wo = w, p.out_ps = c;
-    p.wt = static_cast<const float*>(d_wt);
-    p.bias = static_cast<const float*>(d_bias);
-    p.kh = p.kw = k, p.sh = p.sw = 1, p.pt = p.pl = k / 2;
-    p.act = act;
-    p.res = d_res;
-    p.res_ps = c;
-    p.dt = dt;
-    p.wtab = d_tab;
-    ppocr::launch_depthwise(p, nullptr);
-    if (hipDeviceSynchronize() != hipSuccess) rc = 1;
-    if (rc == 0) {
-      if (dt == ppocr::DT_BF16) {
-        std::vector<uint16_t> hb(px * c);
-        if (hipMemcpy(hb.data(), d_out, hb.size() * 2, hipMemcpyDeviceToHost) != hipSuccess) rc = 1;
-        for (size_t i = 0; i < hb.size(); ++i) out[i] = from_bf16(hb[i]);
-      } else if (hipMemcpy(out, d_out, px * c * 4, hipMemcpyDeviceToHost) != hipSuccess) {
-        rc = 1;
-      }
-    }
-  }
-  for (void* ptr : {d_in, d_wt, d_bias, d_res, d_out, d_tab})
-    if (ptr) (void)hipFree(ptr);
-  return rc;
+  return run_depthwise(x, n, h, w, c, weight, bias, k, act, res, dt, table, out, nullptr, nullptr);
+}
+
+// ppocr_probe_depthwise (no residual, no table) also leaving the SE channel
+// sums of its stored output: *rows = depthwise_se_blocks() partial rows per
+// image and se_part [n][*rows][c] (room for n * ceil(h / 4) * ceil(w / 8)
+// rows).  Returns 0, 1 on a HIP error, 2 when the layer leaves no sums.
+int ppocr_probe_depthwise_se(const float* x, int n, int h, int w, int c, const float* weight, const float* bias,
+                             int act, int dt, float* out, int* rows, float* se_part) {
+  return run_depthwise(x, n, h, w, c, weight, bias, 3, act, nullptr, dt, 0, out, rows, se_part);
 }
 
 // Depthwise with the gate-residual prologue (fp32): x = h + h * gate[n]

@@ -219,8 +219,9 @@ def test_gelu_epilogue_at_infinities_and_large_values():
 
 
 # (n, h, w, c, act, bias, residual): the bf16 3x3 tiled kernel with 8
-# channels per lane, on maps of at most 16 rows (16-pixel-wide tiles) and
-# taller ones (8-pixel-wide), with row, column and channel-block tails.
+# channels per lane, on maps whose height is a multiple of 4 but not of 8
+# (4-row tiles, 16 pixels wide) and others (8-row tiles, 8 pixels wide),
+# with row, column and channel-block tails.
 TILED8_CASES = [
     (2, 6, 80, 64, ACT_NONE, True, False),
     (1, 12, 37, 72, ACT_HSWISH, True, True),
@@ -253,3 +254,47 @@ def test_bf16_tiled8_depthwise_matches_float64(case):
     assert np.all(err <= tol), (float(err.max()), np.unravel_index(np.argmax(err - tol), err.shape))
     # Every output is finite and written (no stale pixels past the tiles).
     assert np.all(np.isfinite(out))
+
+
+# (n, h, w, c, dt, rows per image): the SE channel sums the tiled 3x3
+# kernels leave with their outputs, one row per tile of an image.  bf16 maps
+# whose height is a multiple of 4 but not of 8 take 4-row tiles 16 pixels
+# wide, the others 8-row tiles 8 pixels wide (fp32 always).
+DW_SE_CASES = [
+    (3, 12, 80, 128, 1, 5 * 3),
+    (2, 6, 37, 64, 1, 5 * 1),
+    (1, 52, 92, 256, 1, 6 * 13),
+    (2, 29, 45, 72, 1, 6 * 4),
+    (2, 12, 40, 32, 0, 5 * 2),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", DW_SE_CASES, ids=lambda c: "x".join(map(str, c[:4])) + ("-bf16" if c[4] else "-f32"))
+def test_tiled_depthwise_se_sums_match_stored_outputs(case):
+    """Summed over an image's rows, the partial sums equal the channel sums
+    of the stored (rounded) outputs up to fp32 summation order, and there
+    is one row per tile of the image."""
+    n, h, wd, c, dt, want_rows = case
+    lib = _lib()
+    f = ctypes.POINTER(ctypes.c_float)
+    i = ctypes.c_int
+    lib.ppocr_probe_depthwise_se.argtypes = [f, i, i, i, i, f, f, i, i, f, ctypes.POINTER(i), f]
+    lib.ppocr_probe_depthwise_se.restype = i
+    rng = np.random.default_rng(5 + h + wd + c + dt)
+    x = rng.uniform(-1, 1, (n, h, wd, c)).astype(np.float32)
+    w = rng.uniform(-0.5, 0.5, (c, 3, 3)).astype(np.float32)
+    b = rng.uniform(-0.5, 0.5, c).astype(np.float32)
+    out = np.empty_like(x)
+    rows = ctypes.c_int(0)
+    part = np.full((n * (h // 4 + 1) * (wd // 8 + 1), c), np.nan, np.float32)
+    assert lib.ppocr_probe_depthwise_se(_ptr(x), n, h, wd, c, _ptr(w), _ptr(b), ACT_NONE, dt, _ptr(out),
+                                        ctypes.byref(rows), _ptr(part)) == 0
+    assert rows.value == want_rows
+    sums = part[:n * rows.value].reshape(n, rows.value, c).astype(np.float64).sum(axis=1)
+    want = out.astype(np.float64).sum(axis=(1, 2))
+    scale = np.abs(out).astype(np.float64).sum(axis=(1, 2))
+    assert np.all(np.abs(sums - want) <= 1e-5 * scale + 1e-6), float(np.max(np.abs(sums - want) / (scale + 1)))
+    ref = depthwise_ref(bf16_round(x) if dt else x, w, b, ACT_NONE, None)
+    tol = (2.0 ** -8 if dt else 1e-5) * np.abs(ref) + 1e-5
+    assert np.all(np.abs(out - ref) <= tol)
