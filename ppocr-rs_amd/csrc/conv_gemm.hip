@@ -2063,8 +2063,7 @@ static void launch_tile_shape(const ConvParams& p, int M, hipStream_t s) {
   launch_tile<T, kTileBM[I], kTileBN[I], kTileWM[I], 4 / kTileWM[I]>(p, M, s);
 }
 
-// Compute units of the current device, looked up once per device.
-static int device_cus() {
+int device_cus() {
   static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;

@@ -215,6 +215,9 @@ struct PairBf16Params {
   int out_ps;
 };
 bool pair_bf16_supported(int C, int H2, int Co);
+// Compute units of the current device (256 when it cannot be queried),
+// looked up once per device.
+int device_cus();
 std::string pair_bf16_kernel_name(const PairBf16Params& p);
 void launch_pair_bf16(const PairBf16Params& p, hipStream_t s);
 

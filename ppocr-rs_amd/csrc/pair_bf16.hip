@@ -35,7 +35,6 @@
 //
 // Cost per pixel row (C = 128): 512 bytes of HBM traffic, 131 kFLOP on the
 // matrix cores, and 256 GELUs on the vector ALUs, which bound the kernel.
-#include <atomic>
 #include <stdexcept>
 
 #include "device_math.h"
@@ -202,29 +201,17 @@ __global__ __launch_bounds__(64 * kPairWaves) void pair_bf16_kernel(PairBf16Para
   }
 }
 
-int pair_device_cus() {
-  static std::atomic<int> cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int v = cached[dev].load(std::memory_order_relaxed);
-  if (v <= 0) {
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-    cached[dev].store(v, std::memory_order_relaxed);
-  }
-  return v;
-}
-
 // Rows per wave block: 32 where that still gives every wave of the grid a
 // block, else 16.
 int pair_rows(int M) {
-  const long slots = (long)pair_device_cus() * kPairWaves;
+  const long slots = (long)device_cus() * kPairWaves;
   return (M + 31) / 32 >= slots ? 32 : 16;
 }
 
 template <int C, int MB>
 void launch_c(const PairBf16Params& p, hipStream_t s) {
   const int nrb = (p.M + 16 * MB - 1) / (16 * MB);
-  const dim3 grid((unsigned)std::max(1, std::min(pair_device_cus(), nrb)));
+  const dim3 grid((unsigned)std::max(1, std::min(device_cus(), nrb)));
   const dim3 block(64 * kPairWaves);
   if (p.gate) {
     if (p.residual)
