@@ -878,11 +878,15 @@ static void launch_dw_wave(const DwParams& p, hipStream_t s) {
 // over 4 outputs on the detector's fp32 maps, more blocks for the same
 // work and less tail; on bf16 maps 1.03-1.04x on the recognizer's 6- and
 // 12-row maps too), 8-row tiles except for bf16 maps whose height is a
-// multiple of 4 but not of 8, which take 4-row tiles and leave no lane row
-// idle (the recognizer's 12-row maps 1.23-1.25x, the detector's 52-row
-// map 1.03x; measured on the isolated layers, identical outputs).
+// multiple of 4 but not of 8, which take 4-row tiles, and bf16 maps of 6
+// rows, which take 2-row tiles, so that no lane row is idle (the
+// recognizer's 12-row maps 1.23-1.25x, its 6-row maps 1.07x, the
+// detector's 52-row map 1.03x; measured on the isolated layers, identical
+// outputs).
 constexpr int kDw3C4B = 8, kDw3XR = 2;
-constexpr int dw3_ty(int dt, int ho) { return dt == DT_BF16 && ho % 8 != 0 && ho % 4 == 0 ? 4 : 8; }
+constexpr int dw3_ty(int dt, int ho) {
+  return dt != DT_BF16 ? 8 : ho % 8 != 0 && ho % 4 == 0 ? 4 : ho % 4 != 0 && ho % 2 == 0 && ho <= 8 ? 2 : 8;
+}
 static int dw3_tx(int dt, int ho) { return 256 / (kDw3C4B * dw3_ty(dt, ho)) * kDw3XR; }
 
 int depthwise_se_blocks(const DwParams& p) {
@@ -934,12 +938,14 @@ static void launch_dw_typed(const DwParams& p, hipStream_t s) {
   if (p.sh == 1 && p.sw == 1) {
     if (p.kh == 3 && p.kw == 3) {
       if constexpr (sizeof(T) == 2) {
-        const bool short_tiles = dw3_ty(DT_BF16, p.Ho) == 4;
+        const int ty = dw3_ty(DT_BF16, p.Ho);
         if (dw3_tiled8(p))
-          return short_tiles ? launch_dw_tiled8<3, 3, 4, kDw3XR, kDw3C4B>(p, s)
-                             : launch_dw_tiled8<3, 3, 8, kDw3XR, kDw3C4B>(p, s);
-        return short_tiles ? launch_dw_tiled<T, 3, 3, 4, kDw3XR, kDw3C4B>(p, s)
-                           : launch_dw_tiled<T, 3, 3, 8, kDw3XR, kDw3C4B>(p, s);
+          return ty == 2   ? launch_dw_tiled8<3, 3, 2, kDw3XR, kDw3C4B>(p, s)
+                 : ty == 4 ? launch_dw_tiled8<3, 3, 4, kDw3XR, kDw3C4B>(p, s)
+                           : launch_dw_tiled8<3, 3, 8, kDw3XR, kDw3C4B>(p, s);
+        return ty == 2   ? launch_dw_tiled<T, 3, 3, 2, kDw3XR, kDw3C4B>(p, s)
+               : ty == 4 ? launch_dw_tiled<T, 3, 3, 4, kDw3XR, kDw3C4B>(p, s)
+                         : launch_dw_tiled<T, 3, 3, 8, kDw3XR, kDw3C4B>(p, s);
       }
       return launch_dw_tiled<T, 3, 3, 8, kDw3XR, kDw3C4B>(p, s);
     }
