@@ -883,14 +883,24 @@ static void launch_dw_wave(const DwParams& p, hipStream_t s) {
 // recognizer's 12-row maps 1.23-1.25x, its 6-row maps 1.07x, the
 // detector's 52-row map 1.03x; measured on the isolated layers, identical
 // outputs).
+// bf16 maps of 3 and 4 rows (the recognizer's last stage) take the tiled
+// kernel with 4-row tiles too, in place of the vertical strips (1.38x on
+// 256x3x80x768, identical outputs), and leave SE sums.
 constexpr int kDw3C4B = 8, kDw3XR = 2;
 constexpr int dw3_ty(int dt, int ho) {
-  return dt != DT_BF16 ? 8 : ho % 8 != 0 && ho % 4 == 0 ? 4 : ho % 4 != 0 && ho % 2 == 0 && ho <= 8 ? 2 : 8;
+  return dt != DT_BF16                   ? 8
+         : ho <= 4                       ? 4
+         : ho % 8 != 0 && ho % 4 == 0    ? 4
+         : ho % 4 != 0 && ho % 2 == 0 && ho <= 8 ? 2
+                                         : 8;
 }
 static int dw3_tx(int dt, int ho) { return 256 / (kDw3C4B * dw3_ty(dt, ho)) * kDw3XR; }
+// Stride-1 3x3 layers on the tiled kernels: more than 4 output rows, or 3
+// or 4 rows in bf16.
+static bool dw3_tiled_rows(int dt, int ho) { return ho > 4 || (dt == DT_BF16 && ho >= 3); }
 
 int depthwise_se_blocks(const DwParams& p) {
-  if (!(p.kh == 3 && p.kw == 3 && p.sh == 1 && p.sw == 1 && p.Ho > 4)) return 0;
+  if (!(p.kh == 3 && p.kw == 3 && p.sh == 1 && p.sw == 1 && dw3_tiled_rows(p.dt, p.Ho))) return 0;
   const int tx = dw3_tx(p.dt, p.Ho), ty = dw3_ty(p.dt, p.Ho);
   return ((p.Wo + tx - 1) / tx) * ((p.Ho + ty - 1) / ty);
 }
@@ -933,7 +943,7 @@ static void launch_dw_typed(const DwParams& p, hipStream_t s) {
   // (the recognizer's last stage), where the LDS tile would load its halo
   // rows for only a few output rows: vertical strips.
   if (p.kh == 3 && p.kw == 3 && p.sh == 2) return launch_dw_strip<T, 3, 3, 3, 2>(p, s);
-  if (p.kh == 3 && p.kw == 3 && p.sh == 1 && p.Ho <= 4)
+  if (p.kh == 3 && p.kw == 3 && p.sh == 1 && !dw3_tiled_rows(p.dt, p.Ho))
     return p.Ho == 3 ? launch_dw_strip<T, 3, 3, 3, 1>(p, s) : launch_dw_strip<T, 3, 3, 4, 1>(p, s);
   if (p.sh == 1 && p.sw == 1) {
     if (p.kh == 3 && p.kw == 3) {
@@ -971,7 +981,7 @@ const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho, int dt
   if (table && depthwise_uses_mfma(kh, kw, sh, sw, dt, Ho, C))
     return kh == 5 ? "depthwise_mfma<5x5>" : kh == 7 ? "depthwise_mfma<7x7>" : "depthwise_mfma<9x9>";
   if (kh == 3 && kw == 3 && sh == 2) return "depthwise_strip<3x3,s2>";
-  if (kh == 3 && kw == 3 && sh == 1 && Ho <= 4) return "depthwise_strip<3x3>";
+  if (kh == 3 && kw == 3 && sh == 1 && !dw3_tiled_rows(dt, Ho)) return "depthwise_strip<3x3>";
   if (sh == 1 && sw == 1) {
     if (kh == 3 && kw == 3) return dt == DT_BF16 && C % 8 == 0 && groups8 ? "depthwise_tiled8<3x3>" : "depthwise_tiled<3x3>";
     if (kh == kw && (kh == 5 || kh == 7 || kh == 9))

@@ -220,11 +220,13 @@ def test_gelu_epilogue_at_infinities_and_large_values():
 
 # (n, h, w, c, act, bias, residual): the bf16 3x3 tiled kernel with 8
 # channels per lane, on maps whose height is a multiple of 4 but not of 8
-# (4-row tiles, 16 pixels wide), of 6 rows (2-row tiles, 32 wide) and
-# others (8-row tiles, 8 pixels wide), with row, column and channel-block
-# tails.
+# or is 3 (4-row tiles, 16 pixels wide), of 6 rows (2-row tiles, 32 wide)
+# and others (8-row tiles, 8 pixels wide), with row, column and
+# channel-block tails.
 TILED8_CASES = [
     (2, 6, 80, 64, ACT_NONE, True, False),
+    (4, 3, 80, 96, ACT_NONE, True, True),
+    (2, 4, 19, 24, ACT_RELU, True, False),
     (1, 12, 37, 72, ACT_HSWISH, True, True),
     (3, 7, 21, 8, ACT_RELU, False, True),
     (1, 29, 45, 136, ACT_NONE, True, False),
@@ -259,13 +261,15 @@ def test_bf16_tiled8_depthwise_matches_float64(case):
 
 # (n, h, w, c, dt, rows per image): the SE channel sums the tiled 3x3
 # kernels leave with their outputs, one row per tile of an image.  bf16 maps
-# whose height is a multiple of 4 but not of 8 take 4-row tiles 16 pixels
-# wide, 6-row ones 2-row tiles 32 pixels wide, the others 8-row tiles 8
-# pixels wide (fp32 always).
+# of 3 or 4 rows, or whose height is a multiple of 4 but not of 8, take
+# 4-row tiles 16 pixels wide, 6-row ones 2-row tiles 32 pixels wide, the
+# others 8-row tiles 8 pixels wide (fp32 always).
 DW_SE_CASES = [
     (3, 12, 80, 128, 1, 5 * 3),
     (2, 6, 37, 64, 1, 2 * 3),
     (1, 6, 80, 512, 1, 3 * 3),
+    (2, 3, 80, 768, 1, 5 * 1),
+    (1, 4, 21, 64, 1, 2 * 1),
     (1, 52, 92, 256, 1, 6 * 13),
     (2, 29, 45, 72, 1, 6 * 4),
     (2, 12, 40, 32, 0, 5 * 2),
