@@ -258,11 +258,14 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
 // measured 1.31-1.37x on the recognizer's 6- and 12-row maps and 1.28x on
 // the detector's 104 x 184 map, with bit-identical outputs (same taps in the
 // same (ky, kx) order).  SE partial sums as the 4-channel form leaves them.
-template <int KH, int KW, int TY, int XR, int C8B>
+// SH, SW: the layer's strides (the input tile spans (TY - 1) SH + KH rows
+// and (TX - 1) SW + KW columns).
+template <int KH, int KW, int TY, int XR, int C8B, int SH = 1, int SW = 1>
 __global__ __launch_bounds__(256) void depthwise_tiled8_kernel(DwParams p) {
   constexpr int XG = 256 / (C8B * TY);  // lane groups along x
   constexpr int TX = XG * XR;
-  constexpr int IH = TY + KH - 1, IW = TX + KW - 1;
+  constexpr int IH = (TY - 1) * SH + KH, IW = (TX - 1) * SW + KW;
+  constexpr int WN = (XR - 1) * SW + KW;  // input pixels of a lane's window row
   constexpr int IWP = IW | 1;  // odd row pitch (pixels)
   static_assert(IH * IWP * C8B >= 512, "the SE reduction reuses the tile");
   __shared__ uint4 tile[IH * IWP * C8B];
@@ -303,7 +306,7 @@ __global__ __launch_bounds__(256) void depthwise_tiled8_kernel(DwParams p) {
     for (int i = 0; i < NL; ++i) {
       const int px = tid / C8B + i * STEP;
       const int iy = px / IW, ix = px - iy * IW;
-      const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
+      const int gy = oy0 * SH - p.pt + iy, gx = ox0 * SW - p.pl + ix;
       v[i] = make_uint4(0, 0, 0, 0);
       if (px < IH * IW && cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W)
         v[i] = *reinterpret_cast<const uint4*>(base + ((size_t)gy * p.W + gx) * p.in_ps);
@@ -329,10 +332,10 @@ __global__ __launch_bounds__(256) void depthwise_tiled8_kernel(DwParams p) {
   for (int r = 0; r < XR; ++r) acc[r][0] = acc[r][1] = f4_zero();
 #pragma unroll 1
   for (int ky = 0; ky < KH; ++ky) {
-    float4 win[XR + KW - 1][2];
+    float4 win[WN][2];
 #pragma unroll
-    for (int j = 0; j < XR + KW - 1; ++j) {
-      const uint4 u = tile[((ty + ky) * IWP + xg * XR + j) * C8B + c8];
+    for (int j = 0; j < WN; ++j) {
+      const uint4 u = tile[((ty * SH + ky) * IWP + xg * XR * SW + j) * C8B + c8];
       win[j][0] = unpack_bf16x4(u.x, u.y);
       win[j][1] = unpack_bf16x4(u.z, u.w);
     }
@@ -343,10 +346,10 @@ __global__ __launch_bounds__(256) void depthwise_tiled8_kernel(DwParams p) {
         const float4 w = taps[((ky * KW + kx) * C8B + c8) * 2 + h];
 #pragma unroll
         for (int r = 0; r < XR; ++r) {
-          acc[r][h].x = fmaf(win[r + kx][h].x, w.x, acc[r][h].x);
-          acc[r][h].y = fmaf(win[r + kx][h].y, w.y, acc[r][h].y);
-          acc[r][h].z = fmaf(win[r + kx][h].z, w.z, acc[r][h].z);
-          acc[r][h].w = fmaf(win[r + kx][h].w, w.w, acc[r][h].w);
+          acc[r][h].x = fmaf(win[r * SW + kx][h].x, w.x, acc[r][h].x);
+          acc[r][h].y = fmaf(win[r * SW + kx][h].y, w.y, acc[r][h].y);
+          acc[r][h].z = fmaf(win[r * SW + kx][h].z, w.z, acc[r][h].z);
+          acc[r][h].w = fmaf(win[r * SW + kx][h].w, w.w, acc[r][h].w);
         }
       }
     }
@@ -912,11 +915,11 @@ static bool dw3_tiled8(const DwParams& p) {
          (((uintptr_t)p.in | (uintptr_t)p.out | (uintptr_t)p.res) & 15) == 0;
 }
 
-template <int KH, int KW, int TY, int XR, int C8B>
+template <int KH, int KW, int TY, int XR, int C8B, int SH = 1, int SW = 1>
 static void launch_dw_tiled8(const DwParams& p, hipStream_t s) {
   constexpr int TX = 256 / (C8B * TY) * XR;
   const long tiles = (long)((p.Wo + TX - 1) / TX) * ((p.Ho + TY - 1) / TY) * p.N * ((p.C + 8 * C8B - 1) / (8 * C8B));
-  hipLaunchKernelGGL((depthwise_tiled8_kernel<KH, KW, TY, XR, C8B>), dim3((unsigned)((tiles + 7) / 8 * 8)),
+  hipLaunchKernelGGL((depthwise_tiled8_kernel<KH, KW, TY, XR, C8B, SH, SW>), dim3((unsigned)((tiles + 7) / 8 * 8)),
                      dim3(256), 0, s, p);
 }
 
@@ -942,7 +945,22 @@ static void launch_dw_typed(const DwParams& p, hipStream_t s) {
   // 3x3 with vertical stride 2 (stage entries), and maps of at most 4 rows
   // (the recognizer's last stage), where the LDS tile would load its halo
   // rows for only a few output rows: vertical strips.
-  if (p.kh == 3 && p.kw == 3 && p.sh == 2) return launch_dw_strip<T, 3, 3, 3, 2>(p, s);
+  if (p.kh == 3 && p.kw == 3 && p.sh == 2) {
+    // bf16 stage entries on the 8-channel tiled kernel: stride (2, 1) (the
+    // recognizer's) with the stride-1 tile rows of the output height,
+    // stride (2, 2) (the detector's) with 4-row tiles of one output per
+    // lane (1.66-1.85x and 1.38-1.72x over the strips, identical outputs).
+    if constexpr (sizeof(T) == 2) {
+      if (dw3_tiled8(p) && p.sw == 2) return launch_dw_tiled8<3, 3, 4, 1, kDw3C4B, 2, 2>(p, s);
+      if (dw3_tiled8(p) && p.sw == 1) {
+        const int ty = dw3_ty(DT_BF16, p.Ho);
+        return ty == 2   ? launch_dw_tiled8<3, 3, 2, kDw3XR, kDw3C4B, 2, 1>(p, s)
+               : ty == 4 ? launch_dw_tiled8<3, 3, 4, kDw3XR, kDw3C4B, 2, 1>(p, s)
+                         : launch_dw_tiled8<3, 3, 8, kDw3XR, kDw3C4B, 2, 1>(p, s);
+      }
+    }
+    return launch_dw_strip<T, 3, 3, 3, 2>(p, s);
+  }
   if (p.kh == 3 && p.kw == 3 && p.sh == 1 && !dw3_tiled_rows(p.dt, p.Ho))
     return p.Ho == 3 ? launch_dw_strip<T, 3, 3, 3, 1>(p, s) : launch_dw_strip<T, 3, 3, 4, 1>(p, s);
   if (p.sh == 1 && p.sw == 1) {
@@ -980,7 +998,8 @@ bool depthwise_gate_residual_supported(int kh, int kw, int sh, int sw) {
 const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho, int dt, bool table, int C, bool groups8) {
   if (table && depthwise_uses_mfma(kh, kw, sh, sw, dt, Ho, C))
     return kh == 5 ? "depthwise_mfma<5x5>" : kh == 7 ? "depthwise_mfma<7x7>" : "depthwise_mfma<9x9>";
-  if (kh == 3 && kw == 3 && sh == 2) return "depthwise_strip<3x3,s2>";
+  if (kh == 3 && kw == 3 && sh == 2)
+    return dt == DT_BF16 && C % 8 == 0 && groups8 && sw <= 2 ? "depthwise_tiled8<3x3,s2>" : "depthwise_strip<3x3,s2>";
   if (kh == 3 && kw == 3 && sh == 1 && !dw3_tiled_rows(dt, Ho)) return "depthwise_strip<3x3>";
   if (sh == 1 && sw == 1) {
     if (kh == 3 && kw == 3) return dt == DT_BF16 && C % 8 == 0 && groups8 ? "depthwise_tiled8<3x3>" : "depthwise_tiled<3x3>";

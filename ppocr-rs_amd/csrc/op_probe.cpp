@@ -114,15 +114,18 @@ int run_conv(const float* x, int n, int h, int w, int c, const float* weight, co
 // ppocr_probe_depthwise, and with se_rows the SE channel sums the layer
 // leaves: *se_rows = depthwise_se_blocks() and se_part [n][*se_rows][c].
 int run_depthwise(const float* x, int n, int h, int w, int c, const float* weight, const float* bias, int k, int act,
-                  const float* res, int dt, int table, float* out, int* se_rows, float* se_part) {
+                  const float* res, int dt, int table, float* out, int* se_rows, float* se_part, int sh = 1,
+                  int sw = 1) {
   const size_t px = (size_t)n * h * w;
+  const int ho = (h + 2 * (k / 2) - k) / sh + 1, wo = (w + 2 * (k / 2) - k) / sw + 1;
+  const size_t opx = (size_t)n * ho * wo;
   std::vector<float> packed((size_t)k * k * c);
   for (int ch = 0; ch < c; ++ch)
     for (int t = 0; t < k * k; ++t) packed[(size_t)t * c + ch] = weight[(size_t)ch * k * k + t];
   void* d_in = upload(x, px * c, dt);
   void* d_wt = upload(packed.data(), packed.size(), ppocr::DT_F32);
   void* d_bias = bias ? upload(bias, c, ppocr::DT_F32) : nullptr;
-  void* d_res = res ? upload(res, px * c, dt) : nullptr;
+  void* d_res = res ? upload(res, opx * c, dt) : nullptr;
   void *d_out = nullptr, *d_tab = nullptr, *d_se = nullptr;
   int rc = 0;
   const size_t es = dt == ppocr::DT_BF16 ? 2 : 4;
@@ -133,17 +136,17 @@ int run_depthwise(const float* x, int n, int h, int w, int c, const float* weigh
         hipMemcpy(d_tab, tab.data(), tab.size() * 2, hipMemcpyHostToDevice) != hipSuccess)
       rc = 1;
   }
-  if (rc || !d_in || !d_wt || (bias && !d_bias) || (res && !d_res) || hipMalloc(&d_out, px * c * es) != hipSuccess) {
+  if (rc || !d_in || !d_wt || (bias && !d_bias) || (res && !d_res) || hipMalloc(&d_out, opx * c * es) != hipSuccess) {
     rc = 1;
   } else {
     ppocr::DwParams p{};
     p.in = d_in;
     p.N = n, p.H = h, p.W = w, p.C = c, p.in_ps = c;
     p.out = d_out;
-    p.Ho = h, p.Wo = w, p.out_ps = c;
+    p.Ho = ho, p.Wo = wo, p.out_ps = c;
     p.wt = static_cast<const float*>(d_wt);
     p.bias = static_cast<const float*>(d_bias);
-    p.kh = p.kw = k, p.sh = p.sw = 1, p.pt = p.pl = k / 2;
+    p.kh = p.kw = k, p.sh = sh, p.sw = sw, p.pt = p.pl = k / 2;
     p.act = act;
     p.res = d_res;
     p.res_ps = c;
@@ -162,10 +165,10 @@ int run_depthwise(const float* x, int n, int h, int w, int c, const float* weigh
       rc = 1;
     if (rc == 0) {
       if (dt == ppocr::DT_BF16) {
-        std::vector<uint16_t> hb(px * c);
+        std::vector<uint16_t> hb(opx * c);
         if (hipMemcpy(hb.data(), d_out, hb.size() * 2, hipMemcpyDeviceToHost) != hipSuccess) rc = 1;
         for (size_t i = 0; i < hb.size(); ++i) out[i] = from_bf16(hb[i]);
-      } else if (hipMemcpy(out, d_out, px * c * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+      } else if (hipMemcpy(out, d_out, opx * c * 4, hipMemcpyDeviceToHost) != hipSuccess) {
         rc = 1;
       }
     }
@@ -331,6 +334,19 @@ const char* ppocr_probe_conv_kernel(int n, int h, int w, int c, int co, int kh, 
 int ppocr_probe_depthwise(const float* x, int n, int h, int w, int c, const float* weight, const float* bias, int k,
                           int act, const float* res, int dt, int table, float* out) {
   return run_depthwise(x, n, h, w, c, weight, bias, k, act, res, dt, table, out, nullptr, nullptr);
+}
+
+// A 3x3 depthwise (pads 1, no residual, no table) with strides (sh, sw):
+// out [n][(h - 1) / sh + 1][(w - 1) / sw + 1][c].  Returns 0, or 1 on a HIP
+// error.
+int ppocr_probe_depthwise_strided(const float* x, int n, int h, int w, int c, const float* weight, const float* bias,
+                                  int sh, int sw, int act, int dt, float* out) {
+  return run_depthwise(x, n, h, w, c, weight, bias, 3, act, nullptr, dt, 0, out, nullptr, nullptr, sh, sw);
+}
+
+// The kernel instance ppocr_probe_depthwise_strided runs.
+const char* ppocr_probe_depthwise_strided_kernel(int h, int c, int sh, int sw, int dt) {
+  return ppocr::depthwise_kernel_name(3, 3, sh, sw, (h - 1) / sh + 1, dt, false, c);
 }
 
 // ppocr_probe_depthwise (no residual, no table) also leaving the SE channel

@@ -305,3 +305,47 @@ def test_tiled_depthwise_se_sums_match_stored_outputs(case):
     ref = depthwise_ref(bf16_round(x) if dt else x, w, b, ACT_NONE, None)
     tol = (2.0 ** -8 if dt else 1e-5) * np.abs(ref) + 1e-5
     assert np.all(np.abs(out - ref) <= tol)
+
+
+# (n, h, w, c, sh, sw, dt, kernel): 3x3 stage-entry depthwise layers (pads
+# 1) with vertical stride 2: bf16 ones on the 8-channel tiled kernel
+# (stride (2, 1), the recognizer's, with the output height's tile rows;
+# stride (2, 2), the detector's, with 4-row tiles), fp32 on the strips;
+# row, column and channel-block tails.
+DW_STRIDED_CASES = [
+    (4, 12, 80, 256, 2, 1, 1, "depthwise_tiled8<3x3,s2>"),
+    (4, 6, 37, 64, 2, 1, 1, "depthwise_tiled8<3x3,s2>"),
+    (2, 13, 23, 96, 2, 1, 1, "depthwise_tiled8<3x3,s2>"),
+    (2, 52, 92, 128, 2, 2, 1, "depthwise_tiled8<3x3,s2>"),
+    (1, 27, 45, 24, 2, 2, 1, "depthwise_tiled8<3x3,s2>"),
+    (2, 12, 30, 32, 2, 2, 0, "depthwise_strip<3x3,s2>"),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", DW_STRIDED_CASES,
+                         ids=lambda c: "x".join(map(str, c[:4])) + f"-s{c[4]}{c[5]}" + ("-bf16" if c[6] else "-f32"))
+def test_strided_depthwise_matches_float64(case):
+    """Stride (sh, sw) with pads 1 is the stride-1 'same' convolution taken
+    at every sh-th row and sw-th column."""
+    n, h, wd, c, sh, sw, dt, want_kernel = case
+    lib = _lib()
+    f = ctypes.POINTER(ctypes.c_float)
+    i = ctypes.c_int
+    lib.ppocr_probe_depthwise_strided.argtypes = [f, i, i, i, i, f, f, i, i, i, i, f]
+    lib.ppocr_probe_depthwise_strided.restype = i
+    lib.ppocr_probe_depthwise_strided_kernel.argtypes = [i, i, i, i, i]
+    lib.ppocr_probe_depthwise_strided_kernel.restype = ctypes.c_char_p
+    assert lib.ppocr_probe_depthwise_strided_kernel(h, c, sh, sw, dt).decode() == want_kernel
+    rng = np.random.default_rng(11 + h + wd + c + sw)
+    x = rng.uniform(-1, 1, (n, h, wd, c)).astype(np.float32)
+    w = rng.uniform(-0.5, 0.5, (c, 3, 3)).astype(np.float32)
+    b = rng.uniform(-0.5, 0.5, c).astype(np.float32)
+    ho, wo = (h - 1) // sh + 1, (wd - 1) // sw + 1
+    out = np.full((n, ho, wo, c), np.nan, np.float32)
+    assert lib.ppocr_probe_depthwise_strided(_ptr(x), n, h, wd, c, _ptr(w), _ptr(b), sh, sw, ACT_HSWISH, dt,
+                                             _ptr(out)) == 0
+    ref = depthwise_ref(bf16_round(x) if dt else x, w, b, ACT_HSWISH, None)[:, ::sh, ::sw]
+    tol = (2.0 ** -8 if dt else 1e-5) * np.abs(ref) + 1e-5
+    err = np.abs(out - ref)
+    assert np.all(err <= tol), (float(err.max()), np.unravel_index(np.argmax(err - tol), err.shape))
