@@ -88,11 +88,15 @@ __global__ __launch_bounds__(256) void depthwise_kernel(DwParams p) {
 // tiles of 16 channels (less halo per output row; measured faster than
 // wider XR, which costs occupancy).  Taps accumulate in (ky, kx) order as
 // the generic kernel does.
-template <typename T, int KH, int KW, int TY, int XR = 4, int C4B = 8>
+// SH, SW: the layer's strides (the input tile spans (TY - 1) SH + KH rows
+// and (TX - 1) SW + KW columns; the gate-residual prologue is stride 1).
+template <typename T, int KH, int KW, int TY, int XR = 4, int C4B = 8, int SH = 1, int SW = 1>
 __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
   constexpr int XG = 256 / (C4B * TY);    // lane groups along x
   constexpr int TX = XG * XR;
-  constexpr int IH = TY + KH - 1, IW = TX + KW - 1;
+  constexpr int IH = (TY - 1) * SH + KH, IW = (TX - 1) * SW + KW;
+  constexpr int WN = (XR - 1) * SW + KW;  // input pixels of a lane's window row
+  static_assert(KH != 7 || (SH == 1 && SW == 1), "the gate-residual prologue is stride 1");
   constexpr int IWP = IW | 1;  // odd row pitch (pixels)
   __shared__ float4 tile[IH * IWP * C4B];
   __shared__ float4 taps[KH * KW * C4B];
@@ -173,7 +177,7 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
     for (int i = 0; i < NL; ++i) {
       const int px = tid / C4B + i * STEP;
       const int iy = px / IW, ix = px - iy * IW;
-      const int gy = oy0 - p.pt + iy, gx = ox0 - p.pl + ix;
+      const int gy = oy0 * SH - p.pt + iy, gx = ox0 * SW - p.pl + ix;
       v[i] = f4_zero();
       if (px < IH * IW && cok && (unsigned)gy < (unsigned)p.H && (unsigned)gx < (unsigned)p.W)
         v[i] = ld4<T>(base + ((size_t)gy * p.W + gx) * p.in_ps);
@@ -202,18 +206,18 @@ __global__ __launch_bounds__(256) void depthwise_tiled_kernel(DwParams p) {
   // One row window live at a time keeps the kernel free of register spills.
 #pragma unroll 1
   for (int ky = 0; ky < KH; ++ky) {
-    float4 win[XR + KW - 1];
+    float4 win[WN];
 #pragma unroll
-    for (int j = 0; j < XR + KW - 1; ++j) win[j] = tile[((ty + ky) * IWP + xg * XR + j) * C4B + c4];
+    for (int j = 0; j < WN; ++j) win[j] = tile[((ty * SH + ky) * IWP + xg * XR * SW + j) * C4B + c4];
 #pragma unroll
     for (int kx = 0; kx < KW; ++kx) {
       float4 w = taps[(ky * KW + kx) * C4B + c4];
 #pragma unroll
       for (int r = 0; r < XR; ++r) {
-        acc[r].x = fmaf(win[r + kx].x, w.x, acc[r].x);
-        acc[r].y = fmaf(win[r + kx].y, w.y, acc[r].y);
-        acc[r].z = fmaf(win[r + kx].z, w.z, acc[r].z);
-        acc[r].w = fmaf(win[r + kx].w, w.w, acc[r].w);
+        acc[r].x = fmaf(win[r * SW + kx].x, w.x, acc[r].x);
+        acc[r].y = fmaf(win[r * SW + kx].y, w.y, acc[r].y);
+        acc[r].z = fmaf(win[r * SW + kx].z, w.z, acc[r].z);
+        acc[r].w = fmaf(win[r * SW + kx].w, w.w, acc[r].w);
       }
     }
   }
@@ -859,12 +863,12 @@ static void launch_dw_strip(const DwParams& p, hipStream_t s) {
   hipLaunchKernelGGL((depthwise_strip_kernel<T, KH, KW, R, SH>), dim3(blocks_for(total)), dim3(256), 0, s, p);
 }
 
-template <typename T, int KH, int KW, int TY, int XR = 4, int C4B = 8>
+template <typename T, int KH, int KW, int TY, int XR = 4, int C4B = 8, int SH = 1, int SW = 1>
 static void launch_dw_tiled(const DwParams& p, hipStream_t s) {
   constexpr int TX = 256 / (C4B * TY) * XR;
   const long tiles = (long)((p.Wo + TX - 1) / TX) * ((p.Ho + TY - 1) / TY) * p.N * ((p.C + 4 * C4B - 1) / (4 * C4B));
-  hipLaunchKernelGGL((depthwise_tiled_kernel<T, KH, KW, TY, XR, C4B>), dim3((unsigned)((tiles + 7) / 8 * 8)), dim3(256),
-                     0, s, p);
+  hipLaunchKernelGGL((depthwise_tiled_kernel<T, KH, KW, TY, XR, C4B, SH, SW>), dim3((unsigned)((tiles + 7) / 8 * 8)),
+                     dim3(256), 0, s, p);
 }
 
 template <typename T, int KH, int KW>
@@ -946,18 +950,26 @@ static void launch_dw_typed(const DwParams& p, hipStream_t s) {
   // (the recognizer's last stage), where the LDS tile would load its halo
   // rows for only a few output rows: vertical strips.
   if (p.kh == 3 && p.kw == 3 && p.sh == 2) {
-    // bf16 stage entries on the 8-channel tiled kernel: stride (2, 1) (the
-    // recognizer's) with the stride-1 tile rows of the output height,
-    // stride (2, 2) (the detector's) with 4-row tiles of one output per
-    // lane (1.66-1.85x and 1.38-1.72x over the strips, identical outputs).
-    if constexpr (sizeof(T) == 2) {
-      if (dw3_tiled8(p) && p.sw == 2) return launch_dw_tiled8<3, 3, 4, 1, kDw3C4B, 2, 2>(p, s);
-      if (dw3_tiled8(p) && p.sw == 1) {
-        const int ty = dw3_ty(DT_BF16, p.Ho);
-        return ty == 2   ? launch_dw_tiled8<3, 3, 2, kDw3XR, kDw3C4B, 2, 1>(p, s)
-               : ty == 4 ? launch_dw_tiled8<3, 3, 4, kDw3XR, kDw3C4B, 2, 1>(p, s)
-                         : launch_dw_tiled8<3, 3, 8, kDw3XR, kDw3C4B, 2, 1>(p, s);
-      }
+    // Stage entries on the tiled kernels: stride (2, 1) (the recognizer's)
+    // with the bf16 stride-1 tile rows of the output height, stride (2, 2)
+    // (the detector's) with 4-row tiles of one output per lane (over the
+    // strips, identical outputs: bf16 on the 8-channel kernel 1.66-1.85x
+    // and 1.38-1.72x, fp32 1.06-1.12x and 1.10-1.37x).
+    if (p.sw == 2) {
+      if constexpr (sizeof(T) == 2)
+        if (dw3_tiled8(p)) return launch_dw_tiled8<3, 3, 4, 1, kDw3C4B, 2, 2>(p, s);
+      return launch_dw_tiled<T, 3, 3, 4, 1, kDw3C4B, 2, 2>(p, s);
+    }
+    if (p.sw == 1) {
+      const int ty = dw3_ty(DT_BF16, p.Ho);
+      if constexpr (sizeof(T) == 2)
+        if (dw3_tiled8(p))
+          return ty == 2   ? launch_dw_tiled8<3, 3, 2, kDw3XR, kDw3C4B, 2, 1>(p, s)
+                 : ty == 4 ? launch_dw_tiled8<3, 3, 4, kDw3XR, kDw3C4B, 2, 1>(p, s)
+                           : launch_dw_tiled8<3, 3, 8, kDw3XR, kDw3C4B, 2, 1>(p, s);
+      return ty == 2   ? launch_dw_tiled<T, 3, 3, 2, kDw3XR, kDw3C4B, 2, 1>(p, s)
+             : ty == 4 ? launch_dw_tiled<T, 3, 3, 4, kDw3XR, kDw3C4B, 2, 1>(p, s)
+                       : launch_dw_tiled<T, 3, 3, 8, kDw3XR, kDw3C4B, 2, 1>(p, s);
     }
     return launch_dw_strip<T, 3, 3, 3, 2>(p, s);
   }
@@ -999,7 +1011,9 @@ const char* depthwise_kernel_name(int kh, int kw, int sh, int sw, int Ho, int dt
   if (table && depthwise_uses_mfma(kh, kw, sh, sw, dt, Ho, C))
     return kh == 5 ? "depthwise_mfma<5x5>" : kh == 7 ? "depthwise_mfma<7x7>" : "depthwise_mfma<9x9>";
   if (kh == 3 && kw == 3 && sh == 2)
-    return dt == DT_BF16 && C % 8 == 0 && groups8 && sw <= 2 ? "depthwise_tiled8<3x3,s2>" : "depthwise_strip<3x3,s2>";
+    return sw > 2                                     ? "depthwise_strip<3x3,s2>"
+           : dt == DT_BF16 && C % 8 == 0 && groups8 ? "depthwise_tiled8<3x3,s2>"
+                                                      : "depthwise_tiled<3x3,s2>";
   if (kh == 3 && kw == 3 && sh == 1 && !dw3_tiled_rows(dt, Ho)) return "depthwise_strip<3x3>";
   if (sh == 1 && sw == 1) {
     if (kh == 3 && kw == 3) return dt == DT_BF16 && C % 8 == 0 && groups8 ? "depthwise_tiled8<3x3>" : "depthwise_tiled<3x3>";

@@ -308,17 +308,20 @@ def test_tiled_depthwise_se_sums_match_stored_outputs(case):
 
 
 # (n, h, w, c, sh, sw, dt, kernel): 3x3 stage-entry depthwise layers (pads
-# 1) with vertical stride 2: bf16 ones on the 8-channel tiled kernel
-# (stride (2, 1), the recognizer's, with the output height's tile rows;
-# stride (2, 2), the detector's, with 4-row tiles), fp32 on the strips;
-# row, column and channel-block tails.
+# 1) with vertical stride 2 on the tiled kernels (bf16 on the 8-channel
+# form, fp32 on the 4-channel one): stride (2, 1), the recognizer's, with
+# the output height's tile rows; stride (2, 2), the detector's, with 4-row
+# tiles; row, column and channel-block tails.
 DW_STRIDED_CASES = [
     (4, 12, 80, 256, 2, 1, 1, "depthwise_tiled8<3x3,s2>"),
     (4, 6, 37, 64, 2, 1, 1, "depthwise_tiled8<3x3,s2>"),
     (2, 13, 23, 96, 2, 1, 1, "depthwise_tiled8<3x3,s2>"),
     (2, 52, 92, 128, 2, 2, 1, "depthwise_tiled8<3x3,s2>"),
     (1, 27, 45, 24, 2, 2, 1, "depthwise_tiled8<3x3,s2>"),
-    (2, 12, 30, 32, 2, 2, 0, "depthwise_strip<3x3,s2>"),
+    (2, 12, 30, 32, 2, 2, 0, "depthwise_tiled<3x3,s2>"),
+    (3, 13, 41, 36, 2, 2, 0, "depthwise_tiled<3x3,s2>"),
+    (4, 6, 50, 96, 2, 1, 0, "depthwise_tiled<3x3,s2>"),
+    (4, 12, 21, 48, 2, 1, 0, "depthwise_tiled<3x3,s2>"),
 ]
 
 
