@@ -2038,8 +2038,12 @@ int conv_tile_cols(int M, int cols, int dt) {
 // CUs holding two tiles set the time: splits for about eight workgroups per
 // CU (measured on the detector's 13x23 and 52x92 layers: 1.2-1.4x faster
 // with the finish pass included; shallower K or more tiles measured
-// slower).  Each split keeps at least 8 K slices (the load pipeline is 3-4
-// slices deep), at most 16 splits.
+// slower).  fp32 layers keep that up to 640 tiles (the batch-1 medium
+// detector's 104x184 3x3 layers with 64 output channels, 598 tiles: head
+// conv_down 1.26x, stem3 1.08x; the same bf16 layers measured 0.7-0.8x
+// split, their faster MFMAs leaving less to share).  Each split keeps at
+// least 8 K slices (the load pipeline is 3-4 slices deep), at most 16
+// splits.
 int conv_split_k(int M, int Co, int K, int dt) {
   const int t = pick_tile(M, Co, dt);
   const long tiles = (long)((M + kTileBM[t] - 1) / kTileBM[t]) * ((Co + kTileBN[t] - 1) / kTileBN[t]);
@@ -2049,7 +2053,7 @@ int conv_split_k(int M, int Co, int K, int dt) {
   long s;
   if (tiles < 192)
     s = (512 + tiles - 1) / tiles;
-  else if (tiles <= 560 && nk >= 48)
+  else if (tiles <= (dt == DT_F32 ? 640 : 560) && nk >= 48)
     s = (2048 + tiles - 1) / tiles;
   else
     return 1;
