@@ -2040,8 +2040,11 @@ int conv_tile_cols(int M, int cols, int dt) {
 // with the finish pass included; shallower K or more tiles measured
 // slower).  fp32 layers keep that up to 640 tiles (the batch-1 medium
 // detector's 104x184 3x3 layers with 64 output channels, 598 tiles: head
-// conv_down 1.26x, stem3 1.08x; the same bf16 layers measured 0.7-0.8x
-// split, their faster MFMAs leaving less to share).  Each split keeps at
+// conv_down 1.22x, stem3 1.11x; the same bf16 layers measured 0.7-0.8x
+// split, their faster MFMAs leaving less to share), with splits for about
+// four workgroups per CU (its 26x46 layers: 1024 -> 512 split 7 ways took
+// 1.09x the unsplit time, 4 ways 1.01x; 13x23 896 -> 1792 4 ways 0.92x,
+// 7 ways 0.96x).  Each split keeps at
 // least 8 K slices (the load pipeline is 3-4 slices deep), at most 16
 // splits.
 int conv_split_k(int M, int Co, int K, int dt) {
@@ -2054,7 +2057,7 @@ int conv_split_k(int M, int Co, int K, int dt) {
   if (tiles < 192)
     s = (512 + tiles - 1) / tiles;
   else if (tiles <= (dt == DT_F32 ? 640 : 560) && nk >= 48)
-    s = (2048 + tiles - 1) / tiles;
+    s = ((dt == DT_F32 ? 1024 : 2048) + tiles - 1) / tiles;
   else
     return 1;
   s = std::min<long>(s, nk / 8);
