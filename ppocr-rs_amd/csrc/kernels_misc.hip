@@ -1826,12 +1826,17 @@ __global__ __launch_bounds__(1024) void softmax_rows_kernel(float* x, int cols) 
   for (int i = threadIdx.x; i < cols; i += blockDim.x) row[i] = fast_exp(row[i] - m) * rcp;
 }
 
-// Even row lengths up to 2048 * PER (the recognizers' 6.9k-18.7k classes):
-// the row is read once into registers (PER float2 per thread; rows are
-// 8-byte aligned), so it crosses HBM once each way instead of being read
-// for the maximum, again for the sum and again for the store.
-template <int PER>
-__global__ __launch_bounds__(1024) void softmax_rows_reg_kernel(float* x, int cols) {
+// Even row lengths up to 2 * NT * PER (the recognizers' 6.9k-18.7k
+// classes): the row is read once into registers (PER float2 per thread;
+// rows are 8-byte aligned), so it crosses HBM once each way instead of being
+// read for the maximum, again for the sum and again for the store.  NT = 1024
+// threads for few rows (latency); 256 for 2048 rows or more of up to 8192
+// classes (80 VGPRs: six blocks per CU instead of two, so that other rows
+// load while one block reduces; tiny recognizer at batch 64 1.008x).  The
+// 256-thread form of longer rows holds 40 float2 a thread in 176 VGPRs,
+// two blocks per CU, and measured even to 0.998x (18.7k classes).
+template <int PER, int NT = 1024>
+__global__ __launch_bounds__(NT) void softmax_rows_reg_kernel(float* x, int cols) {
   __shared__ float red[16];
   float2* row = reinterpret_cast<float2*>(x + (size_t)blockIdx.x * cols);
   const int n2 = cols >> 1;
@@ -1839,7 +1844,7 @@ __global__ __launch_bounds__(1024) void softmax_rows_reg_kernel(float* x, int co
   float m = -INFINITY;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const int i = threadIdx.x + j * 1024;
+    const int i = threadIdx.x + j * NT;
     v[j] = i < n2 ? row[i] : make_float2(-INFINITY, -INFINITY);
     m = fmaxf(m, fmaxf(v[j].x, v[j].y));
   }
@@ -1847,7 +1852,7 @@ __global__ __launch_bounds__(1024) void softmax_rows_reg_kernel(float* x, int co
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    if (threadIdx.x + j * 1024 < n2) {
+    if (threadIdx.x + j * NT < n2) {
       v[j].x = fast_exp(v[j].x - m);
       v[j].y = fast_exp(v[j].y - m);
       s += v[j].x + v[j].y;
@@ -1857,7 +1862,7 @@ __global__ __launch_bounds__(1024) void softmax_rows_reg_kernel(float* x, int co
   const float rcp = 1.0f / s;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const int i = threadIdx.x + j * 1024;
+    const int i = threadIdx.x + j * NT;
     if (i < n2) row[i] = make_float2(v[j].x * rcp, v[j].y * rcp);
   }
 }
@@ -1866,7 +1871,10 @@ void launch_softmax_rows(float* x, long rows, int cols, hipStream_t s) {
   const int per = (cols / 2 + 1023) / 1024;
   const bool even = cols % 2 == 0 && reinterpret_cast<uintptr_t>(x) % 8 == 0;
   const dim3 grid((unsigned)rows), block(1024);
-  if (even && per <= 4)
+  const int per256 = (cols / 2 + 255) / 256;
+  if (even && rows >= 2048 && per256 <= 16)
+    hipLaunchKernelGGL((softmax_rows_reg_kernel<16, 256>), grid, dim3(256), 0, s, x, cols);
+  else if (even && per <= 4)
     hipLaunchKernelGGL(softmax_rows_reg_kernel<4>, grid, block, 0, s, x, cols);
   else if (even && per <= 10)
     hipLaunchKernelGGL(softmax_rows_reg_kernel<10>, grid, block, 0, s, x, cols);
