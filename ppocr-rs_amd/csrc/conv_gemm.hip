@@ -910,38 +910,21 @@ __device__ __forceinline__ void finish_db_regs(const ConvParams& p, floatx4 (&ac
 // as inline assembly, which the compiler's wait insertion does not see (it
 // would otherwise wait for every load in flight before each read).
 
-typedef int int32x4_t __attribute__((ext_vector_type(4)));
-
 // Offset past the end of every buffer the direct kernel reads (their sizes
 // are checked below 2^31 bytes at launch): loads there return zero.
 constexpr unsigned kOutOfRange = 0x80000000u;
-
-// Raw buffer resource over `bytes` bytes at `base` (stride 0, 32-bit
-// format): the descriptor of the gfx9 family.
-__device__ __forceinline__ int32x4_t buffer_resource(const void* base, unsigned bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  int32x4_t r;
-  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-  r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu));
-  r.z = __builtin_amdgcn_readfirstlane((int)bytes);
-  r.w = 0x00020000;
-  return r;
-}
 
 __device__ void llvm_raw_buffer_load_lds(int32x4_t rsrc, __attribute__((address_space(3))) uint32_t* lds, int size,
                                          int voffset, int soffset, int offset,
                                          int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
 
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2v __attribute__((ext_vector_type(2)));
 __device__ u32x2 llvm_raw_buffer_load_v2i32(int32x4_t rsrc, int voffset, int soffset,
                                             int aux) __asm("llvm.amdgcn.raw.buffer.load.v2i32");
 __device__ floatx4 llvm_raw_buffer_load_v4f32(int32x4_t rsrc, int voffset, int soffset,
                                               int aux) __asm("llvm.amdgcn.raw.buffer.load.v4f32");
 __device__ void llvm_raw_buffer_store_v2i32(u32x2 v, int32x4_t rsrc, int voffset, int soffset,
                                             int aux) __asm("llvm.amdgcn.raw.buffer.store.v2i32");
-__device__ void llvm_raw_buffer_store_v2f32(f32x2v v, int32x4_t rsrc, int voffset, int soffset,
-                                            int aux) __asm("llvm.amdgcn.raw.buffer.store.v2f32");
 typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
 __device__ u32x4v llvm_raw_buffer_load_v4i32(int32x4_t rsrc, int voffset, int soffset,
                                              int aux) __asm("llvm.amdgcn.raw.buffer.load.v4i32");

@@ -18,6 +18,29 @@ namespace ppocr {
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
+// Raw buffer access: vector memory instructions through a buffer resource,
+// with a 32-bit lane offset and a wave-uniform offset in a scalar register
+// (no 64-bit address per access), range-checked by the hardware: loads past
+// the resource's size return zero and stores there are dropped.
+typedef int int32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+
+// Raw buffer resource over `bytes` bytes at `base` (stride 0, 32-bit
+// format): the descriptor of the gfx9 family.
+__device__ __forceinline__ int32x4_t buffer_resource(const void* base, unsigned bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  int32x4_t r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu));
+  r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+  r.w = 0x00020000;
+  return r;
+}
+__device__ f32x2v llvm_raw_buffer_load_v2f32(int32x4_t rsrc, int voffset, int soffset,
+                                             int aux) __asm("llvm.amdgcn.raw.buffer.load.v2f32");
+__device__ void llvm_raw_buffer_store_v2f32(f32x2v v, int32x4_t rsrc, int voffset, int soffset,
+                                            int aux) __asm("llvm.amdgcn.raw.buffer.store.v2f32");
+
 // Merges two partial softmax reductions (max m, sum of exp(x - m), last index
 // of the max) into (m, s, i).  Empty partials (s == 0, m = -inf) contribute
 // nothing; equal maxima keep the larger index.

@@ -1830,22 +1830,28 @@ __global__ __launch_bounds__(1024) void softmax_rows_kernel(float* x, int cols) 
 // classes): the row is read once into registers (PER float2 per thread;
 // rows are 8-byte aligned), so it crosses HBM once each way instead of being
 // read for the maximum, again for the sum and again for the store.  NT = 1024
-// threads for few rows (latency); 256 for 2048 rows or more of up to 8192
-// classes (80 VGPRs: six blocks per CU instead of two, so that other rows
-// load while one block reduces; tiny recognizer at batch 64 1.008x).  The
-// 256-thread form of longer rows holds 40 float2 a thread in 176 VGPRs,
-// two blocks per CU, and measured even to 0.998x (18.7k classes).
+// threads for few rows (latency); 256 for 2048 rows or more, so that other
+// rows load while one block reduces (50 VGPRs at PER = 16, eight blocks per
+// CU; 93 at PER = 40, five).
 template <int PER, int NT = 1024>
 __global__ __launch_bounds__(NT) void softmax_rows_reg_kernel(float* x, int cols) {
   __shared__ float red[16];
-  float2* row = reinterpret_cast<float2*>(x + (size_t)blockIdx.x * cols);
+  // The row through a buffer resource: the lane's byte offset 8 * tid in one
+  // register and chunk j's offset 8 * NT * j in a scalar one, so no 64-bit
+  // address per chunk stays live from the loads to the stores.  Accesses are
+  // limited to the row by the lane conditions (none rely on range checks).
+  const int32x4_t row = buffer_resource(x + (size_t)blockIdx.x * cols, (unsigned)cols * 4u);
   const int n2 = cols >> 1;
+  const int vo = (int)threadIdx.x * 8;
   float2 v[PER];
   float m = -INFINITY;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const int i = threadIdx.x + j * NT;
-    v[j] = i < n2 ? row[i] : make_float2(-INFINITY, -INFINITY);
+    v[j] = make_float2(-INFINITY, -INFINITY);
+    if ((int)threadIdx.x + j * NT < n2) {
+      const f32x2v u = llvm_raw_buffer_load_v2f32(row, vo, j * NT * 8, 0);
+      v[j] = make_float2(u.x, u.y);
+    }
     m = fmaxf(m, fmaxf(v[j].x, v[j].y));
   }
   m = block_reduce(m, red, true);
@@ -1861,10 +1867,11 @@ __global__ __launch_bounds__(NT) void softmax_rows_reg_kernel(float* x, int cols
   s = block_reduce(s, red, false);
   const float rcp = 1.0f / s;
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int i = threadIdx.x + j * NT;
-    if (i < n2) row[i] = make_float2(v[j].x * rcp, v[j].y * rcp);
-  }
+  for (int j = 0; j < PER; ++j)
+    if ((int)threadIdx.x + j * NT < n2) {
+      const f32x2v o = {v[j].x * rcp, v[j].y * rcp};
+      llvm_raw_buffer_store_v2f32(o, row, vo, j * NT * 8, 0);
+    }
 }
 
 void launch_softmax_rows(float* x, long rows, int cols, hipStream_t s) {
@@ -1874,6 +1881,8 @@ void launch_softmax_rows(float* x, long rows, int cols, hipStream_t s) {
   const int per256 = (cols / 2 + 255) / 256;
   if (even && rows >= 2048 && per256 <= 16)
     hipLaunchKernelGGL((softmax_rows_reg_kernel<16, 256>), grid, dim3(256), 0, s, x, cols);
+  else if (even && rows >= 2048 && per256 <= 40)
+    hipLaunchKernelGGL((softmax_rows_reg_kernel<40, 256>), grid, dim3(256), 0, s, x, cols);
   else if (even && per <= 4)
     hipLaunchKernelGGL(softmax_rows_reg_kernel<4>, grid, block, 0, s, x, cols);
   else if (even && per <= 10)
